@@ -1,0 +1,296 @@
+#!/usr/bin/env python3
+"""Benchmark of the paged-KV decode/verify hot path on one MI355X.
+
+Metric: paged decode-attention us/layer + HBM GB/s (% of
+peak) at 4K/32K context, verify k=4.  The headline `value` is the achieved
+algorithmic HBM throughput (GB/s) of a Llama-3-8B-shaped 32K-context decode
+layer-step (attention of one query over 32768 keys, 32 q / 8 KV heads,
+head_dim 128, block_size 16, fragmented 131072-block pool).  A step is one
+such layer-step; steps rotate over the 32 layers of the model (4 GiB of K/V)
+so the 256 MB Infinity Cache cannot hold the working set.
+
+Also reported: us per layer-step for all five BASELINE configs, the verify
+(k=4) / single-query step ratio at 4K, the cost of an O(1) rollback, the
+roofline of the dominant kernel (per-launch HIP-event durations), and the
+CPU oracle (oracle/sde_oracle.c, OpenMP) timed on a bounded sample.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import re
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E spec sheet
+HEADLINE = "llama3_8b_32k"
+KERNEL = "attn_partition_kernel"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse_args():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--cpu-seconds", type=float, default=10.0,
+                   help="approximate CPU work of the baseline sample")
+    p.add_argument("--only-headline", action="store_true")
+    return p.parse_args()
+
+
+class Timer:
+    """Per-launch HIP events on the current stream + a bracket around all."""
+
+    def __init__(self, torch, n):
+        self.torch = torch
+        self.ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                   for _ in range(n)]
+        self.t0 = torch.cuda.Event(enable_timing=True)
+        self.t1 = torch.cuda.Event(enable_timing=True)
+
+    def run(self, fn, steps, warmup, per_launch=True):
+        torch = self.torch
+        for i in range(warmup):
+            fn(i)
+        torch.cuda.synchronize()
+        self.t0.record()
+        for i in range(steps):
+            if per_launch:
+                self.ev[i][0].record()
+            fn(i)
+            if per_launch:
+                self.ev[i][1].record()
+        self.t1.record()
+        torch.cuda.synchronize()
+        total_ms = self.t0.elapsed_time(self.t1)
+        launch_ms = [s.elapsed_time(e) for s, e in self.ev[:steps]] if per_launch else []
+        return total_ms / steps, (float(np.mean(launch_ms)) if launch_ms else None)
+
+
+def make_rotation_cache(torch, W, w, n_layers, l_max, pool_blocks, seed):
+    """A cache of n_layers layers of l_max tokens each, tables a seeded
+    permutation of the pool, the whole pool filled with N(0,1) fp16."""
+    from speculative_decode_engine_amd import KVCache
+    nblk = -(-l_max // w.block_size)
+    rng = np.random.default_rng(seed)
+    tables = W.make_tables(rng, n_layers, nblk, pool_blocks)
+    cache = KVCache(n_layers, w.kv_dim, nblk, w.block_size, pool_blocks)
+    for l in range(n_layers):
+        cache.set_block_table(l, tables[l])
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    cache.pool.view(torch.float16).normal_(generator=g)
+    torch.cuda.synchronize()
+    return cache
+
+
+def bench_config(torch, W, w, steps, warmup, mode):
+    """Times one layer-step of workload w.  mode: 'attn' (attention only),
+    'decode' (append 1 + 1-query attention), 'verify' (append k+1 +
+    (k+1)-query causal attention).  Returns a dict."""
+    n_q = 1 if mode in ("attn", "decode") else w.n_queries
+    n_app = 0 if mode == "attn" else n_q
+    pos_base = w.ctx if mode != "attn" else w.l_max - 1
+    l_max = pos_base + n_q
+    # rotate over enough layers to exceed the Infinity Cache (>= 512 MiB)
+    per_layer = 4 * w.kv_dim * l_max
+    n_layers = max(1, min(w.n_layers, math.ceil(512 * 2 ** 20 / per_layer)))
+    nblk = -(-l_max // w.block_size)
+    pool_blocks = max(w.pool_blocks, n_layers * nblk)
+    cache = make_rotation_cache(torch, W, w, n_layers, l_max, pool_blocks, w.seed)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(w.seed + 100)
+    q = torch.randn(n_layers, n_q, w.nh * w.dph, device="cuda", generator=gen)
+    k = torch.randn(n_layers, max(n_app, 1), w.kv_dim, device="cuda", generator=gen)
+    v = torch.randn(n_layers, max(n_app, 1), w.kv_dim, device="cuda", generator=gen)
+    out = torch.empty(n_q, w.nh * w.dph, device="cuda")
+    ws = torch.empty(max(cache.workspace_size(w.nh, w.nkv, w.dph, n_q, l_max), 4) // 4 + 1,
+                     device="cuda")
+
+    def step(i):
+        l = i % n_layers
+        if n_app:
+            cache.append(l, k[l], v[l], pos_base)
+        cache.attention(l, q[l], w.nh, w.nkv, w.dph, pos_base, out=out, workspace=ws)
+
+    timer = Timer(torch, steps)
+    ms, launch_ms = timer.run(step, steps, warmup, per_launch=(n_app == 0))
+    nbytes = w.algorithmic_bytes(l_max=l_max, n_app=n_app, n_queries=n_q)
+    res = dict(mode=mode, n_queries=n_q, keys=l_max, rotated_layers=n_layers,
+               us_per_layer_step=round(ms * 1e3, 3), algorithmic_bytes=nbytes,
+               gbps=round(nbytes / (ms * 1e-3) / 1e9, 1),
+               frac_of_hbm_peak=round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+               flops=w.attention_flops(pos_base, n_q))
+    if launch_ms is not None:
+        res["kernel_us"] = round(launch_ms * 1e3, 3)
+        res["kernel_gbps"] = round(nbytes / (launch_ms * 1e-3) / 1e9, 1)
+    cache.free()
+    return res
+
+
+def bench_rollback(torch, W, steps=2000):
+    """us per O(1) rollback (host bookkeeping + one stream-ordered 4-byte
+    device write) at 4K and 32K context: must not depend on context."""
+    from speculative_decode_engine_amd import KVCache
+    out = {}
+    for ctx in (4096, 32768):
+        cache = KVCache(1, 1024, ctx // 16 + 1, 16, pool_blocks=ctx // 16 + 1, pool="library")
+        cache.set_seq_len(ctx + 5)
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        for i in range(steps):
+            cache.rollback(ctx + 1 + (i % 5) if i % 2 == 0 else ctx + 1)
+            cache.set_seq_len(ctx + 5)
+        torch.cuda.synchronize()
+        out[f"ctx{ctx}"] = round((time.perf_counter() - t) / (2 * steps) * 1e6, 3)
+        cache.free()
+    return out
+
+
+def cpu_baseline(W, w, seconds):
+    """The CPU oracle's tile restatement of attention.h (OpenMP over
+    (query, head) pairs) on one 32K-key layer-step of the same shape, run
+    repeatedly for about `seconds`."""
+    from oracle import paged_kv as O
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
+    rng = np.random.default_rng(w.seed)
+    l_max = w.l_max
+    nblk = l_max // w.block_size
+    pool = 2 * nblk
+    m = O.PagedKVModel(1, w.kv_dim, nblk, w.block_size, pool)
+    m.set_block_table(0, rng.permutation(pool)[:nblk])
+    m.pool[...] = (rng.standard_normal(m.pool.shape, dtype=np.float32)
+                   .astype(np.float16).view(np.uint16))
+    q = W.queries(rng, 1, w.nh, w.dph)
+    reps = 0
+    t0 = time.perf_counter()
+    while True:
+        m.attention(0, q, w.nh, w.nkv, w.dph, l_max - 1, mode="tiled", threads=threads)
+        reps += 1
+        if time.perf_counter() - t0 >= seconds:
+            break
+    dt = (time.perf_counter() - t0) / reps
+    nbytes = w.algorithmic_bytes(l_max=l_max, n_app=0, n_queries=1)
+    cpu_model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return dict(value=round(nbytes / dt / 1e9, 3), unit="GB/s", cores=threads, kind="port",
+                us_per_layer_step=round(dt * 1e6, 1),
+                sample=f"{reps} x one {l_max}-key layer-step ({w.nh}q/{w.nkv}kv heads, dph "
+                       f"{w.dph}, bs {w.block_size}), fp32 tile restatement of attention.h "
+                       f"in C, {threads} OpenMP threads, {cpu_model}")
+
+
+def measured_traffic(workload: str):
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE + WRITE_SIZE, copy-kernel calibrated), if present."""
+    f = ROOT / "profiles" / f"{KERNEL}_{workload}_traffic.md"
+    if not f.exists():
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", f.read_text())
+    return float(m.group(1)) if m else None
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); this build's "
+              "path is single-GPU, see DESIGN.md for how it would shard.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from speculative_decode_engine_amd import _native
+    from speculative_decode_engine_amd import workloads as W
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    _native.load()
+    torch.cuda.set_device(0)
+    steps, warmup = args.steps, args.warmup
+
+    w = W.CONFIGS[HEADLINE]
+    log(f"[bench] headline {HEADLINE}: {steps} steps, {warmup} warmup")
+    head = bench_config(torch, W, w, steps, warmup, "attn")
+    log("[bench]", json.dumps(head))
+
+    configs = {HEADLINE: head}
+    extra = {}
+    if not args.only_headline:
+        w3 = W.CONFIGS["llama3_8b_verify"]
+        ver = bench_config(torch, W, w3, steps, warmup, "verify")
+        dec = bench_config(torch, W, w3, steps, warmup, "decode")
+        att4 = bench_config(torch, W, w3, steps, warmup, "attn")
+        configs["llama3_8b_verify"] = ver
+        configs["llama3_8b_4k_decode"] = dec
+        configs["llama3_8b_4k_attn"] = att4
+        extra["verify_over_decode"] = round(ver["us_per_layer_step"] / dec["us_per_layer_step"], 3)
+        for name in ("tiny", "tinyllama"):
+            configs[name] = bench_config(torch, W, W.CONFIGS[name], steps, warmup, "decode")
+        w5 = W.CONFIGS["qwen25_7b_selfspec"]
+        configs["qwen25_7b_selfspec_verify"] = bench_config(torch, W, w5, steps, warmup, "verify")
+        configs["qwen25_7b_selfspec_draft"] = bench_config(torch, W, w5, steps, warmup, "decode")
+        extra["rollback_us"] = bench_rollback(torch, W)
+        for k_, v_ in configs.items():
+            log(f"[bench] {k_}: {v_['us_per_layer_step']} us/layer-step, {v_['gbps']} GB/s")
+
+    kernel_us = head["kernel_us"]
+    nbytes = head["algorithmic_bytes"]
+    achieved = nbytes / (kernel_us * 1e-6) / 1e9
+    roofline = dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBPS, unit="GB/s",
+                    frac=round(achieved / HBM_PEAK_GBPS, 4),
+                    traffic=measured_traffic(HEADLINE), kernel=KERNEL,
+                    bytes_per_launch=nbytes, kernel_us=kernel_us)
+
+    cpu = None
+    if not args.no_cpu:
+        log("[bench] cpu baseline ...")
+        cpu = cpu_baseline(W, w, args.cpu_seconds)
+        log("[bench] cpu", json.dumps(cpu))
+
+    line = {
+        "metric": "paged decode-attn us/layer + HBM GB/s (% peak) at ctx 4K/32K, verify k=4",
+        "value": head["gbps"],
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(head["us_per_layer_step"] / 1e3, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16 K/V, f32 q/accumulate",
+        "data": "synthetic: N(0,1) fp16 K/V filling the pool, N(0,1) fp32 q, seeded "
+                "fragmented block tables",
+        "config": {"workload": HEADLINE, "keys": head["keys"], "nh": w.nh, "nkv": w.nkv,
+                   "head_dim": w.dph, "block_size": w.block_size, "pool_blocks": w.pool_blocks,
+                   "rotated_layers": head["rotated_layers"], "us_per_layer_step":
+                       head["us_per_layer_step"], "frac_of_hbm_peak": head["frac_of_hbm_peak"]},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "configs": configs,
+        **extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

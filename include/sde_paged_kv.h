@@ -1,0 +1,200 @@
+/*
+ * sde_paged_kv.h — C-ABI of the MI355X (gfx950) paged KV cache and paged
+ * GQA decode/verify attention.
+ *
+ * Every entry point is plain C: opaque handles, raw device pointers, sizes,
+ * and a hipStream_t passed as `void*` (NULL = the default stream).  No entry
+ * point ever exits the process; each returns an `sde_status` code and does
+ * no device work when it rejects its arguments.
+ *
+ * Reference interface replaced (arkhamHack/speculative_decode_engine):
+ *   cuda/include/kv_cache.h:5-79       cache layout, host + device API
+ *   cuda/src/kv_cache.cu:8-120         alloc/free/reset/append/read/rollback
+ *   cuda/include/attention.h:21-164    device_flash_attention_gqa / dispatch
+ *   cuda/src/kernels.cu:546-548        set_seq_len_kernel
+ *   cuda/src/kernels.cu:826-844        cublas_kv_append_kernel
+ *   cuda/src/kernels.cu:904-940        cublas_attention_kernel
+ *
+ * Physical layout (identical to kv_cache.h:5-18 so cache bytes match the
+ * reference bit for bit): the pool is `pool_blocks` blocks; block b holds
+ *   K: fp16[block_size][kv_dim]   then   V: fp16[block_size][kv_dim]
+ * with all KV heads interleaved in each token row (kv_dim = n_kv_heads *
+ * head_dim).  Token `pos` of layer `l` lives in physical block
+ * table[l][pos / block_size], slot pos % block_size.
+ */
+#ifndef SDE_PAGED_KV_H
+#define SDE_PAGED_KV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct sde_kv_cache sde_kv_cache; /* opaque; owns tables + seq_len */
+typedef void* sde_stream_t;               /* hipStream_t, NULL = default   */
+
+typedef enum sde_status {
+  SDE_OK = 0,
+  SDE_ERR_INVALID_ARGUMENT = 1, /* null pointer, negative count, bad config  */
+  SDE_ERR_CAPACITY = 2,         /* position beyond the layer's mapped blocks */
+  SDE_ERR_RANGE = 3,            /* table entry outside pool, bad rollback    */
+  SDE_ERR_UNSUPPORTED = 4,      /* attention type / head_dim / block_size    */
+  SDE_ERR_WORKSPACE = 5,        /* caller workspace smaller than required    */
+  SDE_ERR_HIP = 6,              /* a HIP runtime call failed                 */
+  SDE_ERR_NO_DEVICE = 7         /* no usable gfx950 device                   */
+} sde_status;
+
+/* AttentionType values of cuda/include/config.h:51-56. */
+typedef enum sde_attention_type {
+  SDE_ATTN_SOFTMAX = 0,
+  SDE_ATTN_SLIDING_WINDOW = 1, /* reserved in the reference: unsupported */
+  SDE_ATTN_KDA = 2,            /* reserved in the reference: unsupported */
+  SDE_ATTN_LINEAR = 3          /* reserved in the reference: unsupported */
+} sde_attention_type;
+
+/* Runtime form of the reference's compile-time bounds (config.h:8-12) and
+ * of kv_cache_alloc's arguments (kv_cache.h:56-57).  pool_blocks == 0 means
+ * the reference sizing n_layers * max_blocks_per_layer (kv_cache.cu:15). */
+typedef struct sde_kv_config {
+  int32_t n_layers;
+  int32_t kv_dim;               /* reference KVCache::d_head (kv_cache.h:42) */
+  int32_t max_blocks_per_layer; /* reference MAX_KV_BLOCKS (config.h:12)     */
+  int32_t block_size;           /* reference KV_BLOCK_SIZE (config.h:10)     */
+  int32_t pool_blocks;          /* reference KVCache::pool_size              */
+} sde_kv_config;
+
+/* Device-side view of a cache, a plain POD like the reference KVCache that
+ * loop drivers copy by value into kernels (kernels.cu:3614-3630). */
+typedef struct sde_kv_view {
+  uint16_t* pool;        /* fp16 bits, pool_blocks * 2*block_size*kv_dim  */
+  int32_t* block_tables; /* [n_layers][max_blocks_per_layer]              */
+  int32_t* seq_len;      /* one int32 on the device (write-only bookkeeping) */
+  int32_t n_layers;
+  int32_t kv_dim;
+  int32_t block_size;
+  int32_t max_blocks_per_layer;
+  int32_t pool_blocks;
+  int32_t reserved;
+} sde_kv_view;
+
+/* Message for a status code; never NULL. */
+const char* sde_status_string(int status);
+
+/* Host-only check of a configuration (no device work).  Rules:
+ * n_layers, kv_dim, max_blocks_per_layer >= 1; block_size in [1, 1024];
+ * pool_blocks >= 0 (0 = reference sizing) and >= max_blocks_per_layer. */
+int sde_kv_config_validate(const sde_kv_config* cfg);
+
+/* Bytes of the pool a configuration needs (0 on an invalid config). */
+size_t sde_kv_pool_bytes(const sde_kv_config* cfg);
+
+/* kv_cache_alloc (kv_cache.h:56-57, kv_cache.cu:8-42): allocate and zero
+ * the pool, the per-layer tables and seq_len; layer l gets the reference's
+ * static assignment table[l][b] = l*max_blocks_per_layer + b when that fits
+ * the pool (otherwise tables start as -1 = unmapped).  seq_len = 0. */
+int sde_kv_cache_create(const sde_kv_config* cfg, sde_kv_cache** out);
+
+/* As sde_kv_cache_create, but the caller owns the pool memory (a device
+ * buffer of at least sde_kv_pool_bytes(cfg) bytes, 16-byte aligned).  The
+ * pool is not cleared.  No counterpart in the reference: it lets a host
+ * framework (e.g. a caching allocator) own the 8 GiB pools. */
+int sde_kv_cache_create_external(const sde_kv_config* cfg, void* d_pool,
+                                 size_t pool_bytes, sde_kv_cache** out);
+
+/* kv_cache_free (kv_cache.h:60, kv_cache.cu:44-48).  NULL is accepted. */
+int sde_kv_cache_destroy(sde_kv_cache* cache);
+
+/* kv_cache_reset (kv_cache.h:63, kv_cache.cu:50-52): seq_len = 0 on the
+ * host mirror and (stream-ordered) on the device.  Tables and pool kept. */
+int sde_kv_reset(sde_kv_cache* cache, sde_stream_t stream);
+
+/* Map logical blocks [0, n_blocks) of `layer` to physical blocks (host
+ * array).  Replaces the static assignment of kv_cache.cu:29-37; every entry
+ * must lie in [0, pool_blocks).  Synchronous. */
+int sde_kv_set_block_table(sde_kv_cache* cache, int layer,
+                           const int32_t* host_table, int n_blocks);
+
+/* Copy the first n_blocks entries of a layer's table to host memory. */
+int sde_kv_get_block_table(const sde_kv_cache* cache, int layer,
+                           int32_t* host_table, int n_blocks);
+
+/* Host mirror of KVCache::seq_len. */
+int sde_kv_seq_len(const sde_kv_cache* cache, int* out_len);
+
+/* Synchronous read of the device-side seq_len word (what the reference's
+ * loop drivers write, kernels.cu:2459, 3068-3069); for checks and tests. */
+int sde_kv_device_seq_len(const sde_kv_cache* cache, int* out_len);
+
+/* set_seq_len_kernel (kernels.cu:546-548): seq_len = len, on the host and
+ * stream-ordered on the device.  0 <= len <= capacity. */
+int sde_kv_set_seq_len(sde_kv_cache* cache, int len, sde_stream_t stream);
+
+/* kv_cache_rollback (kv_cache.h:79, kv_cache.cu:116-120) as used by the
+ * loop drivers (kernels.cu:2457-2459, 3068-3069): seq_len = target_len.
+ * O(1): moves no pool bytes; stale K/V are overwritten by later appends.
+ * Requires 0 <= target_len <= current seq_len. */
+int sde_kv_rollback(sde_kv_cache* cache, int target_len, sde_stream_t stream);
+
+/* cublas_kv_append_kernel (kernels.cu:826-844) / kv_cache_append
+ * (kv_cache.cu:70-93): write n_tokens fp32 K and V rows ([n_tokens][kv_dim]
+ * device arrays) as fp16 (round-to-nearest-even) at positions
+ * pos_base .. pos_base+n_tokens-1 of `layer`.  seq_len is not changed (the
+ * reference loop drivers advance it separately).  Every position must be
+ * mapped: pos_base + n_tokens <= mapped blocks * block_size.  n_tokens == 0
+ * is a no-op (the row pointers may then be NULL); so for the two below. */
+int sde_kv_append(sde_kv_cache* cache, int layer, const float* d_k,
+                  const float* d_v, int pos_base, int n_tokens,
+                  sde_stream_t stream);
+
+/* As sde_kv_append with fp16 rows (raw bits, [n_tokens][kv_dim]) copied
+ * without conversion.  No counterpart in the reference: a prefill helper
+ * that lands pre-quantised context rows. */
+int sde_kv_write_fp16(sde_kv_cache* cache, int layer, const uint16_t* d_k,
+                      const uint16_t* d_v, int pos_base, int n_tokens,
+                      sde_stream_t stream);
+
+/* kv_cache_read (kv_cache.cu:95-114) over a range: K[pos..pos+n) and
+ * V[pos..pos+n) of `layer` widened exactly to fp32 into [n][kv_dim]. */
+int sde_kv_gather(const sde_kv_cache* cache, int layer, int pos,
+                  int n_tokens, float* d_k, float* d_v, sde_stream_t stream);
+
+/* Device-side view (pointers + shape) for in-tree HIP callers. */
+int sde_kv_get_view(const sde_kv_cache* cache, sde_kv_view* out);
+
+/* Workspace bytes sde_paged_attention needs for any call with these head
+ * shapes, n_queries, and pos_base + n_queries <= max_total_len. */
+size_t sde_paged_attention_workspace_size(const sde_kv_cache* cache, int nh,
+                                          int nkv, int dph, int n_queries,
+                                          int max_total_len);
+
+/* cublas_attention_kernel (kernels.cu:904-940) + device_flash_attention_gqa
+ * (attention.h:21-127): causal paged GQA attention for n_queries queries.
+ * d_q, d_out: fp32 [n_queries][nh*dph] (q with RoPE applied).  Query m sees
+ * keys/values at positions [0, pos_base+m+1) of `layer`; query head h reads
+ * KV head h*nkv/nh (attention.h:37); scale dph^-1/2.  n_queries = 1 is a
+ * decode step, n_queries = k+1 the speculative verify window.
+ * d_workspace may be NULL (the cache then keeps its own, grown on demand);
+ * otherwise it must hold sde_paged_attention_workspace_size(...) bytes.
+ * Supported: dph in {64, 128}, block_size a multiple of 8, nkv | nh,
+ * n_queries * nh/nkv <= 64. */
+int sde_paged_attention(sde_kv_cache* cache, int layer, const float* d_q,
+                        float* d_out, int nh, int nkv, int dph, int pos_base,
+                        int n_queries, void* d_workspace,
+                        size_t workspace_bytes, sde_stream_t stream);
+
+/* device_attention_dispatch (attention.h:140-164) as a host entry point:
+ * SDE_ATTN_SOFTMAX runs sde_paged_attention; the reserved types return
+ * SDE_ERR_UNSUPPORTED (where the reference traps) and launch nothing. */
+int sde_attention_dispatch(int attn_type, sde_kv_cache* cache, int layer,
+                           const float* d_q, float* d_out, int nh, int nkv,
+                           int dph, int pos_base, int n_queries,
+                           void* d_workspace, size_t workspace_bytes,
+                           sde_stream_t stream);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* SDE_PAGED_KV_H */

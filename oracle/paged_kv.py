@@ -1,0 +1,240 @@
+"""CPU oracle for the paged-KV hot path (TEST INFRASTRUCTURE ONLY).
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
+import this module, and only as the checker or the timed CPU baseline.
+
+Two layers:
+  * `lib()`: the C restatement in oracle/sde_oracle.c (built by
+    oracle/Makefile into oracle/_build/libsde_oracle.so): fp16 conversion,
+    append / gather on a raw pool, the literal tile-by-tile attention of
+    attention.h:21-127, and an fp64 brute force.
+  * `PagedKVModel`: the cache state as numpy bytes (pool + tables + seq_len)
+    driven through the C functions, for scripted append / rollback / re-append
+    sequences checked bit for bit (kv_cache.cu:70-120, kernels.cu:2457-2466).
+And `attention_f64_np`, an independent vectorised numpy softmax attention
+over gathered (contiguous) K/V.
+
+Reference: arkhamHack/speculative_decode_engine, cuda/include/kv_cache.h,
+cuda/src/kv_cache.cu, cuda/include/attention.h, cuda/src/kernels.cu.
+"""
+from __future__ import annotations
+
+import ctypes
+import hashlib
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "_build" / "libsde_oracle.so"
+
+_lib = None
+
+_f32p = ctypes.POINTER(ctypes.c_float)
+_f64p = ctypes.POINTER(ctypes.c_double)
+_u16p = ctypes.POINTER(ctypes.c_uint16)
+_i32p = ctypes.POINTER(ctypes.c_int32)
+_ci = ctypes.c_int
+
+
+def build() -> Path:
+    """Compiles the C oracle (make -C oracle)."""
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    return LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise RuntimeError(f"{LIB_PATH} missing; run `make -C oracle` or __graft_entry__.build()")
+    L = ctypes.CDLL(str(LIB_PATH))
+    L.oracle_f32_to_f16.restype = ctypes.c_uint16
+    L.oracle_f32_to_f16.argtypes = [ctypes.c_float]
+    L.oracle_f16_to_f32.restype = ctypes.c_float
+    L.oracle_f16_to_f32.argtypes = [ctypes.c_uint16]
+    L.oracle_f32_to_f16_array.argtypes = [_f32p, _u16p, ctypes.c_size_t]
+    L.oracle_f16_to_f32_array.argtypes = [_u16p, _f32p, ctypes.c_size_t]
+    L.oracle_kv_append.argtypes = [_u16p, _i32p, _ci, _ci, _f32p, _f32p, _ci, _ci]
+    L.oracle_kv_write_fp16.argtypes = [_u16p, _i32p, _ci, _ci, _u16p, _u16p, _ci, _ci]
+    L.oracle_kv_gather.argtypes = [_u16p, _i32p, _ci, _ci, _ci, _ci, _f32p, _f32p]
+    L.oracle_attention_tiled.argtypes = [_f32p, _f32p, _u16p, _i32p, _ci, _ci, _ci, _ci, _ci, _ci]
+    L.oracle_attention_f64.argtypes = [_f32p, _f64p, _u16p, _i32p, _ci, _ci, _ci, _ci, _ci, _ci]
+    L.oracle_paged_attention.restype = _ci
+    L.oracle_paged_attention.argtypes = [_f32p, _f32p, _f64p, _u16p, _i32p, _ci, _ci, _ci, _ci,
+                                         _ci, _ci, _ci, _ci, _ci]
+    L.oracle_max_threads.restype = _ci
+    _lib = L
+    return L
+
+
+def _p(a: np.ndarray, t):
+    return a.ctypes.data_as(t)
+
+
+def f32_to_f16_bits(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint16)
+    lib().oracle_f32_to_f16_array(_p(x, _f32p), _p(out, _u16p), x.size)
+    return out
+
+
+def f16_bits_to_f32(h: np.ndarray) -> np.ndarray:
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    out = np.empty(h.shape, dtype=np.float32)
+    lib().oracle_f16_to_f32_array(_p(h, _u16p), _p(out, _f32p), h.size)
+    return out
+
+
+class PagedKVModel:
+    """Cache state on the CPU: the pool as uint16 bits with the reference
+    layout [pool_blocks][2 (K,V)][block_size][kv_dim], per-layer tables, and
+    the seq_len integer (kv_cache.h:27-51)."""
+
+    def __init__(self, n_layers: int, kv_dim: int, max_blocks_per_layer: int,
+                 block_size: int = 16, pool_blocks: int = 0):
+        self.n_layers = n_layers
+        self.kv_dim = kv_dim
+        self.max_blocks = max_blocks_per_layer
+        self.bs = block_size
+        self.pool_blocks = pool_blocks or n_layers * max_blocks_per_layer
+        # kv_cache_alloc zeroes the pool and assigns blocks statically when
+        # they fit (kv_cache.cu:16-37).
+        self.pool = np.zeros((self.pool_blocks, 2, block_size, kv_dim), dtype=np.uint16)
+        self.tables = np.full((n_layers, max_blocks_per_layer), -1, dtype=np.int32)
+        self.n_mapped = np.zeros(n_layers, dtype=np.int64)
+        if n_layers * max_blocks_per_layer <= self.pool_blocks:
+            self.tables[:] = np.arange(n_layers * max_blocks_per_layer,
+                                       dtype=np.int32).reshape(n_layers, -1)
+            self.n_mapped[:] = max_blocks_per_layer
+        self.seq_len = 0
+
+    def set_block_table(self, layer: int, table) -> None:
+        t = np.asarray(table, dtype=np.int32)
+        assert t.ndim == 1 and t.size <= self.max_blocks
+        assert np.all((t >= 0) & (t < self.pool_blocks))
+        self.tables[layer, : t.size] = t
+        self.n_mapped[layer] = t.size
+
+    def _table(self, layer: int) -> np.ndarray:
+        return np.ascontiguousarray(self.tables[layer])
+
+    def append(self, layer: int, k: np.ndarray, v: np.ndarray, pos_base: int) -> None:
+        k = np.ascontiguousarray(k, dtype=np.float32).reshape(-1, self.kv_dim)
+        v = np.ascontiguousarray(v, dtype=np.float32).reshape(-1, self.kv_dim)
+        assert pos_base >= 0 and pos_base + k.shape[0] <= self.n_mapped[layer] * self.bs
+        t = self._table(layer)
+        lib().oracle_kv_append(_p(self.pool, _u16p), _p(t, _i32p), self.kv_dim, self.bs,
+                               _p(k, _f32p), _p(v, _f32p), pos_base, k.shape[0])
+
+    def write_fp16(self, layer: int, k16: np.ndarray, v16: np.ndarray, pos_base: int) -> None:
+        k16 = np.ascontiguousarray(k16).view(np.uint16).reshape(-1, self.kv_dim)
+        v16 = np.ascontiguousarray(v16).view(np.uint16).reshape(-1, self.kv_dim)
+        assert pos_base >= 0 and pos_base + k16.shape[0] <= self.n_mapped[layer] * self.bs
+        t = self._table(layer)
+        lib().oracle_kv_write_fp16(_p(self.pool, _u16p), _p(t, _i32p), self.kv_dim, self.bs,
+                                   _p(k16, _u16p), _p(v16, _u16p), pos_base, k16.shape[0])
+
+    def gather(self, layer: int, pos: int, n: int) -> tuple[np.ndarray, np.ndarray]:
+        assert pos >= 0 and pos + n <= self.n_mapped[layer] * self.bs
+        k = np.empty((n, self.kv_dim), dtype=np.float32)
+        v = np.empty((n, self.kv_dim), dtype=np.float32)
+        t = self._table(layer)
+        lib().oracle_kv_gather(_p(self.pool, _u16p), _p(t, _i32p), self.kv_dim, self.bs,
+                               pos, n, _p(k, _f32p), _p(v, _f32p))
+        return k, v
+
+    def set_seq_len(self, n: int) -> None:
+        assert 0 <= n <= self.max_blocks * self.bs
+        self.seq_len = n
+
+    def rollback(self, target_len: int) -> None:
+        """kv_cache_rollback / set_seq_len_kernel: an integer assignment."""
+        assert 0 <= target_len <= self.seq_len
+        self.seq_len = target_len
+
+    def pool_sha256(self) -> str:
+        return hashlib.sha256(self.pool.tobytes()).hexdigest()
+
+    def attention(self, layer: int, q: np.ndarray, nh: int, nkv: int, dph: int,
+                  pos_base: int, mode: str = "tiled", threads: int = 1) -> np.ndarray:
+        """cublas_attention_kernel semantics (kernels.cu:904-940): q fp32
+        [M][nh*dph]; query m sees pos_base+m+1 keys.  mode 'tiled' = the
+        literal fp32 restatement of attention.h; 'f64' = fp64 brute force."""
+        q = np.ascontiguousarray(q, dtype=np.float32).reshape(-1, nh * dph)
+        M = q.shape[0]
+        assert pos_base + M <= self.n_mapped[layer] * self.bs
+        t = self._table(layer)
+        out = np.zeros((M, nh * dph), dtype=np.float32)
+        out64 = np.zeros((M, nh * dph), dtype=np.float64)
+        lib().oracle_paged_attention(_p(q, _f32p), _p(out, _f32p), _p(out64, _f64p),
+                                     _p(self.pool, _u16p), _p(t, _i32p), self.kv_dim, self.bs,
+                                     nh, nkv, dph, pos_base, M, 0 if mode == "tiled" else 1,
+                                     threads)
+        return out if mode == "tiled" else out64
+
+    def attention_one(self, layer: int, q: np.ndarray, nh: int, nkv: int, dph: int,
+                      total_len: int) -> np.ndarray:
+        """device_flash_attention_gqa with an explicit total_len (any value
+        >= 0, including 0) for one query."""
+        q = np.ascontiguousarray(q, dtype=np.float32).reshape(nh * dph)
+        out = np.zeros(nh * dph, dtype=np.float32)
+        t = self._table(layer)
+        lib().oracle_attention_tiled(_p(q, _f32p), _p(out, _f32p), _p(self.pool, _u16p),
+                                     _p(t, _i32p), self.kv_dim, self.bs, nh, nkv, dph, total_len)
+        return out
+
+
+def run_script(model: PagedKVModel, ops, on_checkpoint=None, on_attend=None) -> list:
+    """Executes a workloads.scripted_rounds op list on the CPU model.
+    Returns [(label, seq_len, pool_sha256)] at every checkpoint."""
+    marks = []
+    for op in ops:
+        kind = op[0]
+        if kind == "write_fp16":
+            model.write_fp16(op[1], op[3], op[4], op[2])
+        elif kind == "append":
+            model.append(op[1], op[3], op[4], op[2])
+        elif kind == "set_seq_len":
+            model.set_seq_len(op[1])
+        elif kind == "rollback":
+            model.rollback(op[1])
+        elif kind == "checkpoint":
+            marks.append((op[1], model.seq_len, model.pool_sha256()))
+            if on_checkpoint is not None:
+                on_checkpoint(op[1], model)
+        elif kind == "attend":
+            if on_attend is not None:
+                on_attend(model, op[1], op[2], op[3])
+        else:
+            raise ValueError(f"unknown op {kind}")
+    return marks
+
+
+def attention_f64_np(q: np.ndarray, K: np.ndarray, V: np.ndarray, nh: int, nkv: int,
+                     dph: int, pos_base: int) -> np.ndarray:
+    """softmax(q K^T / sqrt(dph)) V in fp64 with numpy, on contiguous
+    (already gathered) K, V [L][nkv*dph]; query m sees pos_base+m+1 keys;
+    head h uses KV head h*nkv//nh.  Returns float64 [M][nh*dph]."""
+    q = np.asarray(q, dtype=np.float64).reshape(-1, nh, dph)
+    M = q.shape[0]
+    L_all = pos_base + M
+    K = np.asarray(K[:L_all], dtype=np.float64).reshape(L_all, nkv, dph)
+    V = np.asarray(V[:L_all], dtype=np.float64).reshape(L_all, nkv, dph)
+    kvh_of = (np.arange(nh) * nkv) // nh
+    out = np.zeros((M, nh, dph), dtype=np.float64)
+    scale = 1.0 / np.sqrt(dph)
+    for kvh in range(nkv):
+        heads = np.nonzero(kvh_of == kvh)[0]
+        Kg = K[:, kvh, :]  # [L][dph]
+        Vg = V[:, kvh, :]
+        for m in range(M):
+            L = pos_base + m + 1
+            logits = (q[m, heads] @ Kg[:L].T) * scale  # [heads][L]
+            logits -= logits.max(axis=1, keepdims=True)
+            w = np.exp(logits)
+            w /= w.sum(axis=1, keepdims=True)
+            out[m, heads] = w @ Vg[:L]
+    return out.reshape(M, nh * dph)

@@ -1,0 +1,12 @@
+"""MI355X (gfx950) paged KV cache and paged GQA decode/verify attention.
+
+The product is libsde_paged.so (C-ABI in include/sde_paged_kv.h, HIP kernels
+in csrc/).  This package holds its ctypes binding, a host-side mirror of the
+reference KVCache API (kv_cache.py) and the benchmark workloads.
+"""
+from .kv_cache import (ATTN_KDA, ATTN_LINEAR, ATTN_SLIDING_WINDOW, ATTN_SOFTMAX, KVCache,
+                       kv_cache_alloc, kv_cache_free, kv_cache_reset)
+from ._native import SDEError
+
+__all__ = ["KVCache", "kv_cache_alloc", "kv_cache_free", "kv_cache_reset", "SDEError",
+           "ATTN_SOFTMAX", "ATTN_SLIDING_WINDOW", "ATTN_KDA", "ATTN_LINEAR"]

@@ -1,0 +1,102 @@
+"""CPU checks of the C-ABI library (no kernel launches): it loads, exports
+every function include/sde_paged_kv.h declares, and rejects bad arguments
+on the host with the documented status codes before touching a device."""
+import ctypes
+import subprocess
+
+import pytest
+
+from speculative_decode_engine_amd import _native as N
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return N.load()
+
+
+def test_exports_every_header_function(lib):
+    declared = N.header_functions()
+    assert len(declared) >= 20
+    out = subprocess.run(["nm", "-D", "--defined-only", str(N.LIB_PATH)], capture_output=True,
+                         text=True, check=True).stdout
+    exported = {ln.split()[-1] for ln in out.splitlines() if " T " in ln}
+    missing = [f for f in declared if f not in exported]
+    assert not missing, missing
+    for f in declared:
+        assert hasattr(lib, f)
+    assert set(declared) == set(N.PROTOTYPES)  # the ctypes binding covers the header
+
+
+def test_single_hip_runtime_in_process(lib):
+    assert len(N.hip_runtime_paths()) == 1
+
+
+def test_status_strings(lib):
+    for code in range(8):
+        s = N.status_string(code)
+        assert s and s != "unknown status"
+    assert N.status_string(99) == "unknown status"
+
+
+@pytest.mark.parametrize("cfg,ok", [
+    ((4, 128, 9, 16, 64), True),
+    ((4, 128, 9, 16, 0), True),
+    ((0, 128, 9, 16, 0), False),      # no layers
+    ((4, 0, 9, 16, 0), False),        # no features
+    ((4, 128, 0, 16, 0), False),      # no blocks
+    ((4, 128, 9, 0, 0), False),       # block size 0
+    ((4, 128, 9, 2048, 0), False),    # block size too large
+    ((4, 128, 9, 16, 8), False),      # pool smaller than one layer's table
+    ((4, 128, 9, 16, -1), False),
+    ((1 << 20, 128, 1 << 12, 16, 0), False),  # pool block count overflows int32
+])
+def test_config_validation(lib, cfg, ok):
+    c = N.KVConfig(*cfg)
+    st = lib.sde_kv_config_validate(ctypes.byref(c))
+    assert (st == N.SDE_OK) == ok
+    nbytes = lib.sde_kv_pool_bytes(ctypes.byref(c))
+    if ok:
+        pool = cfg[4] or cfg[0] * cfg[2]
+        assert nbytes == pool * 2 * cfg[3] * cfg[1] * 2
+    else:
+        assert nbytes == 0
+        h = ctypes.c_void_p()
+        assert lib.sde_kv_cache_create(ctypes.byref(c), ctypes.byref(h)) == \
+            N.SDE_ERR_INVALID_ARGUMENT
+        assert not h
+
+
+def test_pool_bytes_of_32k_config_needs_64bit(lib):
+    c = N.KVConfig(32, 1024, 2048, 16, 131072)
+    assert lib.sde_kv_pool_bytes(ctypes.byref(c)) == 131072 * 2 * 16 * 1024 * 2  # 8 GiB
+
+
+def test_null_handles_rejected(lib):
+    null = ctypes.c_void_p()
+    out = ctypes.c_int()
+    assert lib.sde_kv_cache_destroy(null) == N.SDE_OK
+    assert lib.sde_kv_seq_len(null, ctypes.byref(out)) == N.SDE_ERR_INVALID_ARGUMENT
+    assert lib.sde_kv_set_seq_len(null, 0, null) == N.SDE_ERR_INVALID_ARGUMENT
+    assert lib.sde_kv_rollback(null, 0, null) == N.SDE_ERR_INVALID_ARGUMENT
+    assert lib.sde_kv_append(null, 0, null, null, 0, 1, null) == N.SDE_ERR_INVALID_ARGUMENT
+    assert lib.sde_kv_gather(null, 0, 0, 1, null, null, null) == N.SDE_ERR_INVALID_ARGUMENT
+    assert lib.sde_paged_attention(null, 0, null, null, 4, 2, 64, 0, 1, null, 0, null) == \
+        N.SDE_ERR_INVALID_ARGUMENT
+    c = N.KVConfig(1, 64, 4, 16, 0)
+    h = ctypes.c_void_p()
+    assert lib.sde_kv_cache_create_external(ctypes.byref(c), null, 1 << 20, ctypes.byref(h)) \
+        == N.SDE_ERR_INVALID_ARGUMENT
+    assert lib.sde_kv_cache_create(ctypes.byref(c), None) == N.SDE_ERR_INVALID_ARGUMENT
+
+
+def test_reserved_attention_types_unsupported(lib):
+    null = ctypes.c_void_p()
+    for t in (N.SDE_ATTN_SLIDING_WINDOW, N.SDE_ATTN_KDA, N.SDE_ATTN_LINEAR, 7):
+        # where the reference traps (attention.h:158-162), the ABI returns a code
+        assert lib.sde_attention_dispatch(t, null, 0, null, null, 4, 2, 64, 0, 1, null, 0,
+                                          null) == N.SDE_ERR_UNSUPPORTED
+
+
+def test_workspace_size_query_is_host_only(lib):
+    null = ctypes.c_void_p()
+    assert lib.sde_paged_attention_workspace_size(null, 32, 8, 128, 1, 32768) == 0

@@ -1,0 +1,337 @@
+"""Pins the CPU oracle (oracle/) before anything is checked against it.
+
+The reference has no golden vectors for this path, so each oracle function
+is pinned by an independent formulation or a closed form:
+  * fp16 conversion: numpy's IEEE binary16 cast, exhaustively for fp16->fp32
+    and on random + boundary + tie values for fp32->fp16;
+  * paged layout (kv_cache.h:5-18, kv_cache.cu:58-93): numpy fancy indexing
+    of the [block][K|V][slot][kv_dim] pool, block-table permutation
+    invariance, the contiguous special case block_size=1, untouched bytes;
+  * rollback (kernels.cu:2457-2466): pool bytes unchanged, re-append only
+    rewrites [target, target+n);
+  * attention (attention.h:21-127): the fp32 tile restatement against an
+    fp64 brute force in C, a vectorised numpy softmax, and torch's
+    scaled_dot_product_attention (float64, CPU); closed forms (total_len=0,
+    one key, uniform logits, one-hot logits); causal window = independent
+    single-query calls; and planted mistakes (head mapping, scale,
+    off-by-one length, K/V swap) that the 2e-3 tolerance must catch.
+"""
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from speculative_decode_engine_amd import workloads as W
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+ATOL, RTOL = 2e-3, 1e-2  # north_star tolerance for attention outputs
+
+
+# ---- fp16 conversion ------------------------------------------------------------
+
+def test_f16_to_f32_exhaustive(oracle):
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    got = oracle.f16_bits_to_f32(bits)
+    want = bits.view(np.float16).astype(np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def test_f32_to_f16_matches_numpy_rne(oracle):
+    rng = np.random.default_rng(0)
+    parts = [
+        rng.standard_normal(200_000).astype(np.float32),
+        (rng.standard_normal(50_000) * 1e4).astype(np.float32),
+        (rng.standard_normal(50_000) * 1e-5).astype(np.float32),   # fp16 subnormals
+        np.exp(rng.uniform(-30, 12, 100_000)).astype(np.float32),  # all exponents
+        np.array([0.0, -0.0, 65504, 65519.996, 65520, 1e9, -1e9, np.inf, -np.inf,
+                  2.0 ** -24, 2.0 ** -25, 3 * 2.0 ** -26, 2.0 ** -14, 6.1e-5], np.float32),
+    ]
+    # exact ties: halfway between adjacent fp16 values (both parities)
+    h = np.arange(0, 0x7bff, 7, dtype=np.uint16).view(np.float16).astype(np.float64)
+    nxt = (np.arange(0, 0x7bff, 7, dtype=np.uint16) + 1).view(np.float16).astype(np.float64)
+    parts.append(((h + nxt) / 2).astype(np.float32))
+    x = np.concatenate(parts)
+    x = np.concatenate([x, -x])
+    with np.errstate(over="ignore"):
+        want = x.astype(np.float16).view(np.uint16)
+    got = oracle.f32_to_f16_bits(x)
+    assert np.array_equal(got, want)
+
+
+def test_f32_to_f16_nan_stays_nan(oracle):
+    x = np.array([np.nan, -np.nan], np.float32)
+    got = oracle.f32_to_f16_bits(x).view(np.float16)
+    assert np.all(np.isnan(got))
+
+
+# ---- layout / append / gather / rollback -----------------------------------------
+
+def _model_with_tables(oracle, n_layers=3, kv_dim=24, nblk=5, bs=4, pool=40, seed=1):
+    rng = np.random.default_rng(seed)
+    tables = W.make_tables(rng, n_layers, nblk, pool)
+    m = oracle.PagedKVModel(n_layers, kv_dim, nblk, bs, pool)
+    for l in range(n_layers):
+        m.set_block_table(l, tables[l])
+    return m, tables, rng
+
+
+def test_append_layout_against_numpy_indexing(oracle):
+    m, tables, rng = _model_with_tables(oracle)
+    n = 5 * 4
+    k, v = W.new_kv(rng, n, m.kv_dim)
+    before = m.pool.copy()
+    m.append(1, k, v, 0)
+    pos = np.arange(n)
+    blk = tables[1][pos // m.bs]
+    slot = pos % m.bs
+    assert np.array_equal(m.pool[blk, 0, slot], k.astype(np.float16).view(np.uint16))
+    assert np.array_equal(m.pool[blk, 1, slot], v.astype(np.float16).view(np.uint16))
+    touched = np.zeros(m.pool.shape[0], bool)
+    touched[tables[1]] = True
+    assert np.array_equal(m.pool[~touched], before[~touched])  # other blocks untouched
+
+
+def test_append_gather_roundtrip_and_offsets(oracle):
+    m, tables, rng = _model_with_tables(oracle)
+    k, v = W.new_kv(rng, 7, m.kv_dim)
+    m.append(2, k, v, 9)  # crosses a block boundary (bs=4)
+    gk, gv = m.gather(2, 9, 7)
+    assert np.array_equal(gk, k.astype(np.float16).astype(np.float32))
+    assert np.array_equal(gv, v.astype(np.float16).astype(np.float32))
+    # positions before 9 of that layer are still zero
+    zk, zv = m.gather(2, 0, 9)
+    assert not zk.any() and not zv.any()
+
+
+def test_permutation_invariance(oracle):
+    rng = np.random.default_rng(5)
+    a = oracle.PagedKVModel(1, 16, 6, 8, 20)
+    b = oracle.PagedKVModel(1, 16, 6, 8, 20)
+    ta = rng.permutation(20)[:6]
+    tb = rng.permutation(20)[:6]
+    a.set_block_table(0, ta)
+    b.set_block_table(0, tb)
+    k, v = W.new_kv(rng, 48, 16)
+    a.append(0, k, v, 0)
+    b.append(0, k, v, 0)
+    for x, y in zip(a.gather(0, 0, 48), b.gather(0, 0, 48)):
+        assert np.array_equal(x, y)
+    assert np.array_equal(a.pool[ta], b.pool[tb])
+
+
+def test_block_size_one_is_contiguous(oracle):
+    rng = np.random.default_rng(6)
+    m = oracle.PagedKVModel(1, 8, 10, 1, 10)
+    m.set_block_table(0, np.arange(10))
+    k, v = W.new_kv(rng, 10, 8)
+    m.append(0, k, v, 0)
+    assert np.array_equal(m.pool[:, 0, 0], k.astype(np.float16).view(np.uint16))
+    assert np.array_equal(m.pool[:, 1, 0], v.astype(np.float16).view(np.uint16))
+
+
+def test_static_assignment_matches_reference_alloc(oracle):
+    m = oracle.PagedKVModel(3, 8, 4, 16)  # pool = n_layers * max_blocks
+    assert np.array_equal(m.tables, np.arange(12).reshape(3, 4))  # kv_cache.cu:32-37
+
+
+def test_rollback_moves_no_bytes_and_reappend_is_local(oracle):
+    m, tables, rng = _model_with_tables(oracle, n_layers=1, nblk=6, bs=4, pool=12)
+    k, v = W.new_kv(rng, 20, m.kv_dim)
+    m.append(0, k, v, 0)
+    m.set_seq_len(20)
+    before = m.pool.copy()
+    m.rollback(13)
+    assert m.seq_len == 13 and np.array_equal(m.pool, before)
+    with pytest.raises(AssertionError):
+        m.rollback(14)  # beyond seq_len
+    k2, v2 = W.new_kv(rng, 3, m.kv_dim)
+    m.append(0, k2, v2, 13)
+    gk, gv = m.gather(0, 0, 20)
+    exp_k = k.astype(np.float16).astype(np.float32)
+    exp_k[13:16] = k2.astype(np.float16)
+    exp_v = v.astype(np.float16).astype(np.float32)
+    exp_v[13:16] = v2.astype(np.float16)
+    assert np.array_equal(gk, exp_k) and np.array_equal(gv, exp_v)
+
+
+# ---- attention ---------------------------------------------------------------------
+
+def _attn_case(oracle, nh=4, nkv=2, dph=64, bs=16, L=77, M=1, seed=3, q_scale=1.0):
+    rng = np.random.default_rng(seed)
+    kv_dim = nkv * dph
+    nblk = -(-(L + M) // bs)
+    pool = 2 * nblk + 3
+    m = oracle.PagedKVModel(1, kv_dim, nblk, bs, pool)
+    m.set_block_table(0, rng.permutation(pool)[:nblk])
+    kc, vc = W.context_kv(rng, L + M, kv_dim)
+    m.write_fp16(0, kc, vc, 0)
+    q = W.queries(rng, M, nh, dph) * np.float32(q_scale)
+    K, V = m.gather(0, 0, L + M)
+    return m, q, K, V
+
+
+@pytest.mark.parametrize("nh,nkv,dph,bs", [(4, 2, 64, 16), (32, 8, 128, 16), (28, 4, 128, 32),
+                                           (8, 8, 64, 8), (6, 1, 64, 1)])
+def test_tiled_vs_bruteforce_vs_numpy_vs_torch(oracle, nh, nkv, dph, bs):
+    M = 3
+    m, q, K, V = _attn_case(oracle, nh, nkv, dph, bs, L=70, M=M)
+    pos_base = 70
+    tiled = m.attention(0, q, nh, nkv, dph, pos_base, mode="tiled")
+    f64 = m.attention(0, q, nh, nkv, dph, pos_base, mode="f64")
+    npy = oracle.attention_f64_np(q, K, V, nh, nkv, dph, pos_base)
+    np.testing.assert_allclose(f64, npy, rtol=1e-12, atol=1e-13)
+    np.testing.assert_allclose(tiled, f64, rtol=1e-5, atol=2e-6)
+    # torch SDPA, fp64 on the CPU, GQA by repeating KV heads
+    G = nh // nkv
+    for mq in range(M):
+        Lq = pos_base + mq + 1
+        qt = torch.from_numpy(q[mq].astype(np.float64)).view(nh, 1, dph)
+        kt = torch.from_numpy(K[:Lq].astype(np.float64)).view(Lq, nkv, dph).permute(1, 0, 2)
+        vt = torch.from_numpy(V[:Lq].astype(np.float64)).view(Lq, nkv, dph).permute(1, 0, 2)
+        kt = kt.repeat_interleave(G, dim=0).contiguous()
+        vt = vt.repeat_interleave(G, dim=0).contiguous()
+        ref = torch.nn.functional.scaled_dot_product_attention(qt, kt, vt).reshape(-1).numpy()
+        np.testing.assert_allclose(f64[mq], ref, rtol=1e-10, atol=1e-12)
+
+
+def test_total_len_zero_gives_zeros(oracle):
+    m, q, K, V = _attn_case(oracle)
+    out = m.attention_one(0, q[0], 4, 2, 64, 0)
+    assert not out.any()  # attention.h:120-126 (l = 0 -> inv = 0)
+
+
+def test_single_key_returns_its_value(oracle):
+    m, q, K, V = _attn_case(oracle, nh=4, nkv=2, dph=64)
+    out = m.attention_one(0, q[0], 4, 2, 64, 1)
+    for h in range(4):
+        kvh = h * 2 // 4
+        np.testing.assert_allclose(out[h * 64:(h + 1) * 64], V[0, kvh * 64:(kvh + 1) * 64],
+                                   rtol=1e-6, atol=1e-7)
+
+
+def test_uniform_logits_give_mean_of_values(oracle):
+    m, q, K, V = _attn_case(oracle, nh=4, nkv=2, dph=64, L=50)
+    zq = np.zeros_like(q[0])
+    out = m.attention_one(0, zq, 4, 2, 64, 41)
+    for h in range(4):
+        kvh = h * 2 // 4
+        np.testing.assert_allclose(out[h * 64:(h + 1) * 64],
+                                   V[:41, kvh * 64:(kvh + 1) * 64].mean(axis=0), rtol=1e-5,
+                                   atol=1e-6)
+
+
+def test_one_hot_logits_select_one_value(oracle):
+    """q aligned with one key and scaled up: softmax -> one-hot on that key."""
+    rng = np.random.default_rng(9)
+    dph, nkv, nh, L = 64, 1, 1, 40
+    m = oracle.PagedKVModel(1, dph, 4, 16, 4)
+    m.set_block_table(0, [2, 0, 3, 1])
+    kc = np.zeros((L, dph), np.float16)
+    kc[np.arange(L), np.arange(L) % dph] = 1.0  # orthogonal unit keys
+    vc = rng.standard_normal((L, dph)).astype(np.float16)
+    m.write_fp16(0, kc, vc, 0)
+    j = 23
+    q = np.zeros(dph, np.float32)
+    q[j % dph] = 400.0  # logit gap 400/8 = 50 -> weight ratio e^-50
+    out = m.attention_one(0, q, nh, nkv, dph, L)
+    np.testing.assert_allclose(out, vc[j].astype(np.float32), rtol=1e-6, atol=1e-6)
+
+
+def test_causal_window_equals_single_query_calls(oracle):
+    M = 5
+    m, q, K, V = _attn_case(oracle, nh=8, nkv=2, dph=64, L=60, M=M)
+    win = m.attention(0, q, 8, 2, 64, 60, mode="tiled")
+    for mq in range(M):
+        one = m.attention_one(0, q[mq], 8, 2, 64, 60 + mq + 1)
+        assert np.array_equal(win[mq], one)
+
+
+def _close(a, b):
+    return np.all(np.abs(a - b) <= ATOL + RTOL * np.abs(b))
+
+
+def test_planted_mistakes_exceed_tolerance(oracle):
+    """Mistakes a kernel could plausibly make, planted in a CPU restatement,
+    must all fail the attention tolerance against the oracle."""
+    nh, nkv, dph, pb, M = 8, 2, 64, 90, 3
+    m, q, K, V = _attn_case(oracle, nh, nkv, dph, 16, L=pb, M=M, q_scale=2.0)
+    ref = m.attention(0, q, nh, nkv, dph, pb, mode="f64")
+    good = oracle.attention_f64_np(q, K, V, nh, nkv, dph, pb)
+    assert _close(good, ref)
+
+    def variant(kvh_map=None, scale=None, off=0, swap=False):
+        Kx, Vx = (V, K) if swap else (K, V)
+        qh = q.astype(np.float64).reshape(M, nh, dph)
+        Kh = Kx.astype(np.float64).reshape(-1, nkv, dph)
+        Vh = Vx.astype(np.float64).reshape(-1, nkv, dph)
+        mp = kvh_map if kvh_map is not None else (np.arange(nh) * nkv) // nh
+        sc = scale if scale is not None else 1 / np.sqrt(dph)
+        out = np.zeros((M, nh, dph))
+        for mq in range(M):
+            L = pb + mq + 1 + off
+            lg = np.einsum("hd,lhd->hl", qh[mq], Kh[:L, mp]) * sc
+            w = np.exp(lg - lg.max(1, keepdims=True))
+            w /= w.sum(1, keepdims=True)
+            out[mq] = np.einsum("hl,lhd->hd", w, Vh[:L, mp])
+        return out.reshape(M, -1)
+
+    assert _close(variant(), ref)
+    assert not _close(variant(kvh_map=np.arange(nh) % nkv), ref)  # h % nkv mapping
+    assert not _close(variant(scale=1.0), ref)                      # scale dropped
+    assert not _close(variant(scale=1 / dph), ref)                  # 1/d, not 1/sqrt(d)
+    assert not _close(variant(off=-1), ref)                         # total_len off by one
+    assert not _close(variant(swap=True), ref)                      # K and V regions swapped
+
+
+def test_rope_rotate_half_is_a_rotation():
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal((1, 4 * 64)).astype(np.float32)
+    assert np.array_equal(W.rope_rotate_half(x, 4, 64, 0), x)  # angle 0
+    y = W.rope_rotate_half(x, 4, 64, 129).reshape(4, 64).astype(np.float64)
+    xr = x.reshape(4, 64).astype(np.float64)
+    # as complex numbers z_j = x_j + i x_{j+32}, rotation by pos*theta^(-2j/64)
+    z = xr[:, :32] + 1j * xr[:, 32:]
+    ang = 129 * 10000.0 ** (-np.arange(32) * 2 / 64)
+    zr = z * np.exp(1j * ang)
+    np.testing.assert_allclose(y[:, :32], zr.real, rtol=1e-4, atol=1e-4)
+    np.testing.assert_allclose(y[:, 32:], zr.imag, rtol=1e-4, atol=1e-4)
+
+
+# ---- golden fixtures -----------------------------------------------------------------
+
+def test_tiny_decode_fixture_reproduces(oracle):
+    g = np.load(GOLDEN / "tiny_decode.npz")
+    w = W.CONFIGS["tiny"]
+    m = oracle.PagedKVModel(w.n_layers, w.kv_dim, g["tables"].shape[1], w.block_size,
+                            w.pool_blocks)
+    for layer in range(w.n_layers):
+        m.set_block_table(layer, g["tables"][layer])
+        m.write_fp16(layer, g["ctx_k"][layer], g["ctx_v"][layer], 0)
+        m.append(layer, g["new_k"][layer], g["new_v"][layer], w.ctx)
+        tiled = m.attention(layer, g["q"][layer], w.nh, w.nkv, w.dph, w.ctx, mode="tiled")
+        assert np.array_equal(tiled, g["out_tiled"][layer])
+        f64 = m.attention(layer, g["q"][layer], w.nh, w.nkv, w.dph, w.ctx, mode="f64")
+        np.testing.assert_allclose(f64, g["out_f64"][layer], rtol=1e-12, atol=1e-14)
+    assert m.pool_sha256() == bytes(g["pool_sha256"]).hex()
+
+
+@pytest.mark.parametrize("name", ["tiny", "llama3_8b_verify", "qwen25_7b_selfspec"])
+def test_scripted_hashes_reproduce(oracle, name):
+    spec = json.loads((GOLDEN / "scripted_hashes.json").read_text())[name]
+    w = W.CONFIGS[name]
+    tables, ops = W.scripted_rounds(w, spec["n_layers"], spec["rounds"],
+                                    draft_layers=spec["draft_layers"])
+    m = oracle.PagedKVModel(spec["n_layers"], w.kv_dim, tables.shape[1], w.block_size,
+                            spec["pool_blocks"])
+    for layer in range(spec["n_layers"]):
+        m.set_block_table(layer, tables[layer])
+    marks = oracle.run_script(m, ops)
+    assert [(c["label"], c["seq_len"], c["sha256"]) for c in spec["checkpoints"]] == marks
+    # rollback checkpoints: same bytes as the verify checkpoint before them
+    for a, b in zip(marks, marks[1:]):
+        if b[0].endswith("rollback"):
+            assert a[2] == b[2] and b[1] <= a[1]
