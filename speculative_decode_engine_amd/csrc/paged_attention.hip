@@ -5,32 +5,35 @@
 // out[m][h] = softmax(q[m][h] . K[0..pos_base+m]^T * dph^-1/2) V, with query
 // head h reading KV head h*nkv/nh, keys gathered through the block table.
 //
-// Work decomposition (no MFMA: decode and small-k verify are GEMV-shaped):
-//  * one workgroup of kWaves wave64s per (context partition, KV head, row
-//    group).  The "rows" are the (query, head-in-group) pairs sharing one KV
-//    head, so each K/V byte is read from HBM once for all G*n_queries rows;
-//  * a partition is kWaves * tiles_per_wave tiles of 32 tokens; wave w takes
-//    tiles w, w+kWaves, ...  Each tile's K and V head slices land in the
-//    wave's LDS with direct-to-LDS 16-byte loads (16 lanes cover a 256 B
-//    row for dph 128), K chunk-swizzled so the transposed reads below are
-//    bank-conflict free;
-//  * Q.K: lane (t, half) owns token t and half of the head dimension, reads
-//    its K chunks from LDS and takes fp16 dot2 products with the q group
-//    (scaled by log2(e)/sqrt(dph), rounded to fp16, broadcast from LDS);
-//    the two halves are summed across lanes, leaving row 2i+half's logit;
-//  * online softmax in the exp2 domain with 32-lane max/sum reductions;
-//    probabilities go to LDS as fp16;
-//  * P.V: lane owns a pair of head features; V rows of two tokens are
-//    byte-permuted into (token0, token1) fp16 pairs and dot2-accumulated
-//    against the probability pairs, fp32 accumulators;
-//  * the waves' (max, sum, acc) merge through LDS; a single-partition
-//    context writes the normalised output directly, otherwise per-row
-//    partials go to the workspace and the last workgroup to finish a (KV
-//    head, row group) -- found with one arrival counter per pair -- merges
-//    all partitions with a log-sum-exp combine in partition order, so the
-//    result does not depend on arrival order and one call is one launch.
+// No MFMA: decode and small-k verify are GEMV-shaped and HBM-bound.  The
+// "rows" of a KV head are its (query, head-in-group) pairs, so every K/V
+// byte is read from HBM once for all G*n_queries rows of a row group.  The
+// context of each (KV head, row group) is split into partitions, one
+// workgroup each; a single-partition context writes the normalised output
+// directly, otherwise per-row partials go to the workspace and the last
+// workgroup of a (KV head, row group) to finish -- found with one arrival
+// counter per pair -- merges all partitions with a log-sum-exp combine in
+// partition order, so the result does not depend on arrival order and one
+// call is one launch.  Two kernels:
+//
+//  attn_stream_kernel (up to 4 rows per wave: decode, small windows), one
+//    8-wave workgroup per CU.  K and V stream from HBM straight into VGPRs
+//    in the coalesced load layout (lane = token slot x 16-byte feature
+//    chunk), software-pipelined a tile (32 tokens) ahead; logits are
+//    reduced across the lanes of a token with a transposing DPP butterfly
+//    that leaves each lane one (row, token pair), so the online softmax is a
+//    handful of scalar ops per lane; P.V dot2-accumulates fp16 probability
+//    pairs against byte-permuted V pairs.
+//
+//  attn_partition_kernel (larger row groups: verify windows), 4-wave
+//    workgroups.  K and V land in LDS with direct-to-LDS 16-byte loads, K
+//    chunk-swizzled so the transposed reads are bank-conflict free; lane
+//    (token, half) takes fp16 dot2 products over half the head dimension;
+//    online softmax with DPP/permlane reductions, probabilities to LDS as
+//    fp16; a lane owns a feature pair for P.V.
 #include <hip/hip_runtime.h>
 
+#include <climits>
 #include <cmath>
 #include <cstdlib>
 
@@ -62,18 +65,9 @@ struct AttnArgs {
   int pos_base;  // query m sees positions [0, pos_base+m]
   int L_max;     // pos_base + M
   int n_parts;
-  int tiles_per_wave;
+  int tiles_per_wave;  // attn_partition_kernel: tiles per wave
+  int tiles_per_part;  // attn_stream_kernel: tiles per partition
   float qscale;  // log2(e) / sqrt(dph)
-};
-
-// LDS of one wave: K tile, V tile, P tile; after the tile loop the same bytes
-// hold the wave's merge record (max, sum, acc[dph]) per row.
-template <int DPH, int RPW>
-struct WaveLds {
-  static constexpr int kTileBytes = kTile * DPH * 2;
-  static constexpr int kWork = 2 * kTileBytes + RPW * kTile * 2;
-  static constexpr int kMerge = RPW * (DPH + 2) * 4;
-  static constexpr int kBytes = ((kWork > kMerge ? kWork : kMerge) + 15) / 16 * 16;
 };
 
 __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
@@ -81,17 +75,81 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
                                 __builtin_bit_cast(half2_t, b), c, false);
 }
 
+// Cross-lane moves (gfx950 lane semantics):
+//  * DPP quad_perm [1,0,3,2] / [2,3,0,1] exchange lanes i^1 / i^2, and
+//    row_ror:4 / row_ror:8 rotate each 16-lane row, so four steps reduce
+//    every row of 16 lanes;
+//  * v_permlane16_swap(x, x) returns rows {0,0,2,2} and {1,1,3,3}: one more
+//    step reduces each 32-lane half without mixing the halves;
+//  * v_permlane32_swap(a, b) returns [a.lo | b.lo] and [a.hi | b.hi], so
+//    their sum holds a's half-sum in lanes 0-31 and b's in lanes 32-63.
+__device__ __forceinline__ float dpp_f(float x, int ctrl_sel) {
+  const int v = __builtin_bit_cast(int, x);
+  int r;
+  switch (ctrl_sel) {
+    case 0: r = __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xf, 0xf, false); break;   // i^1
+    case 1: r = __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xf, 0xf, false); break;   // i^2
+    case 2: r = __builtin_amdgcn_update_dpp(0, v, 0x124, 0xf, 0xf, false); break;  // ror 4
+    case 3: r = __builtin_amdgcn_update_dpp(0, v, 0x128, 0xf, 0xf, false); break;  // ror 8
+    default: r = __builtin_amdgcn_update_dpp(0, v, 0x141, 0xf, 0xf, false); break; // i^7 in 8
+  }
+  return __builtin_bit_cast(float, r);
+}
+
+// (even row, odd row) of this lane's pair of 16-lane rows.
+__device__ __forceinline__ float2 row_pair(float x) {
+  const int v = __builtin_bit_cast(int, x);
+  const auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  return make_float2(__builtin_bit_cast(float, (int)p[0]), __builtin_bit_cast(float, (int)p[1]));
+}
+
 // All-reduce within each 32-lane half of the wave.
 __device__ __forceinline__ float half_max(float x) {
 #pragma unroll
-  for (int o = 1; o < 32; o <<= 1) x = fmaxf(x, __shfl_xor(x, o));
-  return x;
+  for (int s = 0; s < 4; s++) x = fmaxf(x, dpp_f(x, s));
+  const float2 p = row_pair(x);
+  return fmaxf(p.x, p.y);
 }
 
 __device__ __forceinline__ float half_sum(float x) {
 #pragma unroll
-  for (int o = 1; o < 32; o <<= 1) x += __shfl_xor(x, o);
-  return x;
+  for (int s = 0; s < 4; s++) x += dpp_f(x, s);
+  const float2 p = row_pair(x);
+  return p.x + p.y;
+}
+
+// Sums a (partial over lanes 0-31 and 32-63) and b likewise: lanes 0-31
+// get a's total, lanes 32-63 b's total.
+__device__ __forceinline__ float half_pair_total(float a, float b) {
+  const auto p = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, a),
+                                                  __builtin_bit_cast(int, b), false, false);
+  return __builtin_bit_cast(float, (int)p[0]) + __builtin_bit_cast(float, (int)p[1]);
+}
+
+// 16 bytes per lane from global memory straight into LDS at lds + 16*lane
+// (global_load_lds_dwordx4, LDS base in M0, which the compiler loads for
+// the "{m0}" input operand).  Issued as inline asm so that
+// the compiler does not add its own conservative vmcnt waits before every
+// LDS read (it cannot tell which of the many in-flight tiles a read
+// touches); every consumer waits explicitly with wait_vmcnt below, and the
+// "memory" clobbers keep LDS accesses on the right side of those waits.
+__device__ __forceinline__ void load_lds16(const void* gptr, const uint16_t* lds) {
+  const uint32_t lds_addr = (uint32_t)(uintptr_t)(lds_ptr_t)(lds);
+  asm volatile("global_load_lds_dwordx4 %0, off" : : "v"(gptr), "{m0}"(lds_addr) : "memory");
+}
+
+// s_waitcnt vmcnt(N): all but the N most recent vector-memory loads done.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 16, "vmcnt");
+  if constexpr (N == 0)
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  else if constexpr (N == 4)
+    asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+  else if constexpr (N == 8)
+    asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+  else
+    static_assert(N == 0 || N == 4 || N == 8, "add the vmcnt value");
 }
 
 __device__ __forceinline__ float lane_value(float x, int lane) {
@@ -139,37 +197,15 @@ __device__ __forceinline__ int kswz(int t) {
     return (t >> 1) & 7;
 }
 
+
+typedef const __attribute__((address_space(4))) int32_t* const_table_t;
+
+// q rows of the row group -> fp16 in LDS, pre-scaled into the exp2 domain;
+// rows past nrows are zero.
 template <int DPH, int RPW>
-__global__ __launch_bounds__(64 * kWaves) void attn_partition_kernel(AttnArgs a) {
-  static_assert(DPH == 64 || DPH == 128, "head_dim");
-  static_assert(RPW % 2 == 0 && RPW <= kMaxRowsPerWave, "rows per wave");
-  constexpr int CH = DPH / 8;       // 16-byte chunks per head row
-  constexpr int TPL = 64 / CH;      // tokens per direct-to-LDS instruction
-  constexpr int NLD = kTile / TPL;  // instructions per tile (per K and per V)
-  constexpr int HCH = CH / 2;       // chunks per lane in Q.K
-  constexpr int RP = RPW / 2;       // row pairs
-  constexpr int DP = DPH / 2;       // fp16 pairs per head row
-  using W = WaveLds<DPH, RPW>;
-
-  __shared__ __attribute__((aligned(16))) uint16_t sQ[RPW * DPH];
-  __shared__ __attribute__((aligned(16))) unsigned char sWave[kWaves][W::kBytes];
-
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  uint16_t* const sK = reinterpret_cast<uint16_t*>(sWave[wave]);
-  uint16_t* const sV = sK + kTile * DPH;
-  uint16_t* const sP = sV + kTile * DPH;
-  const uint32_t* const sV32 = reinterpret_cast<const uint32_t*>(sV);
-  const uint32_t* const sP32 = reinterpret_cast<const uint32_t*>(sP);
-
-  const int part = blockIdx.x;
-  const int kvh = blockIdx.y;
-  const int r0 = blockIdx.z * RPW;
-  const int nrows = min(RPW, a.R - r0);
-  const int t_begin = part * a.tiles_per_wave * kWaves * kTile;
-  const int t_end = min(a.L_max, t_begin + a.tiles_per_wave * kWaves * kTile);
-
-  // q rows of this group -> fp16 in LDS, pre-scaled into the exp2 domain.
+__device__ __forceinline__ void stage_q(const AttnArgs& a, int kvh, int r0, int nrows,
+                                        uint16_t* sQ) {
+  constexpr int DP = DPH / 2;
   for (int idx = threadIdx.x; idx < RPW * DP; idx += 64 * kWaves) {
     const int r = idx / DP;
     const int d2 = idx - r * DP;
@@ -185,217 +221,139 @@ __global__ __launch_bounds__(64 * kWaves) void attn_partition_kernel(AttnArgs a)
     }
     reinterpret_cast<uint32_t*>(sQ)[idx] = packed;
   }
+}
 
-  // Q.K role: token t of the tile, feature half hh.  After the half-sum a
-  // lane holds the logit of row 2i+hh for pair i.
-  const int t = lane & 31;
-  const int hh = lane >> 5;
-  int lim[RP];  // last visible position of row 2i+hh (-1: padding row)
-  float m_run[RP], l_run[RP];
-#pragma unroll
-  for (int i = 0; i < RP; i++) {
-    const int r = 2 * i + hh;
-    lim[i] = (r < nrows) ? a.pos_base + (r0 + r) / a.G : -1;
-    m_run[i] = -INFINITY;
-    l_run[i] = 0.f;
-  }
-  float acc[RPW][2];
-#pragma unroll
-  for (int r = 0; r < RPW; r++) acc[r][0] = acc[r][1] = 0.f;
+// The block table is read-only during the kernel: reading it through the
+// constant address space turns the entries into scalar loads (lgkmcnt),
+// which never wait behind outstanding tile loads (vmcnt).
+__device__ __forceinline__ const_table_t const_table(const AttnArgs& a) {
+  return (const_table_t)a.table;
+}
 
-  __syncthreads();  // sQ complete
+// Physical block of each load group (TPL tokens, one block) of tile ts.
+template <int NLD, int TPL>
+__device__ __forceinline__ void tile_blocks(const AttnArgs& a, const_table_t table, int ts,
+                                            int (&blk)[NLD]) {
+#pragma unroll
+  for (int j = 0; j < NLD; j++) blk[j] = table[min(ts + j * TPL, a.L_max - 1) / a.bs];
+}
 
-  // The waves run different numbers of tiles: only wave-local ordering is
-  // used inside this loop (LDS operations of one wave complete in order).
-  // The table is read-only during the kernel: read it through the constant
-  // address space so entries arrive by scalar loads (lgkmcnt), which do not
-  // wait behind the outstanding direct-to-LDS loads (vmcnt).
-  const __attribute__((address_space(4))) int32_t* const table =
-      (const __attribute__((address_space(4))) int32_t*)a.table;
+// Pool address of this lane's 16-byte chunk `chunk` of token g0 + lane/CH
+// (group start g0 must lie in block `blk`); is_v selects the V half.
+template <int DPH>
+__device__ __forceinline__ const uint16_t* chunk_addr(const AttnArgs& a, int kvh, int blk,
+                                                      int g0, int lane, int chunk, bool is_v) {
+  constexpr int CH = DPH / 8;
+  const int lb = g0 / a.bs;
+  const int slot = g0 - lb * a.bs + lane / CH;
+  return a.pool + ((size_t)blk * 2u * a.bs + slot) * (size_t)a.kv_dim + (size_t)kvh * DPH +
+         (is_v ? (size_t)a.bs * a.kv_dim : 0) + chunk * 8;
+}
 
-  for (int ts = t_begin + wave * kTile; ts < t_end; ts += kWaves * kTile) {
-    // ---- K and V head slices of tokens ts..ts+31 -> this wave's LDS -------
-    int blk[NLD];  // physical block of each instruction group (wave-uniform)
+// Q.K for this lane's token t and feature half hh: s[r] = (q_r . k_t) over
+// the half, for every row (the two halves are combined by the caller).
+template <int DPH, int RPW, bool kQRegs>
+__device__ __forceinline__ void qk_tile(const uint16_t* sK, const uint16_t* sQ,
+                                        const uint4 (&qreg)[kQRegs ? RPW : 1][kQRegs ? DPH / 16 : 1],
+                                        int t, int hh, float (&s)[RPW]) {
+  constexpr int HCH = DPH / 16;
+  uint4 kc[HCH];
 #pragma unroll
-    for (int j = 0; j < NLD; j++) {
-      const int g0 = min(ts + j * TPL, a.L_max - 1);
-      blk[j] = table[g0 / a.bs];
-    }
+  for (int jj = 0; jj < HCH; jj++)
+    kc[jj] = *reinterpret_cast<const uint4*>(sK + t * DPH + ((hh * HCH + jj) ^ kswz<DPH>(t)) * 8);
 #pragma unroll
-    for (int j = 0; j < NLD; j++) {
-      const int g0 = ts + j * TPL;  // wave-uniform; the group shares a block
-      if (g0 < a.L_max) {
-        const int lb = g0 / a.bs;
-        const int tl = j * TPL + lane / CH;
-        const int pc = lane % CH;
-        const int slot = g0 - lb * a.bs + lane / CH;
-        const uint16_t* rowk = a.pool +
-                               ((size_t)blk[j] * 2u * a.bs + slot) * (size_t)a.kv_dim +
-                               (size_t)kvh * DPH;
-        const uint16_t* rowv = rowk + (size_t)a.bs * a.kv_dim;
-        __builtin_amdgcn_global_load_lds((const void*)(rowk + (pc ^ kswz<DPH>(tl)) * 8),
-                                         (lds_ptr_t)(sK + j * 512), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds((const void*)(rowv + pc * 8),
-                                         (lds_ptr_t)(sV + j * 512), 16, 0, 0);
-      }
-    }
-    __builtin_amdgcn_s_waitcnt(0);
-    // Rows past the context may hold stale (even non-finite) bytes; their
-    // probabilities are 0 but 0 * NaN is not, so clear those V rows.
-    const int nvalid = a.L_max - ts;
-    if (nvalid < kTile) {
-      uint32_t* v32 = reinterpret_cast<uint32_t*>(sV);
-      for (int idx = nvalid * DP + lane; idx < kTile * DP; idx += 64) v32[idx] = 0u;
-    }
-
-    // ---- logits ----------------------------------------------------------
-    float s[RPW];
+  for (int r = 0; r < RPW; r++) s[r] = 0.f;
 #pragma unroll
-    for (int r = 0; r < RPW; r++) s[r] = 0.f;
-#pragma unroll
-    for (int jj = 0; jj < HCH; jj++) {
-      const int c = hh * HCH + jj;
-      const uint4 kc =
-          *reinterpret_cast<const uint4*>(sK + t * DPH + (c ^ kswz<DPH>(t)) * 8);
-#pragma unroll
-      for (int r = 0; r < RPW; r++) {
-        const uint4 qc = *reinterpret_cast<const uint4*>(sQ + r * DPH + c * 8);
-        s[r] = dot2(qc.x, kc.x, s[r]);
-        s[r] = dot2(qc.y, kc.y, s[r]);
-        s[r] = dot2(qc.z, kc.z, s[r]);
-        s[r] = dot2(qc.w, kc.w, s[r]);
-      }
-    }
-
-    // ---- online softmax (exp2 domain) ------------------------------------
-    const int tok = ts + t;
-    float alpha[RP];
-#pragma unroll
-    for (int i = 0; i < RP; i++) {
-      const float x0 = s[2 * i] + __shfl_xor(s[2 * i], 32);
-      const float x1 = s[2 * i + 1] + __shfl_xor(s[2 * i + 1], 32);
-      const float x = hh ? x1 : x0;
-      const bool valid = tok <= lim[i];
-      const float tmax = half_max(valid ? x : -INFINITY);
-      const float m_new = fmaxf(m_run[i], tmax);
-      const bool any = m_new != -INFINITY;
-      const float al = any ? __builtin_amdgcn_exp2f(m_run[i] - m_new) : 1.f;
-      const float p = (valid && any) ? __builtin_amdgcn_exp2f(x - m_new) : 0.f;
-      l_run[i] = l_run[i] * al + p;
-      m_run[i] = m_new;
-      alpha[i] = al;
-      sP[(2 * i + hh) * kTile + t] = f2h_bits(p);
-    }
-
-    // ---- P.V ---------------------------------------------------------------
+  for (int jj = 0; jj < HCH; jj++) {
 #pragma unroll
     for (int r = 0; r < RPW; r++) {
-      const float al = lane_value(alpha[r / 2], (r & 1) ? 32 : 0);
-      acc[r][0] *= al;
-      acc[r][1] *= al;
+      uint4 qc;
+      if constexpr (kQRegs)
+        qc = qreg[r][jj];
+      else
+        qc = *reinterpret_cast<const uint4*>(sQ + r * DPH + (hh * HCH + jj) * 8);
+      s[r] = dot2(qc.x, kc[jj].x, s[r]);
+      s[r] = dot2(qc.y, kc[jj].y, s[r]);
+      s[r] = dot2(qc.z, kc[jj].z, s[r]);
+      s[r] = dot2(qc.w, kc[jj].w, s[r]);
     }
-    if constexpr (DPH == 128) {
-#pragma unroll 2
-      for (int jp = 0; jp < kTile / 2; jp++) {
-        const uint32_t v0 = sV32[(2 * jp) * DP + lane];
-        const uint32_t v1 = sV32[(2 * jp + 1) * DP + lane];
-        const uint32_t lo = __builtin_amdgcn_perm(v1, v0, 0x05040100u);
-        const uint32_t hi = __builtin_amdgcn_perm(v1, v0, 0x07060302u);
-#pragma unroll
-        for (int r = 0; r < RPW; r++) {
-          const uint32_t pp = sP32[r * (kTile / 2) + jp];
-          acc[r][0] = dot2(pp, lo, acc[r][0]);
-          acc[r][1] = dot2(pp, hi, acc[r][1]);
-        }
-      }
-    } else {
-      // 32 feature pairs: lanes 0-31 take even token pairs, 32-63 odd ones.
-      const int dp = lane & 31;
-      const int tp = lane >> 5;
-#pragma unroll 2
-      for (int jj = 0; jj < kTile / 4; jj++) {
-        const int jp = 2 * jj + tp;
-        const uint32_t v0 = sV32[(2 * jp) * DP + dp];
-        const uint32_t v1 = sV32[(2 * jp + 1) * DP + dp];
-        const uint32_t lo = __builtin_amdgcn_perm(v1, v0, 0x05040100u);
-        const uint32_t hi = __builtin_amdgcn_perm(v1, v0, 0x07060302u);
-#pragma unroll
-        for (int r = 0; r < RPW; r++) {
-          const uint32_t pp = sP32[r * (kTile / 2) + jp];
-          acc[r][0] = dot2(pp, lo, acc[r][0]);
-          acc[r][1] = dot2(pp, hi, acc[r][1]);
-        }
-      }
-    }
-    // Every LDS read of this tile has returned before the next iteration's
-    // direct-to-LDS loads may overwrite the tile.
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   }
+}
 
-  // ---- per-wave row statistics -> this wave's merge record in LDS --------
-  float* const rec = reinterpret_cast<float*>(sWave[wave]);
+// Online-softmax update of one tile (exp2 domain).  On entry s holds the
+// per-half partial logits of every row; lane (t, hh) ends up owning row
+// 2i+hh of pair i.  Writes p (fp16) through put_p(row, p) and returns the
+// rescale factor of each row pair in alpha.
+template <int RPW, typename PutP>
+__device__ __forceinline__ void softmax_tile(const float (&s)[RPW], int tok, const int (&lim)[RPW / 2],
+                                             float (&m_run)[RPW / 2], float (&l_run)[RPW / 2],
+                                             float (&alpha)[RPW / 2], int hh, PutP put_p) {
 #pragma unroll
-  for (int i = 0; i < RP; i++) {
-    const float lt = half_sum(l_run[i]);
-    if (lane == 0 || lane == 32) {
-      rec[(2 * i + hh) * (DPH + 2)] = m_run[i];
-      rec[(2 * i + hh) * (DPH + 2) + 1] = lt;
+  for (int i = 0; i < RPW / 2; i++) {
+    const float x = half_pair_total(s[2 * i], s[2 * i + 1]);
+    const bool valid = tok <= lim[i];
+    const float tmax = half_max(valid ? x : -INFINITY);
+    const float m_new = fmaxf(m_run[i], tmax);
+    const bool any = m_new != -INFINITY;
+    const float al = any ? __builtin_amdgcn_exp2f(m_run[i] - m_new) : 1.f;
+    const float p = (valid && any) ? __builtin_amdgcn_exp2f(x - m_new) : 0.f;
+    l_run[i] = l_run[i] * al + p;
+    m_run[i] = m_new;
+    alpha[i] = al;
+    put_p(2 * i + hh, p);
+  }
+}
+
+// Emits the merged row: normalised output (single partition) or the
+// partition's partial record (device-scope stores).
+template <int DPH>
+__device__ __forceinline__ void emit_row(const AttnArgs& a, int part, int kvh, int gr, int lane,
+                                         int dcol, float mx, float l, float o0, float o1) {
+  const int m = gr / a.G;
+  const int h = kvh * a.G + (gr - m * a.G);
+  if (a.n_parts == 1) {
+    // attention.h:120-126: normalise unless the sum is tiny or not finite.
+    const float inv = (l > 1e-20f && isfinite(l)) ? 1.f / l : 0.f;
+    *reinterpret_cast<float2*>(a.out + (size_t)m * a.nh * DPH + (size_t)h * DPH + dcol) =
+        make_float2(o0 * inv, o1 * inv);
+  } else {
+    float* pr = a.partials + (((size_t)kvh * a.R + gr) * a.n_parts + part) * (size_t)(DPH + 2);
+    store_dev2(pr + 2 + dcol, o0, o1);
+    if (lane == 0) {
+      store_dev(pr, mx);
+      store_dev(pr + 1, l);
     }
   }
-  if constexpr (DPH == 64) {
-#pragma unroll
-    for (int r = 0; r < RPW; r++) {
-      acc[r][0] += __shfl_xor(acc[r][0], 32);
-      acc[r][1] += __shfl_xor(acc[r][1], 32);
-    }
-  }
+}
+
+// Merges the kWaves per-wave records of rows [0, nrows) (caller has synced
+// after writing them), emits outputs or partials, and for a multi-partition
+// context runs the fused partition combine in the last workgroup.
+// rec_acc(w, r, col) -> &acc of wave w, row r, feature col; rec_ml(w, r) ->
+// &(max, sum) of wave w, row r.
+template <int DPH, typename AccRec, typename MlRec>
+__device__ __forceinline__ void finish_workgroup(const AttnArgs& a, int part, int kvh, int r0,
+                                                 int nrows, int wave, int lane, AccRec rec_acc,
+                                                 MlRec rec_ml) {
   const int dcol = (DPH == 128 ? lane : (lane & 31)) * 2;
-  if (DPH == 128 || lane < 32) {
-#pragma unroll
-    for (int r = 0; r < RPW; r++)
-      *reinterpret_cast<float2*>(rec + r * (DPH + 2) + 2 + dcol) =
-          make_float2(acc[r][0], acc[r][1]);
-  }
-  __syncthreads();
-
-  // ---- merge the waves; wave w finalises rows w, w+kWaves, ... ------------
+  const bool col_lane = DPH == 128 || lane < 32;
   for (int r = wave; r < nrows; r += kWaves) {
     float mx = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kWaves; w++)
-      mx = fmaxf(mx, reinterpret_cast<const float*>(sWave[w])[r * (DPH + 2)]);
+    for (int w = 0; w < kWaves; w++) mx = fmaxf(mx, rec_ml(w, r)[0]);
     float l = 0.f, o0 = 0.f, o1 = 0.f;
 #pragma unroll
     for (int w = 0; w < kWaves; w++) {
-      const float* rw = reinterpret_cast<const float*>(sWave[w]) + r * (DPH + 2);
-      const float mw = rw[0];
+      const float mw = rec_ml(w, r)[0];
       const float wt = (mw == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(mw - mx);
-      l += rw[1] * wt;
-      if (DPH == 128 || lane < 32) {
-        const float2 aw = *reinterpret_cast<const float2*>(rw + 2 + dcol);
+      l += rec_ml(w, r)[1] * wt;
+      if (col_lane) {
+        const float2 aw = *reinterpret_cast<const float2*>(rec_acc(w, r, dcol));
         o0 += aw.x * wt;
         o1 += aw.y * wt;
       }
     }
-    if (DPH == 128 || lane < 32) {
-      const int gr = r0 + r;
-      const int m = gr / a.G;
-      const int h = kvh * a.G + (gr - m * a.G);
-      if (a.n_parts == 1) {
-        // attention.h:120-126: normalise unless the sum is tiny or not finite.
-        const float inv = (l > 1e-20f && isfinite(l)) ? 1.f / l : 0.f;
-        *reinterpret_cast<float2*>(a.out + (size_t)m * a.nh * DPH + (size_t)h * DPH + dcol) =
-            make_float2(o0 * inv, o1 * inv);
-      } else {
-        float* pr = a.partials +
-                    (((size_t)kvh * a.R + gr) * a.n_parts + part) * (size_t)(DPH + 2);
-        store_dev2(pr + 2 + dcol, o0, o1);
-        if (lane == 0) {
-          store_dev(pr, mx);
-          store_dev(pr + 1, l);
-        }
-      }
-    }
+    if (col_lane) emit_row<DPH>(a, part, kvh, r0 + r, lane, dcol, mx, l, o0, o1);
   }
   if (a.n_parts == 1) return;
 
@@ -447,7 +405,7 @@ __global__ __launch_bounds__(64 * kWaves) void attn_partition_kernel(AttnArgs a)
 #pragma unroll
         for (int u = 0; u < kBatch; u++) {
           v[u] = make_float2(0.f, 0.f);
-          if (b0 + u < n && (DPH == 128 || lane < 32))
+          if (b0 + u < n && col_lane)
             v[u] = load_dev2(base + (size_t)(p0 + b0 + u) * (DPH + 2) + 2 + dcol);
         }
 #pragma unroll
@@ -462,7 +420,7 @@ __global__ __launch_bounds__(64 * kWaves) void attn_partition_kernel(AttnArgs a)
     }
     l = half_sum(l);
     l = lane_value(l, 0) + lane_value(l, 32);
-    if (DPH == 128 || lane < 32) {
+    if (col_lane) {
       const int m = gr / a.G;
       const int h = kvh * a.G + (gr - m * a.G);
       const float inv = (l > 1e-20f && isfinite(l)) ? 1.f / l : 0.f;
@@ -470,6 +428,829 @@ __global__ __launch_bounds__(64 * kWaves) void attn_partition_kernel(AttnArgs a)
           make_float2(o0 * inv, o1 * inv);
     }
   }
+}
+
+// ---------------------------------------------------------------------------
+// attn_partition_kernel: K and V both staged in LDS (large row groups).
+// ---------------------------------------------------------------------------
+template <int DPH, int RPW>
+__global__ __launch_bounds__(64 * kWaves) void attn_partition_kernel(AttnArgs a) {
+  static_assert(DPH == 64 || DPH == 128, "head_dim");
+  static_assert(RPW % 2 == 0 && RPW <= kMaxRowsPerWave, "rows per wave");
+  constexpr int CH = DPH / 8;       // 16-byte chunks per head row
+  constexpr int TPL = 64 / CH;      // tokens per load instruction
+  constexpr int NLD = kTile / TPL;  // load instructions per tile (per K and per V)
+  constexpr int RP = RPW / 2;       // row pairs
+  constexpr int DP = DPH / 2;       // fp16 pairs per head row
+
+  __shared__ __attribute__((aligned(16))) uint16_t sQ[RPW * DPH];
+  // The P tile lives behind the V tile.
+  __shared__ __attribute__((aligned(16))) uint16_t sKw[kWaves][kTile * DPH];
+  __shared__ __attribute__((aligned(16))) uint16_t sVw[kWaves][kTile * DPH + RPW * kTile];
+
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  uint16_t* const sK = sKw[wave];
+  uint16_t* const sV = sVw[wave];
+  uint16_t* const sP = sVw[wave] + kTile * DPH;
+  const uint32_t* const sV32 = reinterpret_cast<const uint32_t*>(sV);
+
+  const int part = blockIdx.x;
+  const int kvh = blockIdx.y;
+  const int r0 = blockIdx.z * RPW;
+  const int nrows = min(RPW, a.R - r0);
+  const int t_begin = part * a.tiles_per_wave * kWaves * kTile;
+  const int t_end = min(a.L_max, t_begin + a.tiles_per_wave * kWaves * kTile);
+
+  stage_q<DPH, RPW>(a, kvh, r0, nrows, sQ);
+
+  const int t = lane & 31;
+  const int hh = lane >> 5;
+  int lim[RP];  // last visible position of row 2i+hh (-1: padding row)
+  float m_run[RP], l_run[RP];
+#pragma unroll
+  for (int i = 0; i < RP; i++) {
+    const int r = 2 * i + hh;
+    lim[i] = (r < nrows) ? a.pos_base + (r0 + r) / a.G : -1;
+    m_run[i] = -INFINITY;
+    l_run[i] = 0.f;
+  }
+  float acc[RPW][2];
+#pragma unroll
+  for (int r = 0; r < RPW; r++) acc[r][0] = acc[r][1] = 0.f;
+
+  __syncthreads();  // sQ complete
+  const uint4 no_qreg[1][1] = {};
+
+  const const_table_t table = const_table(a);
+  auto load_tile = [&](int ts_, const int (&blk)[NLD], uint16_t* dst, bool is_v) {
+#pragma unroll
+    for (int j = 0; j < NLD; j++) {
+      const int g0 = ts_ + j * TPL;  // wave-uniform; the group shares a block
+      if (g0 < a.L_max) {
+        const int pc = lane % CH;
+        const int chunk = is_v ? pc : (pc ^ kswz<DPH>(j * TPL + lane / CH));
+        load_lds16(chunk_addr<DPH>(a, kvh, blk[j], g0, lane, chunk, is_v), dst + j * 512);
+      }
+    }
+  };
+
+  // Split-phase pipeline per wave: K(next) streams in during softmax + P.V
+  // of this tile, V(next) during Q.K of the next one.  Loads complete in
+  // issue order, so "vmcnt <= NLD" means all but the last tile-half landed.
+  // The waves run different numbers of tiles: only wave-local ordering is
+  // used inside this loop (LDS operations of one wave complete in order).
+  const int stride = kWaves * kTile;
+  int ts = t_begin + wave * kTile;
+  int blk[NLD];
+  if (ts < t_end) {
+    tile_blocks<NLD, TPL>(a, table, ts, blk);
+    load_tile(ts, blk, sK, false);
+    load_tile(ts, blk, sV, true);
+  }
+  for (; ts < t_end; ts += stride) {
+    const int ts_next = ts + stride;
+    const bool has_next = ts_next < t_end;
+    const bool full = ts + kTile <= a.L_max;
+    const bool next_full = has_next && ts_next + kTile <= a.L_max;
+    int blk_next[NLD];
+    if (has_next) tile_blocks<NLD, TPL>(a, table, ts_next, blk_next);
+
+    if (full)
+      wait_vmcnt<NLD>();  // K(ts) landed; V(ts) may be in flight
+    else
+      wait_vmcnt<0>();
+
+    float s[RPW];
+    qk_tile<DPH, RPW, false>(sK, sQ, no_qreg, t, hh, s);
+    // The K tile has been read: stream the next one in behind this tile.
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    if (has_next) load_tile(ts_next, blk_next, sK, false);
+
+    float alpha[RP];
+    softmax_tile<RPW>(s, ts + t, lim, m_run, l_run, alpha, hh,
+                      [&](int r, float p) { sP[r * kTile + t] = f2h_bits(p); });
+#pragma unroll
+    for (int r = 0; r < RPW; r++) {
+      const float al = lane_value(alpha[r / 2], (r & 1) ? 32 : 0);
+      acc[r][0] *= al;
+      acc[r][1] *= al;
+    }
+
+    if (next_full)
+      wait_vmcnt<NLD>();  // V(ts) landed; K(next) may be in flight
+    else
+      wait_vmcnt<0>();
+    // Rows past the context may hold stale (even non-finite) bytes; their
+    // probabilities are 0 but 0 * NaN is not, so clear those V rows.
+    if (!full) {
+      uint32_t* v32 = reinterpret_cast<uint32_t*>(sV);
+      for (int idx = (a.L_max - ts) * DP + lane; idx < kTile * DP; idx += 64) v32[idx] = 0u;
+    }
+
+    // ---- P.V: 8 tokens (4 probability pairs per row) per step ----------
+    // DPH 128: lane owns feature pair `lane`.  DPH 64: lanes 0-31 take
+    // tokens 0-15 and lanes 32-63 tokens 16-31 of feature pair lane & 31.
+    constexpr int kGroups = (DPH == 128) ? kTile / 8 : kTile / 16;
+    const int dp = (DPH == 128) ? lane : (lane & 31);
+    const int g_base = (DPH == 128) ? 0 : hh * kGroups;
+#pragma unroll
+    for (int gi = 0; gi < kGroups; gi++) {
+      const int g = g_base + gi;
+      uint32_t vv[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) vv[u] = sV32[(8 * g + u) * DP + dp];
+      uint32_t lo[4], hi[4];  // (token 2q, token 2q+1) pairs of both features
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        lo[q] = __builtin_amdgcn_perm(vv[2 * q + 1], vv[2 * q], 0x05040100u);
+        hi[q] = __builtin_amdgcn_perm(vv[2 * q + 1], vv[2 * q], 0x07060302u);
+      }
+#pragma unroll
+      for (int r = 0; r < RPW; r++) {
+        const uint4 pr = *reinterpret_cast<const uint4*>(sP + r * kTile + 8 * g);
+        acc[r][0] = dot2(pr.x, lo[0], acc[r][0]);
+        acc[r][1] = dot2(pr.x, hi[0], acc[r][1]);
+        acc[r][0] = dot2(pr.y, lo[1], acc[r][0]);
+        acc[r][1] = dot2(pr.y, hi[1], acc[r][1]);
+        acc[r][0] = dot2(pr.z, lo[2], acc[r][0]);
+        acc[r][1] = dot2(pr.z, hi[2], acc[r][1]);
+        acc[r][0] = dot2(pr.w, lo[3], acc[r][0]);
+        acc[r][1] = dot2(pr.w, hi[3], acc[r][1]);
+      }
+    }
+    // The V and P tiles have been read: stream the next V tile in.
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    if (has_next) {
+      load_tile(ts_next, blk_next, sV, true);
+#pragma unroll
+      for (int j = 0; j < NLD; j++) blk[j] = blk_next[j];
+    }
+  }
+  wait_vmcnt<0>();
+
+  // ---- per-wave records: accumulator columns [0, DPH/2) in the wave's K
+  // tile, [DPH/2, DPH) in its V tile, (max, sum) in its P tile -------------
+  auto rec_acc = [&](int w, int r, int col) -> float* {
+    float* base = reinterpret_cast<float*>(col < DPH / 2 ? sKw[w] : sVw[w]);
+    return base + r * (DPH / 2) + (col & (DPH / 2 - 1));
+  };
+  auto rec_ml = [&](int w, int r) -> float* {
+    return reinterpret_cast<float*>(sVw[w] + kTile * DPH) + 2 * r;
+  };
+#pragma unroll
+  for (int i = 0; i < RP; i++) {
+    const float lt = half_sum(l_run[i]);
+    if (lane == 0 || lane == 32) {
+      rec_ml(wave, 2 * i + hh)[0] = m_run[i];
+      rec_ml(wave, 2 * i + hh)[1] = lt;
+    }
+  }
+  if constexpr (DPH == 64) {
+    // lanes 32-63 summed the other half of the tokens: fold them in.
+#pragma unroll
+    for (int r = 0; r < RPW; r++) {
+      acc[r][0] = half_pair_total(acc[r][0], acc[r][0]);
+      acc[r][1] = half_pair_total(acc[r][1], acc[r][1]);
+    }
+  }
+  const int dcol = (DPH == 128 ? lane : (lane & 31)) * 2;
+  if (DPH == 128 || lane < 32) {
+#pragma unroll
+    for (int r = 0; r < RPW; r++)
+      *reinterpret_cast<float2*>(rec_acc(wave, r, dcol)) = make_float2(acc[r][0], acc[r][1]);
+  }
+  __syncthreads();
+  finish_workgroup<DPH>(a, part, kvh, r0, nrows, wave, lane, rec_acc, rec_ml);
+}
+
+// ---------------------------------------------------------------------------
+// attn_stream_kernel: decode and short windows (<= kStreamMaxRows rows per
+// wave).  K and V stream from HBM straight into VGPRs in the load layout --
+// lane (slot sl, chunk c) holds features 8c..8c+7 of token j*SL + sl of load
+// j -- software-pipelined across tiles: K of tile i+1 is issued before tile
+// i's logits and V of tile i+1 before tile i's P.V, so each wave keeps a
+// tile of loads in flight while it computes; no LDS holds K or V.
+//  * Q.K: each lane takes dot2 products of its K chunk with the same chunk of
+//    every q row; a transposing butterfly over the CH lanes of a token
+//    leaves each lane the full logits of one (row, token pair);
+//  * softmax: each token slot keeps its own online-softmax state (running
+//    max and sum per row), so a tile needs no cross-slot traffic; the SL
+//    states merge once, when the wave is done;
+//  * P.V: the probability pair of loads 2j', 2j'+1 (fp16x2, broadcast from
+//    its owner lane) dot2-accumulates against the byte-permuted V pairs,
+//    fp32 accumulators.
+// One workgroup of kStreamWaves waves per (partition, KV head, row group),
+// about one workgroup per CU; the partition combine reads every partial in
+// a single round trip.
+// ---------------------------------------------------------------------------
+constexpr int kStreamWaves = 8;
+constexpr int kStreamMaxRows = 4;
+constexpr int kStreamMaxParts = 64;
+
+__device__ __forceinline__ uint32_t pack_h2(float x, float y) {
+  const half2_t h = {(_Float16)x, (_Float16)y};
+  return __builtin_bit_cast(uint32_t, h);
+}
+
+// Sum over the CH lanes holding one token (a 16-lane row, or an 8-lane half
+// row for dph 64); every lane of the group gets the total.
+template <int CH>
+__device__ __forceinline__ float token_sum(float x) {
+  x += dpp_f(x, 0);
+  x += dpp_f(x, 1);
+  if constexpr (CH == 16) {
+    x += dpp_f(x, 2);
+    x += dpp_f(x, 3);
+  } else {
+    x += dpp_f(x, 4);
+  }
+  return x;
+}
+
+// All-reduce over the token slots (lanes with the same chunk c).
+template <int DPH>
+__device__ __forceinline__ float slot_sum(float x) {
+  if constexpr (DPH == 64) x += dpp_f(x, 3);  // slots 2k, 2k+1 share a 16-lane row
+  const float2 p = row_pair(x);
+  x = p.x + p.y;
+  return half_pair_total(x, x);
+}
+
+template <int DPH>
+__device__ __forceinline__ float slot_max(float x) {
+  if constexpr (DPH == 64) x = fmaxf(x, dpp_f(x, 3));
+  const float2 p = row_pair(x);
+  x = fmaxf(p.x, p.y);
+  const auto q = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, x),
+                                                  __builtin_bit_cast(int, x), false, false);
+  return fmaxf(__builtin_bit_cast(float, (int)q[0]), __builtin_bit_cast(float, (int)q[1]));
+}
+
+__device__ __forceinline__ float wave_max(float x) {
+  x = half_max(x);
+  return fmaxf(lane_value(x, 0), lane_value(x, 32));
+}
+
+__device__ __forceinline__ float wave_sum(float x) {
+  x = half_sum(x);
+  return lane_value(x, 0) + lane_value(x, 32);
+}
+
+__device__ __forceinline__ float4 load_dev4(const float* p) {
+  const float2 lo = load_dev2(p);
+  const float2 hi = load_dev2(p + 2);
+  return make_float4(lo.x, lo.y, hi.x, hi.y);
+}
+
+__device__ __forceinline__ uint4 ld16(const char* p) { return *reinterpret_cast<const uint4*>(p); }
+
+// Physical block and in-block slot of the first token of each load group of
+// tile ts (SL tokens per group, SL divides block_size).  Groups at or past
+// L_max are pinned to token L_max-1 so every address stays on written data.
+template <int NLD, int SL>
+__device__ __forceinline__ void tile_groups(const AttnArgs& a, const_table_t table, int ts,
+                                            int (&blk)[NLD], int (&slot)[NLD]) {
+  if (ts + kTile <= a.L_max) {
+    int lb = ts / a.bs;
+    int s = ts - lb * a.bs;
+#pragma unroll
+    for (int j = 0; j < NLD; j++) {
+      blk[j] = table[lb];
+      slot[j] = s;
+      s += SL;
+      if (s == a.bs) {
+        s = 0;
+        ++lb;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < NLD; j++) {
+      const int g = min(ts + j * SL, a.L_max - 1);
+      const int lb = g / a.bs;
+      blk[j] = table[lb];
+      slot[j] = g - lb * a.bs;
+    }
+  }
+}
+
+// Issues the K (is_v false) or V loads of tile ts: load j brings token
+// ts + j*SL + sl, 16-byte chunk c (lane_off = sl*row_bytes + 16c from the
+// group's first token).  Lanes whose token is at or past L_max read the
+// group's first token instead (chunk_off = 16c); their logits are masked.
+// Every path issues the same NLD loads, so the compiler's vmcnt bookkeeping
+// stays exact across tiles.
+template <int DPH>
+__device__ __forceinline__ void stream_load(const AttnArgs& a, const char* head_base, int ts,
+                                            int sl, uint32_t lane_off, uint32_t chunk_off,
+                                            bool is_v, const int (&blk)[kTile / (512 / DPH)],
+                                            const int (&slot)[kTile / (512 / DPH)],
+                                            uint4 (&x)[kTile / (512 / DPH)]) {
+  constexpr int SL = 512 / DPH;
+  constexpr int NLD = kTile / SL;
+  const uint32_t row_bytes = 2u * (uint32_t)a.kv_dim;
+  const uint32_t v_bytes = (uint32_t)a.bs * row_bytes;
+  const bool full = ts + kTile <= a.L_max;
+#pragma unroll
+  for (int j = 0; j < NLD; j++) {
+    const char* ub = head_base + (uint64_t)(uint32_t)blk[j] * (2ull * v_bytes) +
+                     (uint32_t)slot[j] * row_bytes + (is_v ? v_bytes : 0u);
+    const uint32_t off = (full || ts + j * SL + sl < a.L_max) ? lane_off : chunk_off;
+    x[j] = ld16(ub + off);
+  }
+  // Compiler barriers: keep the loads here instead of letting them sink to
+  // their first use a tile later, and keep the scheduler from interleaving
+  // neighbouring tiles' work (code-motion fences only; no wait).
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// Marks the point where a tile's registers are first consumed: the empty
+// asm redefines them, so no use of the tile (and hence no wait for its
+// loads) is hoisted above this point into the previous tile's work.  SITE
+// makes the asm text differ per call site, so identical pins at the heads of
+// two branches are not merged and hoisted into their common predecessor.
+template <int NLD, int SITE>
+__device__ __forceinline__ void pin_arrival(const uint4 (&x)[NLD]) {
+  uint4(&y)[NLD] = const_cast<uint4(&)[NLD]>(x);
+#pragma unroll
+  for (int j = 0; j < NLD; j++) {
+    if constexpr (SITE == 0) asm volatile("; tile 0" : "+v"(y[j].x), "+v"(y[j].y), "+v"(y[j].z), "+v"(y[j].w));
+    else if constexpr (SITE == 1) asm volatile("; tile 1" : "+v"(y[j].x), "+v"(y[j].y), "+v"(y[j].z), "+v"(y[j].w));
+    else if constexpr (SITE == 2) asm volatile("; tile 2" : "+v"(y[j].x), "+v"(y[j].y), "+v"(y[j].z), "+v"(y[j].w));
+    else asm volatile("; tile 3" : "+v"(y[j].x), "+v"(y[j].y), "+v"(y[j].z), "+v"(y[j].w));
+  }
+}
+
+// Lane roles of attn_stream_kernel.  Load role: lane = (slot sl, chunk c),
+// c = lane % CH.  After the transposing reduction of the logits a lane owns
+// one (row r, token pair jp) of its slot: the NV = RPW*NLD partial logits of
+// a lane are halved once per butterfly step (the lane keeps the half named
+// by one bit of c and adds its partner's copy of that half), so after
+// log2(NV)-1 steps a lane holds the full logits of tokens 2jp and 2jp+1 of
+// row r, and the softmax does per-lane scalar work.
+template <int DPH, int RPW>
+struct StreamShape {
+  static constexpr int CH = DPH / 8;                  // lanes per token
+  static constexpr int S = CH == 16 ? 4 : 3;          // butterfly steps over CH lanes
+  static constexpr int SL = 64 / CH;                  // slots
+  static constexpr int NLD = kTile / SL;              // loads per tile (K and V each)
+  static constexpr int NV = RPW * NLD;                // partial logits per lane
+  static constexpr int T = (NV == 32 ? 5 : NV == 16 ? 4 : NV == 8 ? 3 : 2) - 1;  // halving steps
+  static constexpr int RB = RPW == 4 ? 2 : 1;         // bits of r
+  static_assert(T <= S, "more logits than lanes to spread them over");
+  // chunk index of the lane owning (row r, pair jp) (its redundant bits 0)
+  static constexpr int owner(int r, int jp) { return ((r << (T - RB)) | jp) << (S - T); }
+};
+
+// Butterfly step k over the CH lanes of a token: partner lane = c ^ mask,
+// masks {8, 7, 2, 1} (dph 128) or {7, 2, 1} (dph 64) -- row_ror:8,
+// row_half_mirror, quad_perm [2,3,0,1], quad_perm [1,0,3,2]; step k splits on
+// bit S-1-k of c, which the later masks leave unchanged.
+template <int CH>
+__device__ __forceinline__ float bfly(float x, int k) {
+  const int v = __builtin_bit_cast(int, x);
+  int r;
+  switch (CH == 16 ? k : k + 1) {
+    case 0: r = __builtin_amdgcn_update_dpp(0, v, 0x128, 0xf, 0xf, false); break;
+    case 1: r = __builtin_amdgcn_update_dpp(0, v, 0x141, 0xf, 0xf, false); break;
+    case 2: r = __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xf, 0xf, false); break;
+    default: r = __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xf, 0xf, false); break;
+  }
+  return __builtin_bit_cast(float, r);
+}
+
+// Value of lane n of this lane's 16-lane row (DPP row_newbcast:n).
+__device__ __forceinline__ int row_bcast(int v, int n) {
+  switch (n) {
+    case 0: return __builtin_amdgcn_update_dpp(0, v, 0x150, 0xf, 0xf, false);
+    case 1: return __builtin_amdgcn_update_dpp(0, v, 0x151, 0xf, 0xf, false);
+    case 2: return __builtin_amdgcn_update_dpp(0, v, 0x152, 0xf, 0xf, false);
+    case 3: return __builtin_amdgcn_update_dpp(0, v, 0x153, 0xf, 0xf, false);
+    case 4: return __builtin_amdgcn_update_dpp(0, v, 0x154, 0xf, 0xf, false);
+    case 5: return __builtin_amdgcn_update_dpp(0, v, 0x155, 0xf, 0xf, false);
+    case 6: return __builtin_amdgcn_update_dpp(0, v, 0x156, 0xf, 0xf, false);
+    case 7: return __builtin_amdgcn_update_dpp(0, v, 0x157, 0xf, 0xf, false);
+    case 8: return __builtin_amdgcn_update_dpp(0, v, 0x158, 0xf, 0xf, false);
+    case 9: return __builtin_amdgcn_update_dpp(0, v, 0x159, 0xf, 0xf, false);
+    case 10: return __builtin_amdgcn_update_dpp(0, v, 0x15A, 0xf, 0xf, false);
+    case 11: return __builtin_amdgcn_update_dpp(0, v, 0x15B, 0xf, 0xf, false);
+    case 12: return __builtin_amdgcn_update_dpp(0, v, 0x15C, 0xf, 0xf, false);
+    case 13: return __builtin_amdgcn_update_dpp(0, v, 0x15D, 0xf, 0xf, false);
+    case 14: return __builtin_amdgcn_update_dpp(0, v, 0x15E, 0xf, 0xf, false);
+    default: return __builtin_amdgcn_update_dpp(0, v, 0x15F, 0xf, 0xf, false);
+  }
+}
+
+// Value held by the owner of (row r, pair jp) in this lane's slot.  With
+// dph 64 a 16-lane row holds two slots (lane bit 3 = odd slot).
+template <int DPH, int RPW>
+__device__ __forceinline__ uint32_t from_owner(uint32_t x, int r, int jp, bool odd_slot) {
+  using Sh = StreamShape<DPH, RPW>;
+  const int n = Sh::owner(r, jp);
+  const int v = (int)x;
+  if constexpr (DPH == 128) {
+    return (uint32_t)row_bcast(v, n);
+  } else {
+    const int lo = row_bcast(v, n);
+    const int hi = row_bcast(v, n + 8);
+    return (uint32_t)(odd_slot ? hi : lo);
+  }
+}
+
+template <int DPH, int RPW>
+__device__ __forceinline__ float from_owner_f(float x, int r, int jp, bool odd_slot) {
+  return __builtin_bit_cast(
+      float, from_owner<DPH, RPW>(__builtin_bit_cast(uint32_t, x), r, jp, odd_slot));
+}
+
+// Logits of one tile (transposing reduction) and the online-softmax update
+// of the lane's (row, pair): m_run / l_run are the lane's (row, slot) state
+// (l_run a partial sum over the lane's token pairs).  Returns the rescale
+// factor in al_out and the pair's probabilities as fp16x2 in pk_out.
+template <int DPH, int RPW, int SITE>
+__device__ __forceinline__ void stream_qk(int ts, int sl, int c, int min_lim, int my_lim,
+                                          int my_jp, const uint4 (&qr)[RPW],
+                                          const uint4 (&k)[kTile / (512 / DPH)], float& m_run,
+                                          float& l_run, float& al_out, uint32_t& pk_out) {
+  using Sh = StreamShape<DPH, RPW>;
+  constexpr int CH = Sh::CH, S = Sh::S, SL = Sh::SL, NLD = Sh::NLD, NV = Sh::NV, T = Sh::T;
+  pin_arrival<NLD, SITE>(k);
+  float x[NV];
+#pragma unroll
+  for (int r = 0; r < RPW; r++) {
+    const uint4 q4 = qr[r];
+#pragma unroll
+    for (int j = 0; j < NLD; j++) {
+      float t = dot2(q4.x, k[j].x, 0.f);
+      t = dot2(q4.y, k[j].y, t);
+      t = dot2(q4.z, k[j].z, t);
+      t = dot2(q4.w, k[j].w, t);
+      x[r * NLD + j] = t;
+    }
+  }
+  // Transposing butterfly: step kk keeps the half of x whose top index bit
+  // equals bit S-1-kk of c.
+#pragma unroll
+  for (int kk = 0; kk < T; kk++) {
+    const bool f = (c >> (S - 1 - kk)) & 1;
+    const int h = NV >> (kk + 1);
+#pragma unroll
+    for (int i = 0; i < (NV >> 1); i++) {
+      if (i < h) {
+        const float a = x[i], b = x[i + h];
+        const float send = f ? a : b;
+        const float keep = f ? b : a;
+        x[i] = keep + bfly<CH>(send, kk);
+      }
+    }
+  }
+#pragma unroll
+  for (int kk = T; kk < S; kk++) {
+    x[0] += bfly<CH>(x[0], kk);
+    x[1] += bfly<CH>(x[1], kk);
+  }
+  float s0 = x[0], s1 = x[1];
+  // Causal / length mask: token g is visible to the lane's row iff g <= my_lim.
+  if (ts + kTile - 1 > min_lim) {
+    const int g0 = ts + 2 * my_jp * SL + sl;
+    if (g0 > my_lim) s0 = -INFINITY;
+    if (g0 + SL > my_lim) s1 = -INFINITY;
+  }
+  float tmax = fmaxf(s0, s1);
+#pragma unroll
+  for (int kk = Sh::RB; kk < S; kk++) tmax = fmaxf(tmax, bfly<CH>(tmax, kk));
+  const float m_new = fmaxf(m_run, tmax);
+  // Nothing visible yet: base 0 makes every weight exp2(-inf) = 0.
+  const float base = m_new == -INFINITY ? 0.f : m_new;
+  const float al = __builtin_amdgcn_exp2f(m_run - base);
+  const float p0 = __builtin_amdgcn_exp2f(s0 - base);
+  const float p1 = __builtin_amdgcn_exp2f(s1 - base);
+  l_run = l_run * al + (p0 + p1);
+  m_run = m_new;
+  al_out = al;
+  pk_out = pack_h2(p0, p1);
+  // Finish this tile's logits here, in program order (see pin_arrival).
+  asm volatile("" : "+v"(m_run), "+v"(l_run), "+v"(al_out), "+v"(pk_out));
+}
+
+// P.V of one tile: rescales acc by each row's factor and accumulates the
+// probability pairs (from their owners) against the byte-permuted V pairs.
+template <int DPH, int RPW, int SITE>
+__device__ __forceinline__ void stream_pv(int sl, float al, uint32_t pk,
+                                          const uint4 (&v)[kTile / (512 / DPH)],
+                                          float (&acc)[RPW][8]) {
+  constexpr int NLD = StreamShape<DPH, RPW>::NLD;
+  pin_arrival<NLD, SITE>(v);
+  const bool odd_slot = sl & 1;
+#pragma unroll
+  for (int r = 0; r < RPW; r++) {
+    const float a_r = from_owner_f<DPH, RPW>(al, r, 0, odd_slot);
+#pragma unroll
+    for (int e = 0; e < 8; e++) acc[r][e] *= a_r;
+  }
+#pragma unroll
+  for (int jp = 0; jp < NLD / 2; jp++) {
+    uint32_t pp[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; r++) pp[r] = from_owner<DPH, RPW>(pk, r, jp, odd_slot);
+    const uint32_t v0[4] = {v[2 * jp].x, v[2 * jp].y, v[2 * jp].z, v[2 * jp].w};
+    const uint32_t v1[4] = {v[2 * jp + 1].x, v[2 * jp + 1].y, v[2 * jp + 1].z, v[2 * jp + 1].w};
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+      const uint32_t lo = __builtin_amdgcn_perm(v1[w], v0[w], 0x05040100u);
+      const uint32_t hi = __builtin_amdgcn_perm(v1[w], v0[w], 0x07060302u);
+#pragma unroll
+      for (int r = 0; r < RPW; r++) {
+        acc[r][2 * w] = dot2(pp[r], lo, acc[r][2 * w]);
+        acc[r][2 * w + 1] = dot2(pp[r], hi, acc[r][2 * w + 1]);
+      }
+    }
+  }
+  // Finish this tile's P.V here, in program order, so it is not sunk past
+  // the following tiles' work (which would keep its V registers live).
+#pragma unroll
+  for (int r = 0; r < RPW; r++)
+    asm volatile("" : "+v"(acc[r][0]), "+v"(acc[r][1]), "+v"(acc[r][2]), "+v"(acc[r][3]),
+                 "+v"(acc[r][4]), "+v"(acc[r][5]), "+v"(acc[r][6]), "+v"(acc[r][7]));
+}
+
+// Partition combine of attn_stream_kernel, run by the last workgroup of a
+// (KV head, row group): thread (row r, float4 column c4, quarter sub) loads
+// (max, sum, acc[c4]) of partitions sub, sub+4, ... -- every partial in one
+// round trip, no LDS -- weights them by exp2(m_p - max) and the four
+// quarters of a (row, column) (adjacent lanes) reduce through DPP in a fixed
+// order, so the result does not depend on arrival order.
+template <int DPH, int RPW>
+__device__ __forceinline__ void stream_combine(const AttnArgs& a, int kvh, int r0, int nrows) {
+  constexpr int C4 = DPH / 4;
+  constexpr int SUB = 4;
+  constexpr int PMAX = kStreamMaxParts / SUB;
+  static_assert(RPW * C4 * SUB <= 64 * kStreamWaves, "one thread per (row, column, quarter)");
+  const int tid = threadIdx.x;
+  const int sub = tid & (SUB - 1);
+  const int col4 = (tid / SUB) % C4;
+  const int r = tid / (SUB * C4);  // uniform per wave
+  if (r >= nrows) return;
+  const int P = a.n_parts;
+  const size_t row = (size_t)kvh * a.R + r0 + r;
+  const float* ml = a.partials + row * P * 2;
+  const float* accp = a.partials + (size_t)gridDim.y * a.R * P * 2 + row * P * DPH + 4 * col4;
+  float2 e[PMAX];
+  float4 v[PMAX];
+#pragma unroll
+  for (int i = 0; i < PMAX; i++) {
+    const int p = sub + i * SUB;
+    e[i] = make_float2(-INFINITY, 0.f);
+    v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (p < P) {
+      e[i] = load_dev2(ml + (size_t)p * 2);
+      v[i] = load_dev4(accp + (size_t)p * DPH);
+    }
+  }
+  float mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < PMAX; i++) mx = fmaxf(mx, e[i].x);
+  mx = fmaxf(mx, dpp_f(mx, 0));
+  mx = fmaxf(mx, dpp_f(mx, 1));
+  float l = 0.f;
+  float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int i = 0; i < PMAX; i++) {
+    const float w = e[i].x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(e[i].x - mx);
+    l += e[i].y * w;
+    o.x += w * v[i].x;
+    o.y += w * v[i].y;
+    o.z += w * v[i].z;
+    o.w += w * v[i].w;
+  }
+#pragma unroll
+  for (int k = 0; k < 2; k++) {
+    l += dpp_f(l, k);
+    o.x += dpp_f(o.x, k);
+    o.y += dpp_f(o.y, k);
+    o.z += dpp_f(o.z, k);
+    o.w += dpp_f(o.w, k);
+  }
+  if (sub == 0) {
+    // attention.h:120-126: normalise unless the sum is tiny or not finite.
+    const float inv = (l > 1e-20f && isfinite(l)) ? 1.f / l : 0.f;
+    const int gr = r0 + r;
+    const int m = gr / a.G;
+    const int h = kvh * a.G + (gr - m * a.G);
+    float2* dst = reinterpret_cast<float2*>(a.out + (size_t)m * a.nh * DPH + (size_t)h * DPH +
+                                            4 * col4);
+    dst[0] = make_float2(o.x * inv, o.y * inv);
+    dst[1] = make_float2(o.z * inv, o.w * inv);
+  }
+}
+
+template <int DPH, int RPW, int CHUNK>
+__global__ __launch_bounds__(64 * kStreamWaves) void attn_stream_kernel(AttnArgs a) {
+  static_assert(DPH == 64 || DPH == 128, "head_dim");
+  static_assert(RPW == 2 || RPW == 4, "rows per wave");
+  constexpr int CH = DPH / 8;
+  constexpr int SL = 64 / CH;
+  constexpr int NLD = kTile / SL;
+  constexpr int REC = DPH + 2;
+  // Per-wave records (max, sum, acc[DPH]) of every row.
+  __shared__ __attribute__((aligned(16))) float s_buf[kStreamWaves * RPW * REC];
+  __shared__ int s_last;
+
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int sl = lane / CH;
+  const int c = lane % CH;
+  const int part = blockIdx.x;
+  const int kvh = blockIdx.y;
+  const int r0 = blockIdx.z * RPW;
+  const int nrows = min(RPW, a.R - r0);
+  const int n_tiles = (a.L_max + kTile - 1) / kTile;
+  const int tb = part * a.tiles_per_part;
+  const int te = min(n_tiles, tb + a.tiles_per_part);
+
+  using Sh = StreamShape<DPH, RPW>;
+  // This lane's (row, pair) in the transposed layout, and its redundancy.
+  const int prefix = c >> (Sh::S - Sh::T);
+  const int my_r = prefix >> (Sh::T - Sh::RB);
+  const int my_jp = prefix & ((1 << (Sh::T - Sh::RB)) - 1);
+  const bool redundant = (c & ((1 << (Sh::S - Sh::T)) - 1)) != 0;
+
+  // This lane's q chunk (features 8c..8c+7) of every row, loaded before any
+  // K/V load so that waiting for it never waits for tile data; it is scaled
+  // into the exp2 domain and rounded to fp16 pairs once the first tile's
+  // loads are in flight.
+  float2 q_raw[RPW][4];
+#pragma unroll
+  for (int r = 0; r < RPW; r++) {
+    const int gr = min(r0 + r, a.R - 1);  // rows past nrows: zeroed below
+    const int m = gr / a.G;
+    const int h = kvh * a.G + (gr - m * a.G);
+    const float2* qp = reinterpret_cast<const float2*>(a.q + (size_t)m * a.nh * DPH +
+                                                       (size_t)h * DPH + 8 * c);
+#pragma unroll
+    for (int w = 0; w < 4; w++) q_raw[r][w] = qp[w];
+  }
+  // Last visible position of each row (query m sees pos_base + m); rows
+  // past nrows see nothing.
+  int min_lim = INT_MAX, my_lim = -1;
+#pragma unroll
+  for (int r = 0; r < RPW; r++) {
+    const int lim = r < nrows ? a.pos_base + (r0 + r) / a.G : -1;
+    min_lim = min(min_lim, lim);
+    if (r == my_r) my_lim = lim;
+  }
+
+  float m_run = -INFINITY, l_run = 0.f, acc[RPW][8];
+#pragma unroll
+  for (int r = 0; r < RPW; r++)
+#pragma unroll
+    for (int e = 0; e < 8; e++) acc[r][e] = 0.f;
+
+  const const_table_t table = const_table(a);
+  const char* head_base = reinterpret_cast<const char*>(a.pool) + (size_t)kvh * DPH * 2u;
+  const uint32_t lane_off = (uint32_t)sl * 2u * (uint32_t)a.kv_dim + 16u * c;
+  const uint32_t chunk_off = 16u * c;
+  // Wave w takes tiles tb+w, tb+w+W, ... in chunks of CHUNK tiles.  Within
+  // a chunk the code is straight-line (unrolled at compile time): K of tile
+  // i+1 is issued before tile i's logits and V of tile i+1 before tile i's
+  // P.V, so a tile of loads stays in flight while the wave computes, and the
+  // compiler's waits before each use are exact (no loop-carried buffers,
+  // no register copies of in-flight data).  Chunk slots past the wave's
+  // last tile re-read that tile (an L2 hit) and are fully masked.
+  constexpr int W = kStreamWaves;
+  const int first = tb + wave;
+  if (first < te) {
+    const int last = first + ((te - 1 - first) / W) * W;
+    uint4 qr[RPW];
+    for (int c0 = first; c0 < te; c0 += CHUNK * W) {
+      uint4 kbuf[2][NLD], vbuf[2][NLD];
+      int blk[2][NLD], slot[2][NLD];
+      float al;
+      uint32_t pk;
+      tile_groups<NLD, SL>(a, table, min(c0, last) * kTile, blk[0], slot[0]);
+      stream_load<DPH>(a, head_base, min(c0, last) * kTile, sl, lane_off, chunk_off, false,
+                       blk[0], slot[0], kbuf[0]);
+      stream_load<DPH>(a, head_base, min(c0, last) * kTile, sl, lane_off, chunk_off, true,
+                       blk[0], slot[0], vbuf[0]);
+      if (CHUNK > 1)
+        tile_groups<NLD, SL>(a, table, min(c0 + W, last) * kTile, blk[1], slot[1]);
+#pragma unroll
+      for (int i = 0; i < CHUNK; i++) {
+        const int t = c0 + i * W;
+        const int b = i & 1, nb = b ^ 1;
+        const int tn = min(t + W, last);
+        if (i + 1 < CHUNK)
+          stream_load<DPH>(a, head_base, tn * kTile, sl, lane_off, chunk_off, false, blk[nb],
+                           slot[nb], kbuf[nb]);
+        if (i == 0) {
+#pragma unroll
+          for (int r = 0; r < RPW; r++) {
+            const float sc = r < nrows ? a.qscale : 0.f;
+            qr[r] = make_uint4(pack_h2(q_raw[r][0].x * sc, q_raw[r][0].y * sc),
+                               pack_h2(q_raw[r][1].x * sc, q_raw[r][1].y * sc),
+                               pack_h2(q_raw[r][2].x * sc, q_raw[r][2].y * sc),
+                               pack_h2(q_raw[r][3].x * sc, q_raw[r][3].y * sc));
+          }
+        }
+        // A slot past the wave's last tile: every token masked (no-op).
+        const int ts_mask = t <= last ? t * kTile : INT_MAX / 2;
+        stream_qk<DPH, RPW, 0>(ts_mask, sl, c, min_lim, my_lim, my_jp, qr, kbuf[b], m_run, l_run,
+                               al, pk);
+        if (i + 1 < CHUNK) {
+          stream_load<DPH>(a, head_base, tn * kTile, sl, lane_off, chunk_off, true, blk[nb],
+                           slot[nb], vbuf[nb]);
+          if (i + 2 < CHUNK)
+            tile_groups<NLD, SL>(a, table, min(t + 2 * W, last) * kTile, blk[b], slot[b]);
+        }
+        stream_pv<DPH, RPW, 0>(sl, al, pk, vbuf[b], acc);
+      }
+    }
+  }
+
+  // ---- merge the SL slot states of this wave; record per row ------------
+  // l of (row, slot): sum over the row's token-pair owners (redundant lanes
+  // hold copies and contribute 0).
+  float lsum = redundant ? 0.f : l_run;
+#pragma unroll
+  for (int kk = Sh::RB; kk < Sh::S; kk++) lsum += bfly<CH>(lsum, kk);
+  const bool odd_slot = sl & 1;
+#pragma unroll
+  for (int r = 0; r < RPW; r++) {
+    const float m_s = from_owner_f<DPH, RPW>(m_run, r, 0, odd_slot);
+    const float l_s = from_owner_f<DPH, RPW>(lsum, r, 0, odd_slot);
+    const float mx = slot_max<DPH>(m_s);
+    const float f = mx == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_s - mx);
+    const float l = slot_sum<DPH>(l_s * f);
+#pragma unroll
+    for (int e = 0; e < 8; e++) acc[r][e] = slot_sum<DPH>(acc[r][e] * f);
+    float* rec = s_buf + (wave * RPW + r) * REC;
+    if (lane == 0) {
+      rec[0] = mx;
+      rec[1] = l;
+    }
+    if (sl == 0) {
+      float2* dst = reinterpret_cast<float2*>(rec + 2 + 8 * c);
+      dst[0] = make_float2(acc[r][0], acc[r][1]);
+      dst[1] = make_float2(acc[r][2], acc[r][3]);
+      dst[2] = make_float2(acc[r][4], acc[r][5]);
+      dst[3] = make_float2(acc[r][6], acc[r][7]);
+    }
+  }
+  __syncthreads();
+
+  // ---- workgroup merge: thread (row, feature pair) over the waves --------
+  constexpr int DP = DPH / 2;
+  if ((int)threadIdx.x < nrows * DP) {
+    const int r = threadIdx.x / DP;
+    const int dcol = 2 * (threadIdx.x - r * DP);
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kStreamWaves; w++) mx = fmaxf(mx, s_buf[(w * RPW + r) * REC]);
+    float l = 0.f, o0 = 0.f, o1 = 0.f;
+#pragma unroll
+    for (int w = 0; w < kStreamWaves; w++) {
+      const float* rec = s_buf + (w * RPW + r) * REC;
+      const float wt = rec[0] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(rec[0] - mx);
+      l += rec[1] * wt;
+      const float2 x = *reinterpret_cast<const float2*>(rec + 2 + dcol);
+      o0 += x.x * wt;
+      o1 += x.y * wt;
+    }
+    const int gr = r0 + r;
+    if (a.n_parts == 1) {
+      // attention.h:120-126: normalise unless the sum is tiny or not finite.
+      const float inv = (l > 1e-20f && isfinite(l)) ? 1.f / l : 0.f;
+      const int m = gr / a.G;
+      const int h = kvh * a.G + (gr - m * a.G);
+      *reinterpret_cast<float2*>(a.out + (size_t)m * a.nh * DPH + (size_t)h * DPH + dcol) =
+          make_float2(o0 * inv, o1 * inv);
+    } else {
+      const size_t pr = ((size_t)kvh * a.R + gr) * a.n_parts + part;
+      float* acc_base = a.partials + (size_t)gridDim.y * a.R * a.n_parts * 2;
+      store_dev2(acc_base + pr * DPH + dcol, o0, o1);
+      if (dcol == 0) store_dev2(a.partials + pr * 2, mx, l);
+    }
+  }
+  if (a.n_parts == 1) return;
+
+  // ---- the last workgroup of (KV head, row group) combines --------------
+  // Partials are device-scope stores; waiting for them (vmcnt) before the
+  // arrival increment orders them before it.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t* ctr = a.counters + (size_t)kvh * gridDim.z + blockIdx.z;
+    const uint32_t prev =
+        __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int last = prev == (uint32_t)(a.n_parts - 1);
+    if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = last;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  stream_combine<DPH, RPW>(a, kvh, r0, nrows);
 }
 
 }  // namespace attn
@@ -480,9 +1261,12 @@ namespace {
 using namespace sde::attn;
 
 struct Plan {
-  int rpw;
+  bool stream;         // attn_stream_kernel (else attn_partition_kernel)
+  int rpw;             // rows per wave
   int row_groups;
-  int tiles_per_wave;
+  int tiles_per_wave;  // attn_partition_kernel
+  int tiles_per_part;  // attn_stream_kernel
+  int chunk;           // attn_stream_kernel: tiles per unrolled chunk
   int n_parts;
 };
 
@@ -493,8 +1277,13 @@ int env_int(const char* name, int fallback) {
   return v > 0 ? v : fallback;
 }
 
+// Row groups of up to 8 rows (two groups of kStreamMaxRows) take the
+// streaming kernel; larger groups the LDS-staged one.
+bool use_stream(int R) { return R <= 2 * kStreamMaxRows; }
+
 int rows_per_wave(int R) {
-  static const int kChoices[] = {2, 4, 8, 12, 16, 20, 24, 28, 32};
+  if (use_stream(R)) return R <= 2 ? 2 : kStreamMaxRows;
+  static const int kChoices[] = {12, 16, 20, 24, 28, 32};
   if (R > kMaxRowsPerWave) return kMaxRowsPerWave;
   for (int c : kChoices)
     if (c >= R) return c;
@@ -503,26 +1292,74 @@ int rows_per_wave(int R) {
 
 int target_waves() { return env_int("SDE_ATTN_TARGET_WAVES", 2048); }
 
-// Tiles per wave: the fewest that keep the total near target_waves() waves.
-Plan make_plan(int L_max, int nkv, int R) {
+// Streaming kernel: each wave takes tiles_per_wave tiles in chunks of
+// `chunk` (1, 2 or 4, a compile-time unroll).  The largest chunk that still
+// gives at least one workgroup per CU is used; past kStreamMaxParts
+// partitions per (KV head, row group) the waves take several chunks.
+struct StreamSplit {
+  int chunk;
+  int tiles_per_part;
+  int n_parts;
+};
+
+StreamSplit stream_split(int n_tiles, int units, int n_cus) {
+  StreamSplit sp{1, 0, 0};
+  for (int ch : {4, 2, 1}) {
+    const int per = kStreamWaves * ch;
+    if ((int64_t)((n_tiles + per - 1) / per) * units >= n_cus || ch == 1) {
+      sp.chunk = ch;
+      break;
+    }
+  }
+  const int per_chunk = kStreamWaves * sp.chunk;
+  const int chunks = (n_tiles + per_chunk - 1) / per_chunk;  // chunks of all waves
+  const int reps = (chunks + kStreamMaxParts - 1) / kStreamMaxParts;
+  sp.tiles_per_part = per_chunk * reps;
+  sp.n_parts = (n_tiles + sp.tiles_per_part - 1) / sp.tiles_per_part;
+  return sp;
+}
+
+Plan make_plan(int L_max, int nkv, int R, int n_cus) {
   Plan p;
+  p.stream = use_stream(R);
   p.rpw = rows_per_wave(R);
   p.row_groups = (R + p.rpw - 1) / p.rpw;
   const int n_tiles = (L_max + kTile - 1) / kTile;
+  if (p.stream) {
+    const StreamSplit sp = stream_split(n_tiles, nkv * p.row_groups, n_cus);
+    p.chunk = sp.chunk;
+    p.tiles_per_part = sp.tiles_per_part;
+    p.n_parts = sp.n_parts;
+    p.tiles_per_wave = 0;
+    return p;
+  }
+  // Partition kernel: the fewest tiles per wave that keep the total near
+  // target_waves() waves.
   const int64_t work = (int64_t)n_tiles * nkv * p.row_groups;
   const int64_t tw = target_waves();
   p.tiles_per_wave = (int)((work + tw - 1) / tw);
   if (p.tiles_per_wave < 1) p.tiles_per_wave = 1;
   const int per_part = p.tiles_per_wave * kWaves;
   p.n_parts = (n_tiles + per_part - 1) / per_part;
+  p.tiles_per_part = 0;
+  p.chunk = 0;
   return p;
 }
 
-// Upper bound of make_plan(L).n_parts over every L <= max_total_len: with one
+// Upper bound of make_plan(L).n_parts over every L <= max_total_len.
+// Partition kernel: with one
 // tile per wave n_parts = ceil(n_tiles / kWaves); with more, n_tiles/tpw is
 // at most target/(nkv*row_groups).
-int parts_bound(int max_total_len, int nkv, int row_groups) {
+int parts_bound(int max_total_len, int nkv, int R, int n_cus) {
   const int n_tiles = (max_total_len + kTile - 1) / kTile;
+  const int rpw = rows_per_wave(R);
+  const int row_groups = (R + rpw - 1) / rpw;
+  if (use_stream(R)) {
+    // n_parts <= kStreamMaxParts, and <= the ceil(n_tiles / 8) of the
+    // smallest partitions.
+    const int by_len = (n_tiles + kStreamWaves - 1) / kStreamWaves;
+    return by_len < kStreamMaxParts ? by_len : kStreamMaxParts;
+  }
   const int by_len = (n_tiles + kWaves - 1) / kWaves;
   const int64_t per = (int64_t)nkv * row_groups * kWaves;
   const int by_target = (int)((target_waves() + per - 1) / per);
@@ -534,16 +1371,30 @@ size_t partial_bytes(int nkv, int R, int n_parts, int dph) {
 }
 
 template <int DPH>
-int launch_partition(const Plan& p, const AttnArgs& a, dim3 grid, hipStream_t s) {
+int launch(const Plan& p, const AttnArgs& a, int nkv, hipStream_t s) {
+  const dim3 grid(p.n_parts, nkv, p.row_groups);
+  if (p.stream) {
+    const dim3 block(64 * kStreamWaves);
+#define SDE_STREAM(R, C)                                                   \
+  if (p.rpw == R && p.chunk == C) {                                        \
+    attn_stream_kernel<DPH, R, C><<<grid, block, 0, s>>>(a);               \
+    return sde::launch_status();                                           \
+  }
+    SDE_STREAM(2, 1)
+    SDE_STREAM(2, 2)
+    SDE_STREAM(2, 4)
+    SDE_STREAM(4, 1)
+    SDE_STREAM(4, 2)
+    SDE_STREAM(4, 4)
+#undef SDE_STREAM
+    return SDE_ERR_UNSUPPORTED;
+  }
   const dim3 block(64 * kWaves);
   switch (p.rpw) {
 #define SDE_CASE(N)                                              \
   case N:                                                        \
     attn_partition_kernel<DPH, N><<<grid, block, 0, s>>>(a);     \
     break;
-    SDE_CASE(2)
-    SDE_CASE(4)
-    SDE_CASE(8)
     SDE_CASE(12)
     SDE_CASE(16)
     SDE_CASE(20)
@@ -583,9 +1434,7 @@ size_t sde_paged_attention_workspace_size(const sde_kv_cache* cache, int nh,
   if (!cache || nh < 1 || nkv < 1 || nh % nkv != 0 || n_queries < 1 || max_total_len < 1)
     return 0;
   const int R = n_queries * (nh / nkv);
-  const int rpw = rows_per_wave(R);
-  const int row_groups = (R + rpw - 1) / rpw;
-  return partial_bytes(nkv, R, parts_bound(max_total_len, nkv, row_groups), dph);
+  return partial_bytes(nkv, R, parts_bound(max_total_len, nkv, R, cache->n_cus), dph);
 }
 
 int sde_paged_attention(sde_kv_cache* cache, int layer, const float* d_q,
@@ -600,7 +1449,7 @@ int sde_paged_attention(sde_kv_cache* cache, int layer, const float* d_q,
   const int G = nh / nkv;
   const int R = n_queries * G;
   const int L_max = pos_base + n_queries;
-  const Plan plan = make_plan(L_max, nkv, R);
+  const Plan plan = make_plan(L_max, nkv, R, cache->n_cus);
   if ((int64_t)nkv * plan.row_groups > sde::kMaxAttnCounters) return SDE_ERR_UNSUPPORTED;
   const size_t need = partial_bytes(nkv, R, plan.n_parts, dph);
   float* partials = nullptr;
@@ -640,12 +1489,11 @@ int sde_paged_attention(sde_kv_cache* cache, int layer, const float* d_q,
   a.L_max = L_max;
   a.n_parts = plan.n_parts;
   a.tiles_per_wave = plan.tiles_per_wave;
+  a.tiles_per_part = plan.tiles_per_part;
   a.qscale = (float)(kLog2e / std::sqrt((double)dph));
 
   const hipStream_t s = (hipStream_t)stream;
-  const dim3 grid(plan.n_parts, nkv, plan.row_groups);
-  return dph == 128 ? launch_partition<128>(plan, a, grid, s)
-                    : launch_partition<64>(plan, a, grid, s);
+  return dph == 128 ? launch<128>(plan, a, nkv, s) : launch<64>(plan, a, nkv, s);
 }
 
 int sde_attention_dispatch(int attn_type, sde_kv_cache* cache, int layer,

@@ -29,6 +29,7 @@ struct sde_kv_cache {
   // group) of a call; zero at rest (the last arriving workgroup resets its
   // counter), so calls on one cache must be stream-ordered.
   uint32_t* d_counters = nullptr;
+  int n_cus = 256;  // compute units of `device` (sizes attention grids)
 };
 
 namespace sde {
