@@ -9,12 +9,19 @@ head_dim 128, block_size 16, fragmented 131072-block pool).  A step is one
 such layer-step; steps rotate over the 32 layers of the model (4 GiB of K/V)
 so the 256 MB Infinity Cache cannot hold the working set.
 
+Timing: the K timed steps are captured once into a HIP graph (rotating over
+the layers) and replayed between two HIP events on the launch stream, so a
+step costs its kernels plus the graph's inter-kernel gaps, without Python or
+launch overhead; eager per-launch event durations are reported beside it.
+
 Also reported: us per layer-step for all five BASELINE configs, the verify
 (k=4) / single-query step ratio at 4K, the cost of an O(1) rollback, the
-roofline of the dominant kernel (per-launch HIP-event durations), and the
-CPU oracle (oracle/sde_oracle.c, OpenMP) timed on a bounded sample.
+roofline of the dominant kernel, and the CPU oracle (oracle/sde_oracle.c,
+OpenMP) timed on a bounded sample.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+       [--calibrate-copy MiB]  (adds plain device copies of known size, the
+       reference point for rocprofv3 FETCH_SIZE / WRITE_SIZE)
 """
 from __future__ import annotations
 
@@ -34,7 +41,7 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E spec sheet
 HEADLINE = "llama3_8b_32k"
-KERNEL = "attn_partition_kernel"
+KERNEL = "attn_stream_kernel"  # the headline (1-query, GQA 4) path
 
 
 def log(*a):
@@ -50,6 +57,8 @@ def parse_args():
     p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="approximate CPU work of the baseline sample")
     p.add_argument("--only-headline", action="store_true")
+    p.add_argument("--calibrate-copy", type=int, default=0, metavar="MiB",
+                   help="after the benchmark, copy a MiB-sized buffer 5 times")
     return p.parse_args()
 
 
@@ -80,6 +89,32 @@ class Timer:
         total_ms = self.t0.elapsed_time(self.t1)
         launch_ms = [s.elapsed_time(e) for s, e in self.ev[:steps]] if per_launch else []
         return total_ms / steps, (float(np.mean(launch_ms)) if launch_ms else None)
+
+
+def graph_step_ms(torch, step, steps, warmup):
+    """ms per step of `steps` steps captured into one HIP graph and replayed
+    (after `warmup` eager steps and one untimed replay) between two events
+    on the capture/launch stream."""
+    for i in range(max(warmup, 1)):
+        step(i)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            for i in range(steps):
+                step(i)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        g.replay()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        g.replay()
+        e1.record(s)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
 
 
 def make_rotation_cache(torch, W, w, n_layers, l_max, pool_blocks, seed):
@@ -128,17 +163,20 @@ def bench_config(torch, W, w, steps, warmup, mode):
             cache.append(l, k[l], v[l], pos_base)
         cache.attention(l, q[l], w.nh, w.nkv, w.dph, pos_base, out=out, workspace=ws)
 
+    # eager: per-launch HIP events (attention only) and the bracket
     timer = Timer(torch, steps)
-    ms, launch_ms = timer.run(step, steps, warmup, per_launch=(n_app == 0))
+    eager_ms, launch_ms = timer.run(step, steps, warmup, per_launch=(n_app == 0))
+    # timed: the steps captured into one HIP graph, replayed between events
+    ms = graph_step_ms(torch, step, steps, warmup)
     nbytes = w.algorithmic_bytes(l_max=l_max, n_app=n_app, n_queries=n_q)
     res = dict(mode=mode, n_queries=n_q, keys=l_max, rotated_layers=n_layers,
                us_per_layer_step=round(ms * 1e3, 3), algorithmic_bytes=nbytes,
                gbps=round(nbytes / (ms * 1e-3) / 1e9, 1),
                frac_of_hbm_peak=round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
-               flops=w.attention_flops(pos_base, n_q))
+               flops=w.attention_flops(pos_base, n_q),
+               us_per_layer_step_eager=round(eager_ms * 1e3, 3))
     if launch_ms is not None:
-        res["kernel_us"] = round(launch_ms * 1e3, 3)
-        res["kernel_gbps"] = round(nbytes / (launch_ms * 1e-3) / 1e9, 1)
+        res["kernel_us_events"] = round(launch_ms * 1e3, 3)
     cache.free()
     return res
 
@@ -252,13 +290,16 @@ def main():
         for k_, v_ in configs.items():
             log(f"[bench] {k_}: {v_['us_per_layer_step']} us/layer-step, {v_['gbps']} GB/s")
 
-    kernel_us = head["kernel_us"]
+    # One launch per headline step: the graph-replayed step time is the
+    # kernel's average launch duration (plus the graph's inter-kernel gap).
+    kernel_us = head["us_per_layer_step"]
     nbytes = head["algorithmic_bytes"]
     achieved = nbytes / (kernel_us * 1e-6) / 1e9
     roofline = dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBPS, unit="GB/s",
                     frac=round(achieved / HBM_PEAK_GBPS, 4),
                     traffic=measured_traffic(HEADLINE), kernel=KERNEL,
-                    bytes_per_launch=nbytes, kernel_us=kernel_us)
+                    bytes_per_launch=nbytes, kernel_us=kernel_us,
+                    kernel_us_eager_events=head.get("kernel_us_events"))
 
     cpu = None
     if not args.no_cpu:
@@ -289,6 +330,14 @@ def main():
         "configs": configs,
         **extra,
     }
+    if args.calibrate_copy:
+        n = args.calibrate_copy * 2 ** 20 // 4
+        src = torch.ones(n, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"[bench] calibration: 5 copies of {args.calibrate_copy} MiB")
     print(json.dumps(line), flush=True)
 
 

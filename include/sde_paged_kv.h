@@ -178,7 +178,9 @@ size_t sde_paged_attention_workspace_size(const sde_kv_cache* cache, int nh,
  * d_workspace may be NULL (the cache then keeps its own, grown on demand);
  * otherwise it must hold sde_paged_attention_workspace_size(...) bytes.
  * Supported: dph in {64, 128}, block_size a multiple of 8, nkv | nh,
- * n_queries * nh/nkv <= 64. */
+ * 1 <= n_queries <= 4096 and nkv * ceil(n_queries * nh/nkv / 4) <= 4096
+ * (SDE_ERR_UNSUPPORTED otherwise).  Calls on one cache must be ordered on
+ * one stream (they share the cache's arrival counters). */
 int sde_paged_attention(sde_kv_cache* cache, int layer, const float* d_q,
                         float* d_out, int nh, int nkv, int dph, int pos_base,
                         int n_queries, void* d_workspace,

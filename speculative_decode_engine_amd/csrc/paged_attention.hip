@@ -6,31 +6,24 @@
 // head h reading KV head h*nkv/nh, keys gathered through the block table.
 //
 // No MFMA: decode and small-k verify are GEMV-shaped and HBM-bound.  The
-// "rows" of a KV head are its (query, head-in-group) pairs, so every K/V
-// byte is read from HBM once for all G*n_queries rows of a row group.  The
-// context of each (KV head, row group) is split into partitions, one
-// workgroup each; a single-partition context writes the normalised output
-// directly, otherwise per-row partials go to the workspace and the last
-// workgroup of a (KV head, row group) to finish -- found with one arrival
-// counter per pair -- merges all partitions with a log-sum-exp combine in
-// partition order, so the result does not depend on arrival order and one
-// call is one launch.  Two kernels:
+// "rows" of a KV head are its (query, head-in-group) pairs; a row group of up
+// to four rows shares every K/V byte it loads.  The context of each (KV
+// head, row group) is split into partitions, one 8-wave workgroup each
+// (about one per CU); a single-partition context writes the normalised
+// output directly, otherwise per-row partials go to the workspace and the
+// last workgroup of a (KV head, row group) to finish -- found with one
+// arrival counter per pair -- merges all partitions with a log-sum-exp
+// combine in partition order, so the result does not depend on arrival
+// order and one call is one launch.
 //
-//  attn_stream_kernel (up to 4 rows per wave: decode, small windows), one
-//    8-wave workgroup per CU.  K and V stream from HBM straight into VGPRs
-//    in the coalesced load layout (lane = token slot x 16-byte feature
-//    chunk), software-pipelined a tile (32 tokens) ahead; logits are
-//    reduced across the lanes of a token with a transposing DPP butterfly
-//    that leaves each lane one (row, token pair), so the online softmax is a
-//    handful of scalar ops per lane; P.V dot2-accumulates fp16 probability
-//    pairs against byte-permuted V pairs.
-//
-//  attn_partition_kernel (larger row groups: verify windows), 4-wave
-//    workgroups.  K and V land in LDS with direct-to-LDS 16-byte loads, K
-//    chunk-swizzled so the transposed reads are bank-conflict free; lane
-//    (token, half) takes fp16 dot2 products over half the head dimension;
-//    online softmax with DPP/permlane reductions, probabilities to LDS as
-//    fp16; a lane owns a feature pair for P.V.
+// attn_stream_kernel: K and V stream from HBM straight into VGPRs in the
+// coalesced load layout (lane = token slot x 16-byte feature chunk),
+// software-pipelined a tile (32 tokens) ahead; logits are reduced across
+// the lanes of a token with a transposing DPP butterfly that leaves each
+// lane one (row, token pair), so the online softmax is a handful of scalar
+// ops per lane; P.V dot2-accumulates fp16 probability pairs against
+// byte-permuted V pairs.  Row groups of a larger verify window are separate
+// workgroups reading the same K/V (the repeats are L2 hits).
 #include <hip/hip_runtime.h>
 
 #include <climits>
@@ -46,8 +39,6 @@ typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 constexpr int kTile = 32;  // tokens per tile
-constexpr int kWaves = 4;  // waves per workgroup
-constexpr int kMaxRowsPerWave = 32;
 constexpr double kLog2e = 1.4426950408889634;
 
 struct AttnArgs {
@@ -65,7 +56,6 @@ struct AttnArgs {
   int pos_base;  // query m sees positions [0, pos_base+m]
   int L_max;     // pos_base + M
   int n_parts;
-  int tiles_per_wave;  // attn_partition_kernel: tiles per wave
   int tiles_per_part;  // attn_stream_kernel: tiles per partition
   float qscale;  // log2(e) / sqrt(dph)
 };
@@ -103,20 +93,7 @@ __device__ __forceinline__ float2 row_pair(float x) {
   return make_float2(__builtin_bit_cast(float, (int)p[0]), __builtin_bit_cast(float, (int)p[1]));
 }
 
-// All-reduce within each 32-lane half of the wave.
-__device__ __forceinline__ float half_max(float x) {
-#pragma unroll
-  for (int s = 0; s < 4; s++) x = fmaxf(x, dpp_f(x, s));
-  const float2 p = row_pair(x);
-  return fmaxf(p.x, p.y);
-}
 
-__device__ __forceinline__ float half_sum(float x) {
-#pragma unroll
-  for (int s = 0; s < 4; s++) x += dpp_f(x, s);
-  const float2 p = row_pair(x);
-  return p.x + p.y;
-}
 
 // Sums a (partial over lanes 0-31 and 32-63) and b likewise: lanes 0-31
 // get a's total, lanes 32-63 b's total.
@@ -126,58 +103,16 @@ __device__ __forceinline__ float half_pair_total(float a, float b) {
   return __builtin_bit_cast(float, (int)p[0]) + __builtin_bit_cast(float, (int)p[1]);
 }
 
-// 16 bytes per lane from global memory straight into LDS at lds + 16*lane
-// (global_load_lds_dwordx4, LDS base in M0, which the compiler loads for
-// the "{m0}" input operand).  Issued as inline asm so that
-// the compiler does not add its own conservative vmcnt waits before every
-// LDS read (it cannot tell which of the many in-flight tiles a read
-// touches); every consumer waits explicitly with wait_vmcnt below, and the
-// "memory" clobbers keep LDS accesses on the right side of those waits.
-__device__ __forceinline__ void load_lds16(const void* gptr, const uint16_t* lds) {
-  const uint32_t lds_addr = (uint32_t)(uintptr_t)(lds_ptr_t)(lds);
-  asm volatile("global_load_lds_dwordx4 %0, off" : : "v"(gptr), "{m0}"(lds_addr) : "memory");
-}
-
-// s_waitcnt vmcnt(N): all but the N most recent vector-memory loads done.
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 16, "vmcnt");
-  if constexpr (N == 0)
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  else if constexpr (N == 4)
-    asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-  else if constexpr (N == 8)
-    asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-  else
-    static_assert(N == 0 || N == 4 || N == 8, "add the vmcnt value");
-}
-
-__device__ __forceinline__ float lane_value(float x, int lane) {
-  return __builtin_bit_cast(float,
-                            __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), lane));
-}
-
-__device__ __forceinline__ uint16_t f2h_bits(float x) {
-  return __builtin_bit_cast(uint16_t, (_Float16)x);
-}
 
 // Device-scope (agent) relaxed atomic accesses for the partition partials:
 // the stores write through to the device coherence point and the loads do
 // not hit stale lines of another XCD's L2, so publishing partials needs no
 // L2 writeback/invalidate fence (those cost microseconds per workgroup).
-__device__ __forceinline__ void store_dev(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 __device__ __forceinline__ void store_dev2(float* p, float x, float y) {
   const uint64_t bits = (uint64_t)__builtin_bit_cast(uint32_t, x) |
                         ((uint64_t)__builtin_bit_cast(uint32_t, y) << 32);
   __hip_atomic_store(reinterpret_cast<uint64_t*>(p), bits, __ATOMIC_RELAXED,
                      __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ float load_dev(const float* p) {
-  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ __forceinline__ float2 load_dev2(const float* p) {
@@ -187,441 +122,13 @@ __device__ __forceinline__ float2 load_dev2(const float* p) {
                      __builtin_bit_cast(float, (uint32_t)(bits >> 32)));
 }
 
-// Physical 16-byte chunk of logical chunk c of tile token t is c ^ kswz(t):
-// the 16 lanes of a QK read then touch 16 distinct chunk columns.
-template <int DPH>
-__device__ __forceinline__ int kswz(int t) {
-  if constexpr (DPH == 128)
-    return t & 15;
-  else
-    return (t >> 1) & 7;
-}
-
-
 typedef const __attribute__((address_space(4))) int32_t* const_table_t;
-
-// q rows of the row group -> fp16 in LDS, pre-scaled into the exp2 domain;
-// rows past nrows are zero.
-template <int DPH, int RPW>
-__device__ __forceinline__ void stage_q(const AttnArgs& a, int kvh, int r0, int nrows,
-                                        uint16_t* sQ) {
-  constexpr int DP = DPH / 2;
-  for (int idx = threadIdx.x; idx < RPW * DP; idx += 64 * kWaves) {
-    const int r = idx / DP;
-    const int d2 = idx - r * DP;
-    uint32_t packed = 0;
-    if (r < nrows) {
-      const int gr = r0 + r;
-      const int m = gr / a.G;
-      const int h = kvh * a.G + (gr - m * a.G);
-      const float2 qv = *reinterpret_cast<const float2*>(
-          a.q + (size_t)m * a.nh * DPH + (size_t)h * DPH + 2 * d2);
-      const half2_t hv = {(_Float16)(qv.x * a.qscale), (_Float16)(qv.y * a.qscale)};
-      packed = __builtin_bit_cast(uint32_t, hv);
-    }
-    reinterpret_cast<uint32_t*>(sQ)[idx] = packed;
-  }
-}
 
 // The block table is read-only during the kernel: reading it through the
 // constant address space turns the entries into scalar loads (lgkmcnt),
 // which never wait behind outstanding tile loads (vmcnt).
 __device__ __forceinline__ const_table_t const_table(const AttnArgs& a) {
   return (const_table_t)a.table;
-}
-
-// Physical block of each load group (TPL tokens, one block) of tile ts.
-template <int NLD, int TPL>
-__device__ __forceinline__ void tile_blocks(const AttnArgs& a, const_table_t table, int ts,
-                                            int (&blk)[NLD]) {
-#pragma unroll
-  for (int j = 0; j < NLD; j++) blk[j] = table[min(ts + j * TPL, a.L_max - 1) / a.bs];
-}
-
-// Pool address of this lane's 16-byte chunk `chunk` of token g0 + lane/CH
-// (group start g0 must lie in block `blk`); is_v selects the V half.
-template <int DPH>
-__device__ __forceinline__ const uint16_t* chunk_addr(const AttnArgs& a, int kvh, int blk,
-                                                      int g0, int lane, int chunk, bool is_v) {
-  constexpr int CH = DPH / 8;
-  const int lb = g0 / a.bs;
-  const int slot = g0 - lb * a.bs + lane / CH;
-  return a.pool + ((size_t)blk * 2u * a.bs + slot) * (size_t)a.kv_dim + (size_t)kvh * DPH +
-         (is_v ? (size_t)a.bs * a.kv_dim : 0) + chunk * 8;
-}
-
-// Q.K for this lane's token t and feature half hh: s[r] = (q_r . k_t) over
-// the half, for every row (the two halves are combined by the caller).
-template <int DPH, int RPW, bool kQRegs>
-__device__ __forceinline__ void qk_tile(const uint16_t* sK, const uint16_t* sQ,
-                                        const uint4 (&qreg)[kQRegs ? RPW : 1][kQRegs ? DPH / 16 : 1],
-                                        int t, int hh, float (&s)[RPW]) {
-  constexpr int HCH = DPH / 16;
-  uint4 kc[HCH];
-#pragma unroll
-  for (int jj = 0; jj < HCH; jj++)
-    kc[jj] = *reinterpret_cast<const uint4*>(sK + t * DPH + ((hh * HCH + jj) ^ kswz<DPH>(t)) * 8);
-#pragma unroll
-  for (int r = 0; r < RPW; r++) s[r] = 0.f;
-#pragma unroll
-  for (int jj = 0; jj < HCH; jj++) {
-#pragma unroll
-    for (int r = 0; r < RPW; r++) {
-      uint4 qc;
-      if constexpr (kQRegs)
-        qc = qreg[r][jj];
-      else
-        qc = *reinterpret_cast<const uint4*>(sQ + r * DPH + (hh * HCH + jj) * 8);
-      s[r] = dot2(qc.x, kc[jj].x, s[r]);
-      s[r] = dot2(qc.y, kc[jj].y, s[r]);
-      s[r] = dot2(qc.z, kc[jj].z, s[r]);
-      s[r] = dot2(qc.w, kc[jj].w, s[r]);
-    }
-  }
-}
-
-// Online-softmax update of one tile (exp2 domain).  On entry s holds the
-// per-half partial logits of every row; lane (t, hh) ends up owning row
-// 2i+hh of pair i.  Writes p (fp16) through put_p(row, p) and returns the
-// rescale factor of each row pair in alpha.
-template <int RPW, typename PutP>
-__device__ __forceinline__ void softmax_tile(const float (&s)[RPW], int tok, const int (&lim)[RPW / 2],
-                                             float (&m_run)[RPW / 2], float (&l_run)[RPW / 2],
-                                             float (&alpha)[RPW / 2], int hh, PutP put_p) {
-#pragma unroll
-  for (int i = 0; i < RPW / 2; i++) {
-    const float x = half_pair_total(s[2 * i], s[2 * i + 1]);
-    const bool valid = tok <= lim[i];
-    const float tmax = half_max(valid ? x : -INFINITY);
-    const float m_new = fmaxf(m_run[i], tmax);
-    const bool any = m_new != -INFINITY;
-    const float al = any ? __builtin_amdgcn_exp2f(m_run[i] - m_new) : 1.f;
-    const float p = (valid && any) ? __builtin_amdgcn_exp2f(x - m_new) : 0.f;
-    l_run[i] = l_run[i] * al + p;
-    m_run[i] = m_new;
-    alpha[i] = al;
-    put_p(2 * i + hh, p);
-  }
-}
-
-// Emits the merged row: normalised output (single partition) or the
-// partition's partial record (device-scope stores).
-template <int DPH>
-__device__ __forceinline__ void emit_row(const AttnArgs& a, int part, int kvh, int gr, int lane,
-                                         int dcol, float mx, float l, float o0, float o1) {
-  const int m = gr / a.G;
-  const int h = kvh * a.G + (gr - m * a.G);
-  if (a.n_parts == 1) {
-    // attention.h:120-126: normalise unless the sum is tiny or not finite.
-    const float inv = (l > 1e-20f && isfinite(l)) ? 1.f / l : 0.f;
-    *reinterpret_cast<float2*>(a.out + (size_t)m * a.nh * DPH + (size_t)h * DPH + dcol) =
-        make_float2(o0 * inv, o1 * inv);
-  } else {
-    float* pr = a.partials + (((size_t)kvh * a.R + gr) * a.n_parts + part) * (size_t)(DPH + 2);
-    store_dev2(pr + 2 + dcol, o0, o1);
-    if (lane == 0) {
-      store_dev(pr, mx);
-      store_dev(pr + 1, l);
-    }
-  }
-}
-
-// Merges the kWaves per-wave records of rows [0, nrows) (caller has synced
-// after writing them), emits outputs or partials, and for a multi-partition
-// context runs the fused partition combine in the last workgroup.
-// rec_acc(w, r, col) -> &acc of wave w, row r, feature col; rec_ml(w, r) ->
-// &(max, sum) of wave w, row r.
-template <int DPH, typename AccRec, typename MlRec>
-__device__ __forceinline__ void finish_workgroup(const AttnArgs& a, int part, int kvh, int r0,
-                                                 int nrows, int wave, int lane, AccRec rec_acc,
-                                                 MlRec rec_ml) {
-  const int dcol = (DPH == 128 ? lane : (lane & 31)) * 2;
-  const bool col_lane = DPH == 128 || lane < 32;
-  for (int r = wave; r < nrows; r += kWaves) {
-    float mx = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < kWaves; w++) mx = fmaxf(mx, rec_ml(w, r)[0]);
-    float l = 0.f, o0 = 0.f, o1 = 0.f;
-#pragma unroll
-    for (int w = 0; w < kWaves; w++) {
-      const float mw = rec_ml(w, r)[0];
-      const float wt = (mw == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(mw - mx);
-      l += rec_ml(w, r)[1] * wt;
-      if (col_lane) {
-        const float2 aw = *reinterpret_cast<const float2*>(rec_acc(w, r, dcol));
-        o0 += aw.x * wt;
-        o1 += aw.y * wt;
-      }
-    }
-    if (col_lane) emit_row<DPH>(a, part, kvh, r0 + r, lane, dcol, mx, l, o0, o1);
-  }
-  if (a.n_parts == 1) return;
-
-  // ---- fused partition combine: the last workgroup of (kvh, row group) ----
-  // Every partial was stored at device scope; waiting for their completion
-  // (vmcnt) before the arrival increment orders them before it, and the last
-  // arriver reads them back with device-scope loads.
-  __shared__ int s_last;
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t* ctr = a.counters + (size_t)kvh * gridDim.z + blockIdx.z;
-    const uint32_t prev =
-        __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const int last = prev == (uint32_t)(a.n_parts - 1);
-    if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = last;
-  }
-  __syncthreads();
-  if (!s_last) return;
-
-  // Latency-tolerant merge: lane p reads partition p's (max, sum); the
-  // accumulator rows are loaded kBatch partitions at a time before use.
-  constexpr int kBatch = 16;
-  for (int r = wave; r < nrows; r += kWaves) {
-    const int gr = r0 + r;
-    const float* base = a.partials + ((size_t)kvh * a.R + gr) * a.n_parts * (size_t)(DPH + 2);
-    float mx = -INFINITY;
-    for (int p0 = 0; p0 < a.n_parts; p0 += 64) {
-      const int p = p0 + lane;
-      const float mp = p < a.n_parts ? load_dev(base + (size_t)p * (DPH + 2)) : -INFINITY;
-      mx = fmaxf(mx, half_max(mp));
-    }
-    mx = fmaxf(lane_value(mx, 0), lane_value(mx, 32));
-    float l = 0.f, o0 = 0.f, o1 = 0.f;
-    for (int p0 = 0; p0 < a.n_parts; p0 += 64) {
-      const int p = p0 + lane;
-      float wt = 0.f;  // weight of partition p0+lane (0: absent or no visible key)
-      if (p < a.n_parts) {
-        const float mp = load_dev(base + (size_t)p * (DPH + 2));
-        if (mp != -INFINITY) {
-          wt = __builtin_amdgcn_exp2f(mp - mx);
-          l += load_dev(base + (size_t)p * (DPH + 2) + 1) * wt;
-        }
-      }
-      const int n = min(64, a.n_parts - p0);
-      for (int b0 = 0; b0 < n; b0 += kBatch) {
-        float2 v[kBatch];
-#pragma unroll
-        for (int u = 0; u < kBatch; u++) {
-          v[u] = make_float2(0.f, 0.f);
-          if (b0 + u < n && col_lane)
-            v[u] = load_dev2(base + (size_t)(p0 + b0 + u) * (DPH + 2) + 2 + dcol);
-        }
-#pragma unroll
-        for (int u = 0; u < kBatch; u++) {
-          if (b0 + u < n) {
-            const float wu = lane_value(wt, b0 + u);
-            o0 += v[u].x * wu;
-            o1 += v[u].y * wu;
-          }
-        }
-      }
-    }
-    l = half_sum(l);
-    l = lane_value(l, 0) + lane_value(l, 32);
-    if (col_lane) {
-      const int m = gr / a.G;
-      const int h = kvh * a.G + (gr - m * a.G);
-      const float inv = (l > 1e-20f && isfinite(l)) ? 1.f / l : 0.f;
-      *reinterpret_cast<float2*>(a.out + (size_t)m * a.nh * DPH + (size_t)h * DPH + dcol) =
-          make_float2(o0 * inv, o1 * inv);
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------
-// attn_partition_kernel: K and V both staged in LDS (large row groups).
-// ---------------------------------------------------------------------------
-template <int DPH, int RPW>
-__global__ __launch_bounds__(64 * kWaves) void attn_partition_kernel(AttnArgs a) {
-  static_assert(DPH == 64 || DPH == 128, "head_dim");
-  static_assert(RPW % 2 == 0 && RPW <= kMaxRowsPerWave, "rows per wave");
-  constexpr int CH = DPH / 8;       // 16-byte chunks per head row
-  constexpr int TPL = 64 / CH;      // tokens per load instruction
-  constexpr int NLD = kTile / TPL;  // load instructions per tile (per K and per V)
-  constexpr int RP = RPW / 2;       // row pairs
-  constexpr int DP = DPH / 2;       // fp16 pairs per head row
-
-  __shared__ __attribute__((aligned(16))) uint16_t sQ[RPW * DPH];
-  // The P tile lives behind the V tile.
-  __shared__ __attribute__((aligned(16))) uint16_t sKw[kWaves][kTile * DPH];
-  __shared__ __attribute__((aligned(16))) uint16_t sVw[kWaves][kTile * DPH + RPW * kTile];
-
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  uint16_t* const sK = sKw[wave];
-  uint16_t* const sV = sVw[wave];
-  uint16_t* const sP = sVw[wave] + kTile * DPH;
-  const uint32_t* const sV32 = reinterpret_cast<const uint32_t*>(sV);
-
-  const int part = blockIdx.x;
-  const int kvh = blockIdx.y;
-  const int r0 = blockIdx.z * RPW;
-  const int nrows = min(RPW, a.R - r0);
-  const int t_begin = part * a.tiles_per_wave * kWaves * kTile;
-  const int t_end = min(a.L_max, t_begin + a.tiles_per_wave * kWaves * kTile);
-
-  stage_q<DPH, RPW>(a, kvh, r0, nrows, sQ);
-
-  const int t = lane & 31;
-  const int hh = lane >> 5;
-  int lim[RP];  // last visible position of row 2i+hh (-1: padding row)
-  float m_run[RP], l_run[RP];
-#pragma unroll
-  for (int i = 0; i < RP; i++) {
-    const int r = 2 * i + hh;
-    lim[i] = (r < nrows) ? a.pos_base + (r0 + r) / a.G : -1;
-    m_run[i] = -INFINITY;
-    l_run[i] = 0.f;
-  }
-  float acc[RPW][2];
-#pragma unroll
-  for (int r = 0; r < RPW; r++) acc[r][0] = acc[r][1] = 0.f;
-
-  __syncthreads();  // sQ complete
-  const uint4 no_qreg[1][1] = {};
-
-  const const_table_t table = const_table(a);
-  auto load_tile = [&](int ts_, const int (&blk)[NLD], uint16_t* dst, bool is_v) {
-#pragma unroll
-    for (int j = 0; j < NLD; j++) {
-      const int g0 = ts_ + j * TPL;  // wave-uniform; the group shares a block
-      if (g0 < a.L_max) {
-        const int pc = lane % CH;
-        const int chunk = is_v ? pc : (pc ^ kswz<DPH>(j * TPL + lane / CH));
-        load_lds16(chunk_addr<DPH>(a, kvh, blk[j], g0, lane, chunk, is_v), dst + j * 512);
-      }
-    }
-  };
-
-  // Split-phase pipeline per wave: K(next) streams in during softmax + P.V
-  // of this tile, V(next) during Q.K of the next one.  Loads complete in
-  // issue order, so "vmcnt <= NLD" means all but the last tile-half landed.
-  // The waves run different numbers of tiles: only wave-local ordering is
-  // used inside this loop (LDS operations of one wave complete in order).
-  const int stride = kWaves * kTile;
-  int ts = t_begin + wave * kTile;
-  int blk[NLD];
-  if (ts < t_end) {
-    tile_blocks<NLD, TPL>(a, table, ts, blk);
-    load_tile(ts, blk, sK, false);
-    load_tile(ts, blk, sV, true);
-  }
-  for (; ts < t_end; ts += stride) {
-    const int ts_next = ts + stride;
-    const bool has_next = ts_next < t_end;
-    const bool full = ts + kTile <= a.L_max;
-    const bool next_full = has_next && ts_next + kTile <= a.L_max;
-    int blk_next[NLD];
-    if (has_next) tile_blocks<NLD, TPL>(a, table, ts_next, blk_next);
-
-    if (full)
-      wait_vmcnt<NLD>();  // K(ts) landed; V(ts) may be in flight
-    else
-      wait_vmcnt<0>();
-
-    float s[RPW];
-    qk_tile<DPH, RPW, false>(sK, sQ, no_qreg, t, hh, s);
-    // The K tile has been read: stream the next one in behind this tile.
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    if (has_next) load_tile(ts_next, blk_next, sK, false);
-
-    float alpha[RP];
-    softmax_tile<RPW>(s, ts + t, lim, m_run, l_run, alpha, hh,
-                      [&](int r, float p) { sP[r * kTile + t] = f2h_bits(p); });
-#pragma unroll
-    for (int r = 0; r < RPW; r++) {
-      const float al = lane_value(alpha[r / 2], (r & 1) ? 32 : 0);
-      acc[r][0] *= al;
-      acc[r][1] *= al;
-    }
-
-    if (next_full)
-      wait_vmcnt<NLD>();  // V(ts) landed; K(next) may be in flight
-    else
-      wait_vmcnt<0>();
-    // Rows past the context may hold stale (even non-finite) bytes; their
-    // probabilities are 0 but 0 * NaN is not, so clear those V rows.
-    if (!full) {
-      uint32_t* v32 = reinterpret_cast<uint32_t*>(sV);
-      for (int idx = (a.L_max - ts) * DP + lane; idx < kTile * DP; idx += 64) v32[idx] = 0u;
-    }
-
-    // ---- P.V: 8 tokens (4 probability pairs per row) per step ----------
-    // DPH 128: lane owns feature pair `lane`.  DPH 64: lanes 0-31 take
-    // tokens 0-15 and lanes 32-63 tokens 16-31 of feature pair lane & 31.
-    constexpr int kGroups = (DPH == 128) ? kTile / 8 : kTile / 16;
-    const int dp = (DPH == 128) ? lane : (lane & 31);
-    const int g_base = (DPH == 128) ? 0 : hh * kGroups;
-#pragma unroll
-    for (int gi = 0; gi < kGroups; gi++) {
-      const int g = g_base + gi;
-      uint32_t vv[8];
-#pragma unroll
-      for (int u = 0; u < 8; u++) vv[u] = sV32[(8 * g + u) * DP + dp];
-      uint32_t lo[4], hi[4];  // (token 2q, token 2q+1) pairs of both features
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        lo[q] = __builtin_amdgcn_perm(vv[2 * q + 1], vv[2 * q], 0x05040100u);
-        hi[q] = __builtin_amdgcn_perm(vv[2 * q + 1], vv[2 * q], 0x07060302u);
-      }
-#pragma unroll
-      for (int r = 0; r < RPW; r++) {
-        const uint4 pr = *reinterpret_cast<const uint4*>(sP + r * kTile + 8 * g);
-        acc[r][0] = dot2(pr.x, lo[0], acc[r][0]);
-        acc[r][1] = dot2(pr.x, hi[0], acc[r][1]);
-        acc[r][0] = dot2(pr.y, lo[1], acc[r][0]);
-        acc[r][1] = dot2(pr.y, hi[1], acc[r][1]);
-        acc[r][0] = dot2(pr.z, lo[2], acc[r][0]);
-        acc[r][1] = dot2(pr.z, hi[2], acc[r][1]);
-        acc[r][0] = dot2(pr.w, lo[3], acc[r][0]);
-        acc[r][1] = dot2(pr.w, hi[3], acc[r][1]);
-      }
-    }
-    // The V and P tiles have been read: stream the next V tile in.
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    if (has_next) {
-      load_tile(ts_next, blk_next, sV, true);
-#pragma unroll
-      for (int j = 0; j < NLD; j++) blk[j] = blk_next[j];
-    }
-  }
-  wait_vmcnt<0>();
-
-  // ---- per-wave records: accumulator columns [0, DPH/2) in the wave's K
-  // tile, [DPH/2, DPH) in its V tile, (max, sum) in its P tile -------------
-  auto rec_acc = [&](int w, int r, int col) -> float* {
-    float* base = reinterpret_cast<float*>(col < DPH / 2 ? sKw[w] : sVw[w]);
-    return base + r * (DPH / 2) + (col & (DPH / 2 - 1));
-  };
-  auto rec_ml = [&](int w, int r) -> float* {
-    return reinterpret_cast<float*>(sVw[w] + kTile * DPH) + 2 * r;
-  };
-#pragma unroll
-  for (int i = 0; i < RP; i++) {
-    const float lt = half_sum(l_run[i]);
-    if (lane == 0 || lane == 32) {
-      rec_ml(wave, 2 * i + hh)[0] = m_run[i];
-      rec_ml(wave, 2 * i + hh)[1] = lt;
-    }
-  }
-  if constexpr (DPH == 64) {
-    // lanes 32-63 summed the other half of the tokens: fold them in.
-#pragma unroll
-    for (int r = 0; r < RPW; r++) {
-      acc[r][0] = half_pair_total(acc[r][0], acc[r][0]);
-      acc[r][1] = half_pair_total(acc[r][1], acc[r][1]);
-    }
-  }
-  const int dcol = (DPH == 128 ? lane : (lane & 31)) * 2;
-  if (DPH == 128 || lane < 32) {
-#pragma unroll
-    for (int r = 0; r < RPW; r++)
-      *reinterpret_cast<float2*>(rec_acc(wave, r, dcol)) = make_float2(acc[r][0], acc[r][1]);
-  }
-  __syncthreads();
-  finish_workgroup<DPH>(a, part, kvh, r0, nrows, wave, lane, rec_acc, rec_ml);
 }
 
 // ---------------------------------------------------------------------------
@@ -653,21 +160,6 @@ __device__ __forceinline__ uint32_t pack_h2(float x, float y) {
   return __builtin_bit_cast(uint32_t, h);
 }
 
-// Sum over the CH lanes holding one token (a 16-lane row, or an 8-lane half
-// row for dph 64); every lane of the group gets the total.
-template <int CH>
-__device__ __forceinline__ float token_sum(float x) {
-  x += dpp_f(x, 0);
-  x += dpp_f(x, 1);
-  if constexpr (CH == 16) {
-    x += dpp_f(x, 2);
-    x += dpp_f(x, 3);
-  } else {
-    x += dpp_f(x, 4);
-  }
-  return x;
-}
-
 // All-reduce over the token slots (lanes with the same chunk c).
 template <int DPH>
 __device__ __forceinline__ float slot_sum(float x) {
@@ -685,16 +177,6 @@ __device__ __forceinline__ float slot_max(float x) {
   const auto q = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, x),
                                                   __builtin_bit_cast(int, x), false, false);
   return fmaxf(__builtin_bit_cast(float, (int)q[0]), __builtin_bit_cast(float, (int)q[1]));
-}
-
-__device__ __forceinline__ float wave_max(float x) {
-  x = half_max(x);
-  return fmaxf(lane_value(x, 0), lane_value(x, 32));
-}
-
-__device__ __forceinline__ float wave_sum(float x) {
-  x = half_sum(x);
-  return lane_value(x, 0) + lane_value(x, 32);
 }
 
 __device__ __forceinline__ float4 load_dev4(const float* p) {
@@ -1261,109 +743,48 @@ namespace {
 using namespace sde::attn;
 
 struct Plan {
-  bool stream;         // attn_stream_kernel (else attn_partition_kernel)
-  int rpw;             // rows per wave
+  int rpw;             // rows per wave (2 or kStreamMaxRows)
   int row_groups;
-  int tiles_per_wave;  // attn_partition_kernel
-  int tiles_per_part;  // attn_stream_kernel
-  int chunk;           // attn_stream_kernel: tiles per unrolled chunk
+  int chunk;           // tiles per unrolled chunk (1, 2 or 4)
+  int tiles_per_part;  // tiles per partition (workgroup)
   int n_parts;
 };
 
-int env_int(const char* name, int fallback) {
-  const char* s = std::getenv(name);
-  if (!s || !*s) return fallback;
-  const int v = std::atoi(s);
-  return v > 0 ? v : fallback;
-}
+int rows_per_wave(int R) { return R <= 2 ? 2 : kStreamMaxRows; }
 
-// Row groups of up to 8 rows (two groups of kStreamMaxRows) take the
-// streaming kernel; larger groups the LDS-staged one.
-bool use_stream(int R) { return R <= 2 * kStreamMaxRows; }
-
-int rows_per_wave(int R) {
-  if (use_stream(R)) return R <= 2 ? 2 : kStreamMaxRows;
-  static const int kChoices[] = {12, 16, 20, 24, 28, 32};
-  if (R > kMaxRowsPerWave) return kMaxRowsPerWave;
-  for (int c : kChoices)
-    if (c >= R) return c;
-  return kMaxRowsPerWave;
-}
-
-int target_waves() { return env_int("SDE_ATTN_TARGET_WAVES", 2048); }
-
-// Streaming kernel: each wave takes tiles_per_wave tiles in chunks of
-// `chunk` (1, 2 or 4, a compile-time unroll).  The largest chunk that still
-// gives at least one workgroup per CU is used; past kStreamMaxParts
-// partitions per (KV head, row group) the waves take several chunks.
-struct StreamSplit {
-  int chunk;
-  int tiles_per_part;
-  int n_parts;
-};
-
-StreamSplit stream_split(int n_tiles, int units, int n_cus) {
-  StreamSplit sp{1, 0, 0};
-  for (int ch : {4, 2, 1}) {
-    const int per = kStreamWaves * ch;
-    if ((int64_t)((n_tiles + per - 1) / per) * units >= n_cus || ch == 1) {
-      sp.chunk = ch;
-      break;
-    }
-  }
-  const int per_chunk = kStreamWaves * sp.chunk;
-  const int chunks = (n_tiles + per_chunk - 1) / per_chunk;  // chunks of all waves
-  const int reps = (chunks + kStreamMaxParts - 1) / kStreamMaxParts;
-  sp.tiles_per_part = per_chunk * reps;
-  sp.n_parts = (n_tiles + sp.tiles_per_part - 1) / sp.tiles_per_part;
-  return sp;
-}
-
+// Each wave takes its tiles in chunks of `chunk` (1, 2 or 4, a compile-time
+// unroll).  The largest chunk that still gives at least one workgroup per CU
+// is used; past kStreamMaxParts partitions per (KV head, row group) the
+// waves take several chunks.
 Plan make_plan(int L_max, int nkv, int R, int n_cus) {
   Plan p;
-  p.stream = use_stream(R);
   p.rpw = rows_per_wave(R);
   p.row_groups = (R + p.rpw - 1) / p.rpw;
   const int n_tiles = (L_max + kTile - 1) / kTile;
-  if (p.stream) {
-    const StreamSplit sp = stream_split(n_tiles, nkv * p.row_groups, n_cus);
-    p.chunk = sp.chunk;
-    p.tiles_per_part = sp.tiles_per_part;
-    p.n_parts = sp.n_parts;
-    p.tiles_per_wave = 0;
-    return p;
+  const int64_t units = (int64_t)nkv * p.row_groups;
+  p.chunk = 1;
+  for (int ch : {4, 2}) {
+    const int per = kStreamWaves * ch;
+    if ((int64_t)((n_tiles + per - 1) / per) * units >= n_cus) {
+      p.chunk = ch;
+      break;
+    }
   }
-  // Partition kernel: the fewest tiles per wave that keep the total near
-  // target_waves() waves.
-  const int64_t work = (int64_t)n_tiles * nkv * p.row_groups;
-  const int64_t tw = target_waves();
-  p.tiles_per_wave = (int)((work + tw - 1) / tw);
-  if (p.tiles_per_wave < 1) p.tiles_per_wave = 1;
-  const int per_part = p.tiles_per_wave * kWaves;
-  p.n_parts = (n_tiles + per_part - 1) / per_part;
-  p.tiles_per_part = 0;
-  p.chunk = 0;
+  const int per_chunk = kStreamWaves * p.chunk;
+  const int chunks = (n_tiles + per_chunk - 1) / per_chunk;
+  const int reps = (chunks + kStreamMaxParts - 1) / kStreamMaxParts;
+  p.tiles_per_part = per_chunk * reps;
+  p.n_parts = (n_tiles + p.tiles_per_part - 1) / p.tiles_per_part;
   return p;
 }
 
-// Upper bound of make_plan(L).n_parts over every L <= max_total_len.
-// Partition kernel: with one
-// tile per wave n_parts = ceil(n_tiles / kWaves); with more, n_tiles/tpw is
-// at most target/(nkv*row_groups).
-int parts_bound(int max_total_len, int nkv, int R, int n_cus) {
+// Upper bound of make_plan(L).n_parts over every L <= max_total_len: a
+// partition holds at least kStreamWaves tiles and there are at most
+// kStreamMaxParts of them.
+int parts_bound(int max_total_len) {
   const int n_tiles = (max_total_len + kTile - 1) / kTile;
-  const int rpw = rows_per_wave(R);
-  const int row_groups = (R + rpw - 1) / rpw;
-  if (use_stream(R)) {
-    // n_parts <= kStreamMaxParts, and <= the ceil(n_tiles / 8) of the
-    // smallest partitions.
-    const int by_len = (n_tiles + kStreamWaves - 1) / kStreamWaves;
-    return by_len < kStreamMaxParts ? by_len : kStreamMaxParts;
-  }
-  const int by_len = (n_tiles + kWaves - 1) / kWaves;
-  const int64_t per = (int64_t)nkv * row_groups * kWaves;
-  const int by_target = (int)((target_waves() + per - 1) / per);
-  return by_len < by_target ? by_len : by_target;
+  const int by_len = (n_tiles + kStreamWaves - 1) / kStreamWaves;
+  return by_len < kStreamMaxParts ? by_len : kStreamMaxParts;
 }
 
 size_t partial_bytes(int nkv, int R, int n_parts, int dph) {
@@ -1373,39 +794,20 @@ size_t partial_bytes(int nkv, int R, int n_parts, int dph) {
 template <int DPH>
 int launch(const Plan& p, const AttnArgs& a, int nkv, hipStream_t s) {
   const dim3 grid(p.n_parts, nkv, p.row_groups);
-  if (p.stream) {
-    const dim3 block(64 * kStreamWaves);
-#define SDE_STREAM(R, C)                                                   \
-  if (p.rpw == R && p.chunk == C) {                                        \
-    attn_stream_kernel<DPH, R, C><<<grid, block, 0, s>>>(a);               \
-    return sde::launch_status();                                           \
+  const dim3 block(64 * kStreamWaves);
+#define SDE_STREAM(R, C)                                     \
+  if (p.rpw == R && p.chunk == C) {                          \
+    attn_stream_kernel<DPH, R, C><<<grid, block, 0, s>>>(a); \
+    return sde::launch_status();                             \
   }
-    SDE_STREAM(2, 1)
-    SDE_STREAM(2, 2)
-    SDE_STREAM(2, 4)
-    SDE_STREAM(4, 1)
-    SDE_STREAM(4, 2)
-    SDE_STREAM(4, 4)
+  SDE_STREAM(2, 1)
+  SDE_STREAM(2, 2)
+  SDE_STREAM(2, 4)
+  SDE_STREAM(4, 1)
+  SDE_STREAM(4, 2)
+  SDE_STREAM(4, 4)
 #undef SDE_STREAM
-    return SDE_ERR_UNSUPPORTED;
-  }
-  const dim3 block(64 * kWaves);
-  switch (p.rpw) {
-#define SDE_CASE(N)                                              \
-  case N:                                                        \
-    attn_partition_kernel<DPH, N><<<grid, block, 0, s>>>(a);     \
-    break;
-    SDE_CASE(12)
-    SDE_CASE(16)
-    SDE_CASE(20)
-    SDE_CASE(24)
-    SDE_CASE(28)
-    SDE_CASE(32)
-#undef SDE_CASE
-    default:
-      return SDE_ERR_UNSUPPORTED;
-  }
-  return sde::launch_status();
+  return SDE_ERR_UNSUPPORTED;
 }
 
 int check_attention(const sde_kv_cache* c, int layer, const float* d_q,
@@ -1434,7 +836,7 @@ size_t sde_paged_attention_workspace_size(const sde_kv_cache* cache, int nh,
   if (!cache || nh < 1 || nkv < 1 || nh % nkv != 0 || n_queries < 1 || max_total_len < 1)
     return 0;
   const int R = n_queries * (nh / nkv);
-  return partial_bytes(nkv, R, parts_bound(max_total_len, nkv, R, cache->n_cus), dph);
+  return partial_bytes(nkv, R, parts_bound(max_total_len), dph);
 }
 
 int sde_paged_attention(sde_kv_cache* cache, int layer, const float* d_q,
@@ -1488,7 +890,6 @@ int sde_paged_attention(sde_kv_cache* cache, int layer, const float* d_q,
   a.pos_base = pos_base;
   a.L_max = L_max;
   a.n_parts = plan.n_parts;
-  a.tiles_per_wave = plan.tiles_per_wave;
   a.tiles_per_part = plan.tiles_per_part;
   a.qscale = (float)(kLog2e / std::sqrt((double)dph));
 
