@@ -1,0 +1,645 @@
+/*
+ * sde/attention_device.hpp — HIP device side of the MI355X (gfx950) paged KV
+ * cache and paged GQA attention, for in-kernel callers (persistent /
+ * megakernel decode loops) and for libsde_paged's own kernels.
+ *
+ * Reference device interface replaced (arkhamHack/speculative_decode_engine):
+ *   cuda/include/kv_cache.h:70-79     kv_cache_append / kv_cache_read /
+ *                                     kv_cache_rollback (device functions)
+ *   cuda/include/attention.h:21-29    device_flash_attention_gqa
+ *   cuda/include/attention.h:140-150  device_attention_dispatch
+ * with the cache passed as the POD sde_kv_view (sde_kv_get_view), whose pool
+ * and table layout is the reference's (kv_cache.h:5-18).
+ *
+ * The functions in namespace sde are block-cooperative like the reference's:
+ * every thread of the calling block calls them with the same arguments
+ * (blockDim.x a multiple of 64).  They need no caller scratch.  Building
+ * blocks of the streaming attention live in namespace sde::attn.
+ */
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <climits>
+#include <cstdint>
+
+#include "sde_paged_kv.h"
+
+namespace sde {
+namespace attn {
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+constexpr int kTile = 32;          // tokens per tile
+constexpr int kStreamMaxRows = 4;  // rows (query, q head) per wave
+constexpr double kLog2e = 1.4426950408889634;
+
+// Where a (layer, context) of the paged cache lives: the pool, that layer's
+// block table, and L_max, the number of positions [0, L_max) the window can
+// see (every position below it has been written).
+struct TileSource {
+  const uint16_t* pool;
+  const int32_t* table;
+  int kv_dim;
+  int bs;
+  int L_max;
+};
+
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, a),
+                                __builtin_bit_cast(half2_t, b), c, false);
+}
+
+// Cross-lane moves (gfx950 lane semantics):
+//  * DPP quad_perm [1,0,3,2] / [2,3,0,1] exchange lanes i^1 / i^2, and
+//    row_ror:4 / row_ror:8 rotate each 16-lane row, so four steps reduce
+//    every row of 16 lanes;
+//  * v_permlane16_swap(x, x) returns rows {0,0,2,2} and {1,1,3,3}: one more
+//    step reduces each 32-lane half without mixing the halves;
+//  * v_permlane32_swap(a, b) returns [a.lo | b.lo] and [a.hi | b.hi], so
+//    their sum holds a's half-sum in lanes 0-31 and b's in lanes 32-63.
+__device__ __forceinline__ float dpp_f(float x, int ctrl_sel) {
+  const int v = __builtin_bit_cast(int, x);
+  int r;
+  switch (ctrl_sel) {
+    case 0: r = __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xf, 0xf, false); break;   // i^1
+    case 1: r = __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xf, 0xf, false); break;   // i^2
+    case 2: r = __builtin_amdgcn_update_dpp(0, v, 0x124, 0xf, 0xf, false); break;  // ror 4
+    case 3: r = __builtin_amdgcn_update_dpp(0, v, 0x128, 0xf, 0xf, false); break;  // ror 8
+    default: r = __builtin_amdgcn_update_dpp(0, v, 0x141, 0xf, 0xf, false); break; // i^7 in 8
+  }
+  return __builtin_bit_cast(float, r);
+}
+
+// (even row, odd row) of this lane's pair of 16-lane rows.
+__device__ __forceinline__ float2 row_pair(float x) {
+  const int v = __builtin_bit_cast(int, x);
+  const auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  return make_float2(__builtin_bit_cast(float, (int)p[0]), __builtin_bit_cast(float, (int)p[1]));
+}
+
+
+
+// Sums a (partial over lanes 0-31 and 32-63) and b likewise: lanes 0-31
+// get a's total, lanes 32-63 b's total.
+__device__ __forceinline__ float half_pair_total(float a, float b) {
+  const auto p = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, a),
+                                                  __builtin_bit_cast(int, b), false, false);
+  return __builtin_bit_cast(float, (int)p[0]) + __builtin_bit_cast(float, (int)p[1]);
+}
+
+
+typedef const __attribute__((address_space(4))) int32_t* const_table_t;
+
+// The block table is read-only during the kernel: reading it through the
+// constant address space turns the entries into scalar loads (lgkmcnt),
+// which never wait behind outstanding tile loads (vmcnt).
+__device__ __forceinline__ const_table_t const_table(const TileSource& a) {
+  return (const_table_t)a.table;
+}
+
+__device__ __forceinline__ uint32_t pack_h2(float x, float y) {
+  const half2_t h = {(_Float16)x, (_Float16)y};
+  return __builtin_bit_cast(uint32_t, h);
+}
+
+// All-reduce over the token slots (lanes with the same chunk c).
+template <int DPH>
+__device__ __forceinline__ float slot_sum(float x) {
+  if constexpr (DPH == 64) x += dpp_f(x, 3);  // slots 2k, 2k+1 share a 16-lane row
+  const float2 p = row_pair(x);
+  x = p.x + p.y;
+  return half_pair_total(x, x);
+}
+
+template <int DPH>
+__device__ __forceinline__ float slot_max(float x) {
+  if constexpr (DPH == 64) x = fmaxf(x, dpp_f(x, 3));
+  const float2 p = row_pair(x);
+  x = fmaxf(p.x, p.y);
+  const auto q = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, x),
+                                                  __builtin_bit_cast(int, x), false, false);
+  return fmaxf(__builtin_bit_cast(float, (int)q[0]), __builtin_bit_cast(float, (int)q[1]));
+}
+
+__device__ __forceinline__ uint4 ld16(const char* p) { return *reinterpret_cast<const uint4*>(p); }
+
+// Physical block and in-block slot of the first token of each load group of
+// tile ts (SL tokens per group, SL divides block_size).  Groups at or past
+// L_max are pinned to token L_max-1 so every address stays on written data.
+template <int NLD, int SL>
+__device__ __forceinline__ void tile_groups(const TileSource& a, const_table_t table, int ts,
+                                            int (&blk)[NLD], int (&slot)[NLD]) {
+  if (ts + kTile <= a.L_max) {
+    int lb = ts / a.bs;
+    int s = ts - lb * a.bs;
+#pragma unroll
+    for (int j = 0; j < NLD; j++) {
+      blk[j] = table[lb];
+      slot[j] = s;
+      s += SL;
+      if (s == a.bs) {
+        s = 0;
+        ++lb;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < NLD; j++) {
+      const int g = min(ts + j * SL, a.L_max - 1);
+      const int lb = g / a.bs;
+      blk[j] = table[lb];
+      slot[j] = g - lb * a.bs;
+    }
+  }
+}
+
+// Issues the K (is_v false) or V loads of tile ts: load j brings token
+// ts + j*SL + sl, 16-byte chunk c (lane_off = sl*row_bytes + 16c from the
+// group's first token).  Lanes whose token is at or past L_max read the
+// group's first token instead (chunk_off = 16c); their logits are masked.
+// Every path issues the same NLD loads, so the compiler's vmcnt bookkeeping
+// stays exact across tiles.
+template <int DPH>
+__device__ __forceinline__ void stream_load(const TileSource& a, const char* head_base, int ts,
+                                            int sl, uint32_t lane_off, uint32_t chunk_off,
+                                            bool is_v, const int (&blk)[kTile / (512 / DPH)],
+                                            const int (&slot)[kTile / (512 / DPH)],
+                                            uint4 (&x)[kTile / (512 / DPH)]) {
+  constexpr int SL = 512 / DPH;
+  constexpr int NLD = kTile / SL;
+  const uint32_t row_bytes = 2u * (uint32_t)a.kv_dim;
+  const uint32_t v_bytes = (uint32_t)a.bs * row_bytes;
+  const bool full = ts + kTile <= a.L_max;
+#pragma unroll
+  for (int j = 0; j < NLD; j++) {
+    const char* ub = head_base + (uint64_t)(uint32_t)blk[j] * (2ull * v_bytes) +
+                     (uint32_t)slot[j] * row_bytes + (is_v ? v_bytes : 0u);
+    const uint32_t off = (full || ts + j * SL + sl < a.L_max) ? lane_off : chunk_off;
+    x[j] = ld16(ub + off);
+  }
+  // Compiler barriers: keep the loads here instead of letting them sink to
+  // their first use a tile later, and keep the scheduler from interleaving
+  // neighbouring tiles' work (code-motion fences only; no wait).
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// Marks the point where a tile's registers are first consumed: the empty
+// asm redefines them, so no use of the tile (and hence no wait for its
+// loads) is hoisted above this point into the previous tile's work.  SITE
+// makes the asm text differ per call site, so identical pins at the heads of
+// two branches are not merged and hoisted into their common predecessor.
+template <int NLD, int SITE>
+__device__ __forceinline__ void pin_arrival(const uint4 (&x)[NLD]) {
+  uint4(&y)[NLD] = const_cast<uint4(&)[NLD]>(x);
+#pragma unroll
+  for (int j = 0; j < NLD; j++) {
+    if constexpr (SITE == 0) asm volatile("; tile 0" : "+v"(y[j].x), "+v"(y[j].y), "+v"(y[j].z), "+v"(y[j].w));
+    else if constexpr (SITE == 1) asm volatile("; tile 1" : "+v"(y[j].x), "+v"(y[j].y), "+v"(y[j].z), "+v"(y[j].w));
+    else if constexpr (SITE == 2) asm volatile("; tile 2" : "+v"(y[j].x), "+v"(y[j].y), "+v"(y[j].z), "+v"(y[j].w));
+    else asm volatile("; tile 3" : "+v"(y[j].x), "+v"(y[j].y), "+v"(y[j].z), "+v"(y[j].w));
+  }
+}
+
+// Lane roles of the streaming attention.  Load role: lane = (slot sl, chunk c),
+// c = lane % CH.  After the transposing reduction of the logits a lane owns
+// one (row r, token pair jp) of its slot: the NV = RPW*NLD partial logits of
+// a lane are halved once per butterfly step (the lane keeps the half named
+// by one bit of c and adds its partner's copy of that half), so after
+// log2(NV)-1 steps a lane holds the full logits of tokens 2jp and 2jp+1 of
+// row r, and the softmax does per-lane scalar work.
+template <int DPH, int RPW>
+struct StreamShape {
+  static constexpr int CH = DPH / 8;                  // lanes per token
+  static constexpr int S = CH == 16 ? 4 : 3;          // butterfly steps over CH lanes
+  static constexpr int SL = 64 / CH;                  // slots
+  static constexpr int NLD = kTile / SL;              // loads per tile (K and V each)
+  static constexpr int NV = RPW * NLD;                // partial logits per lane
+  static constexpr int T = (NV == 32 ? 5 : NV == 16 ? 4 : NV == 8 ? 3 : 2) - 1;  // halving steps
+  static constexpr int RB = RPW == 4 ? 2 : 1;         // bits of r
+  static_assert(T <= S, "more logits than lanes to spread them over");
+  // chunk index of the lane owning (row r, pair jp) (its redundant bits 0)
+  static constexpr int owner(int r, int jp) { return ((r << (T - RB)) | jp) << (S - T); }
+};
+
+// Butterfly step k over the CH lanes of a token: partner lane = c ^ mask,
+// masks {8, 7, 2, 1} (dph 128) or {7, 2, 1} (dph 64) -- row_ror:8,
+// row_half_mirror, quad_perm [2,3,0,1], quad_perm [1,0,3,2]; step k splits on
+// bit S-1-k of c, which the later masks leave unchanged.
+template <int CH>
+__device__ __forceinline__ float bfly(float x, int k) {
+  const int v = __builtin_bit_cast(int, x);
+  int r;
+  switch (CH == 16 ? k : k + 1) {
+    case 0: r = __builtin_amdgcn_update_dpp(0, v, 0x128, 0xf, 0xf, false); break;
+    case 1: r = __builtin_amdgcn_update_dpp(0, v, 0x141, 0xf, 0xf, false); break;
+    case 2: r = __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xf, 0xf, false); break;
+    default: r = __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xf, 0xf, false); break;
+  }
+  return __builtin_bit_cast(float, r);
+}
+
+// Value of lane n of this lane's 16-lane row (DPP row_newbcast:n).
+__device__ __forceinline__ int row_bcast(int v, int n) {
+  switch (n) {
+    case 0: return __builtin_amdgcn_update_dpp(0, v, 0x150, 0xf, 0xf, false);
+    case 1: return __builtin_amdgcn_update_dpp(0, v, 0x151, 0xf, 0xf, false);
+    case 2: return __builtin_amdgcn_update_dpp(0, v, 0x152, 0xf, 0xf, false);
+    case 3: return __builtin_amdgcn_update_dpp(0, v, 0x153, 0xf, 0xf, false);
+    case 4: return __builtin_amdgcn_update_dpp(0, v, 0x154, 0xf, 0xf, false);
+    case 5: return __builtin_amdgcn_update_dpp(0, v, 0x155, 0xf, 0xf, false);
+    case 6: return __builtin_amdgcn_update_dpp(0, v, 0x156, 0xf, 0xf, false);
+    case 7: return __builtin_amdgcn_update_dpp(0, v, 0x157, 0xf, 0xf, false);
+    case 8: return __builtin_amdgcn_update_dpp(0, v, 0x158, 0xf, 0xf, false);
+    case 9: return __builtin_amdgcn_update_dpp(0, v, 0x159, 0xf, 0xf, false);
+    case 10: return __builtin_amdgcn_update_dpp(0, v, 0x15A, 0xf, 0xf, false);
+    case 11: return __builtin_amdgcn_update_dpp(0, v, 0x15B, 0xf, 0xf, false);
+    case 12: return __builtin_amdgcn_update_dpp(0, v, 0x15C, 0xf, 0xf, false);
+    case 13: return __builtin_amdgcn_update_dpp(0, v, 0x15D, 0xf, 0xf, false);
+    case 14: return __builtin_amdgcn_update_dpp(0, v, 0x15E, 0xf, 0xf, false);
+    default: return __builtin_amdgcn_update_dpp(0, v, 0x15F, 0xf, 0xf, false);
+  }
+}
+
+// Value held by the owner of (row r, pair jp) in this lane's slot.  With
+// dph 64 a 16-lane row holds two slots (lane bit 3 = odd slot).
+template <int DPH, int RPW>
+__device__ __forceinline__ uint32_t from_owner(uint32_t x, int r, int jp, bool odd_slot) {
+  using Sh = StreamShape<DPH, RPW>;
+  const int n = Sh::owner(r, jp);
+  const int v = (int)x;
+  if constexpr (DPH == 128) {
+    return (uint32_t)row_bcast(v, n);
+  } else {
+    const int lo = row_bcast(v, n);
+    const int hi = row_bcast(v, n + 8);
+    return (uint32_t)(odd_slot ? hi : lo);
+  }
+}
+
+template <int DPH, int RPW>
+__device__ __forceinline__ float from_owner_f(float x, int r, int jp, bool odd_slot) {
+  return __builtin_bit_cast(
+      float, from_owner<DPH, RPW>(__builtin_bit_cast(uint32_t, x), r, jp, odd_slot));
+}
+
+// Logits of one tile (transposing reduction) and the online-softmax update
+// of the lane's (row, pair): m_run / l_run are the lane's (row, slot) state
+// (l_run a partial sum over the lane's token pairs).  Returns the rescale
+// factor in al_out and the pair's probabilities as fp16x2 in pk_out.
+template <int DPH, int RPW, int SITE>
+__device__ __forceinline__ void stream_qk(int ts, int sl, int c, int min_lim, int my_lim,
+                                          int my_jp, const uint4 (&qr)[RPW],
+                                          const uint4 (&k)[kTile / (512 / DPH)], float& m_run,
+                                          float& l_run, float& al_out, uint32_t& pk_out) {
+  using Sh = StreamShape<DPH, RPW>;
+  constexpr int CH = Sh::CH, S = Sh::S, SL = Sh::SL, NLD = Sh::NLD, NV = Sh::NV, T = Sh::T;
+  pin_arrival<NLD, SITE>(k);
+  float x[NV];
+#pragma unroll
+  for (int r = 0; r < RPW; r++) {
+    const uint4 q4 = qr[r];
+#pragma unroll
+    for (int j = 0; j < NLD; j++) {
+      float t = dot2(q4.x, k[j].x, 0.f);
+      t = dot2(q4.y, k[j].y, t);
+      t = dot2(q4.z, k[j].z, t);
+      t = dot2(q4.w, k[j].w, t);
+      x[r * NLD + j] = t;
+    }
+  }
+  // Transposing butterfly: step kk keeps the half of x whose top index bit
+  // equals bit S-1-kk of c.
+#pragma unroll
+  for (int kk = 0; kk < T; kk++) {
+    const bool f = (c >> (S - 1 - kk)) & 1;
+    const int h = NV >> (kk + 1);
+#pragma unroll
+    for (int i = 0; i < (NV >> 1); i++) {
+      if (i < h) {
+        const float a = x[i], b = x[i + h];
+        const float send = f ? a : b;
+        const float keep = f ? b : a;
+        x[i] = keep + bfly<CH>(send, kk);
+      }
+    }
+  }
+#pragma unroll
+  for (int kk = T; kk < S; kk++) {
+    x[0] += bfly<CH>(x[0], kk);
+    x[1] += bfly<CH>(x[1], kk);
+  }
+  float s0 = x[0], s1 = x[1];
+  // Causal / length mask: token g is visible to the lane's row iff g <= my_lim.
+  if (ts + kTile - 1 > min_lim) {
+    const int g0 = ts + 2 * my_jp * SL + sl;
+    if (g0 > my_lim) s0 = -INFINITY;
+    if (g0 + SL > my_lim) s1 = -INFINITY;
+  }
+  float tmax = fmaxf(s0, s1);
+#pragma unroll
+  for (int kk = Sh::RB; kk < S; kk++) tmax = fmaxf(tmax, bfly<CH>(tmax, kk));
+  const float m_new = fmaxf(m_run, tmax);
+  // Nothing visible yet: base 0 makes every weight exp2(-inf) = 0.
+  const float base = m_new == -INFINITY ? 0.f : m_new;
+  const float al = __builtin_amdgcn_exp2f(m_run - base);
+  const float p0 = __builtin_amdgcn_exp2f(s0 - base);
+  const float p1 = __builtin_amdgcn_exp2f(s1 - base);
+  l_run = l_run * al + (p0 + p1);
+  m_run = m_new;
+  al_out = al;
+  pk_out = pack_h2(p0, p1);
+  // Finish this tile's logits here, in program order (see pin_arrival).
+  asm volatile("" : "+v"(m_run), "+v"(l_run), "+v"(al_out), "+v"(pk_out));
+}
+
+// P.V of one tile: rescales acc by each row's factor and accumulates the
+// probability pairs (from their owners) against the byte-permuted V pairs.
+template <int DPH, int RPW, int SITE>
+__device__ __forceinline__ void stream_pv(int sl, float al, uint32_t pk,
+                                          const uint4 (&v)[kTile / (512 / DPH)],
+                                          float (&acc)[RPW][8]) {
+  constexpr int NLD = StreamShape<DPH, RPW>::NLD;
+  pin_arrival<NLD, SITE>(v);
+  const bool odd_slot = sl & 1;
+#pragma unroll
+  for (int r = 0; r < RPW; r++) {
+    const float a_r = from_owner_f<DPH, RPW>(al, r, 0, odd_slot);
+#pragma unroll
+    for (int e = 0; e < 8; e++) acc[r][e] *= a_r;
+  }
+#pragma unroll
+  for (int jp = 0; jp < NLD / 2; jp++) {
+    uint32_t pp[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; r++) pp[r] = from_owner<DPH, RPW>(pk, r, jp, odd_slot);
+    const uint32_t v0[4] = {v[2 * jp].x, v[2 * jp].y, v[2 * jp].z, v[2 * jp].w};
+    const uint32_t v1[4] = {v[2 * jp + 1].x, v[2 * jp + 1].y, v[2 * jp + 1].z, v[2 * jp + 1].w};
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+      const uint32_t lo = __builtin_amdgcn_perm(v1[w], v0[w], 0x05040100u);
+      const uint32_t hi = __builtin_amdgcn_perm(v1[w], v0[w], 0x07060302u);
+#pragma unroll
+      for (int r = 0; r < RPW; r++) {
+        acc[r][2 * w] = dot2(pp[r], lo, acc[r][2 * w]);
+        acc[r][2 * w + 1] = dot2(pp[r], hi, acc[r][2 * w + 1]);
+      }
+    }
+  }
+  // Finish this tile's P.V here, in program order, so it is not sunk past
+  // the following tiles' work (which would keep its V registers live).
+#pragma unroll
+  for (int r = 0; r < RPW; r++)
+    asm volatile("" : "+v"(acc[r][0]), "+v"(acc[r][1]), "+v"(acc[r][2]), "+v"(acc[r][3]),
+                 "+v"(acc[r][4]), "+v"(acc[r][5]), "+v"(acc[r][6]), "+v"(acc[r][7]));
+}
+
+
+// Streams the tiles first, first+stride, ... (< te) of KV head kvh through
+// this wave: the online softmax of the wave's rows (q_raw: this lane's
+// chunk, features 8c..8c+7, of each row in fp32) accumulates into
+// (m_run, l_run, acc).  Rows r >= nrows and positions past each row's limit
+// (my_lim for the lane's own row, min_lim the smallest over rows) are
+// masked.  Tiles are taken in chunks of CHUNK, unrolled at compile time:
+// K of tile i+1 is issued before tile i's logits and V of tile i+1 before
+// tile i's P.V, so a tile of loads stays in flight while the wave computes,
+// and no in-flight register is carried across a loop edge (the compiler
+// would copy it, which waits for it).  Chunk slots past the wave's last tile
+// re-read that tile (an L2 hit) and are fully masked.
+template <int DPH, int RPW, int CHUNK>
+__device__ __forceinline__ void wave_attend(const TileSource& src, int kvh, int first, int te,
+                                            int stride, int nrows, int min_lim, int my_lim,
+                                            float qscale, const float2 (&q_raw)[RPW][4],
+                                            float& m_run, float& l_run, float (&acc)[RPW][8]) {
+  using Sh = StreamShape<DPH, RPW>;
+  constexpr int CH = Sh::CH, SL = Sh::SL, NLD = Sh::NLD;
+  const int lane = threadIdx.x & 63;
+  const int sl = lane / CH;
+  const int c = lane % CH;
+  const int my_jp = (c >> (Sh::S - Sh::T)) & ((1 << (Sh::T - Sh::RB)) - 1);
+  const const_table_t table = const_table(src);
+  const char* head_base = reinterpret_cast<const char*>(src.pool) + (size_t)kvh * DPH * 2u;
+  const uint32_t lane_off = (uint32_t)sl * 2u * (uint32_t)src.kv_dim + 16u * c;
+  const uint32_t chunk_off = 16u * c;
+  if (first >= te) return;
+  const int last = first + ((te - 1 - first) / stride) * stride;
+  uint4 qr[RPW];
+  for (int c0 = first; c0 < te; c0 += CHUNK * stride) {
+    uint4 kbuf[2][NLD], vbuf[2][NLD];
+    int blk[2][NLD], slot[2][NLD];
+    float al;
+    uint32_t pk;
+    tile_groups<NLD, SL>(src, table, min(c0, last) * kTile, blk[0], slot[0]);
+    stream_load<DPH>(src, head_base, min(c0, last) * kTile, sl, lane_off, chunk_off, false,
+                     blk[0], slot[0], kbuf[0]);
+    stream_load<DPH>(src, head_base, min(c0, last) * kTile, sl, lane_off, chunk_off, true,
+                     blk[0], slot[0], vbuf[0]);
+    if (CHUNK > 1)
+      tile_groups<NLD, SL>(src, table, min(c0 + stride, last) * kTile, blk[1], slot[1]);
+#pragma unroll
+    for (int i = 0; i < CHUNK; i++) {
+      const int t = c0 + i * stride;
+      const int b = i & 1, nb = b ^ 1;
+      const int tn = min(t + stride, last);
+      if (i + 1 < CHUNK)
+        stream_load<DPH>(src, head_base, tn * kTile, sl, lane_off, chunk_off, false, blk[nb],
+                         slot[nb], kbuf[nb]);
+      if (i == 0) {
+        // q is scaled into the exp2 domain and rounded to fp16 pairs once
+        // this chunk's loads are in flight (q was loaded before them, so
+        // this waits for no tile data).
+#pragma unroll
+        for (int r = 0; r < RPW; r++) {
+          const float sc = r < nrows ? qscale : 0.f;
+          qr[r] = make_uint4(pack_h2(q_raw[r][0].x * sc, q_raw[r][0].y * sc),
+                             pack_h2(q_raw[r][1].x * sc, q_raw[r][1].y * sc),
+                             pack_h2(q_raw[r][2].x * sc, q_raw[r][2].y * sc),
+                             pack_h2(q_raw[r][3].x * sc, q_raw[r][3].y * sc));
+        }
+      }
+      // A slot past the wave's last tile: every token masked (no-op).
+      const int ts_mask = t <= last ? t * kTile : INT_MAX / 2;
+      stream_qk<DPH, RPW, 0>(ts_mask, sl, c, min_lim, my_lim, my_jp, qr, kbuf[b], m_run, l_run,
+                             al, pk);
+      if (i + 1 < CHUNK) {
+        stream_load<DPH>(src, head_base, tn * kTile, sl, lane_off, chunk_off, true, blk[nb],
+                         slot[nb], vbuf[nb]);
+        if (i + 2 < CHUNK)
+          tile_groups<NLD, SL>(src, table, min(t + 2 * stride, last) * kTile, blk[b], slot[b]);
+      }
+      stream_pv<DPH, RPW, 0>(sl, al, pk, vbuf[b], acc);
+    }
+  }
+}
+
+// Merges the token slots' softmax states of this wave: per row r, mx[r] and
+// l[r] (the same in every lane) and acc[r][e] rescaled to mx[r] and summed
+// over the slots (every lane holds the total of its chunk c).
+template <int DPH, int RPW>
+__device__ __forceinline__ void wave_merge_slots(float m_run, float l_run, float (&acc)[RPW][8],
+                                                 float (&mx)[RPW], float (&l)[RPW]) {
+  using Sh = StreamShape<DPH, RPW>;
+  constexpr int CH = Sh::CH;
+  const int lane = threadIdx.x & 63;
+  const int sl = lane / CH;
+  const int c = lane % CH;
+  // l of (row, slot): sum over the row's token-pair owners (redundant lanes
+  // hold copies and contribute 0).
+  const bool redundant = (c & ((1 << (Sh::S - Sh::T)) - 1)) != 0;
+  float lsum = redundant ? 0.f : l_run;
+#pragma unroll
+  for (int kk = Sh::RB; kk < Sh::S; kk++) lsum += bfly<CH>(lsum, kk);
+  const bool odd_slot = sl & 1;
+#pragma unroll
+  for (int r = 0; r < RPW; r++) {
+    const float m_s = from_owner_f<DPH, RPW>(m_run, r, 0, odd_slot);
+    const float l_s = from_owner_f<DPH, RPW>(lsum, r, 0, odd_slot);
+    mx[r] = slot_max<DPH>(m_s);
+    const float f = mx[r] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_s - mx[r]);
+    l[r] = slot_sum<DPH>(l_s * f);
+#pragma unroll
+    for (int e = 0; e < 8; e++) acc[r][e] = slot_sum<DPH>(acc[r][e] * f);
+  }
+}
+
+// attention.h:120-126: normalise unless the sum is tiny or not finite.
+__device__ __forceinline__ float finish_scale(float l) {
+  return (l > 1e-20f && isfinite(l)) ? 1.f / l : 0.f;
+}
+
+// One query, all heads, all of [0, total_len) on one block (no split):
+// wave w takes the (KV head, group of up to four q heads) units w, w+nw, ...
+template <int DPH>
+__device__ __forceinline__ void block_attend(const float* q_all, float* out, const sde_kv_view& kv,
+                                             int layer, int nh, int nkv, int total_len) {
+  constexpr int RPW = kStreamMaxRows;
+  constexpr int CH = DPH / 8;
+  const int G = nh / nkv;
+  const int groups = (G + RPW - 1) / RPW;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nw = blockDim.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int sl = lane / CH;
+  const int c = lane % CH;
+  const TileSource src{kv.pool, kv.block_tables + (size_t)layer * kv.max_blocks_per_layer,
+                       kv.kv_dim, kv.block_size, total_len};
+  const int n_tiles = (total_len + kTile - 1) / kTile;
+  const float qscale = (float)(kLog2e / __builtin_sqrt((double)DPH));
+  using Sh = StreamShape<DPH, RPW>;
+  const int my_r = (c >> (Sh::S - Sh::T)) >> (Sh::T - Sh::RB);
+  for (int u = wave; u < nkv * groups; u += nw) {
+    const int kvh = u / groups;
+    const int h0 = kvh * G + (u - kvh * groups) * RPW;
+    const int nrows = min(RPW, kvh * G + G - h0);
+    float2 q_raw[RPW][4];
+#pragma unroll
+    for (int r = 0; r < RPW; r++) {
+      const float2* qp = reinterpret_cast<const float2*>(q_all + (size_t)min(h0 + r, nh - 1) * DPH +
+                                                         8 * c);
+#pragma unroll
+      for (int w = 0; w < 4; w++) q_raw[r][w] = qp[w];
+    }
+    const int min_lim = nrows < RPW ? -1 : total_len - 1;
+    const int my_lim = my_r < nrows ? total_len - 1 : -1;
+    float m_run = -INFINITY, l_run = 0.f, acc[RPW][8];
+#pragma unroll
+    for (int r = 0; r < RPW; r++)
+#pragma unroll
+      for (int e = 0; e < 8; e++) acc[r][e] = 0.f;
+    wave_attend<DPH, RPW, 2>(src, kvh, 0, n_tiles, 1, nrows, min_lim, my_lim, qscale, q_raw,
+                             m_run, l_run, acc);
+    float mx[RPW], l[RPW];
+    wave_merge_slots<DPH, RPW>(m_run, l_run, acc, mx, l);
+    if (sl == 0) {
+#pragma unroll
+      for (int r = 0; r < RPW; r++) {
+        if (r < nrows) {
+          const float inv = finish_scale(l[r]);
+          float4* dst = reinterpret_cast<float4*>(out + (size_t)(h0 + r) * DPH + 8 * c);
+          dst[0] = make_float4(acc[r][0] * inv, acc[r][1] * inv, acc[r][2] * inv, acc[r][3] * inv);
+          dst[1] = make_float4(acc[r][4] * inv, acc[r][5] * inv, acc[r][6] * inv, acc[r][7] * inv);
+        }
+      }
+    }
+  }
+}
+
+}  // namespace attn
+
+// ---- reference-named device API (block-cooperative) ---------------------
+
+// kv_cache.h:70-72 / kv_cache.cu:70-93: fp32 k, v [kv_dim] -> fp16 (RNE) at
+// position `current_seq_len` of `layer`.  Positions outside the layer's
+// table are ignored (the reference does not check).
+__device__ inline void kv_cache_append(const sde_kv_view& kv, int layer, const float* k,
+                                       const float* v, int current_seq_len) {
+  const int lb = current_seq_len / kv.block_size;
+  if (layer >= 0 && layer < kv.n_layers && current_seq_len >= 0 && lb < kv.max_blocks_per_layer) {
+    const int pb = kv.block_tables[(size_t)layer * kv.max_blocks_per_layer + lb];
+    uint16_t* kd = kv.pool + ((size_t)pb * 2u * kv.block_size + (current_seq_len - lb * kv.block_size)) *
+                                 (size_t)kv.kv_dim;
+    uint16_t* vd = kd + (size_t)kv.block_size * kv.kv_dim;
+    for (int i = threadIdx.x; i < kv.kv_dim; i += blockDim.x) {
+      kd[i] = __builtin_bit_cast(uint16_t, (_Float16)k[i]);
+      vd[i] = __builtin_bit_cast(uint16_t, (_Float16)v[i]);
+    }
+  }
+  __syncthreads();
+}
+
+// kv_cache.h:74-75 / kv_cache.cu:95-114: K[pos], V[pos] of `layer`, widened
+// exactly to fp32 [kv_dim].
+__device__ inline void kv_cache_read(const sde_kv_view& kv, int layer, int pos, float* k_out,
+                                     float* v_out) {
+  const int lb = pos / kv.block_size;
+  if (layer >= 0 && layer < kv.n_layers && pos >= 0 && lb < kv.max_blocks_per_layer) {
+    const int pb = kv.block_tables[(size_t)layer * kv.max_blocks_per_layer + lb];
+    const uint16_t* ks = kv.pool + ((size_t)pb * 2u * kv.block_size + (pos - lb * kv.block_size)) *
+                                       (size_t)kv.kv_dim;
+    const uint16_t* vs = ks + (size_t)kv.block_size * kv.kv_dim;
+    for (int i = threadIdx.x; i < kv.kv_dim; i += blockDim.x) {
+      k_out[i] = (float)__builtin_bit_cast(_Float16, ks[i]);
+      v_out[i] = (float)__builtin_bit_cast(_Float16, vs[i]);
+    }
+  }
+  __syncthreads();
+}
+
+// kv_cache.h:77-79 / kv_cache.cu:116-120: O(1) rewind, seq_len <-
+// target_len, written by thread 0 of block 0; the pool keeps its bytes
+// (positions >= target_len are overwritten by later appends).
+__device__ inline void kv_cache_rollback(const sde_kv_view& kv, int target_len) {
+  if (threadIdx.x == 0 && blockIdx.x == 0) *kv.seq_len = target_len;
+  __syncthreads();
+}
+
+// attention.h:21-127: attention of one query (q_all fp32 [nh*dph], RoPE
+// applied) over positions [0, total_len) of `layer`: q head h reads KV head
+// h*nkv/nh, scale dph^-1/2; attn_out fp32 [nh*dph] is fully written
+// (zeros when total_len is 0).  head_dim 64 or 128, block_size a multiple
+// of 8, nkv | nh; returns SDE_ERR_UNSUPPORTED (writing nothing) otherwise.
+__device__ inline int device_flash_attention_gqa(const float* q_all, float* attn_out,
+                                                 const sde_kv_view& kv, int layer, int nh, int nkv,
+                                                 int dph, int total_len) {
+  if (nkv < 1 || nh % nkv != 0 || kv.block_size % 8 != 0 || total_len < 0) return SDE_ERR_UNSUPPORTED;
+  if (dph == 128)
+    attn::block_attend<128>(q_all, attn_out, kv, layer, nh, nkv, total_len);
+  else if (dph == 64)
+    attn::block_attend<64>(q_all, attn_out, kv, layer, nh, nkv, total_len);
+  else
+    return SDE_ERR_UNSUPPORTED;
+  __syncthreads();
+  return SDE_OK;
+}
+
+// attention.h:140-164: SDE_ATTN_SOFTMAX runs device_flash_attention_gqa; the
+// types the reference reserves (and traps on) return SDE_ERR_UNSUPPORTED.
+__device__ inline int device_attention_dispatch(int attn_type, const float* q_all, float* attn_out,
+                                                const sde_kv_view& kv, int layer, int nh, int nkv,
+                                                int dph, int total_len) {
+  if (attn_type != SDE_ATTN_SOFTMAX) return SDE_ERR_UNSUPPORTED;
+  return device_flash_attention_gqa(q_all, attn_out, kv, layer, nh, nkv, dph, total_len);
+}
+
+}  // namespace sde

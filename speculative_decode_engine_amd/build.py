@@ -24,6 +24,11 @@ OFFLOAD_ARCH = "gfx950"
 
 SOURCES = ["kv_cache.hip", "paged_attention.hip"]
 
+# Test infrastructure: kernels that call the device-side API of
+# include/sde/attention_device.hpp from inside a caller's kernel.
+DEVICE_TEST_SRC = REPO_ROOT / "tests" / "device" / "device_api_test.hip"
+DEVICE_TEST_LIB = REPO_ROOT / "tests" / "device" / "libsde_device_test.so"
+
 HIP_FLAGS = [
     f"--offload-arch={OFFLOAD_ARCH}",
     "-O3",
@@ -75,7 +80,19 @@ def build(verbose: bool = False) -> Path:
     os.replace(tmp, LIB_PATH)
     if verbose:
         print(f"built {LIB_PATH}")
+    build_device_tests(verbose)
     return LIB_PATH
+
+
+def build_device_tests(verbose: bool = False) -> Path:
+    """Compiles the device-API test kernels into their own library."""
+    tmp = DEVICE_TEST_LIB.with_suffix(".so.tmp")
+    _run([hipcc(), *HIP_FLAGS, "-shared", str(DEVICE_TEST_SRC), "-o", str(tmp),
+          f"-L{PKG_DIR}", "-lsde_paged", "-Wl,-rpath,$ORIGIN/../../speculative_decode_engine_amd"])
+    os.replace(tmp, DEVICE_TEST_LIB)
+    if verbose:
+        print(f"built {DEVICE_TEST_LIB}")
+    return DEVICE_TEST_LIB
 
 
 if __name__ == "__main__":

@@ -30,79 +30,26 @@
 #include <cmath>
 #include <cstdlib>
 
+#include "sde/attention_device.hpp"
 #include "sde_internal.hpp"
 
 namespace sde {
 namespace attn {
 
-typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
-
-constexpr int kTile = 32;  // tokens per tile
-constexpr double kLog2e = 1.4426950408889634;
-
 struct AttnArgs {
-  const uint16_t* pool;
-  const int32_t* table;  // this layer's block table
+  TileSource src;        // pool, this layer's table, kv_dim, block_size, L_max
   const float* q;        // [M][nh*dph]
   float* out;            // [M][nh*dph]
   float* partials;       // [nkv][R][n_parts][dph+2] = (max, sum, acc[dph])
   uint32_t* counters;    // [nkv][row_groups] arrival counters, zero at rest
-  int kv_dim;
-  int bs;
   int nh;
   int G;         // query heads per KV head
   int R;         // rows per KV head = M * G (row = m*G + g)
   int pos_base;  // query m sees positions [0, pos_base+m]
-  int L_max;     // pos_base + M
   int n_parts;
   int tiles_per_part;  // attn_stream_kernel: tiles per partition
   float qscale;  // log2(e) / sqrt(dph)
 };
-
-__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
-  return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, a),
-                                __builtin_bit_cast(half2_t, b), c, false);
-}
-
-// Cross-lane moves (gfx950 lane semantics):
-//  * DPP quad_perm [1,0,3,2] / [2,3,0,1] exchange lanes i^1 / i^2, and
-//    row_ror:4 / row_ror:8 rotate each 16-lane row, so four steps reduce
-//    every row of 16 lanes;
-//  * v_permlane16_swap(x, x) returns rows {0,0,2,2} and {1,1,3,3}: one more
-//    step reduces each 32-lane half without mixing the halves;
-//  * v_permlane32_swap(a, b) returns [a.lo | b.lo] and [a.hi | b.hi], so
-//    their sum holds a's half-sum in lanes 0-31 and b's in lanes 32-63.
-__device__ __forceinline__ float dpp_f(float x, int ctrl_sel) {
-  const int v = __builtin_bit_cast(int, x);
-  int r;
-  switch (ctrl_sel) {
-    case 0: r = __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xf, 0xf, false); break;   // i^1
-    case 1: r = __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xf, 0xf, false); break;   // i^2
-    case 2: r = __builtin_amdgcn_update_dpp(0, v, 0x124, 0xf, 0xf, false); break;  // ror 4
-    case 3: r = __builtin_amdgcn_update_dpp(0, v, 0x128, 0xf, 0xf, false); break;  // ror 8
-    default: r = __builtin_amdgcn_update_dpp(0, v, 0x141, 0xf, 0xf, false); break; // i^7 in 8
-  }
-  return __builtin_bit_cast(float, r);
-}
-
-// (even row, odd row) of this lane's pair of 16-lane rows.
-__device__ __forceinline__ float2 row_pair(float x) {
-  const int v = __builtin_bit_cast(int, x);
-  const auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
-  return make_float2(__builtin_bit_cast(float, (int)p[0]), __builtin_bit_cast(float, (int)p[1]));
-}
-
-
-
-// Sums a (partial over lanes 0-31 and 32-63) and b likewise: lanes 0-31
-// get a's total, lanes 32-63 b's total.
-__device__ __forceinline__ float half_pair_total(float a, float b) {
-  const auto p = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, a),
-                                                  __builtin_bit_cast(int, b), false, false);
-  return __builtin_bit_cast(float, (int)p[0]) + __builtin_bit_cast(float, (int)p[1]);
-}
-
 
 // Device-scope (agent) relaxed atomic accesses for the partition partials:
 // the stores write through to the device coherence point and the loads do
@@ -122,341 +69,14 @@ __device__ __forceinline__ float2 load_dev2(const float* p) {
                      __builtin_bit_cast(float, (uint32_t)(bits >> 32)));
 }
 
-typedef const __attribute__((address_space(4))) int32_t* const_table_t;
-
-// The block table is read-only during the kernel: reading it through the
-// constant address space turns the entries into scalar loads (lgkmcnt),
-// which never wait behind outstanding tile loads (vmcnt).
-__device__ __forceinline__ const_table_t const_table(const AttnArgs& a) {
-  return (const_table_t)a.table;
-}
-
-// ---------------------------------------------------------------------------
-// attn_stream_kernel: decode and short windows (<= kStreamMaxRows rows per
-// wave).  K and V stream from HBM straight into VGPRs in the load layout --
-// lane (slot sl, chunk c) holds features 8c..8c+7 of token j*SL + sl of load
-// j -- software-pipelined across tiles: K of tile i+1 is issued before tile
-// i's logits and V of tile i+1 before tile i's P.V, so each wave keeps a
-// tile of loads in flight while it computes; no LDS holds K or V.
-//  * Q.K: each lane takes dot2 products of its K chunk with the same chunk of
-//    every q row; a transposing butterfly over the CH lanes of a token
-//    leaves each lane the full logits of one (row, token pair);
-//  * softmax: each token slot keeps its own online-softmax state (running
-//    max and sum per row), so a tile needs no cross-slot traffic; the SL
-//    states merge once, when the wave is done;
-//  * P.V: the probability pair of loads 2j', 2j'+1 (fp16x2, broadcast from
-//    its owner lane) dot2-accumulates against the byte-permuted V pairs,
-//    fp32 accumulators.
-// One workgroup of kStreamWaves waves per (partition, KV head, row group),
-// about one workgroup per CU; the partition combine reads every partial in
-// a single round trip.
-// ---------------------------------------------------------------------------
-constexpr int kStreamWaves = 8;
-constexpr int kStreamMaxRows = 4;
-constexpr int kStreamMaxParts = 64;
-
-__device__ __forceinline__ uint32_t pack_h2(float x, float y) {
-  const half2_t h = {(_Float16)x, (_Float16)y};
-  return __builtin_bit_cast(uint32_t, h);
-}
-
-// All-reduce over the token slots (lanes with the same chunk c).
-template <int DPH>
-__device__ __forceinline__ float slot_sum(float x) {
-  if constexpr (DPH == 64) x += dpp_f(x, 3);  // slots 2k, 2k+1 share a 16-lane row
-  const float2 p = row_pair(x);
-  x = p.x + p.y;
-  return half_pair_total(x, x);
-}
-
-template <int DPH>
-__device__ __forceinline__ float slot_max(float x) {
-  if constexpr (DPH == 64) x = fmaxf(x, dpp_f(x, 3));
-  const float2 p = row_pair(x);
-  x = fmaxf(p.x, p.y);
-  const auto q = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, x),
-                                                  __builtin_bit_cast(int, x), false, false);
-  return fmaxf(__builtin_bit_cast(float, (int)q[0]), __builtin_bit_cast(float, (int)q[1]));
-}
-
 __device__ __forceinline__ float4 load_dev4(const float* p) {
   const float2 lo = load_dev2(p);
   const float2 hi = load_dev2(p + 2);
   return make_float4(lo.x, lo.y, hi.x, hi.y);
 }
 
-__device__ __forceinline__ uint4 ld16(const char* p) { return *reinterpret_cast<const uint4*>(p); }
-
-// Physical block and in-block slot of the first token of each load group of
-// tile ts (SL tokens per group, SL divides block_size).  Groups at or past
-// L_max are pinned to token L_max-1 so every address stays on written data.
-template <int NLD, int SL>
-__device__ __forceinline__ void tile_groups(const AttnArgs& a, const_table_t table, int ts,
-                                            int (&blk)[NLD], int (&slot)[NLD]) {
-  if (ts + kTile <= a.L_max) {
-    int lb = ts / a.bs;
-    int s = ts - lb * a.bs;
-#pragma unroll
-    for (int j = 0; j < NLD; j++) {
-      blk[j] = table[lb];
-      slot[j] = s;
-      s += SL;
-      if (s == a.bs) {
-        s = 0;
-        ++lb;
-      }
-    }
-  } else {
-#pragma unroll
-    for (int j = 0; j < NLD; j++) {
-      const int g = min(ts + j * SL, a.L_max - 1);
-      const int lb = g / a.bs;
-      blk[j] = table[lb];
-      slot[j] = g - lb * a.bs;
-    }
-  }
-}
-
-// Issues the K (is_v false) or V loads of tile ts: load j brings token
-// ts + j*SL + sl, 16-byte chunk c (lane_off = sl*row_bytes + 16c from the
-// group's first token).  Lanes whose token is at or past L_max read the
-// group's first token instead (chunk_off = 16c); their logits are masked.
-// Every path issues the same NLD loads, so the compiler's vmcnt bookkeeping
-// stays exact across tiles.
-template <int DPH>
-__device__ __forceinline__ void stream_load(const AttnArgs& a, const char* head_base, int ts,
-                                            int sl, uint32_t lane_off, uint32_t chunk_off,
-                                            bool is_v, const int (&blk)[kTile / (512 / DPH)],
-                                            const int (&slot)[kTile / (512 / DPH)],
-                                            uint4 (&x)[kTile / (512 / DPH)]) {
-  constexpr int SL = 512 / DPH;
-  constexpr int NLD = kTile / SL;
-  const uint32_t row_bytes = 2u * (uint32_t)a.kv_dim;
-  const uint32_t v_bytes = (uint32_t)a.bs * row_bytes;
-  const bool full = ts + kTile <= a.L_max;
-#pragma unroll
-  for (int j = 0; j < NLD; j++) {
-    const char* ub = head_base + (uint64_t)(uint32_t)blk[j] * (2ull * v_bytes) +
-                     (uint32_t)slot[j] * row_bytes + (is_v ? v_bytes : 0u);
-    const uint32_t off = (full || ts + j * SL + sl < a.L_max) ? lane_off : chunk_off;
-    x[j] = ld16(ub + off);
-  }
-  // Compiler barriers: keep the loads here instead of letting them sink to
-  // their first use a tile later, and keep the scheduler from interleaving
-  // neighbouring tiles' work (code-motion fences only; no wait).
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_sched_barrier(0);
-}
-
-// Marks the point where a tile's registers are first consumed: the empty
-// asm redefines them, so no use of the tile (and hence no wait for its
-// loads) is hoisted above this point into the previous tile's work.  SITE
-// makes the asm text differ per call site, so identical pins at the heads of
-// two branches are not merged and hoisted into their common predecessor.
-template <int NLD, int SITE>
-__device__ __forceinline__ void pin_arrival(const uint4 (&x)[NLD]) {
-  uint4(&y)[NLD] = const_cast<uint4(&)[NLD]>(x);
-#pragma unroll
-  for (int j = 0; j < NLD; j++) {
-    if constexpr (SITE == 0) asm volatile("; tile 0" : "+v"(y[j].x), "+v"(y[j].y), "+v"(y[j].z), "+v"(y[j].w));
-    else if constexpr (SITE == 1) asm volatile("; tile 1" : "+v"(y[j].x), "+v"(y[j].y), "+v"(y[j].z), "+v"(y[j].w));
-    else if constexpr (SITE == 2) asm volatile("; tile 2" : "+v"(y[j].x), "+v"(y[j].y), "+v"(y[j].z), "+v"(y[j].w));
-    else asm volatile("; tile 3" : "+v"(y[j].x), "+v"(y[j].y), "+v"(y[j].z), "+v"(y[j].w));
-  }
-}
-
-// Lane roles of attn_stream_kernel.  Load role: lane = (slot sl, chunk c),
-// c = lane % CH.  After the transposing reduction of the logits a lane owns
-// one (row r, token pair jp) of its slot: the NV = RPW*NLD partial logits of
-// a lane are halved once per butterfly step (the lane keeps the half named
-// by one bit of c and adds its partner's copy of that half), so after
-// log2(NV)-1 steps a lane holds the full logits of tokens 2jp and 2jp+1 of
-// row r, and the softmax does per-lane scalar work.
-template <int DPH, int RPW>
-struct StreamShape {
-  static constexpr int CH = DPH / 8;                  // lanes per token
-  static constexpr int S = CH == 16 ? 4 : 3;          // butterfly steps over CH lanes
-  static constexpr int SL = 64 / CH;                  // slots
-  static constexpr int NLD = kTile / SL;              // loads per tile (K and V each)
-  static constexpr int NV = RPW * NLD;                // partial logits per lane
-  static constexpr int T = (NV == 32 ? 5 : NV == 16 ? 4 : NV == 8 ? 3 : 2) - 1;  // halving steps
-  static constexpr int RB = RPW == 4 ? 2 : 1;         // bits of r
-  static_assert(T <= S, "more logits than lanes to spread them over");
-  // chunk index of the lane owning (row r, pair jp) (its redundant bits 0)
-  static constexpr int owner(int r, int jp) { return ((r << (T - RB)) | jp) << (S - T); }
-};
-
-// Butterfly step k over the CH lanes of a token: partner lane = c ^ mask,
-// masks {8, 7, 2, 1} (dph 128) or {7, 2, 1} (dph 64) -- row_ror:8,
-// row_half_mirror, quad_perm [2,3,0,1], quad_perm [1,0,3,2]; step k splits on
-// bit S-1-k of c, which the later masks leave unchanged.
-template <int CH>
-__device__ __forceinline__ float bfly(float x, int k) {
-  const int v = __builtin_bit_cast(int, x);
-  int r;
-  switch (CH == 16 ? k : k + 1) {
-    case 0: r = __builtin_amdgcn_update_dpp(0, v, 0x128, 0xf, 0xf, false); break;
-    case 1: r = __builtin_amdgcn_update_dpp(0, v, 0x141, 0xf, 0xf, false); break;
-    case 2: r = __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xf, 0xf, false); break;
-    default: r = __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xf, 0xf, false); break;
-  }
-  return __builtin_bit_cast(float, r);
-}
-
-// Value of lane n of this lane's 16-lane row (DPP row_newbcast:n).
-__device__ __forceinline__ int row_bcast(int v, int n) {
-  switch (n) {
-    case 0: return __builtin_amdgcn_update_dpp(0, v, 0x150, 0xf, 0xf, false);
-    case 1: return __builtin_amdgcn_update_dpp(0, v, 0x151, 0xf, 0xf, false);
-    case 2: return __builtin_amdgcn_update_dpp(0, v, 0x152, 0xf, 0xf, false);
-    case 3: return __builtin_amdgcn_update_dpp(0, v, 0x153, 0xf, 0xf, false);
-    case 4: return __builtin_amdgcn_update_dpp(0, v, 0x154, 0xf, 0xf, false);
-    case 5: return __builtin_amdgcn_update_dpp(0, v, 0x155, 0xf, 0xf, false);
-    case 6: return __builtin_amdgcn_update_dpp(0, v, 0x156, 0xf, 0xf, false);
-    case 7: return __builtin_amdgcn_update_dpp(0, v, 0x157, 0xf, 0xf, false);
-    case 8: return __builtin_amdgcn_update_dpp(0, v, 0x158, 0xf, 0xf, false);
-    case 9: return __builtin_amdgcn_update_dpp(0, v, 0x159, 0xf, 0xf, false);
-    case 10: return __builtin_amdgcn_update_dpp(0, v, 0x15A, 0xf, 0xf, false);
-    case 11: return __builtin_amdgcn_update_dpp(0, v, 0x15B, 0xf, 0xf, false);
-    case 12: return __builtin_amdgcn_update_dpp(0, v, 0x15C, 0xf, 0xf, false);
-    case 13: return __builtin_amdgcn_update_dpp(0, v, 0x15D, 0xf, 0xf, false);
-    case 14: return __builtin_amdgcn_update_dpp(0, v, 0x15E, 0xf, 0xf, false);
-    default: return __builtin_amdgcn_update_dpp(0, v, 0x15F, 0xf, 0xf, false);
-  }
-}
-
-// Value held by the owner of (row r, pair jp) in this lane's slot.  With
-// dph 64 a 16-lane row holds two slots (lane bit 3 = odd slot).
-template <int DPH, int RPW>
-__device__ __forceinline__ uint32_t from_owner(uint32_t x, int r, int jp, bool odd_slot) {
-  using Sh = StreamShape<DPH, RPW>;
-  const int n = Sh::owner(r, jp);
-  const int v = (int)x;
-  if constexpr (DPH == 128) {
-    return (uint32_t)row_bcast(v, n);
-  } else {
-    const int lo = row_bcast(v, n);
-    const int hi = row_bcast(v, n + 8);
-    return (uint32_t)(odd_slot ? hi : lo);
-  }
-}
-
-template <int DPH, int RPW>
-__device__ __forceinline__ float from_owner_f(float x, int r, int jp, bool odd_slot) {
-  return __builtin_bit_cast(
-      float, from_owner<DPH, RPW>(__builtin_bit_cast(uint32_t, x), r, jp, odd_slot));
-}
-
-// Logits of one tile (transposing reduction) and the online-softmax update
-// of the lane's (row, pair): m_run / l_run are the lane's (row, slot) state
-// (l_run a partial sum over the lane's token pairs).  Returns the rescale
-// factor in al_out and the pair's probabilities as fp16x2 in pk_out.
-template <int DPH, int RPW, int SITE>
-__device__ __forceinline__ void stream_qk(int ts, int sl, int c, int min_lim, int my_lim,
-                                          int my_jp, const uint4 (&qr)[RPW],
-                                          const uint4 (&k)[kTile / (512 / DPH)], float& m_run,
-                                          float& l_run, float& al_out, uint32_t& pk_out) {
-  using Sh = StreamShape<DPH, RPW>;
-  constexpr int CH = Sh::CH, S = Sh::S, SL = Sh::SL, NLD = Sh::NLD, NV = Sh::NV, T = Sh::T;
-  pin_arrival<NLD, SITE>(k);
-  float x[NV];
-#pragma unroll
-  for (int r = 0; r < RPW; r++) {
-    const uint4 q4 = qr[r];
-#pragma unroll
-    for (int j = 0; j < NLD; j++) {
-      float t = dot2(q4.x, k[j].x, 0.f);
-      t = dot2(q4.y, k[j].y, t);
-      t = dot2(q4.z, k[j].z, t);
-      t = dot2(q4.w, k[j].w, t);
-      x[r * NLD + j] = t;
-    }
-  }
-  // Transposing butterfly: step kk keeps the half of x whose top index bit
-  // equals bit S-1-kk of c.
-#pragma unroll
-  for (int kk = 0; kk < T; kk++) {
-    const bool f = (c >> (S - 1 - kk)) & 1;
-    const int h = NV >> (kk + 1);
-#pragma unroll
-    for (int i = 0; i < (NV >> 1); i++) {
-      if (i < h) {
-        const float a = x[i], b = x[i + h];
-        const float send = f ? a : b;
-        const float keep = f ? b : a;
-        x[i] = keep + bfly<CH>(send, kk);
-      }
-    }
-  }
-#pragma unroll
-  for (int kk = T; kk < S; kk++) {
-    x[0] += bfly<CH>(x[0], kk);
-    x[1] += bfly<CH>(x[1], kk);
-  }
-  float s0 = x[0], s1 = x[1];
-  // Causal / length mask: token g is visible to the lane's row iff g <= my_lim.
-  if (ts + kTile - 1 > min_lim) {
-    const int g0 = ts + 2 * my_jp * SL + sl;
-    if (g0 > my_lim) s0 = -INFINITY;
-    if (g0 + SL > my_lim) s1 = -INFINITY;
-  }
-  float tmax = fmaxf(s0, s1);
-#pragma unroll
-  for (int kk = Sh::RB; kk < S; kk++) tmax = fmaxf(tmax, bfly<CH>(tmax, kk));
-  const float m_new = fmaxf(m_run, tmax);
-  // Nothing visible yet: base 0 makes every weight exp2(-inf) = 0.
-  const float base = m_new == -INFINITY ? 0.f : m_new;
-  const float al = __builtin_amdgcn_exp2f(m_run - base);
-  const float p0 = __builtin_amdgcn_exp2f(s0 - base);
-  const float p1 = __builtin_amdgcn_exp2f(s1 - base);
-  l_run = l_run * al + (p0 + p1);
-  m_run = m_new;
-  al_out = al;
-  pk_out = pack_h2(p0, p1);
-  // Finish this tile's logits here, in program order (see pin_arrival).
-  asm volatile("" : "+v"(m_run), "+v"(l_run), "+v"(al_out), "+v"(pk_out));
-}
-
-// P.V of one tile: rescales acc by each row's factor and accumulates the
-// probability pairs (from their owners) against the byte-permuted V pairs.
-template <int DPH, int RPW, int SITE>
-__device__ __forceinline__ void stream_pv(int sl, float al, uint32_t pk,
-                                          const uint4 (&v)[kTile / (512 / DPH)],
-                                          float (&acc)[RPW][8]) {
-  constexpr int NLD = StreamShape<DPH, RPW>::NLD;
-  pin_arrival<NLD, SITE>(v);
-  const bool odd_slot = sl & 1;
-#pragma unroll
-  for (int r = 0; r < RPW; r++) {
-    const float a_r = from_owner_f<DPH, RPW>(al, r, 0, odd_slot);
-#pragma unroll
-    for (int e = 0; e < 8; e++) acc[r][e] *= a_r;
-  }
-#pragma unroll
-  for (int jp = 0; jp < NLD / 2; jp++) {
-    uint32_t pp[RPW];
-#pragma unroll
-    for (int r = 0; r < RPW; r++) pp[r] = from_owner<DPH, RPW>(pk, r, jp, odd_slot);
-    const uint32_t v0[4] = {v[2 * jp].x, v[2 * jp].y, v[2 * jp].z, v[2 * jp].w};
-    const uint32_t v1[4] = {v[2 * jp + 1].x, v[2 * jp + 1].y, v[2 * jp + 1].z, v[2 * jp + 1].w};
-#pragma unroll
-    for (int w = 0; w < 4; w++) {
-      const uint32_t lo = __builtin_amdgcn_perm(v1[w], v0[w], 0x05040100u);
-      const uint32_t hi = __builtin_amdgcn_perm(v1[w], v0[w], 0x07060302u);
-#pragma unroll
-      for (int r = 0; r < RPW; r++) {
-        acc[r][2 * w] = dot2(pp[r], lo, acc[r][2 * w]);
-        acc[r][2 * w + 1] = dot2(pp[r], hi, acc[r][2 * w + 1]);
-      }
-    }
-  }
-  // Finish this tile's P.V here, in program order, so it is not sunk past
-  // the following tiles' work (which would keep its V registers live).
-#pragma unroll
-  for (int r = 0; r < RPW; r++)
-    asm volatile("" : "+v"(acc[r][0]), "+v"(acc[r][1]), "+v"(acc[r][2]), "+v"(acc[r][3]),
-                 "+v"(acc[r][4]), "+v"(acc[r][5]), "+v"(acc[r][6]), "+v"(acc[r][7]));
-}
+constexpr int kStreamWaves = 8;      // waves per workgroup
+constexpr int kStreamMaxParts = 64;  // partitions per (KV head, row group)
 
 // Partition combine of attn_stream_kernel, run by the last workgroup of a
 // (KV head, row group): thread (row r, float4 column c4, quarter sub) loads
@@ -516,8 +136,7 @@ __device__ __forceinline__ void stream_combine(const AttnArgs& a, int kvh, int r
     o.w += dpp_f(o.w, k);
   }
   if (sub == 0) {
-    // attention.h:120-126: normalise unless the sum is tiny or not finite.
-    const float inv = (l > 1e-20f && isfinite(l)) ? 1.f / l : 0.f;
+    const float inv = finish_scale(l);
     const int gr = r0 + r;
     const int m = gr / a.G;
     const int h = kvh * a.G + (gr - m * a.G);
@@ -533,8 +152,6 @@ __global__ __launch_bounds__(64 * kStreamWaves) void attn_stream_kernel(AttnArgs
   static_assert(DPH == 64 || DPH == 128, "head_dim");
   static_assert(RPW == 2 || RPW == 4, "rows per wave");
   constexpr int CH = DPH / 8;
-  constexpr int SL = 64 / CH;
-  constexpr int NLD = kTile / SL;
   constexpr int REC = DPH + 2;
   // Per-wave records (max, sum, acc[DPH]) of every row.
   __shared__ __attribute__((aligned(16))) float s_buf[kStreamWaves * RPW * REC];
@@ -548,25 +165,19 @@ __global__ __launch_bounds__(64 * kStreamWaves) void attn_stream_kernel(AttnArgs
   const int kvh = blockIdx.y;
   const int r0 = blockIdx.z * RPW;
   const int nrows = min(RPW, a.R - r0);
-  const int n_tiles = (a.L_max + kTile - 1) / kTile;
+  const int n_tiles = (a.src.L_max + kTile - 1) / kTile;
   const int tb = part * a.tiles_per_part;
   const int te = min(n_tiles, tb + a.tiles_per_part);
 
   using Sh = StreamShape<DPH, RPW>;
-  // This lane's (row, pair) in the transposed layout, and its redundancy.
-  const int prefix = c >> (Sh::S - Sh::T);
-  const int my_r = prefix >> (Sh::T - Sh::RB);
-  const int my_jp = prefix & ((1 << (Sh::T - Sh::RB)) - 1);
-  const bool redundant = (c & ((1 << (Sh::S - Sh::T)) - 1)) != 0;
+  const int my_r = (c >> (Sh::S - Sh::T)) >> (Sh::T - Sh::RB);
 
   // This lane's q chunk (features 8c..8c+7) of every row, loaded before any
-  // K/V load so that waiting for it never waits for tile data; it is scaled
-  // into the exp2 domain and rounded to fp16 pairs once the first tile's
-  // loads are in flight.
+  // K/V load so that waiting for it never waits for tile data.
   float2 q_raw[RPW][4];
 #pragma unroll
   for (int r = 0; r < RPW; r++) {
-    const int gr = min(r0 + r, a.R - 1);  // rows past nrows: zeroed below
+    const int gr = min(r0 + r, a.R - 1);  // rows past nrows: zeroed by wave_attend
     const int m = gr / a.G;
     const int h = kvh * a.G + (gr - m * a.G);
     const float2* qp = reinterpret_cast<const float2*>(a.q + (size_t)m * a.nh * DPH +
@@ -589,88 +200,19 @@ __global__ __launch_bounds__(64 * kStreamWaves) void attn_stream_kernel(AttnArgs
   for (int r = 0; r < RPW; r++)
 #pragma unroll
     for (int e = 0; e < 8; e++) acc[r][e] = 0.f;
+  // Wave w takes tiles tb+w, tb+w+W, ... of the partition.
+  wave_attend<DPH, RPW, CHUNK>(a.src, kvh, tb + wave, te, kStreamWaves, nrows, min_lim, my_lim,
+                               a.qscale, q_raw, m_run, l_run, acc);
 
-  const const_table_t table = const_table(a);
-  const char* head_base = reinterpret_cast<const char*>(a.pool) + (size_t)kvh * DPH * 2u;
-  const uint32_t lane_off = (uint32_t)sl * 2u * (uint32_t)a.kv_dim + 16u * c;
-  const uint32_t chunk_off = 16u * c;
-  // Wave w takes tiles tb+w, tb+w+W, ... in chunks of CHUNK tiles.  Within
-  // a chunk the code is straight-line (unrolled at compile time): K of tile
-  // i+1 is issued before tile i's logits and V of tile i+1 before tile i's
-  // P.V, so a tile of loads stays in flight while the wave computes, and the
-  // compiler's waits before each use are exact (no loop-carried buffers,
-  // no register copies of in-flight data).  Chunk slots past the wave's
-  // last tile re-read that tile (an L2 hit) and are fully masked.
-  constexpr int W = kStreamWaves;
-  const int first = tb + wave;
-  if (first < te) {
-    const int last = first + ((te - 1 - first) / W) * W;
-    uint4 qr[RPW];
-    for (int c0 = first; c0 < te; c0 += CHUNK * W) {
-      uint4 kbuf[2][NLD], vbuf[2][NLD];
-      int blk[2][NLD], slot[2][NLD];
-      float al;
-      uint32_t pk;
-      tile_groups<NLD, SL>(a, table, min(c0, last) * kTile, blk[0], slot[0]);
-      stream_load<DPH>(a, head_base, min(c0, last) * kTile, sl, lane_off, chunk_off, false,
-                       blk[0], slot[0], kbuf[0]);
-      stream_load<DPH>(a, head_base, min(c0, last) * kTile, sl, lane_off, chunk_off, true,
-                       blk[0], slot[0], vbuf[0]);
-      if (CHUNK > 1)
-        tile_groups<NLD, SL>(a, table, min(c0 + W, last) * kTile, blk[1], slot[1]);
-#pragma unroll
-      for (int i = 0; i < CHUNK; i++) {
-        const int t = c0 + i * W;
-        const int b = i & 1, nb = b ^ 1;
-        const int tn = min(t + W, last);
-        if (i + 1 < CHUNK)
-          stream_load<DPH>(a, head_base, tn * kTile, sl, lane_off, chunk_off, false, blk[nb],
-                           slot[nb], kbuf[nb]);
-        if (i == 0) {
-#pragma unroll
-          for (int r = 0; r < RPW; r++) {
-            const float sc = r < nrows ? a.qscale : 0.f;
-            qr[r] = make_uint4(pack_h2(q_raw[r][0].x * sc, q_raw[r][0].y * sc),
-                               pack_h2(q_raw[r][1].x * sc, q_raw[r][1].y * sc),
-                               pack_h2(q_raw[r][2].x * sc, q_raw[r][2].y * sc),
-                               pack_h2(q_raw[r][3].x * sc, q_raw[r][3].y * sc));
-          }
-        }
-        // A slot past the wave's last tile: every token masked (no-op).
-        const int ts_mask = t <= last ? t * kTile : INT_MAX / 2;
-        stream_qk<DPH, RPW, 0>(ts_mask, sl, c, min_lim, my_lim, my_jp, qr, kbuf[b], m_run, l_run,
-                               al, pk);
-        if (i + 1 < CHUNK) {
-          stream_load<DPH>(a, head_base, tn * kTile, sl, lane_off, chunk_off, true, blk[nb],
-                           slot[nb], vbuf[nb]);
-          if (i + 2 < CHUNK)
-            tile_groups<NLD, SL>(a, table, min(t + 2 * W, last) * kTile, blk[b], slot[b]);
-        }
-        stream_pv<DPH, RPW, 0>(sl, al, pk, vbuf[b], acc);
-      }
-    }
-  }
-
-  // ---- merge the SL slot states of this wave; record per row ------------
-  // l of (row, slot): sum over the row's token-pair owners (redundant lanes
-  // hold copies and contribute 0).
-  float lsum = redundant ? 0.f : l_run;
-#pragma unroll
-  for (int kk = Sh::RB; kk < Sh::S; kk++) lsum += bfly<CH>(lsum, kk);
-  const bool odd_slot = sl & 1;
+  // ---- merge the slot states of this wave; record per row ---------------
+  float mx[RPW], lw[RPW];
+  wave_merge_slots<DPH, RPW>(m_run, l_run, acc, mx, lw);
 #pragma unroll
   for (int r = 0; r < RPW; r++) {
-    const float m_s = from_owner_f<DPH, RPW>(m_run, r, 0, odd_slot);
-    const float l_s = from_owner_f<DPH, RPW>(lsum, r, 0, odd_slot);
-    const float mx = slot_max<DPH>(m_s);
-    const float f = mx == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_s - mx);
-    const float l = slot_sum<DPH>(l_s * f);
-#pragma unroll
-    for (int e = 0; e < 8; e++) acc[r][e] = slot_sum<DPH>(acc[r][e] * f);
     float* rec = s_buf + (wave * RPW + r) * REC;
     if (lane == 0) {
-      rec[0] = mx;
-      rec[1] = l;
+      rec[0] = mx[r];
+      rec[1] = lw[r];
     }
     if (sl == 0) {
       float2* dst = reinterpret_cast<float2*>(rec + 2 + 8 * c);
@@ -702,8 +244,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void attn_stream_kernel(AttnArgs
     }
     const int gr = r0 + r;
     if (a.n_parts == 1) {
-      // attention.h:120-126: normalise unless the sum is tiny or not finite.
-      const float inv = (l > 1e-20f && isfinite(l)) ? 1.f / l : 0.f;
+      const float inv = finish_scale(l);
       const int m = gr / a.G;
       const int h = kvh * a.G + (gr - m * a.G);
       *reinterpret_cast<float2*>(a.out + (size_t)m * a.nh * DPH + (size_t)h * DPH + dcol) =
@@ -876,19 +417,19 @@ int sde_paged_attention(sde_kv_cache* cache, int layer, const float* d_q,
   }
 
   AttnArgs a;
-  a.pool = cache->pool;
-  a.table = sde::layer_table(cache, layer);
+  a.src.pool = cache->pool;
+  a.src.table = sde::layer_table(cache, layer);
+  a.src.kv_dim = cache->cfg.kv_dim;
+  a.src.bs = cache->cfg.block_size;
+  a.src.L_max = L_max;
   a.q = d_q;
   a.out = d_out;
   a.partials = partials;
   a.counters = cache->d_counters;
-  a.kv_dim = cache->cfg.kv_dim;
-  a.bs = cache->cfg.block_size;
   a.nh = nh;
   a.G = G;
   a.R = R;
   a.pos_base = pos_base;
-  a.L_max = L_max;
   a.n_parts = plan.n_parts;
   a.tiles_per_part = plan.tiles_per_part;
   a.qscale = (float)(kLog2e / std::sqrt((double)dph));

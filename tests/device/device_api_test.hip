@@ -1,0 +1,97 @@
+// Test kernels for the device-side API of include/sde/attention_device.hpp
+// (test infrastructure, built beside libsde_paged by its build script): each
+// wraps one reference-named device function in a kernel the way an
+// in-kernel caller (a persistent decode loop) would use it, behind a plain
+// C launcher that tests/test_gpu_device_api.py calls through ctypes.
+#include <hip/hip_runtime.h>
+
+#include "sde/attention_device.hpp"
+#include "sde/kv_cache.hpp"
+
+namespace {
+
+// One block per query, like cublas_attention_kernel (kernels.cu:904-940):
+// query m sees positions [0, pos_base + m].
+__global__ void attention_kernel(sde_kv_view kv, int layer, const float* q, float* out, int nh,
+                                 int nkv, int dph, int pos_base, int attn_type, int* status) {
+  const int m = blockIdx.x;
+  const size_t d = (size_t)nh * dph;
+  const int st = sde::device_attention_dispatch(attn_type, q + m * d, out + m * d, kv, layer, nh,
+                                                nkv, dph, pos_base + m + 1);
+  if (threadIdx.x == 0) status[m] = st;
+}
+
+// One block per appended token (cublas_kv_append_kernel, kernels.cu:826-844).
+__global__ void append_kernel(sde_kv_view kv, int layer, const float* k, const float* v,
+                              int pos_base) {
+  const int m = blockIdx.x;
+  sde::kv_cache_append(kv, layer, k + (size_t)m * kv.kv_dim, v + (size_t)m * kv.kv_dim,
+                       pos_base + m);
+}
+
+__global__ void read_kernel(sde_kv_view kv, int layer, int pos, float* k, float* v) {
+  const int m = blockIdx.x;
+  sde::kv_cache_read(kv, layer, pos + m, k + (size_t)m * kv.kv_dim, v + (size_t)m * kv.kv_dim);
+}
+
+__global__ void rollback_kernel(sde_kv_view kv, int target) { sde::kv_cache_rollback(kv, target); }
+
+int status_of(hipError_t e) { return e == hipSuccess ? 0 : 6; }
+
+}  // namespace
+
+extern "C" {
+
+int sdet_attention(const sde_kv_view* kv, int layer, const float* q, float* out, int nh, int nkv,
+                   int dph, int pos_base, int n_queries, int threads, int attn_type, int* status,
+                   void* stream) {
+  if (!kv || threads < 64 || threads % 64 != 0 || threads > 1024 || n_queries < 1) return 1;
+  attention_kernel<<<n_queries, threads, 0, (hipStream_t)stream>>>(*kv, layer, q, out, nh, nkv, dph,
+                                                                   pos_base, attn_type, status);
+  return status_of(hipGetLastError());
+}
+
+int sdet_append(const sde_kv_view* kv, int layer, const float* k, const float* v, int pos_base,
+                int n, int threads, void* stream) {
+  if (!kv || threads < 64 || threads > 1024 || n < 1) return 1;
+  append_kernel<<<n, threads, 0, (hipStream_t)stream>>>(*kv, layer, k, v, pos_base);
+  return status_of(hipGetLastError());
+}
+
+int sdet_read(const sde_kv_view* kv, int layer, int pos, int n, float* k, float* v, int threads,
+              void* stream) {
+  if (!kv || threads < 64 || threads > 1024 || n < 1) return 1;
+  read_kernel<<<n, threads, 0, (hipStream_t)stream>>>(*kv, layer, pos, k, v);
+  return status_of(hipGetLastError());
+}
+
+// The C++ host names of sde/kv_cache.hpp end to end on a fresh cache:
+// alloc, tables, append M rows at pos_base, set_seq_len, attention of the
+// n_q-query window at q_base, rollback to `rollback_to`; copies the pool to
+// pool_out and the device seq_len to *seq_len_out, then frees the cache.
+int sdet_cpp_pipeline(int n_layers, int kv_dim, int max_blocks, int block_size, int pool_blocks,
+                      const int32_t* tables, int layer, const float* k, const float* v,
+                      int pos_base, int M, const float* q, float* out, int nh, int nkv, int dph,
+                      int q_base, int n_q, int rollback_to, void* pool_out, int* seq_len_out) {
+  sde::KVCache kv;
+  sde::kv_cache_alloc(kv, n_layers, kv_dim, max_blocks, block_size, pool_blocks);
+  for (int l = 0; l < n_layers; l++)
+    sde::kv_cache_set_block_table(kv, l, tables + (size_t)l * max_blocks, max_blocks);
+  sde::cublas_kv_append_kernel(kv, layer, k, v, kv_dim, pos_base, M);
+  sde::set_seq_len_kernel(kv, pos_base + M);
+  sde::cublas_attention_kernel(q, out, kv, layer, nh, nkv, dph, kv_dim, q_base, n_q);
+  sde::kv_cache_rollback(kv, rollback_to);
+  const size_t pool_bytes = (size_t)pool_blocks * 2u * block_size * kv_dim * 2u;
+  hipError_t e = hipMemcpy(pool_out, kv.view.pool, pool_bytes, hipMemcpyDeviceToDevice);
+  if (e == hipSuccess) e = hipMemcpy(seq_len_out, kv.view.seq_len, sizeof(int), hipMemcpyDeviceToHost);
+  sde::kv_cache_free(kv);
+  return status_of(e);
+}
+
+int sdet_rollback(const sde_kv_view* kv, int target, void* stream) {
+  if (!kv) return 1;
+  rollback_kernel<<<1, 64, 0, (hipStream_t)stream>>>(*kv, target);
+  return status_of(hipGetLastError());
+}
+
+}  // extern "C"

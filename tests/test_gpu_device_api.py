@@ -1,0 +1,217 @@
+"""GPU parity of the device-side API (include/sde/attention_device.hpp):
+kv_cache_append / kv_cache_read / kv_cache_rollback and
+device_flash_attention_gqa / device_attention_dispatch called from inside a
+caller's kernel (tests/device/device_api_test.hip), the way the reference's
+persistent decode loop calls them (kv_cache.h:70-79, attention.h:21-164).
+
+Append and read are checked bit-exact against the C-ABI path and the oracle
+byte model; attention against the oracle's fp64 attention with the same
+tolerance as the host entry point (2e-3 abs + 1e-2 rel).
+"""
+import ctypes
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import case_banner
+from speculative_decode_engine_amd import KVCache
+from speculative_decode_engine_amd import _native as N
+from speculative_decode_engine_amd import workloads as W
+from test_gpu_attention import assert_close, build_layer
+
+pytestmark = pytest.mark.gpu
+LIB = Path(__file__).resolve().parent / "device" / "libsde_device_test.so"
+
+
+@pytest.fixture(scope="module")
+def dev(gpu):
+    if not LIB.exists():
+        pytest.fail(f"{LIB} missing: run __graft_entry__.build()")
+    lib = ctypes.CDLL(str(LIB))
+    vp, i = ctypes.c_void_p, ctypes.c_int
+    view_p = ctypes.POINTER(N.KVView)
+    lib.sdet_attention.argtypes = [view_p, i, vp, vp, i, i, i, i, i, i, i, vp, vp]
+    lib.sdet_append.argtypes = [view_p, i, vp, vp, i, i, i, vp]
+    lib.sdet_read.argtypes = [view_p, i, i, i, vp, vp, i, vp]
+    lib.sdet_rollback.argtypes = [view_p, i, vp]
+    for f in (lib.sdet_attention, lib.sdet_append, lib.sdet_read, lib.sdet_rollback):
+        f.restype = i
+    return lib
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def device_attention(dev, cache, q, nh, nkv, dph, pos_base, threads=256, attn_type=0):
+    M = q.shape[0]
+    out = torch.full((M, nh * dph), float("nan"), device="cuda")
+    status = torch.full((M,), -1, dtype=torch.int32, device="cuda")
+    view = cache.view()
+    rc = dev.sdet_attention(ctypes.byref(view), 0, q.data_ptr(), out.data_ptr(), nh, nkv, dph,
+                            pos_base, M, threads, attn_type, status.data_ptr(), _stream())
+    assert rc == 0
+    torch.cuda.synchronize()
+    return out, status.cpu().numpy()
+
+
+@pytest.mark.parametrize("nh,nkv,dph,bs,ctx,M", [
+    (4, 2, 64, 16, 128, 1),       # config 1 shape
+    (32, 4, 64, 16, 2048, 1),     # TinyLlama: G = 8 -> two row groups per KV head
+    (32, 8, 128, 16, 4096, 5),    # Llama-3-8B verify window
+    (28, 4, 128, 32, 1000, 9),    # Qwen2.5-7B (G = 7), block size 32
+    (8, 8, 128, 8, 77, 2),        # MHA, block size 8, ragged last tile
+])
+def test_device_attention_matches_oracle(dev, oracle, nh, nkv, dph, bs, ctx, M):
+    case_banner("device attention", nh, nkv, dph, bs, ctx, M)
+    nblk = -(-(ctx + M) // bs)
+    cache, K, V, rng = build_layer(nh, nkv, dph, bs, ctx, M, nblk + 40, nh + ctx)
+    q = W.queries(rng, M, nh, dph)
+    qd = torch.from_numpy(q).cuda()
+    out, status = device_attention(dev, cache, qd, nh, nkv, dph, ctx)
+    assert (status == 0).all()
+    ref = oracle.attention_f64_np(q, K, V, nh, nkv, dph, ctx)
+    assert_close(out.cpu().numpy(), ref, "device_flash_attention_gqa")
+    host = cache.attention(0, qd, nh, nkv, dph, ctx)
+    torch.cuda.synchronize()
+    assert_close(out.cpu().numpy(), host.cpu().numpy().astype(np.float64), "device vs host entry")
+    cache.free()
+
+
+@pytest.mark.parametrize("threads", [64, 192, 512, 1024])
+def test_device_attention_any_block_size(dev, oracle, threads):
+    case_banner("device attention threads", threads)
+    nh, nkv, dph, ctx = 32, 8, 128, 700
+    cache, K, V, rng = build_layer(nh, nkv, dph, 16, ctx, 1, 80, threads)
+    q = W.queries(rng, 1, nh, dph)
+    out, status = device_attention(dev, cache, torch.from_numpy(q).cuda(), nh, nkv, dph, ctx,
+                                   threads=threads)
+    assert (status == 0).all()
+    assert_close(out.cpu().numpy(), oracle.attention_f64_np(q, K, V, nh, nkv, dph, ctx), "threads")
+    cache.free()
+
+
+def test_device_attention_empty_context_gives_zeros(dev):
+    case_banner("device attention total_len 0")
+    nh, nkv, dph = 8, 2, 64
+    cache = KVCache(1, nkv * dph, 4, 16, 8)
+    q = torch.randn(1, nh * dph, device="cuda")
+    # pos_base -1: query 0 sees positions [0, 0) -- attention.h:120-126 -> zeros
+    out, status = device_attention(dev, cache, q, nh, nkv, dph, -1)
+    assert (status == 0).all()
+    assert torch.count_nonzero(out).item() == 0
+    cache.free()
+
+
+def test_device_dispatch_rejects_reserved_types(dev):
+    case_banner("device dispatch reserved types")
+    nh, nkv, dph = 8, 2, 64
+    cache = KVCache(1, nkv * dph, 4, 16, 8)
+    q = torch.randn(1, nh * dph, device="cuda")
+    for t in (N.SDE_ATTN_SLIDING_WINDOW, N.SDE_ATTN_KDA, N.SDE_ATTN_LINEAR):
+        out, status = device_attention(dev, cache, q, nh, nkv, dph, 10, attn_type=t)
+        assert (status == N.SDE_ERR_UNSUPPORTED).all()
+        assert torch.isnan(out).all()  # nothing written
+    cache.free()
+
+
+@pytest.mark.parametrize("kv_dim,bs,n", [(128, 16, 37), (1024, 16, 9), (512, 32, 70), (96, 8, 5)])
+def test_device_append_and_read_bit_exact(dev, oracle, kv_dim, bs, n):
+    case_banner("device append/read", kv_dim, bs, n)
+    rng = np.random.default_rng(kv_dim + n)
+    nblk = -(-(n + 3) // bs)
+    pool_blocks = 2 * nblk + 3
+    tables = W.make_tables(rng, 2, nblk, pool_blocks)
+    host = KVCache(2, kv_dim, nblk, bs, pool_blocks)
+    devc = KVCache(2, kv_dim, nblk, bs, pool_blocks)
+    for l in range(2):
+        host.set_block_table(l, tables[l])
+        devc.set_block_table(l, tables[l])
+    k, v = W.new_kv(rng, n, kv_dim)
+    k[0, :4] = [65519.0, 65520.0, 1e-8, -0.0]          # overflow boundary, underflow, -0
+    kd, vd = torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda()
+    host.append(1, kd, vd, 3)
+    view = devc.view()
+    assert dev.sdet_append(ctypes.byref(view), 1, kd.data_ptr(), vd.data_ptr(), 3, n, 128,
+                           _stream()) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(devc.pool, host.pool)          # same bytes as the C-ABI append
+    m = oracle.PagedKVModel(2, kv_dim, nblk, bs, pool_blocks)
+    for l in range(2):
+        m.set_block_table(l, tables[l])
+    m.append(1, k, v, 3)
+    assert np.array_equal(devc.pool.cpu().numpy().view(np.uint16).reshape(m.pool.shape), m.pool)
+    ko = torch.empty(n, kv_dim, device="cuda")
+    vo = torch.empty(n, kv_dim, device="cuda")
+    assert dev.sdet_read(ctypes.byref(view), 1, 3, n, ko.data_ptr(), vo.data_ptr(), 256,
+                         _stream()) == 0
+    gk, gv = host.read(1, 3, n)
+    torch.cuda.synchronize()
+    assert torch.equal(ko, gk) and torch.equal(vo, gv)
+    host.free()
+    devc.free()
+
+
+def test_device_rollback_writes_seq_len_only(dev):
+    case_banner("device rollback")
+    cache = KVCache(1, 128, 8, 16, 8)
+    cache.set_seq_len(100)
+    before = cache.pool.clone()
+    view = cache.view()
+    assert dev.sdet_rollback(ctypes.byref(view), 61, _stream()) == 0
+    torch.cuda.synchronize()
+    assert cache.device_seq_len() == 61
+    assert torch.equal(cache.pool, before)
+    cache.free()
+
+
+def test_cpp_host_names_match_the_c_abi(dev, oracle):
+    """sde/kv_cache.hpp (kv_cache_alloc, cublas_kv_append_kernel,
+    cublas_attention_kernel, set_seq_len_kernel, kv_cache_rollback) run end to
+    end in C++ give the same pool bytes, outputs and seq_len as the same
+    steps through the Python binding of the C-ABI."""
+    case_banner("C++ host names")
+    nl, nh, nkv, dph, bs, ctx, M = 2, 32, 8, 128, 16, 300, 5
+    kv_dim = nkv * dph
+    nblk = -(-(ctx + M) // bs)
+    pool_blocks = nl * nblk + 7
+    rng = np.random.default_rng(77)
+    tables = W.make_tables(rng, nl, nblk, pool_blocks).astype(np.int32)
+    k, v = W.new_kv(rng, ctx + M, kv_dim)
+    q = W.queries(rng, M, nh, dph)
+    kd, vd, qd = (torch.from_numpy(x).cuda() for x in (k, v, q))
+    # C++: append all ctx+M rows at 0, window of M queries at ctx, rewind to ctx+2
+    pool_out = torch.empty(pool_blocks * 2 * bs * kv_dim, dtype=torch.int16, device="cuda")
+    out_cpp = torch.empty(M, nh * dph, device="cuda")
+    seq = ctypes.c_int(-1)
+    f = dev.sdet_cpp_pipeline
+    f.restype = ctypes.c_int
+    rc = f(nl, kv_dim, nblk, bs, pool_blocks, tables.ctypes.data_as(ctypes.c_void_p), 1,
+           ctypes.c_void_p(kd.data_ptr()), ctypes.c_void_p(vd.data_ptr()), 0, ctx + M,
+           ctypes.c_void_p(qd.data_ptr()), ctypes.c_void_p(out_cpp.data_ptr()), nh, nkv, dph,
+           ctx, M, ctx + 2, ctypes.c_void_p(pool_out.data_ptr()), ctypes.byref(seq))
+    assert rc == 0
+    torch.cuda.synchronize()
+    # the same through the Python binding
+    cache = KVCache(nl, kv_dim, nblk, bs, pool_blocks, pool="library")
+    for l in range(nl):
+        cache.set_block_table(l, tables[l])
+    cache.append(1, kd, vd, 0)
+    cache.set_seq_len(ctx + M)
+    out_py = cache.attention(1, qd, nh, nkv, dph, ctx)
+    cache.rollback(ctx + 2)
+    torch.cuda.synchronize()
+    assert seq.value == ctx + 2 == cache.device_seq_len()
+    assert torch.equal(out_cpp, out_py)
+    gk, gv = cache.read(1, 0, ctx + M)
+    torch.cuda.synchronize()
+    assert np.array_equal(gk.cpu().numpy(), k.astype(np.float16).astype(np.float32))
+    pool_cpp = pool_out.cpu().numpy().view(np.uint16).reshape(pool_blocks, 2, bs, kv_dim)
+    m = oracle.PagedKVModel(nl, kv_dim, nblk, bs, pool_blocks)
+    for l in range(nl):
+        m.set_block_table(l, tables[l])
+    m.append(1, k, v, 0)
+    assert np.array_equal(pool_cpp, m.pool)           # C++ append: oracle bytes
+    cache.free()
