@@ -50,6 +50,15 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
                                 __builtin_bit_cast(half2_t, b), c, false);
 }
 
+// dot2(a, b, 0) as one VOP3P instruction with an inline-constant addend (the
+// builtin with a 0 addend becomes a register move plus the accumulating
+// VOP2 form).
+__device__ __forceinline__ float dot2_0(uint32_t a, uint32_t b) {
+  float r;
+  asm("v_dot2_f32_f16 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+
 // Cross-lane moves (gfx950 lane semantics):
 //  * DPP quad_perm [1,0,3,2] / [2,3,0,1] exchange lanes i^1 / i^2, and
 //    row_ror:4 / row_ror:8 rotate each 16-lane row, so four steps reduce
@@ -302,7 +311,7 @@ __device__ __forceinline__ void stream_qk(int ts, int sl, int c, int min_lim, in
     const uint4 q4 = qr[r];
 #pragma unroll
     for (int j = 0; j < NLD; j++) {
-      float t = dot2(q4.x, k[j].x, 0.f);
+      float t = dot2_0(q4.x, k[j].x);
       t = dot2(q4.y, k[j].y, t);
       t = dot2(q4.z, k[j].z, t);
       t = dot2(q4.w, k[j].w, t);

@@ -286,35 +286,34 @@ using namespace sde::attn;
 struct Plan {
   int rpw;             // rows per wave (2 or kStreamMaxRows)
   int row_groups;
-  int chunk;           // tiles per unrolled chunk (1, 2 or 4)
+  int chunk;           // tiles per unrolled chunk (1 to 4)
   int tiles_per_part;  // tiles per partition (workgroup)
   int n_parts;
 };
 
 int rows_per_wave(int R) { return R <= 2 ? 2 : kStreamMaxRows; }
 
-// Each wave takes its tiles in chunks of `chunk` (1, 2 or 4, a compile-time
-// unroll).  The largest chunk that still gives at least one workgroup per CU
-// is used; past kStreamMaxParts partitions per (KV head, row group) the
-// waves take several chunks.
+// Sizing: at most one workgroup per CU (a second round of workgroups would
+// double the latency of a latency-bound call), as many partitions as that
+// allows (up to kStreamMaxParts, at least one tile per wave), then the
+// fewest tiles per wave that cover the context.  A wave takes its tiles in
+// chunks of `chunk` (1 to 4, unrolled at compile time), several chunks
+// when it has more than four tiles.
 Plan make_plan(int L_max, int nkv, int R, int n_cus) {
   Plan p;
   p.rpw = rows_per_wave(R);
   p.row_groups = (R + p.rpw - 1) / p.rpw;
   const int n_tiles = (L_max + kTile - 1) / kTile;
   const int64_t units = (int64_t)nkv * p.row_groups;
-  p.chunk = 1;
-  for (int ch : {4, 2}) {
-    const int per = kStreamWaves * ch;
-    if ((int64_t)((n_tiles + per - 1) / per) * units >= n_cus) {
-      p.chunk = ch;
-      break;
-    }
-  }
-  const int per_chunk = kStreamWaves * p.chunk;
-  const int chunks = (n_tiles + per_chunk - 1) / per_chunk;
-  const int reps = (chunks + kStreamMaxParts - 1) / kStreamMaxParts;
-  p.tiles_per_part = per_chunk * reps;
+  int64_t parts = n_cus / units;
+  if (parts < 1) parts = 1;
+  if (parts > kStreamMaxParts) parts = kStreamMaxParts;
+  const int64_t by_len = (n_tiles + kStreamWaves - 1) / kStreamWaves;
+  if (parts > by_len) parts = by_len;
+  const int per_wave = (int)((n_tiles + parts * kStreamWaves - 1) / (parts * kStreamWaves));
+  p.chunk = per_wave <= 3 ? per_wave : 4;
+  const int reps = (per_wave + p.chunk - 1) / p.chunk;
+  p.tiles_per_part = kStreamWaves * p.chunk * reps;
   p.n_parts = (n_tiles + p.tiles_per_part - 1) / p.tiles_per_part;
   return p;
 }
@@ -343,9 +342,11 @@ int launch(const Plan& p, const AttnArgs& a, int nkv, hipStream_t s) {
   }
   SDE_STREAM(2, 1)
   SDE_STREAM(2, 2)
+  SDE_STREAM(2, 3)
   SDE_STREAM(2, 4)
   SDE_STREAM(4, 1)
   SDE_STREAM(4, 2)
+  SDE_STREAM(4, 3)
   SDE_STREAM(4, 4)
 #undef SDE_STREAM
   return SDE_ERR_UNSUPPORTED;
