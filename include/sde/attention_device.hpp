@@ -517,6 +517,301 @@ __device__ __forceinline__ float finish_scale(float l) {
   return (l > 1e-20f && isfinite(l)) ? 1.f / l : 0.f;
 }
 
+// ---- split-context partitions (libsde_paged's kernel and the grid API) ----
+
+// One split-context attention call: rows of KV head kvh are its
+// (query m, head-in-group g) pairs r = m*G + g; row groups of RPW rows; the
+// context [0, L_max) is cut into n_parts partitions of tiles_per_part tiles.
+struct AttnArgs {
+  TileSource src;        // pool, this layer's table, kv_dim, block_size, L_max
+  const float* q;        // [M][nh*dph]
+  float* out;            // [M][nh*dph]
+  float* partials;       // [nkv][R][n_parts][2] (max, sum), then [nkv][R][n_parts][dph] acc
+  uint32_t* counters;    // [nkv][row_groups] arrival counters, zero at rest
+  int nh;
+  int nkv;
+  int G;           // query heads per KV head
+  int R;           // rows per KV head = M * G
+  int row_groups;  // ceil(R / rows per wave)
+  int pos_base;    // query m sees positions [0, pos_base+m]
+  int n_parts;
+  int tiles_per_part;
+  float qscale;    // log2(e) / sqrt(dph)
+};
+
+constexpr int kStreamWaves = 8;      // waves per workgroup of libsde_paged's kernel
+constexpr int kStreamMaxParts = 64;  // partitions per (KV head, row group)
+
+// Device-scope (agent) relaxed atomic accesses for the partition partials:
+// the stores write through to the device coherence point and the loads do
+// not hit stale lines of another XCD's L2, so publishing partials needs no
+// L2 writeback/invalidate fence (those cost microseconds per workgroup).
+__device__ __forceinline__ void store_dev2(float* p, float x, float y) {
+  const uint64_t bits = (uint64_t)__builtin_bit_cast(uint32_t, x) |
+                        ((uint64_t)__builtin_bit_cast(uint32_t, y) << 32);
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), bits, __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ float2 load_dev2(const float* p) {
+  const uint64_t bits = __hip_atomic_load(reinterpret_cast<uint64_t*>(const_cast<float*>(p)),
+                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return make_float2(__builtin_bit_cast(float, (uint32_t)bits),
+                     __builtin_bit_cast(float, (uint32_t)(bits >> 32)));
+}
+
+__device__ __forceinline__ float4 load_dev4(const float* p) {
+  const float2 lo = load_dev2(p);
+  const float2 hi = load_dev2(p + 2);
+  return make_float4(lo.x, lo.y, hi.x, hi.y);
+}
+
+// Partition combine, run by the last workgroup of a (KV head, row group) to
+// finish: thread (row r, float4 column c4, quarter sub) loads (max, sum,
+// acc[c4]) of partitions sub, sub+4, ... -- every partial in one round trip,
+// no LDS -- weights them by exp2(m_p - max) and the four quarters of a (row,
+// column) (adjacent lanes) reduce through DPP in a fixed order, so the
+// result does not depend on arrival order.  Workgroups of fewer than
+// RPW*DPH threads take the (row, column, quarter) triples in turns.
+template <int DPH, int RPW, int WAVES>
+__device__ __forceinline__ void stream_combine(const AttnArgs& a, int kvh, int r0, int nrows) {
+  constexpr int C4 = DPH / 4;
+  constexpr int SUB = 4;
+  constexpr int PMAX = kStreamMaxParts / SUB;
+  const int P = a.n_parts;
+  if ((int)threadIdx.x >= 64 * WAVES) return;  // waves past WAVES idle
+  for (int tid = threadIdx.x; tid < RPW * C4 * SUB; tid += 64 * WAVES) {
+    const int sub = tid & (SUB - 1);
+    const int col4 = (tid / SUB) % C4;
+    const int r = tid / (SUB * C4);  // uniform per wave
+    if (r >= nrows) break;
+    const size_t row = (size_t)kvh * a.R + r0 + r;
+    const float* ml = a.partials + row * P * 2;
+    const float* accp = a.partials + (size_t)a.nkv * a.R * P * 2 + row * P * DPH + 4 * col4;
+    float2 e[PMAX];
+    float4 v[PMAX];
+#pragma unroll
+    for (int i = 0; i < PMAX; i++) {
+      const int p = sub + i * SUB;
+      e[i] = make_float2(-INFINITY, 0.f);
+      v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (p < P) {
+        e[i] = load_dev2(ml + (size_t)p * 2);
+        v[i] = load_dev4(accp + (size_t)p * DPH);
+      }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < PMAX; i++) mx = fmaxf(mx, e[i].x);
+    mx = fmaxf(mx, dpp_f(mx, 0));
+    mx = fmaxf(mx, dpp_f(mx, 1));
+    float l = 0.f;
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int i = 0; i < PMAX; i++) {
+      const float w = e[i].x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(e[i].x - mx);
+      l += e[i].y * w;
+      o.x += w * v[i].x;
+      o.y += w * v[i].y;
+      o.z += w * v[i].z;
+      o.w += w * v[i].w;
+    }
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+      l += dpp_f(l, k);
+      o.x += dpp_f(o.x, k);
+      o.y += dpp_f(o.y, k);
+      o.z += dpp_f(o.z, k);
+      o.w += dpp_f(o.w, k);
+    }
+    if (sub == 0) {
+      const float inv = finish_scale(l);
+      const int gr = r0 + r;
+      const int m = gr / a.G;
+      const int h = kvh * a.G + (gr - m * a.G);
+      float2* dst = reinterpret_cast<float2*>(a.out + (size_t)m * a.nh * DPH + (size_t)h * DPH +
+                                              4 * col4);
+      dst[0] = make_float2(o.x * inv, o.y * inv);
+      dst[1] = make_float2(o.z * inv, o.w * inv);
+    }
+  }
+}
+
+// LDS of stream_item: per-wave records (max, sum, acc[DPH]) of every row.
+template <int DPH, int RPW, int WAVES>
+struct StreamLds {
+  float buf[WAVES * RPW * (DPH + 2)] __attribute__((aligned(16)));
+  int last;
+};
+
+// Partition `part` of (KV head kvh, row group rg) on the calling workgroup:
+// waves 0..WAVES-1 take tiles tb+w, tb+w+WAVES, ... (further waves idle),
+// merge their states through LDS, and either write the normalised output
+// (one partition) or publish a partial and count the arrival; the last
+// arrival combines all partitions.  Every thread of the workgroup calls it.
+template <int DPH, int RPW, int CHUNK, int WAVES>
+__device__ __forceinline__ void stream_item(const AttnArgs& a, int part, int kvh, int rg,
+                                            StreamLds<DPH, RPW, WAVES>& lds) {
+  static_assert(DPH == 64 || DPH == 128, "head_dim");
+  static_assert(RPW == 2 || RPW == 4, "rows per wave");
+  static_assert(RPW * (DPH / 2) <= 64 * WAVES, "one merge thread per (row, feature pair)");
+  constexpr int CH = DPH / 8;
+  constexpr int REC = DPH + 2;
+  float* s_buf = lds.buf;
+
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int sl = lane / CH;
+  const int c = lane % CH;
+  const int r0 = rg * RPW;
+  const int nrows = min(RPW, a.R - r0);
+  const int n_tiles = (a.src.L_max + kTile - 1) / kTile;
+  const int tb = part * a.tiles_per_part;
+  const int te = min(n_tiles, tb + a.tiles_per_part);
+
+  using Sh = StreamShape<DPH, RPW>;
+  const int my_r = (c >> (Sh::S - Sh::T)) >> (Sh::T - Sh::RB);
+
+  if (wave < WAVES) {
+    // This lane's q chunk (features 8c..8c+7) of every row, loaded before
+    // any K/V load so that waiting for it never waits for tile data.
+    float2 q_raw[RPW][4];
+#pragma unroll
+    for (int r = 0; r < RPW; r++) {
+      const int gr = min(r0 + r, a.R - 1);  // rows past nrows: zeroed by wave_attend
+      const int m = gr / a.G;
+      const int h = kvh * a.G + (gr - m * a.G);
+      const float2* qp = reinterpret_cast<const float2*>(a.q + (size_t)m * a.nh * DPH +
+                                                         (size_t)h * DPH + 8 * c);
+#pragma unroll
+      for (int w = 0; w < 4; w++) q_raw[r][w] = qp[w];
+    }
+    // Last visible position of each row (query m sees pos_base + m); rows
+    // past nrows see nothing.
+    int min_lim = INT_MAX, my_lim = -1;
+#pragma unroll
+    for (int r = 0; r < RPW; r++) {
+      const int lim = r < nrows ? a.pos_base + (r0 + r) / a.G : -1;
+      min_lim = min(min_lim, lim);
+      if (r == my_r) my_lim = lim;
+    }
+
+    float m_run = -INFINITY, l_run = 0.f, acc[RPW][8];
+#pragma unroll
+    for (int r = 0; r < RPW; r++)
+#pragma unroll
+      for (int e = 0; e < 8; e++) acc[r][e] = 0.f;
+    wave_attend<DPH, RPW, CHUNK>(a.src, kvh, tb + wave, te, WAVES, nrows, min_lim, my_lim,
+                                 a.qscale, q_raw, m_run, l_run, acc);
+
+    // ---- merge the slot states of this wave; record per row -------------
+    float mx[RPW], lw[RPW];
+    wave_merge_slots<DPH, RPW>(m_run, l_run, acc, mx, lw);
+#pragma unroll
+    for (int r = 0; r < RPW; r++) {
+      float* rec = s_buf + (wave * RPW + r) * REC;
+      if (lane == 0) {
+        rec[0] = mx[r];
+        rec[1] = lw[r];
+      }
+      if (sl == 0) {
+        float2* dst = reinterpret_cast<float2*>(rec + 2 + 8 * c);
+        dst[0] = make_float2(acc[r][0], acc[r][1]);
+        dst[1] = make_float2(acc[r][2], acc[r][3]);
+        dst[2] = make_float2(acc[r][4], acc[r][5]);
+        dst[3] = make_float2(acc[r][6], acc[r][7]);
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- workgroup merge: thread (row, feature pair) over the waves --------
+  constexpr int DP = DPH / 2;
+  if ((int)threadIdx.x < nrows * DP) {
+    const int r = threadIdx.x / DP;
+    const int dcol = 2 * (threadIdx.x - r * DP);
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < WAVES; w++) mx = fmaxf(mx, s_buf[(w * RPW + r) * REC]);
+    float l = 0.f, o0 = 0.f, o1 = 0.f;
+#pragma unroll
+    for (int w = 0; w < WAVES; w++) {
+      const float* rec = s_buf + (w * RPW + r) * REC;
+      const float wt = rec[0] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(rec[0] - mx);
+      l += rec[1] * wt;
+      const float2 x = *reinterpret_cast<const float2*>(rec + 2 + dcol);
+      o0 += x.x * wt;
+      o1 += x.y * wt;
+    }
+    const int gr = r0 + r;
+    if (a.n_parts == 1) {
+      const float inv = finish_scale(l);
+      const int m = gr / a.G;
+      const int h = kvh * a.G + (gr - m * a.G);
+      *reinterpret_cast<float2*>(a.out + (size_t)m * a.nh * DPH + (size_t)h * DPH + dcol) =
+          make_float2(o0 * inv, o1 * inv);
+    } else {
+      const size_t pr = ((size_t)kvh * a.R + gr) * a.n_parts + part;
+      float* acc_base = a.partials + (size_t)a.nkv * a.R * a.n_parts * 2;
+      store_dev2(acc_base + pr * DPH + dcol, o0, o1);
+      if (dcol == 0) store_dev2(a.partials + pr * 2, mx, l);
+    }
+  }
+  if (a.n_parts == 1) return;
+
+  // ---- the last workgroup of (KV head, row group) combines --------------
+  // Partials are device-scope stores; waiting for them (vmcnt) before the
+  // arrival increment orders them before it.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t* ctr = a.counters + (size_t)kvh * a.row_groups + rg;
+    const uint32_t prev =
+        __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int last = prev == (uint32_t)(a.n_parts - 1);
+    if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    lds.last = last;
+  }
+  __syncthreads();
+  if (!lds.last) return;
+  stream_combine<DPH, RPW, WAVES>(a, kvh, r0, nrows);
+}
+
+// Partition sizing shared by libsde_paged and the grid API: at most
+// `blocks` workgroups in all (one per CU for the library), as many
+// partitions per (KV head, row group) as that allows (up to
+// kStreamMaxParts, at least one tile per wave), then the fewest tiles per
+// wave that cover the context.  A wave takes its tiles in chunks of `chunk`
+// (1 to max_chunk, unrolled at compile time), several chunks when it has
+// more than max_chunk tiles.
+struct StreamPlan {
+  int rpw;             // rows per wave (2 or kStreamMaxRows)
+  int row_groups;
+  int chunk;
+  int tiles_per_part;
+  int n_parts;
+};
+
+__host__ __device__ inline StreamPlan stream_plan(int L_max, int nkv, int R, int blocks,
+                                                  int waves, int max_chunk) {
+  StreamPlan p;
+  p.rpw = R <= 2 ? 2 : kStreamMaxRows;
+  p.row_groups = (R + p.rpw - 1) / p.rpw;
+  const int n_tiles = (L_max + kTile - 1) / kTile;
+  const int64_t units = (int64_t)nkv * p.row_groups;
+  int64_t parts = blocks / units;
+  if (parts < 1) parts = 1;
+  if (parts > kStreamMaxParts) parts = kStreamMaxParts;
+  const int64_t by_len = (n_tiles + waves - 1) / waves;
+  if (parts > by_len) parts = by_len;
+  const int per_wave = (int)((n_tiles + parts * waves - 1) / (parts * waves));
+  p.chunk = per_wave < max_chunk ? (per_wave < 1 ? 1 : per_wave) : max_chunk;
+  const int reps = (per_wave + p.chunk - 1) / p.chunk;
+  p.tiles_per_part = waves * p.chunk * (reps < 1 ? 1 : reps);
+  p.n_parts = (n_tiles + p.tiles_per_part - 1) / p.tiles_per_part;
+  return p;
+}
+
 // One query, all heads, all of [0, total_len) on one block (no split):
 // wave w takes the (KV head, group of up to four q heads) units w, w+nw, ...
 template <int DPH>
@@ -649,6 +944,120 @@ __device__ inline int device_attention_dispatch(int attn_type, const float* q_al
                                                 int dph, int total_len) {
   if (attn_type != SDE_ATTN_SOFTMAX) return SDE_ERR_UNSUPPORTED;
   return device_flash_attention_gqa(q_all, attn_out, kv, layer, nh, nkv, dph, total_len);
+}
+
+// ---- grid-cooperative split-context attention (persistent kernels) -------
+
+// Bytes of the workspace of device_flash_attention_gqa_grid for windows of
+// up to n_queries queries over up to max_total_len positions: the arrival
+// counters (one per (KV head, row group), padded to 256 bytes; zero-fill
+// them once before the first call, each call leaves them zero) followed by
+// the partials of at most kStreamMaxParts partitions.
+__host__ __device__ inline size_t grid_attention_workspace_size(int nh, int nkv, int dph,
+                                                                int n_queries, int max_total_len) {
+  if (nh < 1 || nkv < 1 || nh % nkv != 0 || dph < 1 || n_queries < 1 || max_total_len < 1)
+    return 0;
+  const int R = n_queries * (nh / nkv);
+  const int rpw = R <= 2 ? 2 : attn::kStreamMaxRows;
+  const size_t counters = ((size_t)nkv * ((R + rpw - 1) / rpw) * 4 + 255) / 256 * 256;
+  const int n_tiles = (max_total_len + attn::kTile - 1) / attn::kTile;
+  const int by_len = (n_tiles + 3) / 4;  // 4-wave workgroups hold at least 4 tiles
+  const int parts = by_len < attn::kStreamMaxParts ? by_len : attn::kStreamMaxParts;
+  return counters + (size_t)nkv * R * parts * (size_t)(dph + 2) * sizeof(float);
+}
+
+namespace attn {
+template <int DPH, int RPW, int WAVES>
+__device__ __forceinline__ void grid_items(const AttnArgs& a, int units_rg, void* lds_raw) {
+  auto& lds = *reinterpret_cast<StreamLds<DPH, RPW, WAVES>*>(lds_raw);
+  const int n_blocks = gridDim.x * gridDim.y * gridDim.z;
+  const int block = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+  const int items = a.nkv * units_rg * a.n_parts;
+  for (int it = block; it < items; it += n_blocks) {
+    const int part = it % a.n_parts;
+    const int unit = it / a.n_parts;
+    __syncthreads();  // the previous item's readers of lds are done
+    stream_item<DPH, RPW, 2, WAVES>(a, part, unit % a.nkv, unit / a.nkv, lds);
+  }
+}
+}  // namespace attn
+
+// Grid-cooperative form of cublas_attention_kernel (kernels.cu:904-940) for
+// persistent (megakernel) decode loops, where the reference runs
+// device_flash_attention_gqa on block 0 alone (kernels.cu:2727-2739): every
+// block of the caller's grid (any size; blockDim.x >= 256, a multiple of 64)
+// calls it with the same arguments.  q_all fp32 [n_queries][nh*dph]; query m
+// attends causally to positions [0, pos_base+m] of `layer`; attn_out fp32
+// [n_queries][nh*dph].  The context is split into partitions, one per block
+// and (KV head, row group) -- the same kernel body as sde_paged_attention --
+// and the last block to finish a (KV head, row group) combines its
+// partitions, so the call has no grid barrier inside; the output is complete
+// once every block has returned (the caller's next grid barrier).  Two calls
+// that share a workspace need a grid barrier between them.  `workspace`
+// (device memory of grid_attention_workspace_size(...) bytes or more)
+// starts with arrival counters that must be zero before the first call.
+// Uses 17 KiB of LDS.  Returns the same status in every thread: SDE_OK,
+// SDE_ERR_UNSUPPORTED (dph not 64/128, block_size not a multiple of 8,
+// blockDim.x < 256), SDE_ERR_INVALID_ARGUMENT, SDE_ERR_CAPACITY (window past
+// the layer's table) or SDE_ERR_WORKSPACE; nothing is written on error.
+__device__ inline int device_flash_attention_gqa_grid(const float* q_all, float* attn_out,
+                                                      const sde_kv_view& kv, int layer, int nh,
+                                                      int nkv, int dph, int pos_base,
+                                                      int n_queries, void* workspace,
+                                                      size_t workspace_bytes) {
+  using namespace attn;
+  if (blockDim.x < 256 || blockDim.x % 64 != 0) return SDE_ERR_UNSUPPORTED;
+  if ((dph != 64 && dph != 128) || kv.block_size % 8 != 0) return SDE_ERR_UNSUPPORTED;
+  if (nh < 1 || nkv < 1 || nh % nkv != 0 || nkv * dph != kv.kv_dim || layer < 0 ||
+      layer >= kv.n_layers || pos_base < 0 || n_queries < 1 || !q_all || !attn_out || !workspace)
+    return SDE_ERR_INVALID_ARGUMENT;
+  const int L_max = pos_base + n_queries;
+  if ((int64_t)L_max > (int64_t)kv.max_blocks_per_layer * kv.block_size) return SDE_ERR_CAPACITY;
+  if (workspace_bytes < grid_attention_workspace_size(nh, nkv, dph, n_queries, L_max))
+    return SDE_ERR_WORKSPACE;
+
+  const int waves = blockDim.x >= 512 ? kStreamWaves : 4;
+  const int G = nh / nkv;
+  const int R = n_queries * G;
+  const StreamPlan p =
+      stream_plan(L_max, nkv, R, gridDim.x * gridDim.y * gridDim.z, waves, 2);
+  AttnArgs a;
+  a.src = TileSource{kv.pool, kv.block_tables + (size_t)layer * kv.max_blocks_per_layer,
+                     kv.kv_dim, kv.block_size, L_max};
+  a.q = q_all;
+  a.out = attn_out;
+  a.counters = static_cast<uint32_t*>(workspace);
+  a.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) +
+                                        ((size_t)nkv * p.row_groups * 4 + 255) / 256 * 256);
+  a.nh = nh;
+  a.nkv = nkv;
+  a.G = G;
+  a.R = R;
+  a.row_groups = p.row_groups;
+  a.pos_base = pos_base;
+  a.n_parts = p.n_parts;
+  a.tiles_per_part = p.tiles_per_part;
+  a.qscale = (float)(kLog2e / __builtin_sqrt((double)dph));
+
+  __shared__ __attribute__((aligned(16))) char lds[sizeof(StreamLds<128, 4, kStreamWaves>)];
+  const bool w8 = waves == kStreamWaves;
+  if (dph == 128) {
+    if (p.rpw == 2)
+      w8 ? grid_items<128, 2, kStreamWaves>(a, p.row_groups, lds)
+         : grid_items<128, 2, 4>(a, p.row_groups, lds);
+    else
+      w8 ? grid_items<128, 4, kStreamWaves>(a, p.row_groups, lds)
+         : grid_items<128, 4, 4>(a, p.row_groups, lds);
+  } else {
+    if (p.rpw == 2)
+      w8 ? grid_items<64, 2, kStreamWaves>(a, p.row_groups, lds)
+         : grid_items<64, 2, 4>(a, p.row_groups, lds);
+    else
+      w8 ? grid_items<64, 4, kStreamWaves>(a, p.row_groups, lds)
+         : grid_items<64, 4, 4>(a, p.row_groups, lds);
+  }
+  __syncthreads();
+  return SDE_OK;
 }
 
 }  // namespace sde

@@ -169,6 +169,16 @@ size_t sde_paged_attention_workspace_size(const sde_kv_cache* cache, int nh,
                                           int nkv, int dph, int n_queries,
                                           int max_total_len);
 
+/* Workspace bytes of the grid-cooperative device function
+ * sde::device_flash_attention_gqa_grid (include/sde/attention_device.hpp),
+ * which a persistent kernel calls in place of the block-0-only attention of
+ * the reference's megakernel (kernels.cu:2727-2739), for windows of up to
+ * n_queries queries over up to max_total_len positions.  0 for invalid
+ * shapes.  The workspace's leading arrival counters must be zero before its
+ * first use (every call leaves them zero). */
+size_t sde_grid_attention_workspace_size(int nh, int nkv, int dph, int n_queries,
+                                         int max_total_len);
+
 /* cublas_attention_kernel (kernels.cu:904-940) + device_flash_attention_gqa
  * (attention.h:21-127): causal paged GQA attention for n_queries queries.
  * d_q, d_out: fp32 [n_queries][nh*dph] (q with RoPE applied).  Query m sees

@@ -81,6 +81,7 @@ PROTOTYPES = {
     "sde_kv_gather": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _vp, _vp]),
     "sde_kv_get_view": (_c_int, [_vp, ctypes.POINTER(KVView)]),
     "sde_paged_attention_workspace_size": (_sz, [_vp, _c_int, _c_int, _c_int, _c_int, _c_int]),
+    "sde_grid_attention_workspace_size": (_sz, [_c_int, _c_int, _c_int, _c_int, _c_int]),
     "sde_paged_attention": (_c_int, [_vp, _c_int, _vp, _vp, _c_int, _c_int, _c_int, _c_int,
                                      _c_int, _vp, _sz, _vp]),
     "sde_attention_dispatch": (_c_int, [_c_int, _vp, _c_int, _vp, _vp, _c_int, _c_int, _c_int,

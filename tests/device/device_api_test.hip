@@ -3,6 +3,7 @@
 // wraps one reference-named device function in a kernel the way an
 // in-kernel caller (a persistent decode loop) would use it, behind a plain
 // C launcher that tests/test_gpu_device_api.py calls through ctypes.
+#include <hip/hip_cooperative_groups.h>
 #include <hip/hip_runtime.h>
 
 #include "sde/attention_device.hpp"
@@ -36,6 +37,49 @@ __global__ void read_kernel(sde_kv_view kv, int layer, int pos, float* k, float*
 
 __global__ void rollback_kernel(sde_kv_view kv, int target) { sde::kv_cache_rollback(kv, target); }
 
+// Every block of an arbitrary grid calls the grid-cooperative attention.
+__global__ void grid_attention_kernel(sde_kv_view kv, int layer, const float* q, float* out,
+                                      int nh, int nkv, int dph, int pos_base, int n_queries,
+                                      void* ws, size_t ws_bytes, int* status) {
+  const int st = sde::device_flash_attention_gqa_grid(q, out, kv, layer, nh, nkv, dph, pos_base,
+                                                      n_queries, ws, ws_bytes);
+  if (threadIdx.x == 0) status[blockIdx.x] = st;
+}
+
+// A persistent decode / verify loop in one cooperative launch, the shape of
+// the reference's megakernel (kernels.cu:2727-2747, 3043-3093) with the
+// attention spread over the whole grid: for step s and layer l, block 0
+// appends the window's M tokens at pos[s] (block-cooperative
+// kv_cache_append per token), grid barrier, every block runs the grid
+// attention of the window, grid barrier; after the last layer block 0 sets
+// seq_len to the next step's pos (an O(1) rewind when drafts were
+// rejected) or, after the last step, to pos + M.
+__global__ __launch_bounds__(512) void persistent_loop_kernel(sde_kv_view kv, const int* pos, int n_steps, int M,
+                                       int nh, int nkv, int dph, const float* k, const float* v,
+                                       const float* q, float* out, void* ws, size_t ws_bytes,
+                                       int* status) {
+  namespace cg = cooperative_groups;
+  cg::grid_group grid = cg::this_grid();
+  const size_t kvd = (size_t)kv.kv_dim;
+  const size_t qd = (size_t)nh * dph;
+  int st_all = SDE_OK;
+  for (int s = 0; s < n_steps; s++) {
+    for (int l = 0; l < kv.n_layers; l++) {
+      const size_t sl = (size_t)s * kv.n_layers + l;
+      if (blockIdx.x == 0)
+        for (int m = 0; m < M; m++)
+          sde::kv_cache_append(kv, l, k + (sl * M + m) * kvd, v + (sl * M + m) * kvd, pos[s] + m);
+      grid.sync();
+      const int st = sde::device_flash_attention_gqa_grid(q + sl * M * qd, out + sl * M * qd, kv,
+                                                          l, nh, nkv, dph, pos[s], M, ws, ws_bytes);
+      if (st != SDE_OK) st_all = st;
+      grid.sync();
+    }
+    sde::kv_cache_rollback(kv, s + 1 < n_steps ? pos[s + 1] : pos[s] + M);
+  }
+  if (threadIdx.x == 0) status[blockIdx.x] = st_all;
+}
+
 int status_of(hipError_t e) { return e == hipSuccess ? 0 : 6; }
 
 }  // namespace
@@ -49,6 +93,37 @@ int sdet_attention(const sde_kv_view* kv, int layer, const float* q, float* out,
   attention_kernel<<<n_queries, threads, 0, (hipStream_t)stream>>>(*kv, layer, q, out, nh, nkv, dph,
                                                                    pos_base, attn_type, status);
   return status_of(hipGetLastError());
+}
+
+int sdet_grid_attention(const sde_kv_view* kv, int layer, const float* q, float* out, int nh,
+                        int nkv, int dph, int pos_base, int n_queries, int blocks, int threads,
+                        void* ws, size_t ws_bytes, int* status, void* stream) {
+  if (!kv || blocks < 1 || threads < 64 || threads % 64 != 0 || threads > 1024) return 1;
+  grid_attention_kernel<<<blocks, threads, 0, (hipStream_t)stream>>>(
+      *kv, layer, q, out, nh, nkv, dph, pos_base, n_queries, ws, ws_bytes, status);
+  return status_of(hipGetLastError());
+}
+
+// Cooperative launch of persistent_loop_kernel; blocks must all be resident
+// (returns 2 when the device cannot hold that many).
+int sdet_persistent_loop(const sde_kv_view* kv, const int* d_pos, int n_steps, int M, int nh,
+                         int nkv, int dph, const float* k, const float* v, const float* q,
+                         float* out, void* ws, size_t ws_bytes, int* status, int blocks,
+                         int threads, void* stream) {
+  if (!kv || blocks < 1 || threads < 256 || threads % 64 != 0 || threads > 512) return 1;
+  int dev = 0, per_cu = 0, cus = 0, coop = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, persistent_loop_kernel, threads, 0) !=
+          hipSuccess)
+    return 6;
+  if (!coop || blocks > per_cu * cus) return 2;
+  sde_kv_view view = *kv;
+  void* args[] = {&view, (void*)&d_pos, &n_steps, &M, &nh, &nkv, &dph, (void*)&k, (void*)&v,
+                  (void*)&q, &out, &ws, &ws_bytes, &status};
+  return status_of(hipLaunchCooperativeKernel((const void*)persistent_loop_kernel, dim3(blocks),
+                                              dim3(threads), args, 0, (hipStream_t)stream));
 }
 
 int sdet_append(const sde_kv_view* kv, int layer, const float* k, const float* v, int pos_base,

@@ -215,3 +215,135 @@ def test_cpp_host_names_match_the_c_abi(dev, oracle):
     m.append(1, k, v, 0)
     assert np.array_equal(pool_cpp, m.pool)           # C++ append: oracle bytes
     cache.free()
+
+
+# ---- grid-cooperative attention (device_flash_attention_gqa_grid) ----------
+
+def _grid_ws(nh, nkv, dph, M, L):
+    n = N.load().sde_grid_attention_workspace_size(nh, nkv, dph, M, L)
+    assert n > 0
+    return torch.zeros(n // 4 + 1, dtype=torch.int32, device="cuda")
+
+
+def grid_attention(dev, cache, q, nh, nkv, dph, pos_base, blocks, threads, ws, layer=0):
+    M = q.shape[0]
+    out = torch.full((M, nh * dph), float("nan"), device="cuda")
+    status = torch.full((blocks,), -1, dtype=torch.int32, device="cuda")
+    view = cache.view()
+    f = dev.sdet_grid_attention
+    f.restype = ctypes.c_int
+    vp, i = ctypes.c_void_p, ctypes.c_int
+    f.argtypes = [ctypes.POINTER(N.KVView), i, vp, vp, i, i, i, i, i, i, i, vp, ctypes.c_size_t,
+                  vp, vp]
+    assert f(ctypes.byref(view), layer, q.data_ptr(), out.data_ptr(), nh, nkv, dph, pos_base, M,
+             blocks, threads, ws.data_ptr(), ws.numel() * 4, status.data_ptr(), _stream()) == 0
+    torch.cuda.synchronize()
+    return out, status.cpu().numpy()
+
+
+@pytest.mark.parametrize("nh,nkv,dph,bs,ctx,M,blocks,threads", [
+    (32, 8, 128, 16, 32767, 1, 256, 512),   # Llama-3-8B 32K decode, one block per CU
+    (32, 8, 128, 16, 4096, 5, 300, 256),    # verify window, 4-wave blocks
+    (28, 4, 128, 32, 8192, 9, 64, 1024),    # Qwen2.5-7B verify, fewer blocks than items
+    (32, 4, 64, 16, 2048, 1, 37, 320),      # TinyLlama, odd grid, a wave past the four
+    (4, 2, 64, 16, 128, 1, 1, 256),         # config 1 shape on a single block
+    (8, 8, 128, 8, 77, 2, 512, 512),        # ragged last tile, more blocks than work
+])
+def test_grid_attention_matches_oracle_and_host_entry(dev, oracle, nh, nkv, dph, bs, ctx, M,
+                                                      blocks, threads):
+    case_banner("grid attention", nh, nkv, dph, bs, ctx, M, blocks, threads)
+    nblk = -(-(ctx + M) // bs)
+    cache, K, V, rng = build_layer(nh, nkv, dph, bs, ctx, M, nblk + 40, nh + ctx + M)
+    q = W.queries(rng, M, nh, dph)
+    qd = torch.from_numpy(q).cuda()
+    ws = _grid_ws(nh, nkv, dph, M, ctx + M)
+    ref = oracle.attention_f64_np(q, K, V, nh, nkv, dph, ctx)
+    host = cache.attention(0, qd, nh, nkv, dph, ctx)
+    torch.cuda.synchronize()
+    first = None
+    for call in range(2):   # the second call finds the counters the first left at zero
+        out, status = grid_attention(dev, cache, qd, nh, nkv, dph, ctx, blocks, threads, ws)
+        assert (status == 0).all()
+        assert_close(out.cpu().numpy(), ref, f"grid call {call}")
+        assert_close(out.cpu().numpy(), host.cpu().numpy().astype(np.float64), "grid vs host")
+        if first is None:
+            first = out
+        else:
+            assert torch.equal(out, first)   # deterministic
+    nc = (nkv * -(-(M * nh // nkv) // (2 if M * nh // nkv <= 2 else 4)))
+    assert torch.count_nonzero(ws[:nc]).item() == 0   # counters back at zero
+    cache.free()
+
+
+def test_grid_attention_errors_write_nothing(dev):
+    case_banner("grid attention errors")
+    nh, nkv, dph, ctx = 32, 8, 128, 1000
+    cache, K, V, rng = build_layer(nh, nkv, dph, 16, ctx, 1, 80, 5)
+    q = torch.from_numpy(W.queries(rng, 1, nh, dph)).cuda()
+    ws = _grid_ws(nh, nkv, dph, 1, ctx + 1)
+    small = ws[: ws.numel() // 2]
+    out, status = grid_attention(dev, cache, q, nh, nkv, dph, ctx, 16, 512, small)
+    assert (status == N.SDE_ERR_WORKSPACE).all() and torch.isnan(out).all()
+    out, status = grid_attention(dev, cache, q, nh, nkv, dph, ctx, 16, 192, ws)
+    assert (status == N.SDE_ERR_UNSUPPORTED).all() and torch.isnan(out).all()
+    out, status = grid_attention(dev, cache, q, nh, nkv, dph, ctx + 5000, 16, 512, ws)
+    assert (status == N.SDE_ERR_CAPACITY).all() and torch.isnan(out).all()
+    cache.free()
+
+
+def test_persistent_loop_append_verify_rewind(dev, oracle):
+    """One cooperative persistent kernel runs three verify steps of k+1 = 5
+    tokens over 2 layers -- append (block 0), grid barrier, grid attention,
+    grid barrier -- rewinding seq_len between steps to a partial accept; the
+    pool bytes equal the oracle's after the same appends, every window's
+    output matches the oracle's attention, and seq_len ends at pos + M."""
+    case_banner("persistent loop")
+    nl, nh, nkv, dph, bs, M = 2, 32, 8, 128, 16, 5
+    kv_dim = nkv * dph
+    ctx = 3000
+    pos = [ctx, ctx + 3, ctx + 3 + 1]   # 2 then 0 drafts accepted
+    nblk = -(-(pos[-1] + M) // bs)
+    pool_blocks = nl * nblk + 9
+    rng = np.random.default_rng(123)
+    tables = W.make_tables(rng, nl, nblk, pool_blocks)
+    cache = KVCache(nl, kv_dim, nblk, bs, pool_blocks)
+    model = oracle.PagedKVModel(nl, kv_dim, nblk, bs, pool_blocks)
+    kc, vc = W.context_kv(rng, ctx, kv_dim)
+    for l in range(nl):
+        cache.set_block_table(l, tables[l])
+        model.set_block_table(l, tables[l])
+        cache.write_fp16(l, torch.from_numpy(kc.view(np.int16)).cuda(),
+                         torch.from_numpy(vc.view(np.int16)).cuda(), 0)
+        model.write_fp16(l, kc, vc, 0)
+    S = len(pos)
+    k = rng.standard_normal((S, nl, M, kv_dim), dtype=np.float32)
+    v = rng.standard_normal((S, nl, M, kv_dim), dtype=np.float32)
+    q = rng.standard_normal((S, nl, M, nh * dph), dtype=np.float32)
+    out = torch.full((S, nl, M, nh * dph), float("nan"), device="cuda")
+    kd, vd, qd = (torch.from_numpy(x).cuda() for x in (k, v, q))
+    posd = torch.tensor(pos, dtype=torch.int32, device="cuda")
+    ws = _grid_ws(nh, nkv, dph, M, pos[-1] + M)
+    blocks = 256
+    status = torch.full((blocks,), -1, dtype=torch.int32, device="cuda")
+    f = dev.sdet_persistent_loop
+    f.restype = ctypes.c_int
+    view = cache.view()
+    vp = ctypes.c_void_p
+    rc = f(ctypes.byref(view), vp(posd.data_ptr()), S, M, nh, nkv, dph, vp(kd.data_ptr()),
+           vp(vd.data_ptr()), vp(qd.data_ptr()), vp(out.data_ptr()), vp(ws.data_ptr()),
+           ctypes.c_size_t(ws.numel() * 4), vp(status.data_ptr()), blocks, 512, _stream())
+    if rc == 2:
+        pytest.skip("device cannot hold the cooperative grid")
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert (status.cpu().numpy() == 0).all()
+    assert cache.device_seq_len() == pos[-1] + M
+    outs = out.cpu().numpy()
+    for s in range(S):
+        for l in range(nl):
+            model.append(l, k[s, l], v[s, l], pos[s])
+            ref = model.attention(l, q[s, l], nh, nkv, dph, pos[s], mode="f64")
+            assert_close(outs[s, l], ref, f"step {s} layer {l}")
+    pool = cache.pool.cpu().numpy().view(np.uint16).reshape(model.pool.shape)
+    assert np.array_equal(pool, model.pool)
+    cache.free()
