@@ -526,7 +526,7 @@ struct AttnArgs {
   TileSource src;        // pool, this layer's table, kv_dim, block_size, L_max
   const float* q;        // [M][nh*dph]
   float* out;            // [M][nh*dph]
-  float* partials;       // [nkv][R][n_parts][2] (max, sum), then [nkv][R][n_parts][dph] acc
+  float* partials;       // [nkv][R][n_parts][dph] acc, then [nkv][R][n_parts][2] (max, sum)
   uint32_t* counters;    // [nkv][row_groups] arrival counters, zero at rest
   int nh;
   int nkv;
@@ -560,10 +560,72 @@ __device__ __forceinline__ float2 load_dev2(const float* p) {
                      __builtin_bit_cast(float, (uint32_t)(bits >> 32)));
 }
 
-__device__ __forceinline__ float4 load_dev4(const float* p) {
-  const float2 lo = load_dev2(p);
-  const float2 hi = load_dev2(p + 2);
-  return make_float4(lo.x, lo.y, hi.x, hi.y);
+// 16 bytes at base + byte_off with the same device-scope cache policy as
+// load_dev2 (buffer_load_dwordx4 ... sc1; raw buffer, range-checked by
+// `bytes`).  One 16-byte request instead of two 8-byte ones: the combine's
+// partial loads are request-bound.
+__device__ __forceinline__ float4 load_dev16(const float* base, uint32_t bytes,
+                                             uint32_t byte_off) {
+  constexpr int kSc1 = 16;                     // cache policy bit of sc1
+  constexpr int kRsrcWord3 = 0x00020000;       // gfx9 raw buffer, 32-bit data format
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, (int)bytes, kRsrcWord3);
+  // Bit-cast the whole vector: extracting elements of the builtin's integer
+  // vector result makes this compiler shrink the load to one dword.
+  typedef float f4v __attribute__((ext_vector_type(4)));
+  const f4v v = __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, kSc1));
+  return make_float4(v.x, v.y, v.z, v.w);
+}
+
+// One (row, float4 column, quarter `sub`) of the partition combine: loads
+// (max, sum, acc[c4]) of partitions sub, sub+4, ... (PMAX of them, P real),
+// returns this quarter's weighted sum and its (max) in l, o, mx.  Every load
+// is issued unconditionally (indices past P re-read partition P-1, then
+// weigh 0), so they all travel in one round trip: a load under `if (p < P)`
+// gets a wait of its own at the join.
+template <int DPH, int PMAX>
+__device__ __forceinline__ void combine_quarter(const float* ml, const float* acc_all,
+                                                uint32_t acc_bytes, uint32_t acc_off, int P,
+                                                int sub, float& mx, float& l, float4& o) {
+  float2 e[PMAX];
+  float4 v[PMAX];
+#pragma unroll
+  for (int i = 0; i < PMAX; i++) {
+    const int p = min(sub + i * 4, P - 1);
+    v[i] = load_dev16(acc_all, acc_bytes, acc_off + (uint32_t)p * (DPH * 4));
+  }
+  // (max, sum) of partition p is loaded once per wave, by lane p (every
+  // lane of a wave serves one row), and read across lanes.
+  const int lane = threadIdx.x & 63;
+  const float2 mine = load_dev2(ml + (size_t)min(lane, P - 1) * 2);
+#pragma unroll
+  for (int i = 0; i < PMAX; i++) {
+    e[i].x = __shfl(mine.x, sub + i * 4);
+    e[i].y = __shfl(mine.y, sub + i * 4);
+  }
+#pragma unroll
+  for (int i = 0; i < PMAX; i++) {
+    if (sub + i * 4 >= P) {
+      e[i] = make_float2(-INFINITY, 0.f);
+      v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+  mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < PMAX; i++) mx = fmaxf(mx, e[i].x);
+  mx = fmaxf(mx, dpp_f(mx, 0));
+  mx = fmaxf(mx, dpp_f(mx, 1));
+  l = 0.f;
+  o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int i = 0; i < PMAX; i++) {
+    const float w = e[i].x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(e[i].x - mx);
+    l += e[i].y * w;
+    o.x += w * v[i].x;
+    o.y += w * v[i].y;
+    o.z += w * v[i].z;
+    o.w += w * v[i].w;
+  }
 }
 
 // Partition combine, run by the last workgroup of a (KV head, row group) to
@@ -577,7 +639,8 @@ template <int DPH, int RPW, int WAVES>
 __device__ __forceinline__ void stream_combine(const AttnArgs& a, int kvh, int r0, int nrows) {
   constexpr int C4 = DPH / 4;
   constexpr int SUB = 4;
-  constexpr int PMAX = kStreamMaxParts / SUB;
+  static_assert(kStreamMaxParts == 16 * SUB && kStreamMaxParts <= 64, "combine_quarter buckets");
+  static_assert((SUB * C4) % 64 == 0, "each wave's lanes serve one row");
   const int P = a.n_parts;
   if ((int)threadIdx.x >= 64 * WAVES) return;  // waves past WAVES idle
   for (int tid = threadIdx.x; tid < RPW * C4 * SUB; tid += 64 * WAVES) {
@@ -586,36 +649,18 @@ __device__ __forceinline__ void stream_combine(const AttnArgs& a, int kvh, int r
     const int r = tid / (SUB * C4);  // uniform per wave
     if (r >= nrows) break;
     const size_t row = (size_t)kvh * a.R + r0 + r;
-    const float* ml = a.partials + row * P * 2;
-    const float* accp = a.partials + (size_t)a.nkv * a.R * P * 2 + row * P * DPH + 4 * col4;
-    float2 e[PMAX];
-    float4 v[PMAX];
-#pragma unroll
-    for (int i = 0; i < PMAX; i++) {
-      const int p = sub + i * SUB;
-      e[i] = make_float2(-INFINITY, 0.f);
-      v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (p < P) {
-        e[i] = load_dev2(ml + (size_t)p * 2);
-        v[i] = load_dev4(accp + (size_t)p * DPH);
-      }
-    }
-    float mx = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < PMAX; i++) mx = fmaxf(mx, e[i].x);
-    mx = fmaxf(mx, dpp_f(mx, 0));
-    mx = fmaxf(mx, dpp_f(mx, 1));
-    float l = 0.f;
-    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-    for (int i = 0; i < PMAX; i++) {
-      const float w = e[i].x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(e[i].x - mx);
-      l += e[i].y * w;
-      o.x += w * v[i].x;
-      o.y += w * v[i].y;
-      o.z += w * v[i].z;
-      o.w += w * v[i].w;
-    }
+    const size_t acc_floats = (size_t)a.nkv * a.R * P * DPH;
+    const float* ml = a.partials + acc_floats + row * P * 2;
+    const uint32_t acc_bytes = (uint32_t)(acc_floats * 4);
+    const uint32_t acc_off = (uint32_t)((row * P * DPH + 4 * col4) * 4);
+    float mx, l;
+    float4 o;
+    if (P <= 4 * SUB)
+      combine_quarter<DPH, 4>(ml, a.partials, acc_bytes, acc_off, P, sub, mx, l, o);
+    else if (P <= 8 * SUB)
+      combine_quarter<DPH, 8>(ml, a.partials, acc_bytes, acc_off, P, sub, mx, l, o);
+    else
+      combine_quarter<DPH, 16>(ml, a.partials, acc_bytes, acc_off, P, sub, mx, l, o);
 #pragma unroll
     for (int k = 0; k < 2; k++) {
       l += dpp_f(l, k);
@@ -752,9 +797,9 @@ __device__ __forceinline__ void stream_item(const AttnArgs& a, int part, int kvh
           make_float2(o0 * inv, o1 * inv);
     } else {
       const size_t pr = ((size_t)kvh * a.R + gr) * a.n_parts + part;
-      float* acc_base = a.partials + (size_t)a.nkv * a.R * a.n_parts * 2;
-      store_dev2(acc_base + pr * DPH + dcol, o0, o1);
-      if (dcol == 0) store_dev2(a.partials + pr * 2, mx, l);
+      float* ml_base = a.partials + (size_t)a.nkv * a.R * a.n_parts * DPH;
+      store_dev2(a.partials + pr * DPH + dcol, o0, o1);
+      if (dcol == 0) store_dev2(ml_base + pr * 2, mx, l);
     }
   }
   if (a.n_parts == 1) return;
