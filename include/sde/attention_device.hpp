@@ -416,11 +416,78 @@ __device__ __forceinline__ void stream_pv(int sl, float al, uint32_t pk,
 // and no in-flight register is carried across a loop edge (the compiler
 // would copy it, which waits for it).  Chunk slots past the wave's last tile
 // re-read that tile (an L2 hit) and are fully masked.
-template <int DPH, int RPW, int CHUNK>
+// Fused RoPE + append (sde_rope_append_attention): the window's k and v
+// rows before RoPE, and the rotate-half RoPE of rope_apply_inplace
+// (model.cu:281-323): pair (j, j + dph/2) of a head rotates by angle
+// (pos / pos_div) * inv_freq[j], with pos_div the linear / YaRN position
+// divisor (1 otherwise) and inv_freq[j] = theta^(-2j/dph) (theta already
+// NTK-scaled) computed on the host in double precision.
+struct RopeArgs {
+  const float* k_new;  // [M][kv_dim] fp32, before RoPE
+  const float* v_new;  // [M][kv_dim] fp32
+  uint16_t* pool;      // the pool (written)
+  float pos_div;
+  float inv_freq[64];  // dph/2 entries
+};
+
+__device__ __forceinline__ float rope_angle(const RopeArgs& rp, int pos, int j) {
+  return ((float)pos / rp.pos_div) * rp.inv_freq[j];
+}
+
+// Window rows the fused path supports: its (cos, sin) table lives in LDS.
+constexpr int kRopeMaxQueries = 32;
+
+// (cos, sin) of every (window query m, rotation pair j), m-major, into LDS
+// by the whole workgroup (one sincos per entry), then a barrier.
+template <int DPH>
+__device__ __forceinline__ void rope_table(const RopeArgs& rp, int pos_base, int M,
+                                           float2* cs) {
+  constexpr int HALF = DPH / 2;
+  for (int t = threadIdx.x; t < M * HALF; t += blockDim.x) {
+    const int m = t / HALF;
+    float sn, c;
+    sincosf(rope_angle(rp, pos_base + m, t - m * HALF), &sn, &c);
+    cs[t] = make_float2(c, sn);
+  }
+  __syncthreads();
+}
+
+// RoPE of the lane's eight q features (8c..8c+7) of every row, in place,
+// with the window's (cos, sin) table; the partner feature (j + dph/2 or
+// j - dph/2) lives in lane c ^ CH/2 of the same token slot.
+template <int DPH, int RPW>
+__device__ __forceinline__ void rope_q_rows(const float2* cs_tab, float2 (&q)[RPW][4], int r0,
+                                            int G, int R) {
+  constexpr int CH = DPH / 8;
+  constexpr int HALF = DPH / 2;
+  const int c = (threadIdx.x & 63) % CH;
+  const bool first_half = c < CH / 2;
+  const int j0 = (8 * c) % HALF;
+#pragma unroll
+  for (int r = 0; r < RPW; r++) {
+    // rows past R (masked later) reuse the last row's query
+    const float2* t = cs_tab + (min(r0 + r, R - 1) / G) * HALF + j0;
+    float x[8] = {q[r][0].x, q[r][0].y, q[r][1].x, q[r][1].y,
+                  q[r][2].x, q[r][2].y, q[r][3].x, q[r][3].y};
+    float y[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      const float2 k = t[e];
+      const float partner = __shfl_xor(x[e], CH / 2);
+      y[e] = first_half ? x[e] * k.x - partner * k.y : partner * k.y + x[e] * k.x;
+    }
+#pragma unroll
+    for (int w = 0; w < 4; w++) q[r][w] = make_float2(y[2 * w], y[2 * w + 1]);
+  }
+}
+
+template <int DPH, int RPW, int CHUNK, bool ROPE = false>
 __device__ __forceinline__ void wave_attend(const TileSource& src, int kvh, int first, int te,
                                             int stride, int nrows, int min_lim, int my_lim,
                                             float qscale, const float2 (&q_raw)[RPW][4],
-                                            float& m_run, float& l_run, float (&acc)[RPW][8]) {
+                                            float& m_run, float& l_run, float (&acc)[RPW][8],
+                                            const float2* rope_cs = nullptr, int r0 = 0,
+                                            int G = 1, int R = 1) {
   using Sh = StreamShape<DPH, RPW>;
   constexpr int CH = Sh::CH, SL = Sh::SL, NLD = Sh::NLD;
   const int lane = threadIdx.x & 63;
@@ -454,7 +521,25 @@ __device__ __forceinline__ void wave_attend(const TileSource& src, int kvh, int 
       if (i + 1 < CHUNK)
         stream_load<DPH>(src, head_base, tn * kTile, sl, lane_off, chunk_off, false, blk[nb],
                          slot[nb], kbuf[nb]);
-      if (i == 0) {
+      if constexpr (ROPE) {
+        if (i == 0 && c0 == first) {
+          // q rotated by RoPE, then packed like below (once).
+          float2 qv[RPW][4];
+#pragma unroll
+          for (int r = 0; r < RPW; r++)
+#pragma unroll
+            for (int w = 0; w < 4; w++) qv[r][w] = q_raw[r][w];
+          rope_q_rows<DPH, RPW>(rope_cs, qv, r0, G, R);
+#pragma unroll
+          for (int r = 0; r < RPW; r++) {
+            const float sc = r < nrows ? qscale : 0.f;
+            qr[r] = make_uint4(pack_h2(qv[r][0].x * sc, qv[r][0].y * sc),
+                               pack_h2(qv[r][1].x * sc, qv[r][1].y * sc),
+                               pack_h2(qv[r][2].x * sc, qv[r][2].y * sc),
+                               pack_h2(qv[r][3].x * sc, qv[r][3].y * sc));
+          }
+        }
+      } else if (i == 0) {
         // q is scaled into the exp2 domain and rounded to fp16 pairs once
         // this chunk's loads are in flight (q was loaded before them, so
         // this waits for no tile data).
@@ -682,6 +767,44 @@ __device__ __forceinline__ void stream_combine(const AttnArgs& a, int kvh, int r
   }
 }
 
+// The window's rows (positions pos_base .. pos_base+M-1) of KV head kvh:
+// k rotated by RoPE, k and v rounded to fp16 (RNE) into the pool
+// (kv_cache_append, kv_cache.cu:70-93), by the whole workgroup; returns
+// once the stores are visible to the workgroup's loads.
+template <int DPH>
+__device__ __forceinline__ void rope_append_slice(const AttnArgs& a, const RopeArgs& rp,
+                                                  const float2* rope_cs, int kvh) {
+  constexpr int HALF = DPH / 2;
+  const int M = a.R / a.G;
+  const int kvd = a.src.kv_dim;
+  const int bs = a.src.bs;
+  for (int t = threadIdx.x; t < M * HALF; t += blockDim.x) {
+    const int m = t / HALF;
+    const int j = t - m * HALF;
+    const int pos = a.pos_base + m;
+    const float* kin = rp.k_new + (size_t)m * kvd + (size_t)kvh * DPH;
+    const float x0 = kin[j], x1 = kin[j + HALF];
+    const float cs = rope_cs[t].x, sn = rope_cs[t].y;
+    const int lb = pos / bs;
+    const int slot = pos - lb * bs;
+    uint16_t* kd = rp.pool + ((size_t)(uint32_t)a.src.table[lb] * 2u * bs + slot) * kvd +
+                   (size_t)kvh * DPH;
+    kd[j] = __builtin_bit_cast(uint16_t, (_Float16)(x0 * cs - x1 * sn));
+    kd[j + HALF] = __builtin_bit_cast(uint16_t, (_Float16)(x0 * sn + x1 * cs));
+  }
+  for (int t = threadIdx.x; t < M * DPH; t += blockDim.x) {
+    const int m = t / DPH;
+    const int d = t - m * DPH;
+    const int pos = a.pos_base + m;
+    const int lb = pos / bs;
+    const int slot = pos - lb * bs;
+    uint16_t* vd = rp.pool + ((size_t)(uint32_t)a.src.table[lb] * 2u * bs + bs + slot) * kvd +
+                   (size_t)kvh * DPH;
+    vd[d] = __builtin_bit_cast(uint16_t, (_Float16)rp.v_new[(size_t)m * kvd + (size_t)kvh * DPH + d]);
+  }
+  __syncthreads();
+}
+
 // LDS of stream_item: per-wave records (max, sum, acc[DPH]) of every row.
 template <int DPH, int RPW, int WAVES>
 struct StreamLds {
@@ -694,9 +817,11 @@ struct StreamLds {
 // merge their states through LDS, and either write the normalised output
 // (one partition) or publish a partial and count the arrival; the last
 // arrival combines all partitions.  Every thread of the workgroup calls it.
-template <int DPH, int RPW, int CHUNK, int WAVES>
+template <int DPH, int RPW, int CHUNK, int WAVES, bool ROPE = false>
 __device__ __forceinline__ void stream_item(const AttnArgs& a, int part, int kvh, int rg,
-                                            StreamLds<DPH, RPW, WAVES>& lds) {
+                                            StreamLds<DPH, RPW, WAVES>& lds,
+                                            const RopeArgs* rp = nullptr,
+                                            float2* rope_cs = nullptr) {
   static_assert(DPH == 64 || DPH == 128, "head_dim");
   static_assert(RPW == 2 || RPW == 4, "rows per wave");
   static_assert(RPW * (DPH / 2) <= 64 * WAVES, "one merge thread per (row, feature pair)");
@@ -716,6 +841,15 @@ __device__ __forceinline__ void stream_item(const AttnArgs& a, int part, int kvh
 
   using Sh = StreamShape<DPH, RPW>;
   const int my_r = (c >> (Sh::S - Sh::T)) >> (Sh::T - Sh::RB);
+
+  if constexpr (ROPE) {
+    rope_table<DPH>(*rp, a.pos_base, a.R / a.G, rope_cs);
+    // A partition that reads window positions first writes the window's K
+    // (rotated) and V slice of this KV head itself, so no other workgroup
+    // has to finish first; partitions sharing the window write the same
+    // bytes.
+    if (te * kTile > a.pos_base) rope_append_slice<DPH>(a, *rp, rope_cs, kvh);
+  }
 
   if (wave < WAVES) {
     // This lane's q chunk (features 8c..8c+7) of every row, loaded before
@@ -746,8 +880,9 @@ __device__ __forceinline__ void stream_item(const AttnArgs& a, int part, int kvh
     for (int r = 0; r < RPW; r++)
 #pragma unroll
       for (int e = 0; e < 8; e++) acc[r][e] = 0.f;
-    wave_attend<DPH, RPW, CHUNK>(a.src, kvh, tb + wave, te, WAVES, nrows, min_lim, my_lim,
-                                 a.qscale, q_raw, m_run, l_run, acc);
+    wave_attend<DPH, RPW, CHUNK, ROPE>(a.src, kvh, tb + wave, te, WAVES, nrows, min_lim, my_lim,
+                                       a.qscale, q_raw, m_run, l_run, acc, rope_cs, r0, a.G,
+                                       a.R);
 
     // ---- merge the slot states of this wave; record per row -------------
     float mx[RPW], lw[RPW];

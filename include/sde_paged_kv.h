@@ -196,6 +196,43 @@ int sde_paged_attention(sde_kv_cache* cache, int layer, const float* d_q,
                         int n_queries, void* d_workspace,
                         size_t workspace_bytes, sde_stream_t stream);
 
+/* RoPE scaling types: the reference's RopeScalingType (config.h:42-47). */
+enum {
+  SDE_ROPE_NONE = 0,
+  SDE_ROPE_LINEAR = 1,
+  SDE_ROPE_NTK = 2,
+  SDE_ROPE_YARN = 3
+};
+
+typedef struct sde_rope_config {
+  float theta;          /* rope_theta; <= 1e-6 selects 10000 (model.cu:290)  */
+  int32_t scaling_type; /* SDE_ROPE_*                                          */
+  float scaling_factor; /* applies when > 1                                   */
+} sde_rope_config;
+
+/* One layer's KV phase and attention fused in one launch: the work of
+ * model_layer_kv_phase's RoPE and append (model.cu:346-384, i.e.
+ * cublas_rope_kernel kernels.cu:797-817 + cublas_kv_append_kernel
+ * kernels.cu:826-844) and cublas_attention_kernel (kernels.cu:904-940).
+ * d_q fp32 [n_queries][nh*dph] and d_k, d_v fp32 [n_queries][nkv*dph] are
+ * the projections BEFORE RoPE (not modified).  q and k are rotated by
+ * rotate-half RoPE at positions pos_base+m (rope_apply_inplace,
+ * model.cu:281-323: pair (j, j+dph/2), angle = pos' * theta^(-2j/dph), the
+ * frequencies computed in double precision and rounded to fp32; the
+ * rotation in fp32), k and v are appended (fp16 RNE) at those positions,
+ * and query m attends causally to [0, pos_base+m].  Same shapes, limits,
+ * workspace and errors as sde_paged_attention, plus SDE_ERR_INVALID_ARGUMENT
+ * for a NULL d_k / d_v / rope, an unknown scaling type, or unaligned
+ * d_k / d_v, and SDE_ERR_UNSUPPORTED for n_queries > 32 (a verify window is
+ * at most MAX_VERIFY_BATCH = 9 rows, config.h:26; prefill takes the unfused
+ * calls). */
+int sde_rope_append_attention(sde_kv_cache* cache, int layer, const float* d_q,
+                              const float* d_k, const float* d_v, float* d_out,
+                              int nh, int nkv, int dph, int pos_base,
+                              int n_queries, const sde_rope_config* rope,
+                              void* d_workspace, size_t workspace_bytes,
+                              sde_stream_t stream);
+
 /* device_attention_dispatch (attention.h:140-164) as a host entry point:
  * SDE_ATTN_SOFTMAX runs sde_paged_attention; the reserved types return
  * SDE_ERR_UNSUPPORTED (where the reference traps) and launch nothing. */

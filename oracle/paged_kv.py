@@ -213,6 +213,48 @@ def run_script(model: PagedKVModel, ops, on_checkpoint=None, on_attend=None) -> 
     return marks
 
 
+ROPE_NONE, ROPE_LINEAR, ROPE_NTK, ROPE_YARN = 0, 1, 2, 3  # config.h:42-47
+
+
+def rope_inv_freq(dph: int, theta: float = 10000.0, scaling_type: int = ROPE_NONE,
+                  factor: float = 1.0) -> np.ndarray:
+    """Inverse frequencies of rope_apply_inplace (model.cu:281-323): theta
+    (10000 when <= 1e-6), times factor^(dph/(dph-2)) for NTK with factor > 1;
+    inv_freq[j] = exp(-ln(theta) * 2j / dph), in float64 rounded to float32
+    (the rule sde_rope_append_attention states for its table)."""
+    th = float(np.float32(theta))
+    th = th if th > 1e-6 else 10000.0
+    f = float(np.float32(factor))
+    if scaling_type == ROPE_NTK and f > 1.0:
+        th *= f ** (dph / (dph - 2.0))
+    j = np.arange(dph // 2, dtype=np.float64)
+    return np.exp(-np.log(th) * 2.0 * j / dph).astype(np.float32)
+
+
+def rope_rotate_half_f64(x: np.ndarray, n_heads: int, dph: int, positions,
+                         theta: float = 10000.0, scaling_type: int = ROPE_NONE,
+                         factor: float = 1.0) -> np.ndarray:
+    """Rotate-half RoPE of rows x [M][n_heads*dph] at positions[m]
+    (rope_apply_inplace, model.cu:281-323): dim j pairs with j + dph/2,
+    (x0, x1) -> (x0 c - x1 s, x0 s + x1 c) with c, s = cos, sin(angle);
+    angle = float32(float32(pos) / div) * inv_freq[j] as a float32 product,
+    div = factor for linear / YaRN with factor > 1 (else 1).  The rotation
+    is evaluated in float64."""
+    x = np.asarray(x, dtype=np.float64).reshape(-1, n_heads, dph)
+    pos = np.asarray(positions, dtype=np.int64).reshape(-1)
+    assert pos.shape[0] == x.shape[0]
+    inv = rope_inv_freq(dph, theta, scaling_type, factor)
+    f = np.float32(factor)
+    div = f if scaling_type in (ROPE_LINEAR, ROPE_YARN) and f > 1 else np.float32(1.0)
+    ps = (pos.astype(np.float32) / div).astype(np.float32)
+    angle = (ps[:, None] * inv[None, :]).astype(np.float32).astype(np.float64)
+    c, sn = np.cos(angle)[:, None, :], np.sin(angle)[:, None, :]
+    half = dph // 2
+    x0, x1 = x[..., :half], x[..., half:]
+    out = np.concatenate([x0 * c - x1 * sn, x0 * sn + x1 * c], axis=-1)
+    return out.reshape(-1, n_heads * dph)
+
+
 def attention_f64_np(q: np.ndarray, K: np.ndarray, V: np.ndarray, nh: int, nkv: int,
                      dph: int, pos_base: int) -> np.ndarray:
     """softmax(q K^T / sqrt(dph)) V in fp64 with numpy, on contiguous

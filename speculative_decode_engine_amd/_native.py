@@ -30,6 +30,11 @@ SDE_ATTN_SLIDING_WINDOW = 1
 SDE_ATTN_KDA = 2
 SDE_ATTN_LINEAR = 3
 
+SDE_ROPE_NONE = 0
+SDE_ROPE_LINEAR = 1
+SDE_ROPE_NTK = 2
+SDE_ROPE_YARN = 3
+
 
 class KVConfig(ctypes.Structure):
     _fields_ = [
@@ -38,6 +43,14 @@ class KVConfig(ctypes.Structure):
         ("max_blocks_per_layer", ctypes.c_int32),
         ("block_size", ctypes.c_int32),
         ("pool_blocks", ctypes.c_int32),
+    ]
+
+
+class RopeConfig(ctypes.Structure):
+    _fields_ = [
+        ("theta", ctypes.c_float),
+        ("scaling_type", ctypes.c_int32),
+        ("scaling_factor", ctypes.c_float),
     ]
 
 
@@ -84,6 +97,8 @@ PROTOTYPES = {
     "sde_grid_attention_workspace_size": (_sz, [_c_int, _c_int, _c_int, _c_int, _c_int]),
     "sde_paged_attention": (_c_int, [_vp, _c_int, _vp, _vp, _c_int, _c_int, _c_int, _c_int,
                                      _c_int, _vp, _sz, _vp]),
+    "sde_rope_append_attention": (_c_int, [_vp, _c_int, _vp, _vp, _vp, _vp, _c_int, _c_int,
+                                           _c_int, _c_int, _c_int, _vp, _vp, _sz, _vp]),
     "sde_attention_dispatch": (_c_int, [_c_int, _vp, _c_int, _vp, _vp, _c_int, _c_int, _c_int,
                                         _c_int, _c_int, _vp, _sz, _vp]),
 }

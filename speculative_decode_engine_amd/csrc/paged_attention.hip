@@ -42,6 +42,16 @@ __global__ __launch_bounds__(64 * kStreamWaves) void attn_stream_kernel(AttnArgs
   stream_item<DPH, RPW, CHUNK, kStreamWaves>(a, blockIdx.x, blockIdx.y, blockIdx.z, lds);
 }
 
+// attn_stream_kernel with RoPE of q and of the window's k, and the window's
+// append, fused in (sde_rope_append_attention).
+template <int DPH, int RPW, int CHUNK>
+__global__ __launch_bounds__(64 * kStreamWaves) void attn_rope_kernel(AttnArgs a, RopeArgs rp) {
+  __shared__ StreamLds<DPH, RPW, kStreamWaves> lds;
+  __shared__ float2 rope_cs[kRopeMaxQueries * (DPH / 2)];
+  stream_item<DPH, RPW, CHUNK, kStreamWaves, true>(a, blockIdx.x, blockIdx.y, blockIdx.z, lds,
+                                                   &rp, rope_cs);
+}
+
 }  // namespace attn
 }  // namespace sde
 
@@ -63,13 +73,17 @@ size_t partial_bytes(int nkv, int R, int n_parts, int dph) {
 }
 
 template <int DPH>
-int launch(const StreamPlan& p, const AttnArgs& a, int nkv, hipStream_t s) {
+int launch(const StreamPlan& p, const AttnArgs& a, int nkv, hipStream_t s,
+           const RopeArgs* rope = nullptr) {
   const dim3 grid(p.n_parts, nkv, p.row_groups);
   const dim3 block(64 * kStreamWaves);
-#define SDE_STREAM(R, C)                                     \
-  if (p.rpw == R && p.chunk == C) {                          \
-    attn_stream_kernel<DPH, R, C><<<grid, block, 0, s>>>(a); \
-    return sde::launch_status();                             \
+#define SDE_STREAM(R, C)                                              \
+  if (p.rpw == R && p.chunk == C) {                                   \
+    if (rope)                                                         \
+      attn_rope_kernel<DPH, R, C><<<grid, block, 0, s>>>(a, *rope);   \
+    else                                                              \
+      attn_stream_kernel<DPH, R, C><<<grid, block, 0, s>>>(a);        \
+    return sde::launch_status();                                      \
   }
   SDE_STREAM(2, 1)
   SDE_STREAM(2, 2)
@@ -117,12 +131,13 @@ size_t sde_grid_attention_workspace_size(int nh, int nkv, int dph, int n_queries
   return sde::grid_attention_workspace_size(nh, nkv, dph, n_queries, max_total_len);
 }
 
-int sde_paged_attention(sde_kv_cache* cache, int layer, const float* d_q,
-                        float* d_out, int nh, int nkv, int dph, int pos_base,
-                        int n_queries, void* d_workspace, size_t workspace_bytes,
-                        sde_stream_t stream) {
-  int st = check_attention(cache, layer, d_q, d_out, nh, nkv, dph, pos_base, n_queries);
-  if (st != SDE_OK) return st;
+}  // extern "C"
+
+namespace {
+
+int run_attention(sde_kv_cache* cache, int layer, const float* d_q, float* d_out, int nh,
+                  int nkv, int dph, int pos_base, int n_queries, void* d_workspace,
+                  size_t workspace_bytes, sde_stream_t stream, const RopeArgs* rope) {
   sde::DeviceGuard guard(cache->device);
   if (!guard.ok()) return SDE_ERR_HIP;
 
@@ -174,7 +189,56 @@ int sde_paged_attention(sde_kv_cache* cache, int layer, const float* d_q,
   a.qscale = (float)(kLog2e / std::sqrt((double)dph));
 
   const hipStream_t s = (hipStream_t)stream;
-  return dph == 128 ? launch<128>(plan, a, nkv, s) : launch<64>(plan, a, nkv, s);
+  return dph == 128 ? launch<128>(plan, a, nkv, s, rope) : launch<64>(plan, a, nkv, s, rope);
+}
+
+}  // namespace
+
+extern "C" {
+
+int sde_paged_attention(sde_kv_cache* cache, int layer, const float* d_q,
+                        float* d_out, int nh, int nkv, int dph, int pos_base,
+                        int n_queries, void* d_workspace, size_t workspace_bytes,
+                        sde_stream_t stream) {
+  const int st = check_attention(cache, layer, d_q, d_out, nh, nkv, dph, pos_base, n_queries);
+  if (st != SDE_OK) return st;
+  return run_attention(cache, layer, d_q, d_out, nh, nkv, dph, pos_base, n_queries,
+                       d_workspace, workspace_bytes, stream, nullptr);
+}
+
+int sde_rope_append_attention(sde_kv_cache* cache, int layer, const float* d_q,
+                              const float* d_k, const float* d_v, float* d_out, int nh,
+                              int nkv, int dph, int pos_base, int n_queries,
+                              const sde_rope_config* rope, void* d_workspace,
+                              size_t workspace_bytes, sde_stream_t stream) {
+  const int st = check_attention(cache, layer, d_q, d_out, nh, nkv, dph, pos_base, n_queries);
+  if (st != SDE_OK) return st;
+  if (!d_k || !d_v || !rope || rope->scaling_type < SDE_ROPE_NONE ||
+      rope->scaling_type > SDE_ROPE_YARN || !std::isfinite(rope->theta) ||
+      !std::isfinite(rope->scaling_factor))
+    return SDE_ERR_INVALID_ARGUMENT;
+  if ((((uintptr_t)d_k) & 3u) != 0 || (((uintptr_t)d_v) & 3u) != 0)
+    return SDE_ERR_INVALID_ARGUMENT;
+  if (n_queries > kRopeMaxQueries) return SDE_ERR_UNSUPPORTED;
+  // rope_apply_inplace (model.cu:281-323): theta defaults to 10000; NTK
+  // scales theta by factor^(dph/(dph-2)); linear and YaRN divide the
+  // position by the factor; each applies only for a factor above 1.
+  RopeArgs rp;
+  rp.k_new = d_k;
+  rp.v_new = d_v;
+  rp.pool = cache->pool;
+  const double factor = rope->scaling_factor;
+  double theta = rope->theta > 1e-6f ? (double)rope->theta : 10000.0;
+  if (rope->scaling_type == SDE_ROPE_NTK && factor > 1.0)
+    theta *= std::pow(factor, (double)dph / ((double)dph - 2.0));
+  const bool div = (rope->scaling_type == SDE_ROPE_LINEAR || rope->scaling_type == SDE_ROPE_YARN) &&
+                   factor > 1.0;
+  rp.pos_div = div ? rope->scaling_factor : 1.0f;
+  const double log_theta = std::log(theta);
+  for (int j = 0; j < 64; j++)
+    rp.inv_freq[j] = j < dph / 2 ? (float)std::exp(-log_theta * (2.0 * j) / dph) : 0.f;
+  return run_attention(cache, layer, d_q, d_out, nh, nkv, dph, pos_base, n_queries,
+                       d_workspace, workspace_bytes, stream, &rp);
 }
 
 int sde_attention_dispatch(int attn_type, sde_kv_cache* cache, int layer,

@@ -234,6 +234,38 @@ class KVCache:
             "paged_attention")
         return out
 
+    def rope_append_attention(self, layer: int, q: torch.Tensor, k: torch.Tensor,
+                              v: torch.Tensor, nh: int, nkv: int, dph: int, pos_base: int,
+                              theta: float = 10000.0, scaling_type: int = 0,
+                              scaling_factor: float = 1.0, out: Optional[torch.Tensor] = None,
+                              workspace: Optional[torch.Tensor] = None,
+                              stream=None) -> torch.Tensor:
+        """RoPE + append + attention in one launch (model.cu:346-384 with
+        cublas_rope_kernel, cublas_kv_append_kernel and
+        cublas_attention_kernel): q fp32 [M][nh*dph], k and v fp32
+        [M][nkv*dph], all before RoPE; q and k are rotated (rotate-half,
+        model.cu:281-323) at positions pos_base+m, k and v appended there,
+        and query m attends causally to [0, pos_base+m]."""
+        M = q.shape[0] if q.dim() == 2 else 1
+        q = _dev_f32(q.reshape(M, nh * dph), "q", (M, nh * dph))
+        k = _dev_f32(k.reshape(M, self.kv_dim), "k", (M, self.kv_dim))
+        v = _dev_f32(v.reshape(M, self.kv_dim), "v", (M, self.kv_dim))
+        if out is None:
+            out = torch.empty(M, nh * dph, dtype=torch.float32, device=self.device)
+        _dev_f32(out, "out", (M, nh * dph))
+        ws_ptr, ws_bytes = None, 0
+        if workspace is not None:
+            if workspace.device.type != "cuda" or not workspace.is_contiguous():
+                raise ValueError("workspace must be a contiguous CUDA tensor")
+            ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
+        rope = _native.RopeConfig(theta, scaling_type, scaling_factor)
+        check(self._lib.sde_rope_append_attention(
+            self.handle, layer, ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(k.data_ptr()),
+            ctypes.c_void_p(v.data_ptr()), ctypes.c_void_p(out.data_ptr()), nh, nkv, dph,
+            pos_base, M, ctypes.byref(rope), ctypes.c_void_p(ws_ptr), ws_bytes,
+            _stream_handle(stream)), "rope_append_attention")
+        return out
+
 
 # Reference-named entry points (kv_cache.h:56-63).
 def kv_cache_alloc(n_layers: int, d_head: int, max_blocks_per_layer: int,

@@ -335,3 +335,83 @@ def test_scripted_hashes_reproduce(oracle, name):
     for a, b in zip(marks, marks[1:]):
         if b[0].endswith("rollback"):
             assert a[2] == b[2] and b[1] <= a[1]
+
+
+# ---- RoPE restatement (rope_apply_inplace, model.cu:281-323) ----------------
+
+def _rope(oracle, x, nh, dph, pos, **kw):
+    return oracle.rope_rotate_half_f64(x, nh, dph, pos, **kw)
+
+
+def test_rope_f64_is_a_rotation_and_identity_at_zero(oracle):
+    rng = np.random.default_rng(3)
+    nh, dph = 4, 64
+    x = rng.standard_normal((5, nh * dph))
+    pos = np.array([0, 1, 17, 1000, 4095])
+    y = _rope(oracle, x, nh, dph, pos)
+    xr, yr = x.reshape(5, nh, 2, dph // 2), y.reshape(5, nh, 2, dph // 2)
+    np.testing.assert_allclose((yr ** 2).sum(2), (xr ** 2).sum(2), rtol=1e-12)
+    np.testing.assert_array_equal(y[0], x[0])
+
+
+def test_rope_f64_first_pair_turns_by_the_position(oracle):
+    # inv_freq[0] = 1: pair (0, dph/2) of every head turns by exactly pos radians
+    dph = 128
+    x = np.zeros((3, dph))
+    x[:, 0] = 1.0
+    pos = np.array([1, 7, 300])
+    y = _rope(oracle, x, 1, dph, pos)
+    np.testing.assert_allclose(y[:, 0], np.cos(pos), atol=1e-12)
+    np.testing.assert_allclose(y[:, dph // 2], np.sin(pos), atol=1e-12)
+
+
+def test_rope_f64_logits_depend_on_relative_position(oracle):
+    # RoPE's defining property: <R(m) q, R(n) k> depends on m - n only
+    rng = np.random.default_rng(4)
+    dph = 128
+    q, k = rng.standard_normal((1, dph)), rng.standard_normal((1, dph))
+    def logit(m, n):
+        return float((_rope(oracle, q, 1, dph, [m]) @ _rope(oracle, k, 1, dph, [n]).T)[0, 0])
+    for m, n, s in [(10, 3, 100), (500, 499, 1000), (64, 0, 7)]:
+        assert abs(logit(m, n) - logit(m + s, n + s)) < 2e-3 * (1 + abs(logit(m, n)))
+
+
+def test_rope_f64_matches_the_fp32_restatement(oracle):
+    from speculative_decode_engine_amd import workloads as W
+    rng = np.random.default_rng(5)
+    nh, dph = 2, 64
+    x = rng.standard_normal((1, nh * dph)).astype(np.float32)
+    for pos in [0, 3, 129, 2000]:
+        a = _rope(oracle, x, nh, dph, [pos])
+        b = W.rope_rotate_half(x, nh, dph, pos)
+        np.testing.assert_allclose(a, b, atol=2e-4 * (1 + pos / 1000))
+
+
+def test_rope_f64_scaling_modes(oracle):
+    rng = np.random.default_rng(6)
+    nh, dph = 2, 64
+    x = rng.standard_normal((1, nh * dph))
+    # linear and YaRN divide the position (exact here: 96 / 4 = 24)
+    for t in (oracle.ROPE_LINEAR, oracle.ROPE_YARN):
+        np.testing.assert_allclose(_rope(oracle, x, nh, dph, [96], scaling_type=t, factor=4.0),
+                                   _rope(oracle, x, nh, dph, [24]), atol=1e-12)
+    # NTK scales theta; a factor <= 1 changes nothing
+    th = 10000.0 * 2.0 ** (dph / (dph - 2.0))
+    np.testing.assert_allclose(oracle.rope_inv_freq(dph, 10000.0, oracle.ROPE_NTK, 2.0),
+                               oracle.rope_inv_freq(dph, th), rtol=1e-6)
+    np.testing.assert_array_equal(_rope(oracle, x, nh, dph, [50], scaling_type=oracle.ROPE_NTK,
+                                        factor=1.0), _rope(oracle, x, nh, dph, [50]))
+    # theta <= 1e-6 selects 10000 (model.cu:290)
+    np.testing.assert_array_equal(oracle.rope_inv_freq(dph, 0.0), oracle.rope_inv_freq(dph))
+
+
+def test_rope_f64_planted_interleaved_pairing_fails(oracle):
+    # GPT-J pairing (2j, 2j+1) is not the reference's rotate-half pairing
+    from speculative_decode_engine_amd import workloads as W
+    rng = np.random.default_rng(7)
+    dph = 64
+    x = rng.standard_normal((1, dph)).astype(np.float32)
+    perm = np.concatenate([np.arange(0, dph, 2), np.arange(1, dph, 2)])
+    inter = np.empty(dph)
+    inter[perm] = _rope(oracle, x[:, perm], 1, dph, [40])[0]
+    assert np.abs(inter - W.rope_rotate_half(x, 1, dph, 40)[0]).max() > 1e-2
