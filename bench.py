@@ -137,8 +137,11 @@ def make_rotation_cache(torch, W, w, n_layers, l_max, pool_blocks, seed):
 def bench_config(torch, W, w, steps, warmup, mode):
     """Times one layer-step of workload w.  mode: 'attn' (attention only),
     'decode' (append 1 + 1-query attention), 'verify' (append k+1 +
-    (k+1)-query causal attention).  Returns a dict."""
-    n_q = 1 if mode in ("attn", "decode") else w.n_queries
+    (k+1)-query causal attention), and 'decode_fused' / 'verify_fused'
+    (the same steps with RoPE of q and k, append and attention in one
+    sde_rope_append_attention launch).  Returns a dict."""
+    fused = mode.endswith("_fused")
+    n_q = 1 if mode in ("attn", "decode", "decode_fused") else w.n_queries
     n_app = 0 if mode == "attn" else n_q
     pos_base = w.ctx if mode != "attn" else w.l_max - 1
     l_max = pos_base + n_q
@@ -159,13 +162,17 @@ def bench_config(torch, W, w, steps, warmup, mode):
 
     def step(i):
         l = i % n_layers
+        if fused:
+            cache.rope_append_attention(l, q[l], k[l], v[l], w.nh, w.nkv, w.dph, pos_base,
+                                        theta=w.rope_theta, out=out, workspace=ws)
+            return
         if n_app:
             cache.append(l, k[l], v[l], pos_base)
         cache.attention(l, q[l], w.nh, w.nkv, w.dph, pos_base, out=out, workspace=ws)
 
     # eager: per-launch HIP events (attention only) and the bracket
     timer = Timer(torch, steps)
-    eager_ms, launch_ms = timer.run(step, steps, warmup, per_launch=(n_app == 0))
+    eager_ms, launch_ms = timer.run(step, steps, warmup, per_launch=(n_app == 0 or fused))
     # timed: the steps captured into one HIP graph, replayed between events
     ms = graph_step_ms(torch, step, steps, warmup)
     nbytes = w.algorithmic_bytes(l_max=l_max, n_app=n_app, n_queries=n_q)
@@ -281,11 +288,19 @@ def main():
         configs["llama3_8b_4k_decode"] = dec
         configs["llama3_8b_4k_attn"] = att4
         extra["verify_over_decode"] = round(ver["us_per_layer_step"] / dec["us_per_layer_step"], 3)
+        verf = bench_config(torch, W, w3, steps, warmup, "verify_fused")
+        decf = bench_config(torch, W, w3, steps, warmup, "decode_fused")
+        configs["llama3_8b_verify_fused"] = verf
+        configs["llama3_8b_4k_decode_fused"] = decf
+        extra["verify_over_decode_fused"] = round(verf["us_per_layer_step"] /
+                                                  decf["us_per_layer_step"], 3)
         for name in ("tiny", "tinyllama"):
             configs[name] = bench_config(torch, W, W.CONFIGS[name], steps, warmup, "decode")
         w5 = W.CONFIGS["qwen25_7b_selfspec"]
         configs["qwen25_7b_selfspec_verify"] = bench_config(torch, W, w5, steps, warmup, "verify")
         configs["qwen25_7b_selfspec_draft"] = bench_config(torch, W, w5, steps, warmup, "decode")
+        configs["qwen25_7b_selfspec_verify_fused"] = bench_config(torch, W, w5, steps, warmup,
+                                                                  "verify_fused")
         extra["rollback_us"] = bench_rollback(torch, W)
         for k_, v_ in configs.items():
             log(f"[bench] {k_}: {v_['us_per_layer_step']} us/layer-step, {v_['gbps']} GB/s")

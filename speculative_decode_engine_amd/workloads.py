@@ -30,6 +30,7 @@ class Workload:
     n_queries: int    # 1 = decode step, k+1 = verify window
     seed: int
     draft_layers: int = 0  # self-speculative: layers the draft runs
+    rope_theta: float = 10000.0  # the model family's RoPE base (fused-path bench)
     note: str = ""
 
     @property
@@ -83,16 +84,16 @@ CONFIGS: dict[str, Workload] = {
         note="TinyLlama-1.1B-shaped decode: one append + one single-query attention"),
     "llama3_8b_verify": Workload(
         "llama3_8b_verify", n_layers=32, nh=32, nkv=8, dph=128, block_size=16, ctx=4096,
-        pool_blocks=32 * 257, n_queries=5, seed=3,
+        pool_blocks=32 * 257, n_queries=5, seed=3, rope_theta=500000.0,
         note="Llama-3-8B-shaped verify: append k+1=5, causal attention, rollback, re-append"),
     "llama3_8b_32k": Workload(
         "llama3_8b_32k", n_layers=32, nh=32, nkv=8, dph=128, block_size=16, ctx=32767,
-        pool_blocks=131072, n_queries=1, seed=4,
+        pool_blocks=131072, n_queries=1, seed=4, rope_theta=500000.0,
         note="Llama-3-8B-shaped 32K decode: attention over 32768 keys in a fragmented "
              "131072-block pool"),
     "qwen25_7b_selfspec": Workload(
         "qwen25_7b_selfspec", n_layers=28, nh=28, nkv=4, dph=128, block_size=32, ctx=8192,
-        pool_blocks=28 * 257, n_queries=9, seed=5, draft_layers=8,
+        pool_blocks=28 * 257, n_queries=9, seed=5, draft_layers=8, rope_theta=1000000.0,
         note="Qwen2.5-7B-shaped self-spec: 8 draft layers x 8 decode steps, then 9-query "
              "full-depth verify with partial rollback"),
 }
