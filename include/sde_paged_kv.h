@@ -196,6 +196,27 @@ int sde_paged_attention(sde_kv_cache* cache, int layer, const float* d_q,
                         int n_queries, void* d_workspace,
                         size_t workspace_bytes, sde_stream_t stream);
 
+/* Greedy acceptance + O(1) rewind of speculative decoding on the device,
+ * with no host round trip (the reference's host loop kernels.cu:2428-2466
+ * copies the tokens back and rewinds from the host; its megakernel does it
+ * on thread 0, kernels.cu:3050-3072).  d_draft_tokens [k] and
+ * d_target_tokens [k+1] (the verify window's argmaxes) are device int32.
+ * Writes d_result[0..3] = {n_accepted, bonus token, target seq_len, draft
+ * seq_len} and d_result[4 .. 4+n_accepted] = the emitted tokens (accepted
+ * drafts, then the bonus): k+5 int32.  The target cache's seq_len becomes
+ * target_save + n_accepted + 1; the draft cache's draft_save + n_accepted
+ * (the reference's rule), or the target's value when draft is NULL or the
+ * target itself (self-speculation over one cache).  The caches' host copy
+ * of seq_len is refreshed from the device on the next host call that needs
+ * it (sde_kv_seq_len, sde_kv_rollback), which then synchronizes the
+ * device.  0 <= k <= 64; target_save + k + 1 and draft_save + k within the
+ * caches' capacity (SDE_ERR_RANGE otherwise). */
+int sde_spec_accept_greedy(sde_kv_cache* target, sde_kv_cache* draft,
+                           const int32_t* d_draft_tokens,
+                           const int32_t* d_target_tokens, int k,
+                           int target_save, int draft_save, int32_t* d_result,
+                           sde_stream_t stream);
+
 /* RoPE scaling types: the reference's RopeScalingType (config.h:42-47). */
 enum {
   SDE_ROPE_NONE = 0,

@@ -213,6 +213,23 @@ def run_script(model: PagedKVModel, ops, on_checkpoint=None, on_attend=None) -> 
     return marks
 
 
+def spec_accept_greedy(draft_tokens, target_tokens, k: int, target_save: int,
+                       draft_save: int, shared: bool):
+    """Greedy acceptance and rewind of the reference's loop
+    (kernels.cu:2428-2466; megakernel kernels.cu:3050-3072): n = leading
+    drafts equal to the target's argmaxes, emit drafts[:n] + [bonus =
+    target[n]], target seq_len = target_save + n + 1, draft seq_len =
+    draft_save + n (the target's value for one shared cache).  Returns
+    (n, bonus, target_seq, draft_seq, emitted)."""
+    n = 0
+    while n < k and int(draft_tokens[n]) == int(target_tokens[n]):
+        n += 1
+    target_seq = target_save + n + 1
+    draft_seq = target_seq if shared else draft_save + n
+    emitted = [int(t) for t in draft_tokens[:n]] + [int(target_tokens[n])]
+    return n, int(target_tokens[n]), target_seq, draft_seq, emitted
+
+
 ROPE_NONE, ROPE_LINEAR, ROPE_NTK, ROPE_YARN = 0, 1, 2, 3  # config.h:42-47
 
 

@@ -13,6 +13,7 @@
 #include <cstring>
 #include <new>
 
+#include "sde/spec_device.hpp"
 #include "sde_internal.hpp"
 
 namespace sde {
@@ -105,6 +106,20 @@ __global__ __launch_bounds__(kAppendThreads) void gather_kernel(
 // the write stays stream-ordered and safe to record into a HIP graph.
 __global__ void set_seq_len_kernel(int32_t* seq_len, int value) {
   if (threadIdx.x == 0) *seq_len = value;
+}
+
+// sde_spec_accept_greedy: one thread applies the reference's greedy rule.
+__global__ void spec_accept_kernel(const int32_t* draft_tokens, const int32_t* target_tokens,
+                                   int k, int target_save, int draft_save, sde_kv_view target,
+                                   sde_kv_view draft, int has_draft, int32_t* result) {
+  if (threadIdx.x != 0) return;
+  const SpecAccept r = spec_accept_greedy(draft_tokens, target_tokens, k, target_save,
+                                          draft_save, target, has_draft ? &draft : nullptr,
+                                          result + 4);
+  result[0] = r.n_accepted;
+  result[1] = r.bonus;
+  result[2] = r.target_seq;
+  result[3] = r.draft_seq;
 }
 
 }  // namespace kv
@@ -276,7 +291,10 @@ int sde_kv_set_seq_len(sde_kv_cache* cache, int len, sde_stream_t stream) {
   hipLaunchKernelGGL(set_seq_len_kernel, dim3(1), dim3(64), 0,
                      (hipStream_t)stream, cache->d_seq_len, len);
   const int st = sde::launch_status();
-  if (st == SDE_OK) cache->seq_len = len;
+  if (st == SDE_OK) {
+    cache->seq_len = len;
+    cache->seq_len_on_device = false;
+  }
   return st;
 }
 
@@ -284,16 +302,63 @@ int sde_kv_reset(sde_kv_cache* cache, sde_stream_t stream) {
   return sde_kv_set_seq_len(cache, 0, stream);
 }
 
+// Refreshes the host mirror after a device-side rewind (synchronizes).
+static int refresh_seq_len(sde_kv_cache* cache) {
+  if (!cache->seq_len_on_device) return SDE_OK;
+  int v = 0;
+  const int st = sde_kv_device_seq_len(cache, &v);
+  if (st != SDE_OK) return st;
+  cache->seq_len = v;
+  cache->seq_len_on_device = false;
+  return SDE_OK;
+}
+
 int sde_kv_rollback(sde_kv_cache* cache, int target_len, sde_stream_t stream) {
   if (!cache) return SDE_ERR_INVALID_ARGUMENT;
+  const int st = refresh_seq_len(cache);
+  if (st != SDE_OK) return st;
   if (target_len < 0 || target_len > cache->seq_len) return SDE_ERR_RANGE;
   return sde_kv_set_seq_len(cache, target_len, stream);
 }
 
 int sde_kv_seq_len(const sde_kv_cache* cache, int* out_len) {
   if (!cache || !out_len) return SDE_ERR_INVALID_ARGUMENT;
+  const int st = refresh_seq_len(const_cast<sde_kv_cache*>(cache));
+  if (st != SDE_OK) return st;
   *out_len = cache->seq_len;
   return SDE_OK;
+}
+
+int sde_spec_accept_greedy(sde_kv_cache* target, sde_kv_cache* draft,
+                           const int32_t* d_draft_tokens, const int32_t* d_target_tokens, int k,
+                           int target_save, int draft_save, int32_t* d_result,
+                           sde_stream_t stream) {
+  if (!target || !d_target_tokens || !d_result || (k > 0 && !d_draft_tokens))
+    return SDE_ERR_INVALID_ARGUMENT;
+  if (k < 0 || k > 64 || target_save < 0 || draft_save < 0) return SDE_ERR_RANGE;
+  const bool has_draft = draft != nullptr && draft != target;
+  const int64_t t_cap = (int64_t)target->cfg.max_blocks_per_layer * target->cfg.block_size;
+  if ((int64_t)target_save + k + 1 > t_cap) return SDE_ERR_RANGE;
+  if (has_draft) {
+    if (draft->device != target->device) return SDE_ERR_INVALID_ARGUMENT;
+    const int64_t d_cap = (int64_t)draft->cfg.max_blocks_per_layer * draft->cfg.block_size;
+    if ((int64_t)draft_save + k > d_cap) return SDE_ERR_RANGE;
+  }
+  sde::DeviceGuard g(target->device);
+  if (!g.ok()) return SDE_ERR_HIP;
+  sde_kv_view tv, dv{};
+  int st = sde_kv_get_view(target, &tv);
+  if (st == SDE_OK && has_draft) st = sde_kv_get_view(draft, &dv);
+  if (st != SDE_OK) return st;
+  hipLaunchKernelGGL(spec_accept_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream,
+                     d_draft_tokens, d_target_tokens, k, target_save, draft_save, tv, dv,
+                     has_draft ? 1 : 0, d_result);
+  st = sde::launch_status();
+  if (st == SDE_OK) {
+    target->seq_len_on_device = true;
+    if (has_draft) draft->seq_len_on_device = true;
+  }
+  return st;
 }
 
 int sde_kv_device_seq_len(const sde_kv_cache* cache, int* out_len) {

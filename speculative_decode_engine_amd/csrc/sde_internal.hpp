@@ -23,6 +23,7 @@ struct sde_kv_cache {
   std::vector<int32_t> n_mapped;        // leading mapped logical blocks per layer
   int32_t* d_seq_len = nullptr;
   int seq_len = 0;                      // host mirror of *d_seq_len
+  bool seq_len_on_device = false;       // *d_seq_len was set by a device-side rewind
   void* workspace = nullptr;            // internal attention workspace
   size_t workspace_bytes = 0;
   // Arrival counters of the fused partition combine, one per (KV head, row

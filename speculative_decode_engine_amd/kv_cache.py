@@ -267,6 +267,27 @@ class KVCache:
         return out
 
 
+def spec_accept_greedy(target: KVCache, draft: Optional[KVCache], draft_tokens: torch.Tensor,
+                       target_tokens: torch.Tensor, k: int, target_save: int, draft_save: int,
+                       out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    """Greedy acceptance + O(1) rewind on the device (kernels.cu:2428-2466,
+    3050-3072): returns the device int32 result [k+5] = (n_accepted, bonus,
+    target seq_len, draft seq_len, emitted tokens...).  draft None or target
+    = one shared cache (self-speculation)."""
+    for name, t in (("draft_tokens", draft_tokens), ("target_tokens", target_tokens)):
+        if t.device.type != "cuda" or t.dtype != torch.int32 or not t.is_contiguous():
+            raise TypeError(f"{name} must be a contiguous CUDA int32 tensor")
+    if out is None:
+        out = torch.empty(k + 5, dtype=torch.int32, device=target.device)
+    lib = _native.load()
+    check(lib.sde_spec_accept_greedy(
+        target.handle, draft.handle if draft is not None else None,
+        ctypes.c_void_p(draft_tokens.data_ptr()), ctypes.c_void_p(target_tokens.data_ptr()), k,
+        target_save, draft_save, ctypes.c_void_p(out.data_ptr()), _stream_handle(stream)),
+        "spec_accept_greedy")
+    return out
+
+
 # Reference-named entry points (kv_cache.h:56-63).
 def kv_cache_alloc(n_layers: int, d_head: int, max_blocks_per_layer: int,
                    block_size: int = KV_BLOCK_SIZE, pool_blocks: int = 0,

@@ -18,8 +18,9 @@ import torch
 
 from conftest import case_banner
 from test_spec_decode import CFG, K, N_NEW, POSITIONS, PROMPT
+from speculative_decode_engine_amd import KVCache, spec_accept_greedy
 from tiny_llama import (DeviceCache, OracleCache, TinyLlama, greedy, spec_self,
-                        spec_two_model)
+                        spec_two_model, spec_two_model_reference)
 
 pytestmark = pytest.mark.gpu
 
@@ -61,4 +62,79 @@ def test_library_speculation_emits_greedy_tokens(gpu, oracle, seed, mode):
         np.testing.assert_allclose(k, gk, rtol=2e-3, atol=2e-3)
         np.testing.assert_allclose(v, gv, rtol=2e-3, atol=2e-3)
     for c in caches + [gcache]:
+        c.free()
+
+
+# ---- on-device greedy acceptance + rewind (sde_spec_accept_greedy) ----------
+
+@pytest.mark.parametrize("k", [0, 1, 4, 8])
+def test_device_accept_rule_and_rewinds(gpu, oracle, k):
+    case_banner("device accept", k)
+    rng = np.random.default_rng(k)
+    tc = KVCache(1, 64, 8, 16, 8)
+    dc = KVCache(1, 64, 8, 16, 8)
+    for n_match in range(k + 1):
+        ts, ds = 40 + n_match, 30 + n_match
+        tc.set_seq_len(ts + k + 1)
+        dc.set_seq_len(ds + k)
+        drafts = rng.integers(0, 1000, size=k).astype(np.int32)
+        targets = rng.integers(1000, 2000, size=k + 1).astype(np.int32)
+        targets[:n_match] = drafts[:n_match]
+        d = torch.from_numpy(drafts if k else np.zeros(1, np.int32)).cuda()
+        t = torch.from_numpy(targets).cuda()
+        res = spec_accept_greedy(tc, dc, d, t, k, ts, ds).cpu().numpy()
+        n, bonus, t_seq, d_seq, emitted = oracle.spec_accept_greedy(drafts, targets, k, ts, ds,
+                                                                    shared=False)
+        assert list(res[:4]) == [n, bonus, t_seq, d_seq] and n == n_match
+        assert list(res[4:4 + n + 1]) == emitted
+        assert tc.device_seq_len() == t_seq and dc.device_seq_len() == d_seq
+        assert tc.seq_len == t_seq and dc.seq_len == d_seq      # host mirrors refreshed
+    # one shared cache (self-speculation): draft None or the target itself
+    for draft in (None, tc):
+        tc.set_seq_len(50 + k + 1)
+        targets = rng.integers(0, 9, size=k + 1).astype(np.int32)
+        d = torch.from_numpy(np.full(max(k, 1), -1, np.int32)).cuda()
+        res = spec_accept_greedy(tc, draft, d, torch.from_numpy(targets).cuda(), k, 50, 0).cpu()
+        assert list(res[:4].numpy()) == [0, targets[0], 51, 51]
+        assert tc.device_seq_len() == 51
+    tc.free()
+    dc.free()
+
+
+def test_device_accept_errors(gpu):
+    case_banner("device accept errors")
+    tc = KVCache(1, 64, 2, 16, 2)   # capacity 32 positions
+    d = torch.zeros(4, dtype=torch.int32, device="cuda")
+    with pytest.raises(Exception):
+        spec_accept_greedy(tc, None, d, d, 4, 28, 0)        # 28 + 4 + 1 > 32
+    with pytest.raises(Exception):
+        spec_accept_greedy(tc, None, d, d, 65, 0, 0)        # k > 64
+    tc.free()
+
+
+@pytest.mark.parametrize("mode", ["perturbed", "identical"])
+def test_reference_loop_with_device_accept_emits_greedy_tokens(gpu, oracle, mode):
+    """The reference's host loop with acceptance and both rewinds done on the
+    device (only the result row is copied back, as the reference copies
+    tokens) emits the greedy tokens."""
+    case_banner("reference loop, device accept", mode)
+    seed = 2
+    target = TinyLlama(CFG, seed, device="cuda")
+    gcache = DeviceCache(CFG, CFG.n_layers, POSITIONS, seed)
+    ref = greedy(target, gcache, PROMPT, N_NEW)
+    draft = target if mode == "identical" else TinyLlama(
+        CFG, seed + 100, device="cuda", base=target, noise=0.05, n_layers=2)
+    tc = DeviceCache(CFG, CFG.n_layers, POSITIONS, seed)
+    dc = DeviceCache(CFG, draft.n_layers, POSITIONS, seed + 1)
+
+    def accept(drafts, tt, k, ts, ds):
+        d = torch.tensor(drafts if k else [0], dtype=torch.int32, device="cuda")
+        t = tt.reshape(-1).to(torch.int32).contiguous()
+        res = spec_accept_greedy(tc.c, dc.c, d, t, k, ts, ds).cpu().tolist()
+        n = res[0]
+        return n, res[1], res[2], res[3], res[4:4 + n + 1]
+    stats = {}
+    out = spec_two_model_reference(target, draft, tc, dc, PROMPT, N_NEW, K, accept, stats)
+    assert out == ref, stats["accepted"]
+    for c in (gcache, tc, dc):
         c.free()

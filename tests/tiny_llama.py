@@ -307,3 +307,55 @@ def spec_self(model: TinyLlama, cache, prompt, n_new: int, k: int, n_draft: int,
             stats.setdefault("accepted", []).append(n_acc)
         last = tt[n_acc]
     return out[:n_new]
+
+
+def spec_two_model_reference(target: TinyLlama, draft: TinyLlama, tcache, dcache, prompt,
+                             n_new: int, k: int, accept, stats: dict | None = None) -> list[int]:
+    """The reference's multi-kernel host loop (kernels.cu:2314-2475) step for
+    step: host-side seq positions, the draft rewound to draft_save + n_acc
+    (and, when every draft was accepted, one extra draft forward of d_k,
+    kernels.cu:2466-2476), the target to target_save + n_acc + 1.  `accept`
+    does the acceptance and both rewinds: accept(draft_tokens, target_tokens,
+    k, target_save, draft_save) -> (n_acc, bonus, target_seq, draft_seq,
+    emitted), either the oracle's rule plus host rewinds or the device
+    entry point."""
+    last = prefill(target, tcache, prompt)
+    prefill(draft, dcache, prompt)
+    out = [last]
+    target_seq = draft_seq = len(prompt)
+    while len(out) < n_new:
+        cur_k = min(k, n_new - len(out))
+        target_save, draft_save = target_seq, draft_seq
+        drafts, cur = [], last
+        for _ in range(cur_k):
+            x = draft.layers(draft.embed([cur]), dcache, draft_seq, 0, draft.n_layers)
+            draft_seq += 1
+            dcache.set_seq_len(draft_seq)
+            cur = _argmax(draft.logits(x))[0]
+            drafts.append(cur)
+        x = target.layers(target.embed([last] + drafts), tcache, target_seq, 0, target.n_layers)
+        target_seq += cur_k + 1
+        tcache.set_seq_len(target_seq)
+        tt = torch.argmax(target.logits(x), dim=-1)
+        n_acc, bonus, target_seq, draft_seq, emitted = accept(drafts, tt, cur_k, target_save,
+                                                              draft_save)
+        out += emitted
+        if n_acc == cur_k:
+            draft.layers(draft.embed([drafts[-1]]), dcache, draft_seq, 0, draft.n_layers)
+            draft_seq += 1
+            dcache.set_seq_len(draft_seq)
+        if stats is not None:
+            stats.setdefault("accepted", []).append(n_acc)
+        last = bonus
+    return out[:n_new]
+
+
+def host_accept(oracle, tcache, dcache):
+    """The oracle's greedy rule with the rewinds done from the host."""
+    def accept(drafts, tt, k, target_save, draft_save):
+        r = oracle.spec_accept_greedy(drafts, [int(t) for t in tt.reshape(-1).cpu()], k,
+                                      target_save, draft_save, shared=False)
+        tcache.rollback(r[2])
+        dcache.rollback(r[3])
+        return r
+    return accept
