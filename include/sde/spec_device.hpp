@@ -53,4 +53,50 @@ __device__ inline SpecAccept spec_accept_greedy(const int32_t* draft_tokens,
   return r;
 }
 
+
+// ---- stochastic acceptance (kernels.cu:285-291, 319-380, 550-572) ----------
+
+// Philox4x32-10 (Salmon, Moraes, Dror, Shaw: "Parallel random numbers: as
+// easy as 1, 2, 3", SC'11): a counter-based generator, so any (key,
+// counter) pair is a stream position that every thread computes directly.
+// The reference draws from a sequential curand state instead; draws are
+// therefore not the reference's, only their distribution is.
+struct Philox4 {
+  uint32_t v[4];
+};
+
+__host__ __device__ inline Philox4 philox4x32_10(uint32_t c0, uint32_t c1, uint32_t c2,
+                                                 uint32_t c3, uint32_t k0, uint32_t k1) {
+  constexpr uint32_t kM0 = 0xD2511F53u, kM1 = 0xCD9E8D57u;  // round multipliers
+  constexpr uint32_t kW0 = 0x9E3779B9u, kW1 = 0xBB67AE85u;  // key schedule (Weyl)
+  for (int r = 0; r < 10; r++) {
+    const uint64_t p0 = (uint64_t)kM0 * c0;
+    const uint64_t p1 = (uint64_t)kM1 * c2;
+    const uint32_t n0 = (uint32_t)(p1 >> 32) ^ c1 ^ k0;
+    const uint32_t n2 = (uint32_t)(p0 >> 32) ^ c3 ^ k1;
+    c0 = n0;
+    c1 = (uint32_t)p1;
+    c2 = n2;
+    c3 = (uint32_t)p0;
+    k0 += kW0;
+    k1 += kW1;
+  }
+  return Philox4{{c0, c1, c2, c3}};
+}
+
+// Uniform in (0, 1): the top 24 bits, centred in their interval.
+__host__ __device__ inline float philox_uniform(uint32_t x) {
+  return ((float)(x >> 8) + 0.5f) * (1.0f / 16777216.0f);
+}
+
+// The two draws of window row b in one call: [0] the accept test,
+// [1] the token sample.  Counter = (b, offset lo, offset hi, 0).
+__host__ __device__ inline void spec_draws(uint64_t seed, uint64_t offset, int b, float& u_accept,
+                                           float& u_sample) {
+  const Philox4 r = philox4x32_10((uint32_t)b, (uint32_t)offset, (uint32_t)(offset >> 32), 0u,
+                                  (uint32_t)seed, (uint32_t)(seed >> 32));
+  u_accept = philox_uniform(r.v[0]);
+  u_sample = philox_uniform(r.v[1]);
+}
+
 }  // namespace sde

@@ -217,6 +217,32 @@ int sde_spec_accept_greedy(sde_kv_cache* target, sde_kv_cache* draft,
                            int target_save, int draft_save, int32_t* d_result,
                            sde_stream_t stream);
 
+/* Stochastic acceptance (Leviathan / Chen speculative sampling) + O(1)
+ * rewind on the device: the reference's batch_stochastic_accept_kernel
+ * (kernels.cu:550-572: accept draft i iff u < min(1, p_i / q_i), p_i the
+ * target's and q_i the draft's probability of draft token i), its
+ * correction sample on the first rejection (corrected_sample_adjusted_logits,
+ * kernels.cu:319-380: a token from norm(max(0, p - q)), or from p when that
+ * is empty), the bonus sample from p at row k when every draft was
+ * accepted (softmax_sample_temperature_kernel), and the rewinds of
+ * sde_spec_accept_greedy.  d_target_logits fp32 [k+1][vocab] (softmax at
+ * temp_target), d_draft_logits fp32 [k][vocab] (at temp_draft; temperatures
+ * below 1e-6 act as 1e-6), d_draft_tokens int32 [k].  Random draws:
+ * Philox4x32-10 keyed by `seed` at the call index *d_rng_offset (a device
+ * uint64 the call increments), two draws per window row, so a call is a
+ * pure function of its inputs and the offset.  d_result as for
+ * sde_spec_accept_greedy (k+5 int32: n_accepted, emitted token after the
+ * accepted drafts, target seq_len, draft seq_len, emitted tokens).
+ * 0 <= k <= 64, vocab >= 1.  One workgroup per window row. */
+int sde_spec_accept_stochastic(sde_kv_cache* target, sde_kv_cache* draft,
+                               const float* d_target_logits,
+                               const float* d_draft_logits,
+                               const int32_t* d_draft_tokens, int k, int vocab,
+                               float temp_target, float temp_draft, uint64_t seed,
+                               uint64_t* d_rng_offset, int target_save,
+                               int draft_save, int32_t* d_result,
+                               sde_stream_t stream);
+
 /* RoPE scaling types: the reference's RopeScalingType (config.h:42-47). */
 enum {
   SDE_ROPE_NONE = 0,

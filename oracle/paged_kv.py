@@ -230,6 +230,88 @@ def spec_accept_greedy(draft_tokens, target_tokens, k: int, target_save: int,
     return n, int(target_tokens[n]), target_seq, draft_seq, emitted
 
 
+_PHILOX_M = (0xD2511F53, 0xCD9E8D57)   # Salmon et al., SC'11 (Philox4x32)
+_PHILOX_W = (0x9E3779B9, 0xBB67AE85)
+
+
+def philox4x32_10(ctr, key) -> list:
+    """Philox4x32-10 (Salmon, Moraes, Dror, Shaw, "Parallel random numbers:
+    as easy as 1, 2, 3", SC'11), the counter-based generator of
+    sde_spec_accept_stochastic: 10 rounds of two 32x32->64 multiplies,
+    Weyl key schedule.  ctr: 4 uint32, key: 2 uint32; returns 4 uint32."""
+    c = [int(x) & 0xFFFFFFFF for x in ctr]
+    k0, k1 = int(key[0]) & 0xFFFFFFFF, int(key[1]) & 0xFFFFFFFF
+    for _ in range(10):
+        p0 = _PHILOX_M[0] * c[0]
+        p1 = _PHILOX_M[1] * c[2]
+        c = [((p1 >> 32) ^ c[1] ^ k0) & 0xFFFFFFFF, p1 & 0xFFFFFFFF,
+             ((p0 >> 32) ^ c[3] ^ k1) & 0xFFFFFFFF, p0 & 0xFFFFFFFF]
+        k0 = (k0 + _PHILOX_W[0]) & 0xFFFFFFFF
+        k1 = (k1 + _PHILOX_W[1]) & 0xFFFFFFFF
+    return c
+
+
+def spec_draws(seed: int, offset: int, b: int) -> tuple:
+    """(u_accept, u_sample) of window row b of call `offset`: counter
+    (b, offset lo, offset hi, 0), key = seed; u = ((x >> 8) + 0.5) / 2^24."""
+    r = philox4x32_10([b, offset & 0xFFFFFFFF, (offset >> 32) & 0xFFFFFFFF, 0],
+                      [seed & 0xFFFFFFFF, (seed >> 32) & 0xFFFFFFFF])
+    return tuple(float(np.float32(((x >> 8) + 0.5) / 16777216.0)) for x in r[:2])
+
+
+def spec_accept_stochastic(target_logits, draft_logits, draft_tokens, k: int,
+                           temp_target: float, temp_draft: float, seed: int, offset: int,
+                           target_save: int, draft_save: int, shared: bool) -> dict:
+    """Speculative sampling with the reference's rules, in float64:
+    draft token i is accepted iff u_i < min(1, p_i / max(q_i, 1e-36)) with
+    p = softmax(target_logits[i] / T_t), q = softmax(draft_logits[i] / T_d)
+    (batch_stochastic_accept_kernel, kernels.cu:550-572; temperatures below
+    1e-6 act as 1e-6); the first rejection at i emits a token sampled from
+    norm(max(0, p - q)), or from p when that is empty
+    (device_corrected_adjusted_sample, kernels.cu:319-380); with every draft
+    accepted the bonus is sampled from p of row k.  A sample is the smallest
+    token whose cumulative weight reaches u * total.  Rewinds as
+    spec_accept_greedy.  Returns the result and, per row, the distance of
+    the accept test and of the sample from their decision boundaries."""
+    tl = np.asarray(target_logits, np.float64)
+    dl = np.asarray(draft_logits, np.float64) if k else None
+    it, idr = 1.0 / max(temp_target, 1e-6), 1.0 / max(temp_draft, 1e-6)
+
+    def softmax(x):
+        e = np.exp(x - x.max())
+        return e / e.sum()
+    flags, tokens, acc_margin, smp_margin = [], [], [], []
+    for b in range(k + 1):
+        ua, us = spec_draws(seed, offset, b)
+        p = softmax(tl[b] * it)
+        if b < k:
+            q = softmax(dl[b] * idr)
+            d = int(draft_tokens[b])
+            cap = min(1.0, p[d] / max(q[d], 1e-36))
+            flags.append(ua < cap)
+            acc_margin.append(abs(ua - cap))
+            w = np.maximum(p - q, 0.0)
+            if w.sum() <= 1e-20:
+                w = p
+        else:
+            w = p
+        cdf = np.cumsum(w)
+        goal = us * cdf[-1]
+        idx = np.nonzero((cdf >= goal) & (w > 0))[0]
+        tok = int(idx[0]) if idx.size else int(np.nonzero(w > 0)[0][-1])
+        tokens.append(tok)
+        lo = cdf[tok] - w[tok]
+        smp_margin.append(min(abs(goal - lo), abs(cdf[tok] - goal)) / cdf[-1])
+    n = 0
+    while n < k and flags[n]:
+        n += 1
+    t_seq = target_save + n + 1
+    return dict(n_accepted=n, token=tokens[n], target_seq=t_seq,
+                draft_seq=t_seq if shared else draft_save + n,
+                emitted=[int(t) for t in draft_tokens[:n]] + [tokens[n]],
+                flags=flags, tokens=tokens, accept_margin=acc_margin, sample_margin=smp_margin)
+
+
 ROPE_NONE, ROPE_LINEAR, ROPE_NTK, ROPE_YARN = 0, 1, 2, 3  # config.h:42-47
 
 

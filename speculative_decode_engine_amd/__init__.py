@@ -5,9 +5,10 @@ in csrc/).  This package holds its ctypes binding, a host-side mirror of the
 reference KVCache API (kv_cache.py) and the benchmark workloads.
 """
 from .kv_cache import (ATTN_KDA, ATTN_LINEAR, ATTN_SLIDING_WINDOW, ATTN_SOFTMAX, KVCache,
-                       kv_cache_alloc, kv_cache_free, kv_cache_reset, spec_accept_greedy)
+                       kv_cache_alloc, kv_cache_free, kv_cache_reset, spec_accept_greedy,
+                       spec_accept_stochastic)
 from ._native import SDEError
 
 __all__ = ["KVCache", "kv_cache_alloc", "kv_cache_free", "kv_cache_reset", "SDEError",
-           "spec_accept_greedy",
+           "spec_accept_greedy", "spec_accept_stochastic",
            "ATTN_SOFTMAX", "ATTN_SLIDING_WINDOW", "ATTN_KDA", "ATTN_LINEAR"]

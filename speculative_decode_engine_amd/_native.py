@@ -97,6 +97,9 @@ PROTOTYPES = {
     "sde_grid_attention_workspace_size": (_sz, [_c_int, _c_int, _c_int, _c_int, _c_int]),
     "sde_paged_attention": (_c_int, [_vp, _c_int, _vp, _vp, _c_int, _c_int, _c_int, _c_int,
                                      _c_int, _vp, _sz, _vp]),
+    "sde_spec_accept_stochastic": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int,
+                                            ctypes.c_float, ctypes.c_float, ctypes.c_uint64, _vp,
+                                            _c_int, _c_int, _vp, _vp]),
     "sde_spec_accept_greedy": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _vp]),
     "sde_rope_append_attention": (_c_int, [_vp, _c_int, _vp, _vp, _vp, _vp, _c_int, _c_int,
                                            _c_int, _c_int, _c_int, _vp, _vp, _sz, _vp]),

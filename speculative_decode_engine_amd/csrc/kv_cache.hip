@@ -186,8 +186,10 @@ int finish_create(sde_kv_cache* c, sde_kv_cache** out) {
                 hipMemcpyHostToDevice) != hipSuccess ||
       hipMalloc(&c->d_seq_len, sizeof(int32_t)) != hipSuccess ||
       hipMemset(c->d_seq_len, 0, sizeof(int32_t)) != hipSuccess ||
-      hipMalloc(&c->d_counters, sde::kMaxAttnCounters * sizeof(uint32_t)) != hipSuccess ||
-      hipMemset(c->d_counters, 0, sde::kMaxAttnCounters * sizeof(uint32_t)) != hipSuccess ||
+      hipMalloc(&c->d_counters, (sde::kMaxAttnCounters + sde::kSpecScratchWords) *
+                                    sizeof(uint32_t)) != hipSuccess ||
+      hipMemset(c->d_counters, 0, (sde::kMaxAttnCounters + sde::kSpecScratchWords) *
+                                      sizeof(uint32_t)) != hipSuccess ||
       hipDeviceGetAttribute(&c->n_cus, hipDeviceAttributeMultiprocessorCount, c->device) !=
           hipSuccess ||
       hipDeviceSynchronize() != hipSuccess) {

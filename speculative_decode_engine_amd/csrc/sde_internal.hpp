@@ -35,6 +35,10 @@ struct sde_kv_cache {
 
 namespace sde {
 constexpr int kMaxAttnCounters = 4096;
+// Words after the attention counters: the stochastic acceptance's arrival
+// counter (zero at rest) and per-row results (flag, token) of one call.
+constexpr int kSpecScratchWords = 256;
+constexpr int kSpecMaxK = 64;
 }  // namespace sde
 
 namespace sde {

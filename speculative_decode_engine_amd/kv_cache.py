@@ -288,6 +288,39 @@ def spec_accept_greedy(target: KVCache, draft: Optional[KVCache], draft_tokens: 
     return out
 
 
+def spec_accept_stochastic(target: KVCache, draft: Optional[KVCache],
+                           target_logits: torch.Tensor, draft_logits: Optional[torch.Tensor],
+                           draft_tokens: torch.Tensor, k: int, target_save: int,
+                           draft_save: int, seed: int, rng_offset: torch.Tensor,
+                           temp_target: float = 1.0, temp_draft: float = 1.0,
+                           out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    """Speculative sampling acceptance + O(1) rewind on the device
+    (kernels.cu:550-572, 319-380): target_logits fp32 [k+1][V], draft_logits
+    fp32 [k][V], draft_tokens int32 [k], rng_offset a CUDA int64 [1] call
+    counter the call increments.  Returns the device int32 result [k+5] like
+    spec_accept_greedy."""
+    V = target_logits.shape[-1]
+    _dev_f32(target_logits, "target_logits", (k + 1, V))
+    if k:
+        _dev_f32(draft_logits, "draft_logits", (k, V))
+    for name, t, dt in (("draft_tokens", draft_tokens, torch.int32),
+                        ("rng_offset", rng_offset, torch.int64)):
+        if t.device.type != "cuda" or t.dtype != dt or not t.is_contiguous():
+            raise TypeError(f"{name} must be a contiguous CUDA {dt} tensor")
+    if out is None:
+        out = torch.empty(k + 5, dtype=torch.int32, device=target.device)
+    lib = _native.load()
+    check(lib.sde_spec_accept_stochastic(
+        target.handle, draft.handle if draft is not None else None,
+        ctypes.c_void_p(target_logits.data_ptr()),
+        ctypes.c_void_p(draft_logits.data_ptr() if k else 0),
+        ctypes.c_void_p(draft_tokens.data_ptr()), k, V, temp_target, temp_draft,
+        seed & 0xFFFFFFFFFFFFFFFF, ctypes.c_void_p(rng_offset.data_ptr()), target_save,
+        draft_save, ctypes.c_void_p(out.data_ptr()), _stream_handle(stream)),
+        "spec_accept_stochastic")
+    return out
+
+
 # Reference-named entry points (kv_cache.h:56-63).
 def kv_cache_alloc(n_layers: int, d_head: int, max_blocks_per_layer: int,
                    block_size: int = KV_BLOCK_SIZE, pool_blocks: int = 0,

@@ -138,3 +138,93 @@ def test_reference_loop_with_device_accept_emits_greedy_tokens(gpu, oracle, mode
     assert out == ref, stats["accepted"]
     for c in (gcache, tc, dc):
         c.free()
+
+
+# ---- on-device stochastic acceptance (sde_spec_accept_stochastic) -----------
+
+def _stoch(tc, dc, tl, dl, drafts, k, ts, ds, seed, off_t, tt=1.0, td=1.0):
+    from speculative_decode_engine_amd import spec_accept_stochastic
+    tld = torch.from_numpy(np.ascontiguousarray(tl, np.float32)).cuda()
+    dld = torch.from_numpy(np.ascontiguousarray(dl, np.float32)).cuda() if k else None
+    dtk = torch.from_numpy(np.asarray(drafts if k else [0], np.int32)).cuda()
+    return spec_accept_stochastic(tc, dc, tld, dld, dtk, k, ts, ds, seed, off_t, tt, td)
+
+
+@pytest.mark.parametrize("V,k,tt,td", [(8, 1, 1.0, 1.0), (1000, 4, 1.0, 1.0),
+                                       (1000, 8, 0.7, 1.3), (128256, 4, 1.0, 0.8),
+                                       (50, 0, 1.0, 1.0), (300, 3, 1e-8, 1.0)])
+def test_device_stochastic_matches_oracle(gpu, oracle, V, k, tt, td):
+    case_banner("device stochastic", V, k, tt, td)
+    rng = np.random.default_rng(V + k)
+    tc = KVCache(1, 64, 8, 16, 8)
+    dc = KVCache(1, 64, 8, 16, 8)
+    off = torch.zeros(1, dtype=torch.int64, device="cuda")
+    checked = 0
+    for call in range(12):
+        # a flat softmax over 128K tokens puts every sample near a CDF
+        # boundary; language-model logits are peaked
+        tl = rng.standard_normal((k + 1, V)) * (8.0 if V > 10000 else 2.0)
+        dl = tl[:k] + rng.standard_normal((k, V)) * 0.7     # a draft close to the target
+        q = np.exp(dl * (1 / td) - (dl * (1 / td)).max(1, keepdims=True)) if k else None
+        drafts = [int(np.argmax(q[i] * rng.random(V))) for i in range(k)]
+        ts, ds = 20 + call, 10 + call
+        tc.set_seq_len(ts + k + 1)
+        dc.set_seq_len(ds + k)
+        res = _stoch(tc, dc, tl, dl, drafts, k, ts, ds, 1234, off, tt, td).cpu().numpy()
+        r = oracle.spec_accept_stochastic(tl.astype(np.float32), dl.astype(np.float32) if k
+                                          else None, drafts, k, tt, td, 1234, call, ts, ds, False)
+        n = r["n_accepted"]
+        assert int(off.item()) == call + 1
+        # compare unless a decision sits within 1e-4 of its boundary
+        near = min(r["accept_margin"][: min(n + 1, k)] + [1.0]) < 1e-4 or \
+            r["sample_margin"][n] < 1e-5
+        if near:
+            continue
+        checked += 1
+        assert list(res[:4]) == [n, r["token"], r["target_seq"], r["draft_seq"]]
+        assert list(res[4:4 + n + 1]) == r["emitted"]
+        assert tc.device_seq_len() == r["target_seq"] and dc.device_seq_len() == r["draft_seq"]
+    assert checked >= 8
+    tc.free()
+    dc.free()
+
+
+def test_device_speculative_sampling_preserves_the_target_distribution(gpu, oracle):
+    """Leviathan et al.'s theorem on the device: with drafts sampled from q,
+    the first emitted token is distributed as p."""
+    case_banner("device stochastic distribution")
+    rng = np.random.default_rng(8)
+    V, trials = 8, 4000
+    tl = rng.standard_normal((2, V)) * 1.5
+    dl = rng.standard_normal((1, V)) * 1.5
+    p = np.exp(tl[0] - tl[0].max()); p /= p.sum()
+    q = np.exp(dl[0] - dl[0].max()); q /= q.sum()
+    drafts = np.searchsorted(np.cumsum(q), rng.random(trials)).clip(0, V - 1)
+    tc = KVCache(1, 64, 8, 16, 8)
+    off = torch.zeros(1, dtype=torch.int64, device="cuda")
+    tld = torch.from_numpy(tl.astype(np.float32)).cuda()
+    dld = torch.from_numpy(dl.astype(np.float32)).cuda()
+    dtk = torch.from_numpy(drafts.astype(np.int32)).cuda()
+    from speculative_decode_engine_amd import spec_accept_stochastic
+    outs = torch.empty(trials, 6, dtype=torch.int32, device="cuda")
+    for t in range(trials):
+        spec_accept_stochastic(tc, None, tld, dld, dtk[t:t + 1], 1, 5, 0, 77, off, out=outs[t])
+    first = outs[:, 4].cpu().numpy()
+    counts = np.bincount(first, minlength=V)
+    chi2 = ((counts - trials * p) ** 2 / (trials * p)).sum()
+    assert chi2 < 24.3, (counts, trials * p)   # 7 dof, p = 0.001
+    assert int(off.item()) == trials
+    tc.free()
+
+
+def test_device_stochastic_errors(gpu):
+    case_banner("device stochastic errors")
+    tc = KVCache(1, 64, 2, 16, 2)
+    off = torch.zeros(1, dtype=torch.int64, device="cuda")
+    tl = np.zeros((66, 4), np.float32)
+    with pytest.raises(Exception):
+        _stoch(tc, None, tl, tl[:65], [0] * 65, 65, 0, 0, 1, off)   # k > 64
+    with pytest.raises(Exception):
+        _stoch(tc, None, tl[:5], tl[:4], [0] * 4, 4, 28, 0, 1, off)  # past the capacity
+    assert int(off.item()) == 0
+    tc.free()

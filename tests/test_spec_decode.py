@@ -10,6 +10,7 @@ so the rewind is what places the next round's appends.  The planted-mistake
 tests show the check fails for a rewind that keeps one rejected draft or
 drops one accepted token.
 """
+import numpy as np
 import pytest
 
 from tiny_llama import (OracleCache, TinyConfig, TinyLlama, greedy, host_accept, spec_self,
@@ -117,3 +118,63 @@ def test_planted_accept_rule_mistake_breaks_the_loop(oracle):
         tc.rollback(t_seq - 1)
         return n, b, t_seq - 1, d_seq, em
     assert spec_two_model_reference(target, draft, tc, dc, PROMPT, N_NEW, K, bad) != ref
+
+
+# ---- speculative sampling oracle (stochastic acceptance) -------------------
+
+def test_philox_known_answers(oracle):
+    # Random123's known-answer vectors for philox4x32-10
+    kat = [([0, 0, 0, 0], [0, 0], [0x6627e8d5, 0xe169c58d, 0xbc57ac4c, 0x9b00dbd8]),
+           ([0xffffffff] * 4, [0xffffffff] * 2, [0x408f276d, 0x41c83b0e, 0xa20bc7c6, 0x6d5451fd]),
+           ([0x243f6a88, 0x85a308d3, 0x13198a2e, 0x03707344], [0xa4093822, 0x299f31d0],
+            [0xd16cfe09, 0x94fdcceb, 0x5001e420, 0x24126ea1])]
+    for ctr, key, want in kat:
+        assert oracle.philox4x32_10(ctr, key) == want
+
+
+def test_spec_draws_are_uniform(oracle):
+    u = np.array([oracle.spec_draws(7, off, b) for off in range(400) for b in range(5)])
+    assert ((u > 0) & (u < 1)).all()
+    hist, _ = np.histogram(u.ravel(), bins=10, range=(0, 1))
+    chi2 = ((hist - len(u.ravel()) / 10) ** 2 / (len(u.ravel()) / 10)).sum()
+    assert chi2 < 27.9   # 9 dof, p = 0.001
+
+
+def test_speculative_sampling_preserves_the_target_distribution(oracle):
+    """The theorem speculative sampling rests on (Leviathan et al. 2023):
+    the first emitted token is distributed as p, whatever the draft q."""
+    rng = np.random.default_rng(8)
+    V, trials = 8, 6000
+    tl = rng.standard_normal((2, V)) * 1.5
+    dl = rng.standard_normal((1, V)) * 1.5
+    p = np.exp(tl[0] - tl[0].max()); p /= p.sum()
+    q = np.exp(dl[0] - dl[0].max()); q /= q.sum()
+    counts = np.zeros(V)
+    for off in range(trials):
+        # the draft token is sampled from q with an independent Philox draw
+        u = oracle.spec_draws(99, off, 7)[0]
+        d = int(np.searchsorted(np.cumsum(q), u))
+        r = oracle.spec_accept_stochastic(tl, dl, [d], 1, 1.0, 1.0, 5, off, 10, 10, False)
+        counts[r["emitted"][0]] += 1
+    chi2 = ((counts - trials * p) ** 2 / (trials * p)).sum()
+    assert chi2 < 24.3   # 7 dof, p = 0.001
+    # planted mistake: always emitting the draft token (no rejection) is q, not p
+    bad = np.zeros(V)
+    for off in range(trials):
+        u = oracle.spec_draws(99, off, 7)[0]
+        bad[int(np.searchsorted(np.cumsum(q), u))] += 1
+    assert ((bad - trials * p) ** 2 / (trials * p)).sum() > 100
+
+
+def test_speculative_sampling_special_cases(oracle):
+    V = 6
+    tl = np.log(np.array([[.5, .2, .1, .1, .05, .05], [.1, .1, .1, .1, .1, .5]]))
+    # q == p: the residual is empty and every draft is accepted (cap 1)
+    r = oracle.spec_accept_stochastic(tl, tl[:1], [2], 1, 1.0, 1.0, 3, 0, 4, 4, True)
+    assert r["flags"] == [True] and r["n_accepted"] == 1 and r["target_seq"] == 6
+    # a draft token with p = 0 is always rejected; the correction excludes it
+    tl0 = tl.copy()
+    tl0[0, 3] = -np.inf
+    for off in range(50):
+        r = oracle.spec_accept_stochastic(tl0, tl[:1], [3], 1, 1.0, 1.0, 3, off, 4, 4, False)
+        assert r["n_accepted"] == 0 and r["token"] != 3 and r["draft_seq"] == 4
