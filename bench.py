@@ -207,6 +207,36 @@ def bench_rollback(torch, W, steps=2000):
     return out
 
 
+def bench_accept(torch, steps=200, k=4, vocab=128256):
+    """us per on-device acceptance + rewind of a k=4 verify window: greedy
+    (sde_spec_accept_greedy) and speculative sampling over a Llama-3-sized
+    vocabulary (sde_spec_accept_stochastic), graph-replayed like the
+    attention steps."""
+    from speculative_decode_engine_amd import KVCache, spec_accept_greedy, spec_accept_stochastic
+    tc = KVCache(1, 1024, 8, 16, 8, pool="library")
+    dc = KVCache(1, 1024, 8, 16, 8, pool="library")
+    g = torch.Generator(device="cuda")
+    g.manual_seed(9)
+    tl = torch.randn(k + 1, vocab, device="cuda", generator=g) * 4
+    dl = tl[:k] + torch.randn(k, vocab, device="cuda", generator=g)
+    dl = dl.contiguous()
+    drafts = torch.argmax(dl, dim=-1).to(torch.int32)
+    targets = torch.argmax(tl, dim=-1).to(torch.int32)
+    off = torch.zeros(1, dtype=torch.int64, device="cuda")
+    res = torch.empty(k + 5, dtype=torch.int32, device="cuda")
+    out = {}
+    for name, fn in (
+            ("greedy", lambda i: spec_accept_greedy(tc, dc, drafts, targets, k, 64, 60, out=res)),
+            ("stochastic", lambda i: spec_accept_stochastic(tc, dc, tl, dl, drafts, k, 64, 60, 5,
+                                                            off, 1.0, 1.0, out=res))):
+        out[name] = round(graph_step_ms(torch, fn, steps, 10) * 1e3, 3)
+    out["k"] = k
+    out["vocab"] = vocab
+    tc.free()
+    dc.free()
+    return out
+
+
 def cpu_baseline(W, w, seconds):
     """The CPU oracle's tile restatement of attention.h (OpenMP over
     (query, head) pairs) on one 32K-key layer-step of the same shape, run
@@ -302,6 +332,8 @@ def main():
         configs["qwen25_7b_selfspec_verify_fused"] = bench_config(torch, W, w5, steps, warmup,
                                                                   "verify_fused")
         extra["rollback_us"] = bench_rollback(torch, W)
+        extra["accept_us"] = bench_accept(torch)
+        log("[bench] accept", json.dumps(extra["accept_us"]))
         for k_, v_ in configs.items():
             log(f"[bench] {k_}: {v_['us_per_layer_step']} us/layer-step, {v_['gbps']} GB/s")
 
