@@ -269,8 +269,13 @@ def spec_accept_stochastic(target_logits, draft_logits, draft_tokens, k: int,
     1e-6 act as 1e-6); the first rejection at i emits a token sampled from
     norm(max(0, p - q)), or from p when that is empty
     (device_corrected_adjusted_sample, kernels.cu:319-380); with every draft
-    accepted the bonus is sampled from p of row k.  A sample is the smallest
-    token whose cumulative weight reaches u * total.  Rewinds as
+    accepted the bonus is sampled from p of row k.  A sample is the first
+    token, in the order below, whose cumulative weight reaches u * total
+    (and has a positive weight): tokens ordered by vocabulary slice (S =
+    min(ceil(V/4096), 64) slices of L = ceil(V/S) tokens), then by
+    (l % 1024, l // 1024) of the offset l in the slice -- the library's
+    coalescing-friendly inverse-CDF order (index order for V <= 1024; any
+    fixed order samples the same distribution).  Rewinds as
     spec_accept_greedy.  Returns the result and, per row, the distance of
     the accept test and of the sample from their decision boundaries."""
     tl = np.asarray(target_logits, np.float64)
@@ -295,13 +300,20 @@ def spec_accept_stochastic(target_logits, draft_logits, draft_tokens, k: int,
                 w = p
         else:
             w = p
-        cdf = np.cumsum(w)
+        V = w.shape[0]
+        S = min((V + 4095) // 4096, 64)
+        L = (V + S - 1) // S
+        i = np.arange(V)
+        loc = i % L
+        order = np.lexsort((loc // 1024, loc % 1024, i // L))
+        wo = w[order]
+        cdf = np.cumsum(wo)
         goal = us * cdf[-1]
-        idx = np.nonzero((cdf >= goal) & (w > 0))[0]
-        tok = int(idx[0]) if idx.size else int(np.nonzero(w > 0)[0][-1])
-        tokens.append(tok)
-        lo = cdf[tok] - w[tok]
-        smp_margin.append(min(abs(goal - lo), abs(cdf[tok] - goal)) / cdf[-1])
+        idx = np.nonzero((cdf >= goal) & (wo > 0))[0]
+        pos = int(idx[0]) if idx.size else int(np.nonzero(wo > 0)[0][-1])
+        tokens.append(int(order[pos]))
+        lo = cdf[pos] - wo[pos]
+        smp_margin.append(min(abs(goal - lo), abs(cdf[pos] - goal)) / cdf[-1])
     n = 0
     while n < k and flags[n]:
         n += 1

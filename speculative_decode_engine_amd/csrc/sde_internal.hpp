@@ -36,9 +36,11 @@ struct sde_kv_cache {
 namespace sde {
 constexpr int kMaxAttnCounters = 4096;
 // Words after the attention counters: the stochastic acceptance's arrival
-// counter (zero at rest) and per-row results (flag, token) of one call.
-constexpr int kSpecScratchWords = 256;
+// counters (zero at rest), per-row results and per-slice statistics of one
+// call (rows <= kSpecMaxK + 1, slices <= kSpecMaxSlices).
 constexpr int kSpecMaxK = 64;
+constexpr int kSpecMaxSlices = 64;
+constexpr int kSpecScratchWords = 1 + 3 * (kSpecMaxK + 1) + 6 * (kSpecMaxK + 1) * kSpecMaxSlices;
 }  // namespace sde
 
 namespace sde {
