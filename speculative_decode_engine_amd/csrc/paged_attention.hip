@@ -42,6 +42,16 @@ __global__ __launch_bounds__(64 * kStreamWaves) void attn_stream_kernel(AttnArgs
   stream_item<DPH, RPW, CHUNK, kStreamWaves>(a, blockIdx.x, blockIdx.y, blockIdx.z, lds);
 }
 
+// Verify windows whose 8-wave plan leaves long serial tile chains per wave
+// (more than four tiles): 4-wave workgroups, one tile per chunk (136 VGPRs,
+// so three workgroups -- three waves per SIMD -- share a CU and hide each
+// other's load latency).
+template <int DPH, int RPW>
+__global__ __launch_bounds__(256) void attn_stream4_kernel(AttnArgs a) {
+  __shared__ StreamLds<DPH, RPW, 4> lds;
+  stream_item<DPH, RPW, 1, 4>(a, blockIdx.x, blockIdx.y, blockIdx.z, lds);
+}
+
 // attn_stream_kernel with RoPE of q and of the window's k, and the window's
 // append, fused in (sde_rope_append_attention).
 template <int DPH, int RPW, int CHUNK>
@@ -59,13 +69,24 @@ namespace {
 
 using namespace sde::attn;
 
-// Upper bound of stream_plan(L).n_parts over every L <= max_total_len: a
-// partition holds at least kStreamWaves tiles and there are at most
-// kStreamMaxParts of them.
+constexpr int kVerifyWaves = 4;  // waves per workgroup of attn_stream4_kernel
+
+// Upper bound of the plans' n_parts over every L <= max_total_len: a
+// partition holds at least one tile per wave (four waves at least) and
+// there are at most kStreamMaxParts of them.
 int parts_bound(int max_total_len) {
   const int n_tiles = (max_total_len + kTile - 1) / kTile;
-  const int by_len = (n_tiles + kStreamWaves - 1) / kStreamWaves;
+  const int by_len = (n_tiles + kVerifyWaves - 1) / kVerifyWaves;
   return by_len < kStreamMaxParts ? by_len : kStreamMaxParts;
+}
+
+// The plan of a call: 8-wave workgroups, one per CU; or, for windows of
+// more than four rows per KV head whose waves would walk more than four
+// tiles each, 4-wave single-tile-chunk workgroups, three per CU.
+StreamPlan plan_for(int L_max, int nkv, int R, int n_cus, bool fused, bool* four_waves) {
+  const StreamPlan p8 = stream_plan(L_max, nkv, R, n_cus, kStreamWaves, 4);
+  *four_waves = !fused && R > 4 && p8.tiles_per_part > 4 * kStreamWaves;
+  return *four_waves ? stream_plan(L_max, nkv, R, 3 * n_cus, kVerifyWaves, 1) : p8;
 }
 
 size_t partial_bytes(int nkv, int R, int n_parts, int dph) {
@@ -74,9 +95,14 @@ size_t partial_bytes(int nkv, int R, int n_parts, int dph) {
 
 template <int DPH>
 int launch(const StreamPlan& p, const AttnArgs& a, int nkv, hipStream_t s,
-           const RopeArgs* rope = nullptr) {
+           const RopeArgs* rope, bool four_waves) {
   const dim3 grid(p.n_parts, nkv, p.row_groups);
   const dim3 block(64 * kStreamWaves);
+  if (four_waves) {
+    if (p.rpw != 4 || p.chunk != 1) return SDE_ERR_UNSUPPORTED;
+    attn_stream4_kernel<DPH, 4><<<grid, dim3(64 * kVerifyWaves), 0, s>>>(a);
+    return sde::launch_status();
+  }
 #define SDE_STREAM(R, C)                                              \
   if (p.rpw == R && p.chunk == C) {                                   \
     if (rope)                                                         \
@@ -144,7 +170,8 @@ int run_attention(sde_kv_cache* cache, int layer, const float* d_q, float* d_out
   const int G = nh / nkv;
   const int R = n_queries * G;
   const int L_max = pos_base + n_queries;
-  const StreamPlan plan = stream_plan(L_max, nkv, R, cache->n_cus, kStreamWaves, 4);
+  bool four_waves = false;
+  const StreamPlan plan = plan_for(L_max, nkv, R, cache->n_cus, rope != nullptr, &four_waves);
   if ((int64_t)nkv * plan.row_groups > sde::kMaxAttnCounters) return SDE_ERR_UNSUPPORTED;
   const size_t need = partial_bytes(nkv, R, plan.n_parts, dph);
   float* partials = nullptr;
@@ -189,7 +216,8 @@ int run_attention(sde_kv_cache* cache, int layer, const float* d_q, float* d_out
   a.qscale = (float)(kLog2e / std::sqrt((double)dph));
 
   const hipStream_t s = (hipStream_t)stream;
-  return dph == 128 ? launch<128>(plan, a, nkv, s, rope) : launch<64>(plan, a, nkv, s, rope);
+  return dph == 128 ? launch<128>(plan, a, nkv, s, rope, four_waves)
+                    : launch<64>(plan, a, nkv, s, rope, four_waves);
 }
 
 }  // namespace

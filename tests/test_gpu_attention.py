@@ -22,6 +22,11 @@ ATOL, RTOL = 2e-3, 1e-2
 
 
 def assert_close(got, ref, what=""):
+    """The contract (north_star: |err| <= 2e-3 + 1e-2 |ref|), and a tighter
+    regression guard on the kernels' own precision: fp16 q and fp16
+    probabilities keep the error below 2e-3 of the output's scale (measured
+    ~2.5e-4 of it), so a lost partition or a mis-weighted tile, which the
+    contract's absolute term can hide when outputs are ~1e-2, fails here."""
     got = np.asarray(got, np.float64)
     ref = np.asarray(ref, np.float64)
     err = np.abs(got - ref)
@@ -29,6 +34,10 @@ def assert_close(got, ref, what=""):
     assert np.isfinite(got).all(), f"{what}: non-finite output"
     assert not bad.any(), (f"{what}: {bad.sum()} elements out of tolerance, "
                            f"max abs err {err.max():.3e}")
+    if ref.size:
+        scale = np.abs(ref).max()
+        assert err.max() <= 2e-3 * scale + 1e-6, (
+            f"{what}: max abs err {err.max():.3e} above 2e-3 x output scale {scale:.3e}")
 
 
 def build_layer(nh, nkv, dph, bs, ctx, n_app, pool_blocks, seed, layer_slot=0, n_layers=1):
