@@ -71,11 +71,11 @@ __device__ __forceinline__ float dpp_f(float x, int ctrl_sel) {
   const int v = __builtin_bit_cast(int, x);
   int r;
   switch (ctrl_sel) {
-    case 0: r = __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xf, 0xf, false); break;   // i^1
-    case 1: r = __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xf, 0xf, false); break;   // i^2
-    case 2: r = __builtin_amdgcn_update_dpp(0, v, 0x124, 0xf, 0xf, false); break;  // ror 4
-    case 3: r = __builtin_amdgcn_update_dpp(0, v, 0x128, 0xf, 0xf, false); break;  // ror 8
-    default: r = __builtin_amdgcn_update_dpp(0, v, 0x141, 0xf, 0xf, false); break; // i^7 in 8
+    case 0: r = __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xf, 0xf, true); break;   // i^1
+    case 1: r = __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xf, 0xf, true); break;   // i^2
+    case 2: r = __builtin_amdgcn_update_dpp(0, v, 0x124, 0xf, 0xf, true); break;  // ror 4
+    case 3: r = __builtin_amdgcn_update_dpp(0, v, 0x128, 0xf, 0xf, true); break;  // ror 8
+    default: r = __builtin_amdgcn_update_dpp(0, v, 0x141, 0xf, 0xf, true); break; // i^7 in 8
   }
   return __builtin_bit_cast(float, r);
 }
@@ -227,6 +227,7 @@ struct StreamShape {
   static constexpr int NV = RPW * NLD;                // partial logits per lane
   static constexpr int T = (NV == 32 ? 5 : NV == 16 ? 4 : NV == 8 ? 3 : 2) - 1;  // halving steps
   static constexpr int RB = RPW == 4 ? 2 : 1;         // bits of r
+  static constexpr int SF = CH == 16 ? RB : 1;        // select-free butterfly steps
   static_assert(T <= S, "more logits than lanes to spread them over");
   // chunk index of the lane owning (row r, pair jp) (its redundant bits 0)
   static constexpr int owner(int r, int jp) { return ((r << (T - RB)) | jp) << (S - T); }
@@ -241,10 +242,10 @@ __device__ __forceinline__ float bfly(float x, int k) {
   const int v = __builtin_bit_cast(int, x);
   int r;
   switch (CH == 16 ? k : k + 1) {
-    case 0: r = __builtin_amdgcn_update_dpp(0, v, 0x128, 0xf, 0xf, false); break;
-    case 1: r = __builtin_amdgcn_update_dpp(0, v, 0x141, 0xf, 0xf, false); break;
-    case 2: r = __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xf, 0xf, false); break;
-    default: r = __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xf, 0xf, false); break;
+    case 0: r = __builtin_amdgcn_update_dpp(0, v, 0x128, 0xf, 0xf, true); break;
+    case 1: r = __builtin_amdgcn_update_dpp(0, v, 0x141, 0xf, 0xf, true); break;
+    case 2: r = __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xf, 0xf, true); break;
+    default: r = __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xf, 0xf, true); break;
   }
   return __builtin_bit_cast(float, r);
 }
@@ -252,22 +253,22 @@ __device__ __forceinline__ float bfly(float x, int k) {
 // Value of lane n of this lane's 16-lane row (DPP row_newbcast:n).
 __device__ __forceinline__ int row_bcast(int v, int n) {
   switch (n) {
-    case 0: return __builtin_amdgcn_update_dpp(0, v, 0x150, 0xf, 0xf, false);
-    case 1: return __builtin_amdgcn_update_dpp(0, v, 0x151, 0xf, 0xf, false);
-    case 2: return __builtin_amdgcn_update_dpp(0, v, 0x152, 0xf, 0xf, false);
-    case 3: return __builtin_amdgcn_update_dpp(0, v, 0x153, 0xf, 0xf, false);
-    case 4: return __builtin_amdgcn_update_dpp(0, v, 0x154, 0xf, 0xf, false);
-    case 5: return __builtin_amdgcn_update_dpp(0, v, 0x155, 0xf, 0xf, false);
-    case 6: return __builtin_amdgcn_update_dpp(0, v, 0x156, 0xf, 0xf, false);
-    case 7: return __builtin_amdgcn_update_dpp(0, v, 0x157, 0xf, 0xf, false);
-    case 8: return __builtin_amdgcn_update_dpp(0, v, 0x158, 0xf, 0xf, false);
-    case 9: return __builtin_amdgcn_update_dpp(0, v, 0x159, 0xf, 0xf, false);
-    case 10: return __builtin_amdgcn_update_dpp(0, v, 0x15A, 0xf, 0xf, false);
-    case 11: return __builtin_amdgcn_update_dpp(0, v, 0x15B, 0xf, 0xf, false);
-    case 12: return __builtin_amdgcn_update_dpp(0, v, 0x15C, 0xf, 0xf, false);
-    case 13: return __builtin_amdgcn_update_dpp(0, v, 0x15D, 0xf, 0xf, false);
-    case 14: return __builtin_amdgcn_update_dpp(0, v, 0x15E, 0xf, 0xf, false);
-    default: return __builtin_amdgcn_update_dpp(0, v, 0x15F, 0xf, 0xf, false);
+    case 0: return __builtin_amdgcn_update_dpp(0, v, 0x150, 0xf, 0xf, true);
+    case 1: return __builtin_amdgcn_update_dpp(0, v, 0x151, 0xf, 0xf, true);
+    case 2: return __builtin_amdgcn_update_dpp(0, v, 0x152, 0xf, 0xf, true);
+    case 3: return __builtin_amdgcn_update_dpp(0, v, 0x153, 0xf, 0xf, true);
+    case 4: return __builtin_amdgcn_update_dpp(0, v, 0x154, 0xf, 0xf, true);
+    case 5: return __builtin_amdgcn_update_dpp(0, v, 0x155, 0xf, 0xf, true);
+    case 6: return __builtin_amdgcn_update_dpp(0, v, 0x156, 0xf, 0xf, true);
+    case 7: return __builtin_amdgcn_update_dpp(0, v, 0x157, 0xf, 0xf, true);
+    case 8: return __builtin_amdgcn_update_dpp(0, v, 0x158, 0xf, 0xf, true);
+    case 9: return __builtin_amdgcn_update_dpp(0, v, 0x159, 0xf, 0xf, true);
+    case 10: return __builtin_amdgcn_update_dpp(0, v, 0x15A, 0xf, 0xf, true);
+    case 11: return __builtin_amdgcn_update_dpp(0, v, 0x15B, 0xf, 0xf, true);
+    case 12: return __builtin_amdgcn_update_dpp(0, v, 0x15C, 0xf, 0xf, true);
+    case 13: return __builtin_amdgcn_update_dpp(0, v, 0x15D, 0xf, 0xf, true);
+    case 14: return __builtin_amdgcn_update_dpp(0, v, 0x15E, 0xf, 0xf, true);
+    default: return __builtin_amdgcn_update_dpp(0, v, 0x15F, 0xf, 0xf, true);
   }
 }
 
@@ -319,7 +320,10 @@ __device__ __forceinline__ void stream_qk(int ts, int sl, int c, int min_lim, in
     }
   }
   // Transposing butterfly: step kk keeps the half of x whose top index bit
-  // equals bit S-1-kk of c.
+  // equals bit S-1-kk of c.  The first SF steps split on row bits, and the
+  // lane's q rows arrive permuted by those same lane bits (qr[r] holds row
+  // r ^ flip, see q_row_flip), so the half to keep is always the lower one
+  // there -- no per-element select.
 #pragma unroll
   for (int kk = 0; kk < T; kk++) {
     const bool f = (c >> (S - 1 - kk)) & 1;
@@ -327,10 +331,14 @@ __device__ __forceinline__ void stream_qk(int ts, int sl, int c, int min_lim, in
 #pragma unroll
     for (int i = 0; i < (NV >> 1); i++) {
       if (i < h) {
-        const float a = x[i], b = x[i + h];
-        const float send = f ? a : b;
-        const float keep = f ? b : a;
-        x[i] = keep + bfly<CH>(send, kk);
+        if (kk < Sh::SF) {
+          x[i] += bfly<CH>(x[i + h], kk);
+        } else {
+          const float a = x[i], b = x[i + h];
+          const float send = f ? a : b;
+          const float keep = f ? b : a;
+          x[i] = keep + bfly<CH>(send, kk);
+        }
       }
     }
   }
@@ -481,6 +489,39 @@ __device__ __forceinline__ void rope_q_rows(const float2* cs_tab, float2 (&q)[RP
   }
 }
 
+// The lane's row permutation for stream_qk's select-free butterfly steps:
+// bit (RB-1-kk) of the flip is bit (S-1-kk) of the chunk index c, for the
+// first SF steps.  A step can go select-free only if its partner lanes
+// differ in its own flip bit and agree on the earlier ones: with 16 lanes
+// per token the first two partners are c^8 and the 8-lane mirror (both row
+// bits); with 8 lanes the first partner is the 8-lane mirror, which also
+// flips the second bit, so only the first step qualifies.
+template <int DPH, int RPW>
+__device__ __forceinline__ int q_row_flip(int c) {
+  using Sh = StreamShape<DPH, RPW>;
+  int flip = 0;
+#pragma unroll
+  for (int kk = 0; kk < Sh::SF; kk++) flip |= ((c >> (Sh::S - 1 - kk)) & 1) << (Sh::RB - 1 - kk);
+  return flip;
+}
+
+// qr[r] <- packed row r ^ flip (selects on whole rows, once per packing).
+template <int RPW>
+__device__ __forceinline__ void permute_rows(uint4 (&qr)[RPW], int flip) {
+#pragma unroll
+  for (int bit = RPW / 2; bit >= 1; bit >>= 1) {
+    const bool f = flip & bit;
+    uint4 t[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; r++) {
+      const uint4 a = qr[r], b = qr[r ^ bit];
+      t[r] = make_uint4(f ? b.x : a.x, f ? b.y : a.y, f ? b.z : a.z, f ? b.w : a.w);
+    }
+#pragma unroll
+    for (int r = 0; r < RPW; r++) qr[r] = t[r];
+  }
+}
+
 template <int DPH, int RPW, int CHUNK, bool ROPE = false>
 __device__ __forceinline__ void wave_attend(const TileSource& src, int kvh, int first, int te,
                                             int stride, int nrows, int min_lim, int my_lim,
@@ -538,6 +579,7 @@ __device__ __forceinline__ void wave_attend(const TileSource& src, int kvh, int 
                                pack_h2(qv[r][2].x * sc, qv[r][2].y * sc),
                                pack_h2(qv[r][3].x * sc, qv[r][3].y * sc));
           }
+          permute_rows<RPW>(qr, q_row_flip<DPH, RPW>(c));
         }
       } else if (i == 0) {
         // q is scaled into the exp2 domain and rounded to fp16 pairs once
@@ -551,6 +593,7 @@ __device__ __forceinline__ void wave_attend(const TileSource& src, int kvh, int 
                              pack_h2(q_raw[r][2].x * sc, q_raw[r][2].y * sc),
                              pack_h2(q_raw[r][3].x * sc, q_raw[r][3].y * sc));
         }
+        permute_rows<RPW>(qr, q_row_flip<DPH, RPW>(c));
       }
       // A slot past the wave's last tile: every token masked (no-op).
       const int ts_mask = t <= last ? t * kTile : INT_MAX / 2;
