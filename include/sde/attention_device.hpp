@@ -610,33 +610,74 @@ __device__ __forceinline__ void wave_attend(const TileSource& src, int kvh, int 
   }
 }
 
-// Merges the token slots' softmax states of this wave: per row r, mx[r] and
-// l[r] (the same in every lane) and acc[r][e] rescaled to mx[r] and summed
-// over the slots (every lane holds the total of its chunk c).
+// Totals over the four 16-lane rows of four values at once: afterwards lanes
+// of row j hold the total of v[j] (per column).  permlane16_swap exchanges
+// the odd rows of its first operand with the even rows of its second,
+// permlane32_swap the upper half of its first with the lower half of its
+// second, so two row-pair sums and one half-pair sum leave each row with the
+// total of one of the four.
+__device__ __forceinline__ float rows_total4(float v0, float v1, float v2, float v3) {
+  const auto p = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(int, v0),
+                                                  __builtin_bit_cast(int, v1), false, false);
+  const auto q = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(int, v2),
+                                                  __builtin_bit_cast(int, v3), false, false);
+  const float s01 = __builtin_bit_cast(float, (int)p[0]) + __builtin_bit_cast(float, (int)p[1]);
+  const float s23 = __builtin_bit_cast(float, (int)q[0]) + __builtin_bit_cast(float, (int)q[1]);
+  return half_pair_total(s01, s23);
+}
+
+// Where wave_merge_slots leaves the slot totals: 16-lane row j holds row
+// merged_row(j) of the record, features 8c + merged_col(j) + e for
+// e < 2*RPW.
+template <int RPW>
+__device__ __forceinline__ int merged_row(int j) { return RPW == 4 ? j : (j & 1); }
+template <int RPW>
+__device__ __forceinline__ int merged_col(int j) { return RPW == 4 ? 0 : 4 * (j >> 1); }
+
+// Merges the token slots' softmax states of this wave.  Every lane gets
+// m_row / l_row, the max and sum of its own row my_r over all slots, and
+// out[e] (e < 2*RPW), the accumulators rescaled to that max and summed over
+// the slots, spread over the 16-lane rows j = lane/16: row j holds row
+// merged_row(j), features 8c + merged_col(j) + e (c = lane % CH; with
+// dph 64 both halves of a 16-lane row hold the same values).  Four values
+// share each pair of row swaps, so the merge costs a quarter of the
+// cross-lane moves of one all-reduce per value.
 template <int DPH, int RPW>
-__device__ __forceinline__ void wave_merge_slots(float m_run, float l_run, float (&acc)[RPW][8],
-                                                 float (&mx)[RPW], float (&l)[RPW]) {
+__device__ __forceinline__ void wave_merge_slots(float m_run, float l_run,
+                                                 const float (&acc)[RPW][8], float& m_row,
+                                                 float& l_row, float (&out)[2 * RPW]) {
   using Sh = StreamShape<DPH, RPW>;
   constexpr int CH = Sh::CH;
   const int lane = threadIdx.x & 63;
-  const int sl = lane / CH;
   const int c = lane % CH;
+  const bool odd_slot = (lane / CH) & 1;
+  // Lanes of one chunk c share the row my_r, so the slot max of m_run is
+  // the row's max and f_own rescales this lane's (row, slot) state to it.
+  m_row = slot_max<DPH>(m_run);
+  const float f_own = m_row == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run - m_row);
   // l of (row, slot): sum over the row's token-pair owners (redundant lanes
   // hold copies and contribute 0).
   const bool redundant = (c & ((1 << (Sh::S - Sh::T)) - 1)) != 0;
   float lsum = redundant ? 0.f : l_run;
 #pragma unroll
   for (int kk = Sh::RB; kk < Sh::S; kk++) lsum += bfly<CH>(lsum, kk);
-  const bool odd_slot = sl & 1;
+  l_row = slot_sum<DPH>(lsum * f_own);
+  float x[RPW][8];
 #pragma unroll
   for (int r = 0; r < RPW; r++) {
-    const float m_s = from_owner_f<DPH, RPW>(m_run, r, 0, odd_slot);
-    const float l_s = from_owner_f<DPH, RPW>(lsum, r, 0, odd_slot);
-    mx[r] = slot_max<DPH>(m_s);
-    const float f = mx[r] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_s - mx[r]);
-    l[r] = slot_sum<DPH>(l_s * f);
+    const float f = from_owner_f<DPH, RPW>(f_own, r, 0, odd_slot);
 #pragma unroll
-    for (int e = 0; e < 8; e++) acc[r][e] = slot_sum<DPH>(acc[r][e] * f);
+    for (int e = 0; e < 8; e++) {
+      x[r][e] = acc[r][e] * f;
+      if constexpr (DPH == 64) x[r][e] += dpp_f(x[r][e], 3);  // slots 2k, 2k+1 of a row
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 2 * RPW; e++) {
+    if constexpr (RPW == 4)
+      out[e] = rows_total4(x[0][e], x[1][e], x[2][e], x[3][e]);
+    else
+      out[e] = rows_total4(x[0][e], x[1][e], x[0][e + 4], x[1][e + 4]);
   }
 }
 
@@ -848,10 +889,12 @@ __device__ __forceinline__ void rope_append_slice(const AttnArgs& a, const RopeA
   __syncthreads();
 }
 
-// LDS of stream_item: per-wave records (max, sum, acc[DPH]) of every row.
+// LDS of stream_item: per-wave records of every row, acc[DPH] and
+// (max, sum).
 template <int DPH, int RPW, int WAVES>
 struct StreamLds {
-  float buf[WAVES * RPW * (DPH + 2)] __attribute__((aligned(16)));
+  float acc[WAVES * RPW * DPH] __attribute__((aligned(16)));
+  float2 ml[WAVES * RPW];
   int last;
 };
 
@@ -869,8 +912,6 @@ __device__ __forceinline__ void stream_item(const AttnArgs& a, int part, int kvh
   static_assert(RPW == 2 || RPW == 4, "rows per wave");
   static_assert(RPW * (DPH / 2) <= 64 * WAVES, "one merge thread per (row, feature pair)");
   constexpr int CH = DPH / 8;
-  constexpr int REC = DPH + 2;
-  float* s_buf = lds.buf;
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -928,22 +969,15 @@ __device__ __forceinline__ void stream_item(const AttnArgs& a, int part, int kvh
                                        a.R);
 
     // ---- merge the slot states of this wave; record per row -------------
-    float mx[RPW], lw[RPW];
-    wave_merge_slots<DPH, RPW>(m_run, l_run, acc, mx, lw);
-#pragma unroll
-    for (int r = 0; r < RPW; r++) {
-      float* rec = s_buf + (wave * RPW + r) * REC;
-      if (lane == 0) {
-        rec[0] = mx[r];
-        rec[1] = lw[r];
-      }
-      if (sl == 0) {
-        float2* dst = reinterpret_cast<float2*>(rec + 2 + 8 * c);
-        dst[0] = make_float2(acc[r][0], acc[r][1]);
-        dst[1] = make_float2(acc[r][2], acc[r][3]);
-        dst[2] = make_float2(acc[r][4], acc[r][5]);
-        dst[3] = make_float2(acc[r][6], acc[r][7]);
-      }
+    float m_row, l_row, o[2 * RPW];
+    wave_merge_slots<DPH, RPW>(m_run, l_run, acc, m_row, l_row, o);
+    if (sl == 0 && c == Sh::owner(my_r, 0)) lds.ml[wave * RPW + my_r] = make_float2(m_row, l_row);
+    const int j = lane >> 4;
+    if (DPH == 128 || (lane & 8) == 0) {
+      float4* dst = reinterpret_cast<float4*>(lds.acc + (wave * RPW + merged_row<RPW>(j)) * DPH +
+                                              8 * c + merged_col<RPW>(j));
+      dst[0] = make_float4(o[0], o[1], o[2], o[3]);
+      if constexpr (RPW == 4) dst[1] = make_float4(o[4], o[5], o[6], o[7]);
     }
   }
   __syncthreads();
@@ -955,14 +989,14 @@ __device__ __forceinline__ void stream_item(const AttnArgs& a, int part, int kvh
     const int dcol = 2 * (threadIdx.x - r * DP);
     float mx = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < WAVES; w++) mx = fmaxf(mx, s_buf[(w * RPW + r) * REC]);
+    for (int w = 0; w < WAVES; w++) mx = fmaxf(mx, lds.ml[w * RPW + r].x);
     float l = 0.f, o0 = 0.f, o1 = 0.f;
 #pragma unroll
     for (int w = 0; w < WAVES; w++) {
-      const float* rec = s_buf + (w * RPW + r) * REC;
-      const float wt = rec[0] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(rec[0] - mx);
-      l += rec[1] * wt;
-      const float2 x = *reinterpret_cast<const float2*>(rec + 2 + dcol);
+      const float2 ml = lds.ml[w * RPW + r];
+      const float wt = ml.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ml.x - mx);
+      l += ml.y * wt;
+      const float2 x = *reinterpret_cast<const float2*>(lds.acc + (w * RPW + r) * DPH + dcol);
       o0 += x.x * wt;
       o1 += x.y * wt;
     }
@@ -1047,7 +1081,6 @@ __device__ __forceinline__ void block_attend(const float* q_all, float* out, con
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nw = blockDim.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int sl = lane / CH;
   const int c = lane % CH;
   const TileSource src{kv.pool, kv.block_tables + (size_t)layer * kv.max_blocks_per_layer,
                        kv.kv_dim, kv.block_size, total_len};
@@ -1076,18 +1109,24 @@ __device__ __forceinline__ void block_attend(const float* q_all, float* out, con
       for (int e = 0; e < 8; e++) acc[r][e] = 0.f;
     wave_attend<DPH, RPW, 2>(src, kvh, 0, n_tiles, 1, nrows, min_lim, my_lim, qscale, q_raw,
                              m_run, l_run, acc);
-    float mx[RPW], l[RPW];
-    wave_merge_slots<DPH, RPW>(m_run, l_run, acc, mx, l);
-    if (sl == 0) {
+    float m_row, l_row, o[2 * RPW];
+    wave_merge_slots<DPH, RPW>(m_run, l_run, acc, m_row, l_row, o);
+    // 16-lane row j holds row rr of the output; its sum sits in the lanes
+    // of chunk owner(rr, 0).
+    const int j = lane >> 4;
+    const int rr = merged_row<RPW>(j);
+    float l_mine = 0.f;
 #pragma unroll
-      for (int r = 0; r < RPW; r++) {
-        if (r < nrows) {
-          const float inv = finish_scale(l[r]);
-          float4* dst = reinterpret_cast<float4*>(out + (size_t)(h0 + r) * DPH + 8 * c);
-          dst[0] = make_float4(acc[r][0] * inv, acc[r][1] * inv, acc[r][2] * inv, acc[r][3] * inv);
-          dst[1] = make_float4(acc[r][4] * inv, acc[r][5] * inv, acc[r][6] * inv, acc[r][7] * inv);
-        }
-      }
+    for (int r = 0; r < RPW; r++) {
+      const float lr = from_owner_f<DPH, RPW>(l_row, r, 0, false);
+      if (r == rr) l_mine = lr;
+    }
+    if (rr < nrows && (DPH == 128 || (lane & 8) == 0)) {
+      const float inv = finish_scale(l_mine);
+      float4* dst = reinterpret_cast<float4*>(out + (size_t)(h0 + rr) * DPH + 8 * c +
+                                              merged_col<RPW>(j));
+      dst[0] = make_float4(o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv);
+      if constexpr (RPW == 4) dst[1] = make_float4(o[4] * inv, o[5] * inv, o[6] * inv, o[7] * inv);
     }
   }
 }
