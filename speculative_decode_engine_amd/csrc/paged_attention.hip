@@ -36,10 +36,27 @@
 namespace sde {
 namespace attn {
 
+// Workgroup -> (partition, KV head, row group).  Long contexts (waves of
+// four tiles or more) take the KV head fastest in the linear workgroup
+// index: consecutive workgroups then read the adjacent KV-head slices of the
+// same token rows at the same time, which the memory system serves faster
+// than the same slices read by workgroups far apart in dispatch order.
+template <int CHUNK>
+__device__ __forceinline__ int3 stream_coords() {
+  if constexpr (CHUNK < 4) {
+    return make_int3(blockIdx.x, blockIdx.y, blockIdx.z);
+  } else {
+    const int lin = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+    return make_int3((lin / gridDim.y) % gridDim.x, lin % gridDim.y,
+                     lin / (gridDim.x * gridDim.y));
+  }
+}
+
 template <int DPH, int RPW, int CHUNK>
 __global__ __launch_bounds__(64 * kStreamWaves) void attn_stream_kernel(AttnArgs a) {
   __shared__ StreamLds<DPH, RPW, kStreamWaves> lds;
-  stream_item<DPH, RPW, CHUNK, kStreamWaves>(a, blockIdx.x, blockIdx.y, blockIdx.z, lds);
+  const int3 w = stream_coords<CHUNK>();
+  stream_item<DPH, RPW, CHUNK, kStreamWaves>(a, w.x, w.y, w.z, lds);
 }
 
 // Verify windows whose 8-wave plan leaves long serial tile chains per wave
@@ -58,8 +75,8 @@ template <int DPH, int RPW, int CHUNK>
 __global__ __launch_bounds__(64 * kStreamWaves) void attn_rope_kernel(AttnArgs a, RopeArgs rp) {
   __shared__ StreamLds<DPH, RPW, kStreamWaves> lds;
   __shared__ float2 rope_cs[kRopeMaxQueries * (DPH / 2)];
-  stream_item<DPH, RPW, CHUNK, kStreamWaves, true>(a, blockIdx.x, blockIdx.y, blockIdx.z, lds,
-                                                   &rp, rope_cs);
+  const int3 w = stream_coords<CHUNK>();
+  stream_item<DPH, RPW, CHUNK, kStreamWaves, true>(a, w.x, w.y, w.z, lds, &rp, rope_cs);
 }
 
 }  // namespace attn
