@@ -57,6 +57,8 @@ def parse_args():
     p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="approximate CPU work of the baseline sample")
     p.add_argument("--only-headline", action="store_true")
+    p.add_argument("--only-matvec", action="store_true",
+                   help="time only the output projection (sde_matvec) and print its JSON")
     p.add_argument("--calibrate-copy", type=int, default=0, metavar="MiB",
                    help="after the benchmark, copy a MiB-sized buffer 5 times")
     return p.parse_args()
@@ -237,6 +239,58 @@ def bench_accept(torch, steps=200, k=4, vocab=128256):
     return out
 
 
+def bench_matvec(torch, steps, warmup):
+    """The output projection after attention (sde_matvec): us per call and
+    algorithmic GB/s (fp16 weights once + fp32 x, out read when accumulating,
+    out written) at the reference models' Wo / W_down shapes, graph-replayed
+    over >= 512 MiB of distinct weight matrices (beyond the 256 MB Infinity
+    Cache); the C restatement of the reference's per-column loop
+    (oracle_matvec, OpenMP on the host cores) timed beside the Llama-3-8B Wo."""
+    from speculative_decode_engine_amd import matvec, matvec_workspace
+    shapes = [("llama3_8b_wo", 1, 4096, 4096, 1), ("llama3_8b_wo_verify", 5, 4096, 4096, 0),
+              ("llama3_8b_w_down", 1, 14336, 4096, 1), ("qwen25_7b_wo", 1, 3584, 3584, 1),
+              ("tinyllama_wo", 1, 2048, 2048, 1)]
+    out = {}
+    g = torch.Generator(device="cuda")
+    g.manual_seed(21)
+    for name, M, d_in, d_out, acc in shapes:
+        wbytes = d_in * d_out * 2
+        n_mats = max(4, -(-(512 << 20) // wbytes))
+        Ws = [(torch.randn(d_in, d_out, device="cuda", generator=g) * 0.02).half()
+              for _ in range(n_mats)]
+        x = torch.randn(M, d_in, device="cuda", generator=g)
+        y = torch.zeros(M, d_out, device="cuda")
+        ws = matvec_workspace(d_in, d_out, M, "cuda")
+        us = graph_step_ms(torch, lambda i: matvec(x, Ws[i % n_mats], out=y, accumulate=bool(acc),
+                                                    workspace=ws), steps, warmup) * 1e3
+        nbytes = wbytes + M * d_in * 4 + M * d_out * 4 * (2 if acc else 1)
+        gbps = nbytes / (us * 1e-6) / 1e9
+        out[name] = dict(n_rows=M, d_in=d_in, d_out=d_out, accumulate=acc, us=round(us, 3),
+                         algorithmic_bytes=nbytes, gbps=round(gbps, 1),
+                         frac_of_hbm_peak=round(gbps / HBM_PEAK_GBPS, 4))
+        del Ws
+        torch.cuda.empty_cache()
+    try:
+        from oracle import paged_kv as O
+        O.lib()
+        rng = np.random.default_rng(0)
+        xs = rng.standard_normal((1, 4096)).astype(np.float32)
+        Wb = (rng.standard_normal((4096, 4096)) * 0.02).astype(np.float16).view(np.uint16)
+        o = np.zeros((1, 4096), np.float32)
+        O.matvec_ref(xs, Wb, o, True)
+        t = time.perf_counter()
+        reps = 5
+        for _ in range(reps):
+            O.matvec_ref(xs, Wb, o, True)
+        cpu_us = (time.perf_counter() - t) / reps * 1e6
+        out["cpu_llama3_8b_wo"] = dict(us=round(cpu_us, 1), cores=int(O.lib().oracle_max_threads()),
+                                       kind="port", sample="5 x the 4096x4096 Wo of one decode "
+                                       "token, the reference's per-column fp32 loop in C")
+    except Exception as e:  # the CPU leg is a reported baseline only
+        out["cpu_llama3_8b_wo"] = dict(error=str(e))
+    return out
+
+
 def cpu_baseline(W, w, seconds):
     """The CPU oracle's tile restatement of attention.h (OpenMP over
     (query, head) pairs) on one 32K-key layer-step of the same shape, run
@@ -301,6 +355,9 @@ def main():
     _native.load()
     torch.cuda.set_device(0)
     steps, warmup = args.steps, args.warmup
+    if args.only_matvec:
+        print(json.dumps({"matvec": bench_matvec(torch, steps, warmup)}), flush=True)
+        return
 
     w = W.CONFIGS[HEADLINE]
     log(f"[bench] headline {HEADLINE}: {steps} steps, {warmup} warmup")
@@ -334,6 +391,8 @@ def main():
         extra["rollback_us"] = bench_rollback(torch, W)
         extra["accept_us"] = bench_accept(torch)
         log("[bench] accept", json.dumps(extra["accept_us"]))
+        extra["matvec"] = bench_matvec(torch, steps, warmup)
+        log("[bench] matvec", json.dumps(extra["matvec"]))
         for k_, v_ in configs.items():
             log(f"[bench] {k_}: {v_['us_per_layer_step']} us/layer-step, {v_['gbps']} GB/s")
 

@@ -1,0 +1,434 @@
+// Output-projection GEMV (Wo) on gfx950: out[m][c] (+)= sum_r x[m][r] * W[r][c]
+// with fp16 weights W [d_in][d_out] (row-major, the reference's layout,
+// utils.h:410-416 and model.h:19) and fp32 activations and accumulation.
+//
+//   device_matvec_partial        utils.h:417-433
+//   device_matvec_partial_accum  utils.h:437-452 (Wo / W_down in
+//                                coop_layer_forward, kernels.cu:2742-2747)
+//   device_matvec_batched        utils.h:248-280 (the verify window's Wo,
+//                                model.cu:717, 892)
+//   device_matvec_grid           all blocks of a persistent kernel share one
+//                                projection (the step after attention)
+//
+// Layout of the work (libsde_paged's sde_matvec and device_matvec_grid):
+// the columns are cut into tiles of 512 (a wave's 64 lanes x 8 fp16, one
+// 16-byte load per lane covers 1 KiB of a row) and the rows into `splits`
+// ranges, one workgroup per (column tile, row range).  Its waves stream
+// rows w, w+WAVES, ... of the range, two batches of eight 16-byte loads in
+// flight per lane; x[m][r] is wave-uniform (scalar loads).  The waves' sums meet in
+// LDS; each row range publishes a partial per column, and the last
+// workgroup of a column tile to finish (one arrival counter per tile) adds
+// the partials in row-range order, so the result does not depend on
+// arrival order.  HBM-bound: d_in * d_out * 2 bytes of weights per call.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "sde_paged_kv.h"
+
+namespace sde {
+namespace mv {
+
+constexpr int kCols = 512;      // columns per tile: 64 lanes x 8 fp16
+constexpr int kUnroll = 8;      // rows in flight per wave
+constexpr int kMaxSplit = 64;   // row ranges per column tile
+constexpr int kMaxRows = 16;    // rows of x (the verify window is <= 9)
+
+struct MvArgs {
+  const float* x;       // [M][d_in]
+  const uint16_t* W;    // [d_in][d_out] fp16 bits
+  float* out;           // [M][d_out]
+  float* partials;      // [splits][M][d_out]
+  uint32_t* counters;   // [col_tiles] arrival counters, zero at rest
+  int d_in;
+  int d_out;
+  int M;
+  int splits;
+  int rows_per_split;
+  int accumulate;       // out += (1) or out = (0)
+};
+
+struct MvPlan {
+  int col_tiles;
+  int splits;
+  int rows_per_split;
+};
+
+// Row ranges so that col_tiles * splits fills `blocks` workgroups, each wave
+// keeping at least kUnroll rows (one full batch of loads in flight).
+__host__ __device__ inline MvPlan mv_plan(int d_in, int d_out, int blocks, int waves) {
+  MvPlan p;
+  p.col_tiles = (d_out + kCols - 1) / kCols;
+  int s = blocks / p.col_tiles;
+  const int by_rows = d_in / (waves * kUnroll);
+  if (s > by_rows) s = by_rows;
+  if (s > kMaxSplit) s = kMaxSplit;
+  if (s < 1) s = 1;
+  p.rows_per_split = (d_in + s - 1) / s;
+  p.splits = (d_in + p.rows_per_split - 1) / p.rows_per_split;
+  return p;
+}
+
+// Bytes of the workspace (counters, then partials) for any call with these
+// shapes and at most kMaxSplit row ranges.
+__host__ __device__ inline size_t mv_counter_bytes(int d_out) {
+  return ((size_t)((d_out + kCols - 1) / kCols) * 4 + 255) / 256 * 256;
+}
+__host__ __device__ inline size_t mv_workspace_size(int d_in, int d_out, int M) {
+  (void)d_in;
+  return mv_counter_bytes(d_out) + (size_t)kMaxSplit * M * d_out * sizeof(float);
+}
+
+__device__ __forceinline__ void mv_store_dev(float* p, float v) {
+  __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __builtin_bit_cast(uint32_t, v),
+                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float mv_load_dev(const float* p) {
+  return __builtin_bit_cast(
+      float, __hip_atomic_load(reinterpret_cast<uint32_t*>(const_cast<float*>(p)),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+
+__device__ __forceinline__ float h_lo(uint32_t w) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu));
+}
+__device__ __forceinline__ float h_hi(uint32_t w) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+}
+
+// The row range [r0, r1) of W as a raw buffer: loads address it by a
+// scalar row offset plus the lane's 32-bit column offset, so no 64-bit
+// per-lane address is formed.
+struct MvRows {
+  __amdgpu_buffer_rsrc_t rsrc;
+  uint32_t lane_off;   // byte offset of the lane's 16-byte column chunk
+  uint32_t row_bytes;  // d_out * 2
+  int r0, r1;
+};
+
+__device__ __forceinline__ MvRows mv_rows(const MvArgs& a, int r0, int r1, int colc) {
+  constexpr int kRsrcWord3 = 0x00020000;  // gfx9 raw buffer, 32-bit data format
+  MvRows t;
+  t.row_bytes = (uint32_t)a.d_out * 2u;
+  t.rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(a.W + (size_t)r0 * a.d_out), 0,
+      (int)((uint32_t)(r1 - r0) * t.row_bytes), kRsrcWord3);
+  t.lane_off = (uint32_t)colc * 2u;
+  t.r0 = r0;
+  t.r1 = r1;
+  return t;
+}
+
+// U rows r, r+WAVES, ... of the lane's 16-byte column chunk (rows at or
+// past r1 re-read row r1-1).
+template <int WAVES, int U>
+__device__ __forceinline__ void mv_load_batch(const MvRows& t, int r, uint4 (&w)[U]) {
+  typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+#pragma unroll
+  for (int u = 0; u < U; u++) {
+    const int rr = min(r + u * WAVES, t.r1 - 1);
+    const u4v v = __builtin_bit_cast(
+        u4v, __builtin_amdgcn_raw_buffer_load_b128(t.rsrc, t.lane_off,
+                                                   (uint32_t)(rr - t.r0) * t.row_bytes, 0));
+    w[u] = make_uint4(v.x, v.y, v.z, v.w);
+  }
+}
+
+// acc[m][j] += x[m][row] * w[row][j] over the batch's rows below r1 (all
+// of them when FULL: no per-row branch, so the batch's scalar x loads issue
+// together ahead of the multiply-adds).
+template <int MB, int WAVES, int U, bool FULL>
+__device__ __forceinline__ void mv_fma_batch(const struct MvArgs& a, int r, int r1,
+                                             const uint4 (&w)[U], float (&acc)[MB][8]) {
+  float xv[U][MB];
+#pragma unroll
+  for (int u = 0; u < U; u++) {
+    const int rr = FULL ? r + u * WAVES : min(r + u * WAVES, r1 - 1);
+#pragma unroll
+    for (int m = 0; m < MB; m++) xv[u][m] = a.x[(size_t)min(m, a.M - 1) * a.d_in + rr];
+  }
+#pragma unroll
+  for (int u = 0; u < U; u++) {
+    if (FULL || r + u * WAVES < r1) {
+      const uint32_t wd[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
+#pragma unroll
+      for (int m = 0; m < MB; m++) {
+        if (m < a.M) {
+#pragma unroll
+          for (int k = 0; k < 4; k++) {
+            acc[m][2 * k] = fmaf(xv[u][m], h_lo(wd[k]), acc[m][2 * k]);
+            acc[m][2 * k + 1] = fmaf(xv[u][m], h_hi(wd[k]), acc[m][2 * k + 1]);
+          }
+        }
+      }
+    }
+  }
+}
+
+// LDS of one workgroup item: the waves' column sums and the last-arrival flag.
+template <int WAVES>
+struct MvLds {
+  float red[WAVES * kCols] __attribute__((aligned(16)));
+  int last;
+};
+
+// (column tile ct, row range ks) on the calling workgroup; every thread
+// calls it.  MB >= a.M rows of x are unrolled; waves at or past WAVES idle.
+template <int MB, int WAVES>
+__device__ __forceinline__ void mv_item(const MvArgs& a, int ct, int ks, MvLds<WAVES>& lds) {
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int lane = threadIdx.x & 63;
+  const int col = ct * kCols + lane * 8;
+  // Lanes past d_out load the tile's last valid 16 bytes (results unused).
+  const int colc = col < a.d_out ? col : a.d_out - 8;
+  const int r0 = ks * a.rows_per_split;
+  const int r1 = min(a.d_in, r0 + a.rows_per_split);
+  float acc[MB][8];
+#pragma unroll
+  for (int m = 0; m < MB; m++)
+#pragma unroll
+    for (int j = 0; j < 8; j++) acc[m][j] = 0.f;
+
+  if (wave < WAVES) {
+    // Rows r0+wave, r0+wave+WAVES, ... in batches of kUnroll, two batches
+    // in flight: the next batch's loads are issued before this batch's
+    // multiply-adds.  Loads past the range re-read its last row (never
+    // used); x of a batch is fetched with scalar loads ahead of its use.
+    constexpr int U = MB >= 16 ? kUnroll / 2 : kUnroll;  // registers for 16 rows of x
+    const MvRows rows = mv_rows(a, r0, r1, colc);
+    const int step = WAVES * U;
+    uint4 wa[U], wb[U];
+    mv_load_batch<WAVES, U>(rows, r0 + wave, wa);
+    const int last = (U - 1) * WAVES;  // offset of a batch's last row
+    for (int r = r0 + wave; r < r1; r += 2 * step) {
+      mv_load_batch<WAVES, U>(rows, r + step, wb);
+      if (r + last < r1)
+        mv_fma_batch<MB, WAVES, U, true>(a, r, r1, wa, acc);
+      else
+        mv_fma_batch<MB, WAVES, U, false>(a, r, r1, wa, acc);
+      if (r + step >= r1) break;
+      mv_load_batch<WAVES, U>(rows, r + 2 * step, wa);
+      if (r + step + last < r1)
+        mv_fma_batch<MB, WAVES, U, true>(a, r + step, r1, wb, acc);
+      else
+        mv_fma_batch<MB, WAVES, U, false>(a, r + step, r1, wb, acc);
+    }
+  }
+
+  // ---- waves -> one partial per (row of x, column) --------------------
+#pragma unroll
+  for (int m = 0; m < MB; m++) {
+    if (m >= a.M) break;
+    __syncthreads();  // the previous row's sums have been read
+    if (wave < WAVES) {
+      float4* d = reinterpret_cast<float4*>(lds.red + wave * kCols + lane * 8);
+      d[0] = make_float4(acc[m][0], acc[m][1], acc[m][2], acc[m][3]);
+      d[1] = make_float4(acc[m][4], acc[m][5], acc[m][6], acc[m][7]);
+    }
+    __syncthreads();
+    for (int t = threadIdx.x; t < kCols; t += blockDim.x) {
+      const int c = ct * kCols + t;
+      if (c >= a.d_out) break;
+      float v = 0.f;
+#pragma unroll
+      for (int w = 0; w < WAVES; w++) v += lds.red[w * kCols + t];
+      float* o = a.out + (size_t)m * a.d_out + c;
+      if (a.splits == 1)
+        *o = a.accumulate ? *o + v : v;
+      else
+        mv_store_dev(a.partials + ((size_t)ks * a.M + m) * a.d_out + c, v);
+    }
+  }
+  if (a.splits == 1) return;
+
+  // ---- the last row range of this column tile adds the partials -------
+  // The partials are device-scope stores; waiting for them (vmcnt) before
+  // the arrival increment orders them before it.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t* ctr = a.counters + ct;
+    const uint32_t prev =
+        __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int last = prev == (uint32_t)(a.splits - 1);
+    if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    lds.last = last;
+  }
+  __syncthreads();
+  if (!lds.last) return;
+  const int S = a.splits;
+  for (int m = 0; m < a.M; m++) {
+    for (int t = threadIdx.x; t < kCols; t += blockDim.x) {
+      const int c = ct * kCols + t;
+      if (c >= a.d_out) break;
+      const float* p = a.partials + (size_t)m * a.d_out + c;
+      const size_t stride = (size_t)a.M * a.d_out;
+      float v = 0.f;
+      for (int k0 = 0; k0 < S; k0 += 8) {
+        float pv[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) pv[u] = mv_load_dev(p + (size_t)min(k0 + u, S - 1) * stride);
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+          if (k0 + u < S) v += pv[u];
+      }
+      float* o = a.out + (size_t)m * a.d_out + c;
+      *o = a.accumulate ? *o + v : v;
+    }
+  }
+}
+
+// Rows of x rounded up to an unrolled instantiation.
+template <int WAVES>
+__device__ __forceinline__ void mv_item_any(const MvArgs& a, int ct, int ks, MvLds<WAVES>& lds) {
+  if (a.M <= 1)
+    mv_item<1, WAVES>(a, ct, ks, lds);
+  else if (a.M <= 2)
+    mv_item<2, WAVES>(a, ct, ks, lds);
+  else if (a.M <= 4)
+    mv_item<4, WAVES>(a, ct, ks, lds);
+  else if (a.M <= 8)
+    mv_item<8, WAVES>(a, ct, ks, lds);
+  else
+    mv_item<16, WAVES>(a, ct, ks, lds);
+}
+
+}  // namespace mv
+
+// ---- reference-named device API ------------------------------------------
+
+// utils.h:417-452: out[c] (+)= sum_r x[r] * W[r*d_out + c] for c in
+// [col_start, col_start+col_count), by the calling block alone (any
+// blockDim that is a multiple of 64, no LDS).  The stripe's 8-column groups
+// are spread over the waves, and each wave's lanes split the rows of its
+// groups into phases whose sums meet through a lane butterfly; 16-byte
+// weight loads.  Requires d_out % 8 == 0, col_start % 8 == 0 and a
+// 16-byte-aligned W (the reference's shapes); each thread returns once its
+// wave's columns are written (no block barrier, as in the reference).
+namespace mv {
+template <bool ACCUM>
+__device__ __forceinline__ void block_matvec(const float* __restrict__ x,
+                                             const uint16_t* __restrict__ W, float* out,
+                                             int d_in, int d_out, int col_start, int col_count) {
+  const int waves = blockDim.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int lane = threadIdx.x & 63;
+  const int groups = (col_count + 7) / 8;
+  // Groups per wave (a power of two <= 64) and row phases per wave.
+  int gpw = 1;
+  while (gpw < 64 && gpw * waves < groups) gpw *= 2;
+  const int phases = 64 / gpw;
+  for (int g0 = wave * gpw; g0 < groups; g0 += waves * gpw) {
+    const int g = g0 + (lane % gpw);
+    const int p = lane / gpw;
+    const bool live = g < groups;
+    const int col = col_start + 8 * (live ? g : g0);
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int r = p; r < d_in; r += phases * 4) {
+      uint4 w[4];
+      float xv[4];
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        const int rr = r + u * phases;
+        xv[u] = rr < d_in ? x[rr] : 0.f;
+        w[u] = *reinterpret_cast<const uint4*>(W + (size_t)min(rr, d_in - 1) * d_out + col);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        const uint32_t wd[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+          acc[2 * k] = fmaf(xv[u], h_lo(wd[k]), acc[2 * k]);
+          acc[2 * k + 1] = fmaf(xv[u], h_hi(wd[k]), acc[2 * k + 1]);
+        }
+      }
+    }
+    // Sum over the phases (lanes gpw, 2*gpw, ... apart).
+    for (int s = gpw; s < 64; s *= 2)
+#pragma unroll
+      for (int j = 0; j < 8; j++) acc[j] += __shfl_xor(acc[j], s);
+    if (p == 0 && live) {
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const int c = col + j;
+        if (c < col_start + col_count) out[c] = ACCUM ? out[c] + acc[j] : acc[j];
+      }
+    }
+  }
+}
+}  // namespace mv
+
+__device__ inline void device_matvec_partial(const float* __restrict__ x,
+                                             const uint16_t* __restrict__ W, float* out,
+                                             int d_in, int d_out, int col_start,
+                                             int col_count) {
+  mv::block_matvec<false>(x, W, out, d_in, d_out, col_start, col_count);
+}
+
+__device__ inline void device_matvec_partial_accum(const float* __restrict__ x,
+                                                   const uint16_t* __restrict__ W, float* out,
+                                                   int d_in, int d_out, int col_start,
+                                                   int col_count) {
+  mv::block_matvec<true>(x, W, out, d_in, d_out, col_start, col_count);
+}
+
+// utils.h:248-280: g_out[b][c] = sum_r g_x[b*d_in + r] * W[r][c] for b < B,
+// every column, by the calling block.
+__device__ inline void device_matvec_batched(const float* g_x, const uint16_t* W, float* g_out,
+                                             int d_in, int d_out, int B) {
+  for (int b = 0; b < B; b++)
+    mv::block_matvec<false>(g_x + (size_t)b * d_in, W, g_out + (size_t)b * d_out, d_in, d_out,
+                            0, d_out);
+}
+
+// Grid-cooperative projection for persistent kernels: every block of the
+// grid calls it with the same arguments (blockDim.x >= 256, a multiple of
+// 64; any grid size) and blocks take the (column tile, row range) items in
+// turns; out[m][c] (+)= sum_r x[m][r] W[r][c] for m < M <= 16.  The
+// workspace (sde_matvec_workspace_size bytes) starts with arrival counters
+// that must be zero before the first call (every call leaves them zero).
+// Returns SDE_OK in every thread, or an error code before any work; out is
+// complete once the grid has synchronized after the call.
+__device__ inline int device_matvec_grid(const float* x, const uint16_t* W, float* out,
+                                         int d_in, int d_out, int M, int accumulate,
+                                         void* workspace, size_t workspace_bytes) {
+  using namespace mv;
+  if (blockDim.x < 256 || blockDim.x % 64 != 0) return SDE_ERR_UNSUPPORTED;
+  if (d_out % 8 != 0 || (reinterpret_cast<uintptr_t>(W) & 15u) != 0) return SDE_ERR_UNSUPPORTED;
+  if (!x || !W || !out || !workspace || d_in < 1 || d_out < 8 || M < 1 || M > kMaxRows)
+    return SDE_ERR_INVALID_ARGUMENT;
+  if (workspace_bytes < mv_workspace_size(d_in, d_out, M)) return SDE_ERR_WORKSPACE;
+  const bool w8 = blockDim.x >= 512;
+  const MvPlan p = mv_plan(d_in, d_out, gridDim.x * gridDim.y * gridDim.z, w8 ? 8 : 4);
+  MvArgs a;
+  a.x = x;
+  a.W = W;
+  a.out = out;
+  a.counters = static_cast<uint32_t*>(workspace);
+  a.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + mv_counter_bytes(d_out));
+  a.d_in = d_in;
+  a.d_out = d_out;
+  a.M = M;
+  a.splits = p.splits;
+  a.rows_per_split = p.rows_per_split;
+  a.accumulate = accumulate;
+  __shared__ MvLds<8> lds;
+  const int blk = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+  const int nblk = gridDim.x * gridDim.y * gridDim.z;
+  const int items = p.col_tiles * p.splits;
+  for (int it = blk; it < items; it += nblk) {
+    const int ct = it % p.col_tiles;
+    const int ks = it / p.col_tiles;
+    if (w8)
+      mv_item_any<8>(a, ct, ks, lds);
+    else
+      mv_item_any<4>(a, ct, ks, *reinterpret_cast<MvLds<4>*>(&lds));
+    __syncthreads();  // LDS reuse by the block's next item
+  }
+  return SDE_OK;
+}
+
+}  // namespace sde

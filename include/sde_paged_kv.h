@@ -289,6 +289,32 @@ int sde_attention_dispatch(int attn_type, sde_kv_cache* cache, int layer,
                            void* d_workspace, size_t workspace_bytes,
                            sde_stream_t stream);
 
+/* Workspace bytes of sde_matvec and of the grid-cooperative device function
+ * sde::device_matvec_grid (include/sde/matvec_device.hpp) for any call with
+ * these shapes; 0 for invalid shapes.  Zero it once after allocation: its
+ * leading arrival counters must start at zero (every call leaves them
+ * zero). */
+size_t sde_matvec_workspace_size(int d_in, int d_out, int n_rows);
+
+/* The output projection after attention, across all CUs:
+ * d_out[m][c] = (accumulate ? d_out[m][c] : 0) + sum_r d_x[m][r] * W[r][c]
+ * for m < n_rows, c < d_out_dim, with W fp16 bits [d_in][d_out_dim]
+ * (row-major, the SDEC weight layout, model.h:19) and fp32 x, out and
+ * accumulation.  Replaces device_matvec_partial_accum striped over the
+ * blocks of coop_layer_forward (utils.h:437-452, kernels.cu:2742-2747:
+ * g_hidden += Wo(attn), accumulate = 1), device_matvec_batched for the
+ * verify window's Wo (utils.h:248-280, model.cu:717: n_rows = B <= 9,
+ * accumulate = 0) and the multi-kernel path's Wo GEMM + residual add
+ * (kernels.cu:1069-1075, here with fp32 activations).  1 <= n_rows <= 16;
+ * d_out_dim a multiple of 8 and W 16-byte aligned (SDE_ERR_UNSUPPORTED
+ * otherwise).  d_workspace holds sde_matvec_workspace_size(...) bytes
+ * (SDE_ERR_WORKSPACE when smaller); calls sharing a workspace must be
+ * ordered on one stream.  Deterministic: the sum order does not depend on
+ * scheduling. */
+int sde_matvec(const float* d_x, const uint16_t* d_W, float* d_out, int d_in,
+               int d_out_dim, int n_rows, int accumulate, void* d_workspace,
+               size_t workspace_bytes, sde_stream_t stream);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif

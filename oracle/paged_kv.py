@@ -66,6 +66,7 @@ def lib() -> ctypes.CDLL:
     L.oracle_paged_attention.argtypes = [_f32p, _f32p, _f64p, _u16p, _i32p, _ci, _ci, _ci, _ci,
                                          _ci, _ci, _ci, _ci, _ci]
     L.oracle_max_threads.restype = _ci
+    L.oracle_matvec.argtypes = [_f32p, _u16p, _f32p, _ci, _ci, _ci, _ci]
     _lib = L
     return L
 
@@ -391,3 +392,38 @@ def attention_f64_np(q: np.ndarray, K: np.ndarray, V: np.ndarray, nh: int, nkv: 
             w /= w.sum(axis=1, keepdims=True)
             out[m, heads] = w @ Vg[:L]
     return out.reshape(M, nh * dph)
+
+
+# ---- the output projection (Wo) -------------------------------------------
+
+def matvec_ref(x: np.ndarray, W_bits: np.ndarray, out: np.ndarray | None = None,
+               accumulate: bool = False) -> np.ndarray:
+    """device_matvec_partial(_accum) / device_matvec_batched (utils.h:248-280,
+    417-452) restated in C (oracle_matvec): fp32, per column in row order.
+    x fp32 [M][d_in], W_bits uint16 fp16 bits [d_in][d_out]."""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, W_bits.shape[0])
+    W_bits = np.ascontiguousarray(W_bits, dtype=np.uint16)
+    M, d_in = x.shape
+    d_out = W_bits.shape[1]
+    if out is None:
+        out = np.zeros((M, d_out), dtype=np.float32)
+    else:
+        out = np.ascontiguousarray(out, dtype=np.float32).reshape(M, d_out).copy()
+    lib().oracle_matvec(_p(x, _f32p), _p(W_bits, _u16p), _p(out, _f32p), d_in, d_out, M,
+                        int(bool(accumulate)))
+    return out
+
+
+def matvec_f64(x: np.ndarray, W_bits: np.ndarray, out0: np.ndarray | None = None) -> tuple:
+    """Exact-ish float64 product x @ W (W decoded from fp16 bits), plus the
+    per-output magnitude sum_r |x[m][r] * W[r][c]| that bounds an fp32
+    summation's rounding error; out0 (fp32) is added when given."""
+    x64 = np.asarray(x, dtype=np.float64).reshape(-1, W_bits.shape[0])
+    W64 = W_bits.view(np.float16).astype(np.float64)
+    y = x64 @ W64
+    mag = np.abs(x64) @ np.abs(W64)
+    if out0 is not None:
+        o = np.asarray(out0, dtype=np.float64).reshape(y.shape)
+        y = y + o
+        mag = mag + np.abs(o)
+    return y, mag

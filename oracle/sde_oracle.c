@@ -297,3 +297,25 @@ int oracle_max_threads(void) {
   return 1;
 #endif
 }
+
+/* device_matvec_partial_accum / device_matvec_partial (utils.h:417-452),
+ * literally: for each output column c (one thread per column in the
+ * reference), acc = sum over r = 0..d_in-1 of x[r] * float(W[r*d_out + c])
+ * in row order, fp32, multiply-add fused (nvcc contracts `acc += a*b`), then
+ * out[c] = acc or out[c] += acc.  For n_rows rows of x (device_matvec_batched,
+ * utils.h:248-267, is the same per row).  Columns are independent, so the
+ * OpenMP split over columns keeps the reference's per-column order. */
+void oracle_matvec(const float* x, const uint16_t* W, float* out, int d_in, int d_out,
+                   int n_rows, int accumulate) {
+  for (int m = 0; m < n_rows; m++) {
+    const float* xm = x + (size_t)m * d_in;
+    float* om = out + (size_t)m * d_out;
+#pragma omp parallel for schedule(static)
+    for (int c = 0; c < d_out; c++) {
+      float acc = 0.f;
+      for (int r = 0; r < d_in; r++)
+        acc = fmaf(xm[r], oracle_f16_to_f32(W[(size_t)r * d_out + c]), acc);
+      om[c] = accumulate ? om[c] + acc : acc;
+    }
+  }
+}

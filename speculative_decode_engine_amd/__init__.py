@@ -8,7 +8,8 @@ from .kv_cache import (ATTN_KDA, ATTN_LINEAR, ATTN_SLIDING_WINDOW, ATTN_SOFTMAX,
                        kv_cache_alloc, kv_cache_free, kv_cache_reset, spec_accept_greedy,
                        spec_accept_stochastic)
 from ._native import SDEError
+from .matvec import matvec, matvec_workspace
 
 __all__ = ["KVCache", "kv_cache_alloc", "kv_cache_free", "kv_cache_reset", "SDEError",
-           "spec_accept_greedy", "spec_accept_stochastic",
+           "spec_accept_greedy", "spec_accept_stochastic", "matvec", "matvec_workspace",
            "ATTN_SOFTMAX", "ATTN_SLIDING_WINDOW", "ATTN_KDA", "ATTN_LINEAR"]

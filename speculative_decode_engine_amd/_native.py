@@ -105,6 +105,8 @@ PROTOTYPES = {
                                            _c_int, _c_int, _c_int, _vp, _vp, _sz, _vp]),
     "sde_attention_dispatch": (_c_int, [_c_int, _vp, _c_int, _vp, _vp, _c_int, _c_int, _c_int,
                                         _c_int, _c_int, _vp, _sz, _vp]),
+    "sde_matvec_workspace_size": (_sz, [_c_int, _c_int, _c_int]),
+    "sde_matvec": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _sz, _vp]),
 }
 
 _LIB = None

@@ -1,0 +1,106 @@
+// The output projection after attention (Wo), across all CUs, behind the
+// C-ABI: sde_matvec replaces the reference's column-striped
+// device_matvec_partial_accum over the blocks of coop_layer_forward
+// (utils.h:437-452, kernels.cu:2742-2747), device_matvec_batched for the
+// verify window (utils.h:248-280, model.cu:717) and the multi-kernel path's
+// Wo GEMM + residual add (kernels.cu:1069-1075, with fp32 activations as in
+// the other two).  The work layout and its reduction are described in
+// include/sde/matvec_device.hpp.
+#include <hip/hip_runtime.h>
+
+#include "sde/matvec_device.hpp"
+#include "sde_internal.hpp"
+
+namespace sde {
+namespace mv {
+
+constexpr int kWaves = 8;
+
+template <int MB>
+__global__ __launch_bounds__(64 * kWaves) void matvec_kernel(MvArgs a) {
+  __shared__ MvLds<kWaves> lds;
+  mv_item<MB, kWaves>(a, blockIdx.x, blockIdx.y, lds);
+}
+
+}  // namespace mv
+}  // namespace sde
+
+namespace {
+
+using namespace sde::mv;
+
+// Compute units of the current device, cached per device.
+int current_cus(int* status) {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) {
+    *status = SDE_ERR_NO_DEVICE;
+    return 0;
+  }
+  if (dev < 64 && cus[dev] > 0) return cus[dev];
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      n < 1) {
+    *status = SDE_ERR_HIP;
+    return 0;
+  }
+  if (dev < 64) cus[dev] = n;
+  return n;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t sde_matvec_workspace_size(int d_in, int d_out, int M) {
+  if (d_in < 1 || d_out < 8 || M < 1 || M > kMaxRows) return 0;
+  return mv_workspace_size(d_in, d_out, M);
+}
+
+int sde_matvec(const float* d_x, const uint16_t* d_W, float* d_out, int d_in, int d_out_dim,
+               int M, int accumulate, void* d_workspace, size_t workspace_bytes,
+               sde_stream_t stream) {
+  if (!d_x || !d_W || !d_out || d_in < 1 || d_out_dim < 8 || M < 1 || M > kMaxRows)
+    return SDE_ERR_INVALID_ARGUMENT;
+  if (d_out_dim % 8 != 0 || (reinterpret_cast<uintptr_t>(d_W) & 15u) != 0)
+    return SDE_ERR_UNSUPPORTED;
+  int st = SDE_OK;
+  const int n_cus = current_cus(&st);
+  if (st != SDE_OK) return st;
+  const MvPlan p = mv_plan(d_in, d_out_dim, n_cus, kWaves);
+  MvArgs a;
+  a.x = d_x;
+  a.W = d_W;
+  a.out = d_out;
+  a.counters = nullptr;
+  a.partials = nullptr;
+  a.d_in = d_in;
+  a.d_out = d_out_dim;
+  a.M = M;
+  a.splits = p.splits;
+  a.rows_per_split = p.rows_per_split;
+  a.accumulate = accumulate ? 1 : 0;
+  if (p.splits > 1) {
+    if (!d_workspace || workspace_bytes < mv_workspace_size(d_in, d_out_dim, M))
+      return SDE_ERR_WORKSPACE;
+    a.counters = static_cast<uint32_t*>(d_workspace);
+    a.partials = reinterpret_cast<float*>(static_cast<char*>(d_workspace) +
+                                          mv_counter_bytes(d_out_dim));
+  }
+  const dim3 grid(p.col_tiles, p.splits);
+  const dim3 block(64 * kWaves);
+  const hipStream_t s = (hipStream_t)stream;
+  if (M <= 1)
+    sde::mv::matvec_kernel<1><<<grid, block, 0, s>>>(a);
+  else if (M <= 2)
+    sde::mv::matvec_kernel<2><<<grid, block, 0, s>>>(a);
+  else if (M <= 4)
+    sde::mv::matvec_kernel<4><<<grid, block, 0, s>>>(a);
+  else if (M <= 8)
+    sde::mv::matvec_kernel<8><<<grid, block, 0, s>>>(a);
+  else
+    sde::mv::matvec_kernel<16><<<grid, block, 0, s>>>(a);
+  return sde::launch_status();
+}
+
+}  // extern "C"

@@ -415,3 +415,65 @@ def test_rope_f64_planted_interleaved_pairing_fails(oracle):
     inter = np.empty(dph)
     inter[perm] = _rope(oracle, x[:, perm], 1, dph, [40])[0]
     assert np.abs(inter - W.rope_rotate_half(x, 1, dph, 40)[0]).max() > 1e-2
+
+
+# ---- the output projection (Wo) -------------------------------------------------
+# oracle_matvec restates device_matvec_partial(_accum) (utils.h:417-452) in C;
+# it is pinned by closed forms (identity weights, one-hot inputs), by the
+# float64 product, and by planted mistakes (transposed weights, dropped
+# row) that the fp32-summation tolerance must catch.
+
+MV_TOL = 1e-5  # x magnitude sum_r |x_r W_rc|: fp32 summation error bound used by the GPU tests
+
+
+def _mv_case(rng, M, d_in, d_out):
+    x = rng.standard_normal((M, d_in)).astype(np.float32)
+    Wb = (rng.standard_normal((d_in, d_out)) * 0.05).astype(np.float16).view(np.uint16)
+    return x, Wb
+
+
+def test_matvec_identity_and_one_hot_are_exact(oracle):
+    rng = np.random.default_rng(11)
+    d = 96
+    eye = np.eye(d, dtype=np.float16).view(np.uint16)
+    x = rng.standard_normal((2, d)).astype(np.float32)
+    assert np.array_equal(oracle.matvec_ref(x, eye), x)
+    _, Wb = _mv_case(rng, 1, d, 40)
+    for k in (0, 17, d - 1):
+        e = np.zeros((1, d), np.float32)
+        e[0, k] = 1.0
+        got = oracle.matvec_ref(e, Wb)
+        assert np.array_equal(got[0], Wb[k].view(np.float16).astype(np.float32))
+
+
+def test_matvec_accumulate_adds_to_out(oracle):
+    rng = np.random.default_rng(12)
+    x, Wb = _mv_case(rng, 3, 130, 24)
+    out0 = rng.standard_normal((3, 24)).astype(np.float32)
+    prod = oracle.matvec_ref(x, Wb)
+    acc = oracle.matvec_ref(x, Wb, out0, accumulate=True)
+    assert np.array_equal(acc, out0 + prod)  # out[c] += acc: one fp32 add of the same acc
+    y, mag = oracle.matvec_f64(x, Wb, out0)
+    assert np.all(np.abs(acc - y) <= MV_TOL * mag)
+
+
+@pytest.mark.parametrize("M,d_in,d_out", [(1, 1, 8), (1, 4096, 64), (9, 512, 48), (2, 1000, 16)])
+def test_matvec_matches_float64(oracle, M, d_in, d_out):
+    rng = np.random.default_rng(M * 1000 + d_in)
+    x, Wb = _mv_case(rng, M, d_in, d_out)
+    got = oracle.matvec_ref(x, Wb)
+    y, mag = oracle.matvec_f64(x, Wb)
+    assert np.all(np.abs(got - y) <= MV_TOL * mag + 1e-30)
+    # Linearity in x (exact in float64 terms up to the same bound).
+    got2 = oracle.matvec_ref(2.0 * x, Wb)
+    assert np.array_equal(got2, 2.0 * got)  # scaling by 2 is exact in fp32
+
+
+def test_matvec_planted_mistakes_exceed_tolerance(oracle):
+    rng = np.random.default_rng(13)
+    x, Wb = _mv_case(rng, 1, 256, 256)
+    y, mag = oracle.matvec_f64(x, Wb)
+    transposed = oracle.matvec_ref(x, np.ascontiguousarray(Wb.T))
+    assert np.any(np.abs(transposed - y) > MV_TOL * mag)
+    dropped = oracle.matvec_ref(x[:, :-1], np.ascontiguousarray(Wb[:-1]))
+    assert np.any(np.abs(dropped - y) > MV_TOL * mag)
