@@ -32,10 +32,13 @@
 namespace sde {
 namespace mv {
 
-constexpr int kCols = 512;      // columns per tile: 64 lanes x 8 fp16
+constexpr int kRowPhases = 2;   // rows per wave load (lane groups of 64/kRowPhases)
+constexpr int kLanesPerRow = 64 / kRowPhases;
+constexpr int kCols = 8 * kLanesPerRow;  // columns per tile: 8 fp16 per lane
 constexpr int kUnroll = 8;      // rows in flight per wave
 constexpr int kMaxSplit = 64;   // row ranges per column tile
 constexpr int kMaxRows = 16;    // rows of x (the verify window is <= 9)
+constexpr int kChunkRows = 8;   // rows of x per pass (unrolled in registers)
 
 struct MvArgs {
   const float* x;       // [M][d_in]
@@ -59,37 +62,80 @@ struct MvPlan {
 
 // Row ranges so that col_tiles * splits fills `blocks` workgroups, each wave
 // keeping at least kUnroll rows (one full batch of loads in flight).
-__host__ __device__ inline MvPlan mv_plan(int d_in, int d_out, int blocks, int waves) {
+// Rows of x of a pass rounded up to its unrolled instantiation (1, 2, 4, 8).
+__host__ __device__ inline int mv_row_bucket(int rows) {
+  return rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : 8;
+}
+
+// splits * bucket <= kMaxSplit: the combining workgroup then holds every
+// partial of its columns in registers (one round trip).
+__host__ __device__ inline MvPlan mv_plan(int d_in, int d_out, int blocks, int waves, int M) {
   MvPlan p;
   p.col_tiles = (d_out + kCols - 1) / kCols;
   int s = blocks / p.col_tiles;
-  const int by_rows = d_in / (waves * kUnroll);
+  const int by_rows = d_in / (waves * kUnroll * kRowPhases);
   if (s > by_rows) s = by_rows;
-  if (s > kMaxSplit) s = kMaxSplit;
+  const int cap = kMaxSplit / mv_row_bucket(M < kChunkRows ? M : kChunkRows);
+  if (s > cap) s = cap;
   if (s < 1) s = 1;
   p.rows_per_split = (d_in + s - 1) / s;
   p.splits = (d_in + p.rows_per_split - 1) / p.rows_per_split;
   return p;
 }
 
-// Bytes of the workspace (counters, then partials) for any call with these
-// shapes and at most kMaxSplit row ranges.
-__host__ __device__ inline size_t mv_counter_bytes(int d_out) {
-  return ((size_t)((d_out + kCols - 1) / kCols) * 4 + 255) / 256 * 256;
+// Rows of x are taken kChunkRows at a time; each pass has its own arrival
+// counters and partials.  Bytes of the workspace (counters, then partials)
+// for any call with these shapes and at most kMaxSplit row ranges.
+__host__ __device__ inline int mv_passes(int M) { return (M + kChunkRows - 1) / kChunkRows; }
+__host__ __device__ inline int mv_pass_rows(int M) { return M < kChunkRows ? M : kChunkRows; }
+__host__ __device__ inline size_t mv_counter_bytes(int d_out, int M) {
+  return ((size_t)mv_passes(M) * ((d_out + kCols - 1) / kCols) * 4 + 255) / 256 * 256;
+}
+__host__ __device__ inline size_t mv_pass_partial_floats(int d_out, int M) {
+  return (size_t)kMaxSplit * mv_pass_rows(M) * d_out;
 }
 __host__ __device__ inline size_t mv_workspace_size(int d_in, int d_out, int M) {
   (void)d_in;
-  return mv_counter_bytes(d_out) + (size_t)kMaxSplit * M * d_out * sizeof(float);
+  return mv_counter_bytes(d_out, M) +
+         (size_t)mv_passes(M) * mv_pass_partial_floats(d_out, M) * sizeof(float);
 }
 
-__device__ __forceinline__ void mv_store_dev(float* p, float v) {
-  __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __builtin_bit_cast(uint32_t, v),
-                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// The arguments of pass j (rows 8j .. 8j+7 of x) of a call whose whole-call
+// arguments are `a` (a.partials / a.counters at the workspace's areas).
+__host__ __device__ inline MvArgs mv_pass(const MvArgs& a, int j) {
+  MvArgs p = a;
+  p.x = a.x + (size_t)j * kChunkRows * a.d_in;
+  p.out = a.out + (size_t)j * kChunkRows * a.d_out;
+  p.M = a.M - j * kChunkRows < kChunkRows ? a.M - j * kChunkRows : kChunkRows;
+  p.counters = a.counters ? a.counters + (size_t)j * ((a.d_out + kCols - 1) / kCols) : nullptr;
+  p.partials = a.partials ? a.partials + (size_t)j * mv_pass_partial_floats(a.d_out, a.M)
+                          : nullptr;
+  return p;
 }
-__device__ __forceinline__ float mv_load_dev(const float* p) {
-  return __builtin_bit_cast(
-      float, __hip_atomic_load(reinterpret_cast<uint32_t*>(const_cast<float*>(p)),
-                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+
+// 16-byte device-scope (sc1) store / load of the partials through a raw
+// buffer over the partial area (`bytes` long): written through to the
+// device coherence point and read past other XCDs' L2, as agent-scope
+// relaxed atomics are.
+__device__ __forceinline__ void mv_store_dev16(float* base, uint32_t bytes, uint32_t off,
+                                               float4 v) {
+  constexpr int kSc1 = 16;
+  constexpr int kRsrcWord3 = 0x00020000;  // gfx9 raw buffer, 32-bit data format
+  typedef float f4v __attribute__((ext_vector_type(4)));
+  typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(base, 0, (int)bytes, kRsrcWord3);
+  const f4v d = {v.x, v.y, v.z, v.w};
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4v, d), r, off, 0, kSc1);
+}
+__device__ __forceinline__ float4 mv_load_dev16(const float* base, uint32_t bytes, uint32_t off) {
+  constexpr int kSc1 = 16;
+  constexpr int kRsrcWord3 = 0x00020000;
+  typedef float f4v __attribute__((ext_vector_type(4)));
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, (int)bytes, kRsrcWord3);
+  const f4v v = __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kSc1));
+  return make_float4(v.x, v.y, v.z, v.w);
 }
 
 __device__ __forceinline__ float h_lo(uint32_t w) {
@@ -99,79 +145,131 @@ __device__ __forceinline__ float h_hi(uint32_t w) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
 }
 
-// The row range [r0, r1) of W as a raw buffer: loads address it by a
-// scalar row offset plus the lane's 32-bit column offset, so no 64-bit
-// per-lane address is formed.
+// The row range [r0, r1) of W as a raw buffer.  A wave's load covers
+// kRowPhases consecutive rows (lane group rp = lane / kLanesPerRow takes row
+// rb + rp); the whole byte offset is the lane's 32-bit VGPR offset, so rows
+// past r1 fall outside the buffer and load zeros.
 struct MvRows {
   __amdgpu_buffer_rsrc_t rsrc;
-  uint32_t lane_off;   // byte offset of the lane's 16-byte column chunk
+  uint32_t lane_off;   // the lane's column chunk and row phase, bytes
   uint32_t row_bytes;  // d_out * 2
   int r0, r1;
 };
 
-__device__ __forceinline__ MvRows mv_rows(const MvArgs& a, int r0, int r1, int colc) {
+__device__ __forceinline__ MvRows mv_rows(const MvArgs& a, int r0, int r1, int colc, int rp) {
   constexpr int kRsrcWord3 = 0x00020000;  // gfx9 raw buffer, 32-bit data format
   MvRows t;
   t.row_bytes = (uint32_t)a.d_out * 2u;
   t.rsrc = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(a.W + (size_t)r0 * a.d_out), 0,
       (int)((uint32_t)(r1 - r0) * t.row_bytes), kRsrcWord3);
-  t.lane_off = (uint32_t)colc * 2u;
+  t.lane_off = (uint32_t)colc * 2u + (uint32_t)rp * t.row_bytes;
   t.r0 = r0;
   t.r1 = r1;
   return t;
 }
 
-// U rows r, r+WAVES, ... of the lane's 16-byte column chunk (rows at or
-// past r1 re-read row r1-1).
+// The U row blocks rb(u) = r + u * WAVES * kRowPhases of a batch (r the
+// wave's first row block): the lane's 16-byte chunk of row rb(u) + rp.
 template <int WAVES, int U>
 __device__ __forceinline__ void mv_load_batch(const MvRows& t, int r, uint4 (&w)[U]) {
   typedef uint32_t u4v __attribute__((ext_vector_type(4)));
 #pragma unroll
   for (int u = 0; u < U; u++) {
-    const int rr = min(r + u * WAVES, t.r1 - 1);
+    const uint32_t rb = (uint32_t)(r + u * WAVES * kRowPhases - t.r0);
     const u4v v = __builtin_bit_cast(
-        u4v, __builtin_amdgcn_raw_buffer_load_b128(t.rsrc, t.lane_off,
-                                                   (uint32_t)(rr - t.r0) * t.row_bytes, 0));
+        u4v, __builtin_amdgcn_raw_buffer_load_b128(t.rsrc, t.lane_off + rb * t.row_bytes, 0, 0));
     w[u] = make_uint4(v.x, v.y, v.z, v.w);
   }
 }
 
-// acc[m][j] += x[m][row] * w[row][j] over the batch's rows below r1 (all
-// of them when FULL: no per-row branch, so the batch's scalar x loads issue
-// together ahead of the multiply-adds).
+// acc[m][j] += x[m][row] * w[row][j] for the lane's rows of the batch
+// (row rb(u) + rp; rows at or past r1 weigh 0).  When FULL every row of the
+// batch is below r1.  x of the batch's rows is read with scalar loads (the
+// row blocks are wave-uniform) and picked per lane group.
+// x of the lane's row: from xl (the row range staged in LDS as
+// [m][row - r0], `rows` long) when given, else a scalar load per row phase
+// picked per lane group (a single row of x: the whole batch's scalars are
+// loaded ahead).
 template <int MB, int WAVES, int U, bool FULL>
-__device__ __forceinline__ void mv_fma_batch(const struct MvArgs& a, int r, int r1,
+__device__ __forceinline__ void mv_fma_batch(const struct MvArgs& a, int r, int r0, int r1,
+                                             int rp, const float* xl, int rows,
                                              const uint4 (&w)[U], float (&acc)[MB][8]) {
-  float xv[U][MB];
+  float xs[U][kRowPhases];
+  if (MB == 1 && !xl) {
 #pragma unroll
-  for (int u = 0; u < U; u++) {
-    const int rr = FULL ? r + u * WAVES : min(r + u * WAVES, r1 - 1);
+    for (int u = 0; u < U; u++)
 #pragma unroll
-    for (int m = 0; m < MB; m++) xv[u][m] = a.x[(size_t)min(m, a.M - 1) * a.d_in + rr];
+      for (int p = 0; p < kRowPhases; p++)
+        xs[u][p] = a.x[min(r + u * WAVES * kRowPhases + p, a.d_in - 1)];
   }
 #pragma unroll
   for (int u = 0; u < U; u++) {
-    if (FULL || r + u * WAVES < r1) {
-      const uint32_t wd[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
+    const int rb = r + u * WAVES * kRowPhases;
+    const bool live = FULL || rb + rp < r1;
+    const uint32_t wd[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
 #pragma unroll
-      for (int m = 0; m < MB; m++) {
-        if (m < a.M) {
+    for (int m = 0; m < MB; m++) {
+      if (m < a.M) {
+        float xv;
+        if (xl) {
+          xv = xl[m * rows + min(rb + rp, r1 - 1) - r0];
+        } else if (MB == 1) {
+          xv = xs[u][0];
 #pragma unroll
-          for (int k = 0; k < 4; k++) {
-            acc[m][2 * k] = fmaf(xv[u][m], h_lo(wd[k]), acc[m][2 * k]);
-            acc[m][2 * k + 1] = fmaf(xv[u][m], h_hi(wd[k]), acc[m][2 * k + 1]);
-          }
+          for (int p = 1; p < kRowPhases; p++) xv = rp == p ? xs[u][p] : xv;
+        } else {
+          xv = a.x[(size_t)m * a.d_in + min(rb + rp, r1 - 1)];
+        }
+        if (!FULL) xv = live ? xv : 0.f;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+          acc[m][2 * k] = fmaf(xv, h_lo(wd[k]), acc[m][2 * k]);
+          acc[m][2 * k + 1] = fmaf(xv, h_hi(wd[k]), acc[m][2 * k + 1]);
         }
       }
     }
   }
 }
 
+// Sum over the row phases of a wave (lane groups kLanesPerRow apart): every
+// lane gets the total of its column chunk.
+__device__ __forceinline__ float mv_phase_sum(float v) {
+  if constexpr (kRowPhases >= 4) {
+    const auto p = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(int, v),
+                                                    __builtin_bit_cast(int, v), false, false);
+    v = __builtin_bit_cast(float, (int)p[0]) + __builtin_bit_cast(float, (int)p[1]);
+  }
+  if constexpr (kRowPhases >= 2) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, v),
+                                                    __builtin_bit_cast(int, v), false, false);
+    v = __builtin_bit_cast(float, (int)p[0]) + __builtin_bit_cast(float, (int)p[1]);
+  }
+  return v;
+}
+
+// out[m][c..c+3] = v (+ out when accumulating); out may be 4-byte aligned.
+__device__ __forceinline__ void mv_write_out(const struct MvArgs& a, int m, int c, float4 v) {
+  float* o = a.out + (size_t)m * a.d_out + c;
+  if (a.accumulate) {
+    v.x += o[0];
+    v.y += o[1];
+    v.z += o[2];
+    v.w += o[3];
+  }
+  o[0] = v.x;
+  o[1] = v.y;
+  o[2] = v.z;
+  o[3] = v.w;
+}
+
 // LDS of one workgroup item: the waves' column sums and the last-arrival flag.
+constexpr int kXStage = 4096;  // floats of x staged per workgroup item
+
 template <int WAVES>
 struct MvLds {
   float red[WAVES * kCols] __attribute__((aligned(16)));
+  float xs[kXStage];
   int last;
 };
 
@@ -181,7 +279,9 @@ template <int MB, int WAVES>
 __device__ __forceinline__ void mv_item(const MvArgs& a, int ct, int ks, MvLds<WAVES>& lds) {
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int lane = threadIdx.x & 63;
-  const int col = ct * kCols + lane * 8;
+  const int rp = lane / kLanesPerRow;  // row phase
+  const int lc = lane % kLanesPerRow;  // 16-byte column chunk
+  const int col = ct * kCols + lc * 8;
   // Lanes past d_out load the tile's last valid 16 bytes (results unused).
   const int colc = col < a.d_out ? col : a.d_out - 8;
   const int r0 = ks * a.rows_per_split;
@@ -192,54 +292,78 @@ __device__ __forceinline__ void mv_item(const MvArgs& a, int ct, int ks, MvLds<W
 #pragma unroll
     for (int j = 0; j < 8; j++) acc[m][j] = 0.f;
 
+  // Several rows of x: stage the range's x in LDS when it fits.
+  const int xrows = r1 - r0;
+  const float* xl = nullptr;
+  if (MB > 1 && a.M * xrows <= kXStage) {
+    for (int i = threadIdx.x; i < a.M * xrows; i += blockDim.x) {
+      const int m = i / xrows;
+      lds.xs[i] = a.x[(size_t)m * a.d_in + r0 + (i - m * xrows)];
+    }
+    __syncthreads();
+    xl = lds.xs;
+  }
+
   if (wave < WAVES) {
-    // Rows r0+wave, r0+wave+WAVES, ... in batches of kUnroll, two batches
-    // in flight: the next batch's loads are issued before this batch's
-    // multiply-adds.  Loads past the range re-read its last row (never
-    // used); x of a batch is fetched with scalar loads ahead of its use.
-    constexpr int U = MB >= 16 ? kUnroll / 2 : kUnroll;  // registers for 16 rows of x
-    const MvRows rows = mv_rows(a, r0, r1, colc);
-    const int step = WAVES * U;
-    uint4 wa[U], wb[U];
-    mv_load_batch<WAVES, U>(rows, r0 + wave, wa);
-    const int last = (U - 1) * WAVES;  // offset of a batch's last row
-    for (int r = r0 + wave; r < r1; r += 2 * step) {
+    // Row blocks of kRowPhases rows: the wave takes blocks wave, wave +
+    // WAVES, ... of the range, two batches of U per iteration: both
+    // batches' loads are issued before the first batch's multiply-adds.
+    constexpr int U = kUnroll;
+    const MvRows rows = mv_rows(a, r0, r1, colc, rp);
+    const int step = WAVES * U * kRowPhases;   // rows per batch of the workgroup
+    const int last = (U - 1) * WAVES * kRowPhases + kRowPhases - 1;  // a batch's last row
+    const int first = r0 + wave * kRowPhases;
+    for (int r = first; r < r1; r += 2 * step) {
+      uint4 wa[U], wb[U];
+      mv_load_batch<WAVES, U>(rows, r, wa);
       mv_load_batch<WAVES, U>(rows, r + step, wb);
       if (r + last < r1)
-        mv_fma_batch<MB, WAVES, U, true>(a, r, r1, wa, acc);
+        mv_fma_batch<MB, WAVES, U, true>(a, r, r0, r1, rp, xl, xrows, wa, acc);
       else
-        mv_fma_batch<MB, WAVES, U, false>(a, r, r1, wa, acc);
-      if (r + step >= r1) break;
-      mv_load_batch<WAVES, U>(rows, r + 2 * step, wa);
+        mv_fma_batch<MB, WAVES, U, false>(a, r, r0, r1, rp, xl, xrows, wa, acc);
       if (r + step + last < r1)
-        mv_fma_batch<MB, WAVES, U, true>(a, r + step, r1, wb, acc);
-      else
-        mv_fma_batch<MB, WAVES, U, false>(a, r + step, r1, wb, acc);
+        mv_fma_batch<MB, WAVES, U, true>(a, r + step, r0, r1, rp, xl, xrows, wb, acc);
+      else if (r + step < r1)
+        mv_fma_batch<MB, WAVES, U, false>(a, r + step, r0, r1, rp, xl, xrows, wb, acc);
     }
+#pragma unroll
+    for (int m = 0; m < MB; m++)
+#pragma unroll
+      for (int j = 0; j < 8; j++) acc[m][j] = mv_phase_sum(acc[m][j]);
   }
 
   // ---- waves -> one partial per (row of x, column) --------------------
+  // Thread t < 128 sums 4 adjacent columns over the waves; a partial is one
+  // 16-byte device-scope store.
+  const uint32_t part_bytes = (uint32_t)((size_t)a.splits * a.M * a.d_out * sizeof(float));
 #pragma unroll
   for (int m = 0; m < MB; m++) {
     if (m >= a.M) break;
     __syncthreads();  // the previous row's sums have been read
-    if (wave < WAVES) {
-      float4* d = reinterpret_cast<float4*>(lds.red + wave * kCols + lane * 8);
+    if (wave < WAVES && rp == 0) {
+      float4* d = reinterpret_cast<float4*>(lds.red + wave * kCols + lc * 8);
       d[0] = make_float4(acc[m][0], acc[m][1], acc[m][2], acc[m][3]);
       d[1] = make_float4(acc[m][4], acc[m][5], acc[m][6], acc[m][7]);
     }
     __syncthreads();
-    for (int t = threadIdx.x; t < kCols; t += blockDim.x) {
-      const int c = ct * kCols + t;
-      if (c >= a.d_out) break;
-      float v = 0.f;
+    const int t = threadIdx.x;
+    const int c = ct * kCols + 4 * t;
+    if (t < kCols / 4 && c < a.d_out) {
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-      for (int w = 0; w < WAVES; w++) v += lds.red[w * kCols + t];
-      float* o = a.out + (size_t)m * a.d_out + c;
-      if (a.splits == 1)
-        *o = a.accumulate ? *o + v : v;
-      else
-        mv_store_dev(a.partials + ((size_t)ks * a.M + m) * a.d_out + c, v);
+      for (int w = 0; w < WAVES; w++) {
+        const float4 r = *reinterpret_cast<const float4*>(lds.red + w * kCols + 4 * t);
+        v.x += r.x;
+        v.y += r.y;
+        v.z += r.z;
+        v.w += r.w;
+      }
+      if (a.splits == 1) {
+        mv_write_out(a, m, c, v);
+      } else {
+        mv_store_dev16(a.partials, part_bytes,
+                       (uint32_t)((((size_t)ks * a.M + m) * a.d_out + c) * sizeof(float)), v);
+      }
     }
   }
   if (a.splits == 1) return;
@@ -259,24 +383,52 @@ __device__ __forceinline__ void mv_item(const MvArgs& a, int ct, int ks, MvLds<W
   }
   __syncthreads();
   if (!lds.last) return;
+  // Thread (4 columns col4, quarter sub) loads the partials of row ranges
+  // sub, sub+4, ... of every row of x in one round trip (splits * MB <=
+  // kMaxSplit, indices past the last range re-read it and are dropped),
+  // sums them in order, and the quarters of a column (adjacent lanes) add up
+  // through two lane exchanges in a fixed order.
+  constexpr int Q = kMaxSplit / 4 / MB;  // loads per row of x
   const int S = a.splits;
-  for (int m = 0; m < a.M; m++) {
-    for (int t = threadIdx.x; t < kCols; t += blockDim.x) {
-      const int c = ct * kCols + t;
-      if (c >= a.d_out) break;
-      const float* p = a.partials + (size_t)m * a.d_out + c;
-      const size_t stride = (size_t)a.M * a.d_out;
-      float v = 0.f;
-      for (int k0 = 0; k0 < S; k0 += 8) {
-        float pv[8];
+#pragma unroll 1
+  for (int t = threadIdx.x; t < kCols; t += blockDim.x) {
+    const int sub = t & 3;
+    const int c = ct * kCols + 4 * (t >> 2);
+    const int cc = c < a.d_out ? c : a.d_out - 4;
+    float4 pv[MB][Q];
 #pragma unroll
-        for (int u = 0; u < 8; u++) pv[u] = mv_load_dev(p + (size_t)min(k0 + u, S - 1) * stride);
+    for (int m = 0; m < MB; m++) {
 #pragma unroll
-        for (int u = 0; u < 8; u++)
-          if (k0 + u < S) v += pv[u];
+      for (int i = 0; i < Q; i++) {
+        if (m < a.M && i * 4 < S) {
+          const int k = min(sub + 4 * i, S - 1);
+          pv[m][i] = mv_load_dev16(
+              a.partials, part_bytes,
+              (uint32_t)((((size_t)k * a.M + m) * a.d_out + cc) * sizeof(float)));
+        }
       }
-      float* o = a.out + (size_t)m * a.d_out + c;
-      *o = a.accumulate ? *o + v : v;
+    }
+#pragma unroll
+    for (int m = 0; m < MB; m++) {
+      if (m >= a.M) break;
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int i = 0; i < Q; i++) {
+        if (sub + 4 * i < S) {
+          v.x += pv[m][i].x;
+          v.y += pv[m][i].y;
+          v.z += pv[m][i].z;
+          v.w += pv[m][i].w;
+        }
+      }
+#pragma unroll
+      for (int x = 1; x <= 2; x *= 2) {
+        v.x += __shfl_xor(v.x, x);
+        v.y += __shfl_xor(v.y, x);
+        v.z += __shfl_xor(v.z, x);
+        v.w += __shfl_xor(v.w, x);
+      }
+      if (sub == 0 && c < a.d_out) mv_write_out(a, m, c, v);
     }
   }
 }
@@ -290,10 +442,8 @@ __device__ __forceinline__ void mv_item_any(const MvArgs& a, int ct, int ks, MvL
     mv_item<2, WAVES>(a, ct, ks, lds);
   else if (a.M <= 4)
     mv_item<4, WAVES>(a, ct, ks, lds);
-  else if (a.M <= 8)
-    mv_item<8, WAVES>(a, ct, ks, lds);
   else
-    mv_item<16, WAVES>(a, ct, ks, lds);
+    mv_item<8, WAVES>(a, ct, ks, lds);
 }
 
 }  // namespace mv
@@ -402,13 +552,14 @@ __device__ inline int device_matvec_grid(const float* x, const uint16_t* W, floa
     return SDE_ERR_INVALID_ARGUMENT;
   if (workspace_bytes < mv_workspace_size(d_in, d_out, M)) return SDE_ERR_WORKSPACE;
   const bool w8 = blockDim.x >= 512;
-  const MvPlan p = mv_plan(d_in, d_out, gridDim.x * gridDim.y * gridDim.z, w8 ? 8 : 4);
+  const MvPlan p = mv_plan(d_in, d_out, gridDim.x * gridDim.y * gridDim.z, w8 ? 8 : 4, M);
   MvArgs a;
   a.x = x;
   a.W = W;
   a.out = out;
   a.counters = static_cast<uint32_t*>(workspace);
-  a.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + mv_counter_bytes(d_out));
+  a.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) +
+                                        mv_counter_bytes(d_out, M));
   a.d_in = d_in;
   a.d_out = d_out;
   a.M = M;
@@ -418,14 +569,17 @@ __device__ inline int device_matvec_grid(const float* x, const uint16_t* W, floa
   __shared__ MvLds<8> lds;
   const int blk = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
   const int nblk = gridDim.x * gridDim.y * gridDim.z;
-  const int items = p.col_tiles * p.splits;
+  const int per_pass = p.col_tiles * p.splits;
+  const int items = mv_passes(M) * per_pass;
   for (int it = blk; it < items; it += nblk) {
-    const int ct = it % p.col_tiles;
-    const int ks = it / p.col_tiles;
+    const int j = it / per_pass;
+    const int ct = (it - j * per_pass) % p.col_tiles;
+    const int ks = (it - j * per_pass) / p.col_tiles;
+    const MvArgs pa = mv_pass(a, j);
     if (w8)
-      mv_item_any<8>(a, ct, ks, lds);
+      mv_item_any<8>(pa, ct, ks, lds);
     else
-      mv_item_any<4>(a, ct, ks, *reinterpret_cast<MvLds<4>*>(&lds));
+      mv_item_any<4>(pa, ct, ks, *reinterpret_cast<MvLds<4>*>(&lds));
     __syncthreads();  // LDS reuse by the block's next item
   }
   return SDE_OK;

@@ -16,10 +16,11 @@ namespace mv {
 
 constexpr int kWaves = 8;
 
+// Workgroup (column tile x, row range y) of pass z (rows 8z.. of x).
 template <int MB>
 __global__ __launch_bounds__(64 * kWaves) void matvec_kernel(MvArgs a) {
   __shared__ MvLds<kWaves> lds;
-  mv_item<MB, kWaves>(a, blockIdx.x, blockIdx.y, lds);
+  mv_item<MB, kWaves>(mv_pass(a, blockIdx.z), blockIdx.x, blockIdx.y, lds);
 }
 
 }  // namespace mv
@@ -67,7 +68,7 @@ int sde_matvec(const float* d_x, const uint16_t* d_W, float* d_out, int d_in, in
   int st = SDE_OK;
   const int n_cus = current_cus(&st);
   if (st != SDE_OK) return st;
-  const MvPlan p = mv_plan(d_in, d_out_dim, n_cus, kWaves);
+  const MvPlan p = mv_plan(d_in, d_out_dim, n_cus, kWaves, M);
   MvArgs a;
   a.x = d_x;
   a.W = d_W;
@@ -85,21 +86,20 @@ int sde_matvec(const float* d_x, const uint16_t* d_W, float* d_out, int d_in, in
       return SDE_ERR_WORKSPACE;
     a.counters = static_cast<uint32_t*>(d_workspace);
     a.partials = reinterpret_cast<float*>(static_cast<char*>(d_workspace) +
-                                          mv_counter_bytes(d_out_dim));
+                                          mv_counter_bytes(d_out_dim, M));
   }
-  const dim3 grid(p.col_tiles, p.splits);
+  const dim3 grid(p.col_tiles, p.splits, mv_passes(M));
   const dim3 block(64 * kWaves);
   const hipStream_t s = (hipStream_t)stream;
-  if (M <= 1)
+  const int rows = mv_pass_rows(M);
+  if (rows <= 1)
     sde::mv::matvec_kernel<1><<<grid, block, 0, s>>>(a);
-  else if (M <= 2)
+  else if (rows <= 2)
     sde::mv::matvec_kernel<2><<<grid, block, 0, s>>>(a);
-  else if (M <= 4)
+  else if (rows <= 4)
     sde::mv::matvec_kernel<4><<<grid, block, 0, s>>>(a);
-  else if (M <= 8)
-    sde::mv::matvec_kernel<8><<<grid, block, 0, s>>>(a);
   else
-    sde::mv::matvec_kernel<16><<<grid, block, 0, s>>>(a);
+    sde::mv::matvec_kernel<8><<<grid, block, 0, s>>>(a);
   return sde::launch_status();
 }
 

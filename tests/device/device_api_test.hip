@@ -1,4 +1,5 @@
 // Test kernels for the device-side API of include/sde/attention_device.hpp
+// and include/sde/matvec_device.hpp
 // (test infrastructure, built beside libsde_paged by its build script): each
 // wraps one reference-named device function in a kernel the way an
 // in-kernel caller (a persistent decode loop) would use it, behind a plain
@@ -8,6 +9,7 @@
 
 #include "sde/attention_device.hpp"
 #include "sde/kv_cache.hpp"
+#include "sde/matvec_device.hpp"
 
 namespace {
 
@@ -78,6 +80,36 @@ __global__ __launch_bounds__(512) void persistent_loop_kernel(sde_kv_view kv, co
     sde::kv_cache_rollback(kv, s + 1 < n_steps ? pos[s + 1] : pos[s] + M);
   }
   if (threadIdx.x == 0) status[blockIdx.x] = st_all;
+}
+
+// coop_layer_forward's output projection (kernels.cu:2742-2747): blocks
+// take GEMV_COL_TILE-column stripes in turns and fold x @ W[:, stripe] into
+// out with the block-level device_matvec_partial_accum (or the
+// non-accumulating device_matvec_partial).
+__global__ void stripe_matvec_kernel(const float* x, const uint16_t* W, float* out, int d_in,
+                                     int d_out, int col_tile, int accumulate) {
+  for (int ct = blockIdx.x; ct * col_tile < d_out; ct += gridDim.x) {
+    const int cs = ct * col_tile;
+    const int cc = cs + col_tile <= d_out ? col_tile : d_out - cs;
+    if (accumulate)
+      sde::device_matvec_partial_accum(x, W, out, d_in, d_out, cs, cc);
+    else
+      sde::device_matvec_partial(x, W, out, d_in, d_out, cs, cc);
+  }
+}
+
+// device_matvec_batched (utils.h:248-280) by one block.
+__global__ void batched_matvec_kernel(const float* x, const uint16_t* W, float* out, int d_in,
+                                      int d_out, int B) {
+  sde::device_matvec_batched(x, W, out, d_in, d_out, B);
+}
+
+// Every block of an arbitrary grid calls the grid-cooperative projection.
+__global__ void grid_matvec_kernel(const float* x, const uint16_t* W, float* out, int d_in,
+                                   int d_out, int M, int accumulate, void* ws, size_t ws_bytes,
+                                   int* status) {
+  const int st = sde::device_matvec_grid(x, W, out, d_in, d_out, M, accumulate, ws, ws_bytes);
+  if (threadIdx.x == 0) status[blockIdx.x] = st;
 }
 
 int status_of(hipError_t e) { return e == hipSuccess ? 0 : 6; }
@@ -166,6 +198,32 @@ int sdet_cpp_pipeline(int n_layers, int kv_dim, int max_blocks, int block_size, 
 int sdet_rollback(const sde_kv_view* kv, int target, void* stream) {
   if (!kv) return 1;
   rollback_kernel<<<1, 64, 0, (hipStream_t)stream>>>(*kv, target);
+  return status_of(hipGetLastError());
+}
+
+int sdet_stripe_matvec(const float* x, const uint16_t* W, float* out, int d_in, int d_out,
+                       int col_tile, int accumulate, int blocks, int threads, void* stream) {
+  if (blocks < 1 || threads < 64 || threads % 64 != 0 || threads > 1024 || col_tile < 1 ||
+      col_tile % 8 != 0 || d_out % 8 != 0)
+    return 1;
+  stripe_matvec_kernel<<<blocks, threads, 0, (hipStream_t)stream>>>(x, W, out, d_in, d_out,
+                                                                    col_tile, accumulate);
+  return status_of(hipGetLastError());
+}
+
+int sdet_batched_matvec(const float* x, const uint16_t* W, float* out, int d_in, int d_out,
+                        int B, int threads, void* stream) {
+  if (threads < 64 || threads % 64 != 0 || threads > 1024 || d_out % 8 != 0 || B < 1) return 1;
+  batched_matvec_kernel<<<1, threads, 0, (hipStream_t)stream>>>(x, W, out, d_in, d_out, B);
+  return status_of(hipGetLastError());
+}
+
+int sdet_grid_matvec(const float* x, const uint16_t* W, float* out, int d_in, int d_out, int M,
+                     int accumulate, int blocks, int threads, void* ws, size_t ws_bytes,
+                     int* status, void* stream) {
+  if (blocks < 1 || threads < 64 || threads % 64 != 0 || threads > 1024) return 1;
+  grid_matvec_kernel<<<blocks, threads, 0, (hipStream_t)stream>>>(
+      x, W, out, d_in, d_out, M, accumulate, ws, ws_bytes, status);
   return status_of(hipGetLastError());
 }
 

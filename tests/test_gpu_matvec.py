@@ -10,6 +10,9 @@ one-hot inputs), bit-identically across repeated calls (the partial sums
 are added in a fixed order), and at the reference's shapes: Llama-3-8B Wo
 (4096 x 4096) and W_down (14336 -> 4096), Qwen2.5-7B (3584), TinyLlama
 (2048), the tiny model (256), a verify window of 9 rows."""
+import ctypes
+from pathlib import Path
+
 import numpy as np
 import pytest
 import torch
@@ -130,3 +133,126 @@ def test_matvec_errors(gpu):
     torch.cuda.synchronize()
     with pytest.raises(SDEError):
         matvec(big_x, big_W, workspace=ws)
+
+
+# ---- the device-side API (include/sde/matvec_device.hpp) -----------------------
+# Kernels in tests/device/device_api_test.hip call the reference-named
+# block-level functions the way coop_layer_forward does (GEMV_COL_TILE = 128
+# column stripes taken by blocks in turns, config.h:29, kernels.cu:2742-2747),
+# device_matvec_batched from one block, and the grid-cooperative projection
+# from every block of arbitrary grids.
+
+DEV_LIB = Path(__file__).resolve().parent / "device" / "libsde_device_test.so"
+
+
+@pytest.fixture(scope="module")
+def mvdev(gpu):
+    if not DEV_LIB.exists():
+        pytest.fail(f"{DEV_LIB} missing: run __graft_entry__.build()")
+    lib = ctypes.CDLL(str(DEV_LIB))
+    vp, i, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
+    lib.sdet_stripe_matvec.argtypes = [vp, vp, vp, i, i, i, i, i, i, vp]
+    lib.sdet_batched_matvec.argtypes = [vp, vp, vp, i, i, i, i, vp]
+    lib.sdet_grid_matvec.argtypes = [vp, vp, vp, i, i, i, i, i, i, vp, sz, vp, vp]
+    for f in (lib.sdet_stripe_matvec, lib.sdet_batched_matvec, lib.sdet_grid_matvec):
+        f.restype = i
+    return lib
+
+
+def _dev_tensors(gpu, x, Wb, out0):
+    return (torch.from_numpy(x).to(gpu), torch.from_numpy(Wb.view(np.float16)).to(gpu),
+            torch.from_numpy(out0.copy()).to(gpu))
+
+
+@pytest.mark.parametrize("d_in,d_out,tile,blocks,threads,acc", [
+    (4096, 4096, 128, 256, 256, 1),    # Llama-3-8B Wo, the reference's stripes
+    (3584, 3584, 128, 19, 512, 1),     # Qwen2.5-7B, fewer blocks than stripes
+    (14336, 4096, 128, 64, 1024, 1),   # W_down
+    (1000, 1032, 128, 5, 64, 0),       # ragged last stripe, one-wave blocks
+    (256, 256, 48, 3, 320, 0),         # stripes not a power of two, five-wave blocks
+])
+def test_block_matvec_stripes(gpu, mvdev, oracle, d_in, d_out, tile, blocks, threads, acc):
+    case_banner("block matvec", d_in, d_out, tile, blocks, threads, acc)
+    rng = np.random.default_rng(d_in + tile)
+    x, Wb = _case(rng, 1, d_in, d_out)
+    out0 = rng.standard_normal((1, d_out)).astype(np.float32)
+    xt, Wt, ot = _dev_tensors(gpu, x, Wb, out0)
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    assert mvdev.sdet_stripe_matvec(xt.data_ptr(), Wt.data_ptr(), ot.data_ptr(), d_in, d_out,
+                                    tile, acc, blocks, threads, s) == 0
+    torch.cuda.synchronize()
+    y, mag = oracle.matvec_f64(x, Wb, out0 if acc else None)
+    got = ot.cpu().numpy()
+    assert np.all(np.abs(got - y) <= MV_TOL * mag + 1e-30)
+
+
+@pytest.mark.parametrize("B,d_in,d_out,threads", [(5, 4096, 4096, 1024), (9, 3584, 3584, 256),
+                                                  (2, 64, 8, 64)])
+def test_block_matvec_batched(gpu, mvdev, oracle, B, d_in, d_out, threads):
+    case_banner("batched matvec", B, d_in, d_out, threads)
+    rng = np.random.default_rng(B * 7 + d_in)
+    x, Wb = _case(rng, B, d_in, d_out)
+    xt, Wt, ot = _dev_tensors(gpu, x, Wb, np.full((B, d_out), np.nan, np.float32))
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    assert mvdev.sdet_batched_matvec(xt.data_ptr(), Wt.data_ptr(), ot.data_ptr(), d_in, d_out, B,
+                                     threads, s) == 0
+    torch.cuda.synchronize()
+    y, mag = oracle.matvec_f64(x, Wb)
+    assert np.all(np.abs(ot.cpu().numpy() - y) <= MV_TOL * mag + 1e-30)
+
+
+def _grid_mv(mvdev, gpu, xt, Wt, ot, M, d_in, d_out, acc, blocks, threads, ws, ws_bytes=None):
+    status = torch.full((blocks,), -1, dtype=torch.int32, device=gpu)
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    assert mvdev.sdet_grid_matvec(xt.data_ptr(), Wt.data_ptr(), ot.data_ptr(), d_in, d_out, M,
+                                  acc, blocks, threads, ws.data_ptr(),
+                                  ws.numel() if ws_bytes is None else ws_bytes,
+                                  status.data_ptr(), s) == 0
+    torch.cuda.synchronize()
+    return status.cpu().numpy()
+
+
+@pytest.mark.parametrize("M,d_in,d_out,acc,blocks,threads", [
+    (1, 4096, 4096, 1, 256, 512),     # decode Wo on a one-block-per-CU persistent grid
+    (9, 3584, 3584, 0, 300, 256),     # Qwen verify window, 4-wave blocks, two row passes
+    (16, 640, 520, 1, 7, 1024),       # the largest row count, fewer blocks than items
+    (1, 7, 8, 0, 3, 320),             # fewer rows than one batch
+])
+def test_grid_matvec(gpu, mvdev, oracle, M, d_in, d_out, acc, blocks, threads):
+    case_banner("grid matvec", M, d_in, d_out, acc, blocks, threads)
+    rng = np.random.default_rng(M + d_in + blocks)
+    x, Wb = _case(rng, M, d_in, d_out)
+    out0 = rng.standard_normal((M, d_out)).astype(np.float32)
+    xt, Wt, _ = _dev_tensors(gpu, x, Wb, out0)
+    ws = matvec_workspace(d_in, d_out, M, gpu)
+    y, mag = oracle.matvec_f64(x, Wb, out0 if acc else None)
+    first = None
+    for call in range(2):   # the second call finds the counters the first left at zero
+        ot = torch.from_numpy(out0.copy()).to(gpu)
+        status = _grid_mv(mvdev, gpu, xt, Wt, ot, M, d_in, d_out, acc, blocks, threads, ws)
+        assert (status == 0).all()
+        got = ot.cpu().numpy()
+        assert np.all(np.abs(got - y) <= MV_TOL * mag + 1e-30)
+        if first is None:
+            first = got
+        else:
+            assert np.array_equal(got, first)
+    host = matvec(xt, Wt, out=torch.from_numpy(out0.copy()).to(gpu), accumulate=bool(acc))
+    torch.cuda.synchronize()
+    assert np.all(np.abs(host.cpu().numpy() - y) <= MV_TOL * mag + 1e-30)
+
+
+def test_grid_matvec_errors_write_nothing(gpu, mvdev):
+    case_banner("grid matvec errors")
+    rng = np.random.default_rng(1)
+    x, Wb = _case(rng, 1, 4096, 4096)
+    xt, Wt, _ = _dev_tensors(gpu, x, Wb, np.zeros((1, 4096), np.float32))
+    ws = matvec_workspace(4096, 4096, 1, gpu)
+    nan = torch.full((1, 4096), float("nan"), device=gpu)
+    ot = nan.clone()
+    st = _grid_mv(mvdev, gpu, xt, Wt, ot, 1, 4096, 4096, 0, 8, 512, ws, ws.numel() // 2)
+    assert (st == N.SDE_ERR_WORKSPACE).all() and torch.isnan(ot).all()
+    st = _grid_mv(mvdev, gpu, xt, Wt, ot, 1, 4096, 4096, 0, 8, 192, ws)
+    assert (st == N.SDE_ERR_UNSUPPORTED).all() and torch.isnan(ot).all()
+    st = _grid_mv(mvdev, gpu, xt, Wt, ot, 17, 4096, 4096, 0, 8, 512, ws)
+    assert (st == N.SDE_ERR_INVALID_ARGUMENT).all() and torch.isnan(ot).all()
