@@ -43,7 +43,9 @@ typedef enum sde_status {
   SDE_ERR_UNSUPPORTED = 4,      /* attention type / head_dim / block_size    */
   SDE_ERR_WORKSPACE = 5,        /* caller workspace smaller than required    */
   SDE_ERR_HIP = 6,              /* a HIP runtime call failed                 */
-  SDE_ERR_NO_DEVICE = 7         /* no usable gfx950 device                   */
+  SDE_ERR_NO_DEVICE = 7,        /* no usable gfx950 device                   */
+  SDE_ERR_IO = 8,               /* weight file cannot be opened / short read */
+  SDE_ERR_FORMAT = 9            /* weight file header or tensor count bad    */
 } sde_status;
 
 /* AttentionType values of cuda/include/config.h:51-56. */
@@ -314,6 +316,82 @@ size_t sde_matvec_workspace_size(int d_in, int d_out, int n_rows);
 int sde_matvec(const float* d_x, const uint16_t* d_W, float* d_out, int d_in,
                int d_out_dim, int n_rows, int accumulate, void* d_workspace,
                size_t workspace_bytes, sde_stream_t stream);
+
+/* ---- SDEC weight files (model_load_weights, model.cu:68-260) ------------ */
+
+/* ModelConfig (config.h:67-83) as read from an SDEC header, plus the file
+ * version.  v1/v2 files store expanded Wk/Wv and report n_kv_heads =
+ * n_heads; kv_dim = n_kv_heads * (d_model / n_heads). */
+typedef struct sde_model_config {
+  int32_t n_layers;
+  int32_t d_model;
+  int32_t n_heads;
+  int32_t n_kv_heads;
+  int32_t d_ff;
+  int32_t vocab_size;
+  float rope_theta;            /* 10000 before v2                         */
+  int32_t rope_scaling_type;   /* SDE_ROPE_*, 0 before v3                 */
+  float rope_scaling_factor;   /* 1 before v3                             */
+  int32_t attention_type;      /* SDE_ATTN_*, 0 before v4                 */
+  int32_t has_qkv_bias;        /* 0/1, v5                                 */
+  uint32_t version;            /* 1..5                                    */
+} sde_model_config;
+
+/* LayerWeights (model.h:32-47): device pointers to fp16 bits, row-major
+ * [in][out] as in the file; the biases are NULL without has_qkv_bias. */
+typedef struct sde_layer_weights {
+  const uint16_t* rms_attn_weight;  /* [d_model]           */
+  const uint16_t* Wq;               /* [d_model][d_model]  */
+  const uint16_t* Wk;               /* [d_model][kv_dim]   */
+  const uint16_t* Wv;               /* [d_model][kv_dim]   */
+  const uint16_t* Wo;               /* [d_model][d_model]  */
+  const uint16_t* rms_mlp_weight;   /* [d_model]           */
+  const uint16_t* W_gate;           /* [d_model][d_ff]     */
+  const uint16_t* W_up;             /* [d_model][d_ff]     */
+  const uint16_t* W_down;           /* [d_ff][d_model]     */
+  const uint16_t* Wq_bias;          /* [d_model] or NULL   */
+  const uint16_t* Wk_bias;          /* [kv_dim] or NULL    */
+  const uint16_t* Wv_bias;          /* [kv_dim] or NULL    */
+} sde_layer_weights;
+
+/* The global tensors of ModelWeights (model.h:49-55). */
+typedef struct sde_model_globals {
+  const uint16_t* token_embedding;   /* [vocab_size][d_model] */
+  const uint16_t* rms_final_weight;  /* [d_model]             */
+  const uint16_t* output_proj;       /* [d_model][vocab_size] */
+} sde_model_globals;
+
+typedef struct sde_model sde_model;   /* opaque: the weights on one device */
+
+/* Reads and validates an SDEC header (versions 1-5) the way
+ * model_load_weights does (model.cu:83-192): magic "SDEC", version, the
+ * version's fields, n_layers <= 40 (MAX_LAYERS, config.h:21), n_heads |
+ * d_model, n_kv_heads | n_heads (and both >= 1).  Host only.  SDE_ERR_IO
+ * for an unreadable file or a truncated header, SDE_ERR_FORMAT for a bad
+ * magic, version or shape. */
+int sde_model_read_header(const char* path, sde_model_config* cfg);
+
+/* Device bytes sde_model_load allocates for a model of this config (one
+ * arena, every tensor 256-byte aligned); 0 for an invalid config. */
+size_t sde_model_weights_bytes(const sde_model_config* cfg);
+
+/* model_load_weights (model.cu:83-260) onto the current device: the header
+ * as sde_model_read_header, then token_embedding, rms_final_weight,
+ * output_proj and per layer rms_attn, Wq, Wk, Wv, Wo, rms_mlp, W_gate,
+ * W_up, W_down (+ Wq_bias, Wk_bias, Wv_bias with has_qkv_bias), each a
+ * uint32 element count that must equal the shape's, then that many fp16
+ * values.  The file is streamed through pinned staging buffers, disk reads
+ * overlapping host-to-device copies.  On any error nothing stays allocated
+ * and *out is NULL (SDE_ERR_FORMAT for a count mismatch, SDE_ERR_IO for a
+ * short read).  cfg_out may be NULL. */
+int sde_model_load(const char* path, sde_model** out, sde_model_config* cfg_out);
+
+int sde_model_get_config(const sde_model* model, sde_model_config* cfg);
+int sde_model_get_layer(const sde_model* model, int layer, sde_layer_weights* out);
+int sde_model_get_globals(const sde_model* model, sde_model_globals* out);
+
+/* model_free (model.cu:54-65). */
+int sde_model_free(sde_model* model);
 
 #ifdef __cplusplus
 } /* extern "C" */

@@ -24,6 +24,8 @@ SDE_ERR_UNSUPPORTED = 4
 SDE_ERR_WORKSPACE = 5
 SDE_ERR_HIP = 6
 SDE_ERR_NO_DEVICE = 7
+SDE_ERR_IO = 8
+SDE_ERR_FORMAT = 9
 
 SDE_ATTN_SOFTMAX = 0
 SDE_ATTN_SLIDING_WINDOW = 1
@@ -68,6 +70,39 @@ class KVView(ctypes.Structure):
     ]
 
 
+class ModelConfig(ctypes.Structure):
+    """sde_model_config: ModelConfig (config.h:67-83) + the SDEC version."""
+    _fields_ = [
+        ("n_layers", ctypes.c_int32),
+        ("d_model", ctypes.c_int32),
+        ("n_heads", ctypes.c_int32),
+        ("n_kv_heads", ctypes.c_int32),
+        ("d_ff", ctypes.c_int32),
+        ("vocab_size", ctypes.c_int32),
+        ("rope_theta", ctypes.c_float),
+        ("rope_scaling_type", ctypes.c_int32),
+        ("rope_scaling_factor", ctypes.c_float),
+        ("attention_type", ctypes.c_int32),
+        ("has_qkv_bias", ctypes.c_int32),
+        ("version", ctypes.c_uint32),
+    ]
+
+
+LAYER_TENSORS = ("rms_attn_weight", "Wq", "Wk", "Wv", "Wo", "rms_mlp_weight", "W_gate", "W_up",
+                 "W_down", "Wq_bias", "Wk_bias", "Wv_bias")
+GLOBAL_TENSORS = ("token_embedding", "rms_final_weight", "output_proj")
+
+
+class LayerWeights(ctypes.Structure):
+    """sde_layer_weights: device pointers (model.h:32-47)."""
+    _fields_ = [(n, ctypes.c_void_p) for n in LAYER_TENSORS]
+
+
+class ModelGlobals(ctypes.Structure):
+    """sde_model_globals: device pointers (model.h:49-55)."""
+    _fields_ = [(n, ctypes.c_void_p) for n in GLOBAL_TENSORS]
+
+
 _c_int = ctypes.c_int
 _vp = ctypes.c_void_p
 _sz = ctypes.c_size_t
@@ -106,6 +141,13 @@ PROTOTYPES = {
     "sde_attention_dispatch": (_c_int, [_c_int, _vp, _c_int, _vp, _vp, _c_int, _c_int, _c_int,
                                         _c_int, _c_int, _vp, _sz, _vp]),
     "sde_matvec_workspace_size": (_sz, [_c_int, _c_int, _c_int]),
+    "sde_model_read_header": (_c_int, [ctypes.c_char_p, ctypes.POINTER(ModelConfig)]),
+    "sde_model_weights_bytes": (_sz, [ctypes.POINTER(ModelConfig)]),
+    "sde_model_load": (_c_int, [ctypes.c_char_p, ctypes.POINTER(_vp), ctypes.POINTER(ModelConfig)]),
+    "sde_model_get_config": (_c_int, [_vp, ctypes.POINTER(ModelConfig)]),
+    "sde_model_get_layer": (_c_int, [_vp, _c_int, ctypes.POINTER(LayerWeights)]),
+    "sde_model_get_globals": (_c_int, [_vp, ctypes.POINTER(ModelGlobals)]),
+    "sde_model_free": (_c_int, [_vp]),
     "sde_matvec": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _sz, _vp]),
 }
 

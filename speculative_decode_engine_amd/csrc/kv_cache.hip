@@ -222,6 +222,8 @@ const char* sde_status_string(int status) {
     case SDE_ERR_WORKSPACE: return "workspace too small";
     case SDE_ERR_HIP: return "HIP runtime error";
     case SDE_ERR_NO_DEVICE: return "no usable device";
+    case SDE_ERR_IO: return "weight file cannot be read";
+    case SDE_ERR_FORMAT: return "bad weight file header or tensor size";
     default: return "unknown status";
   }
 }

@@ -1,0 +1,112 @@
+"""SDEC loading onto the GPU (sde_model_load, model.cu:83-260): every
+tensor of files of versions 1, 3 and 5 arrives bit-exact at its device
+address, 256-byte aligned; count mismatches and truncated data are
+rejected with nothing left allocated; and a loaded layer's Wo feeds the
+output projection (sde_matvec) to the float64 product."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import case_banner
+from speculative_decode_engine_amd import SDEError, matvec
+from speculative_decode_engine_amd import _native as N
+from speculative_decode_engine_amd import sdec
+from test_sdec import cfg_for, random_tensors
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("version", [1, 3, 5])
+def test_load_is_bit_exact(gpu, tmp_path, version):
+    case_banner("sdec load", version)
+    c = cfg_for(version)
+    t = random_tensors(c, version)
+    p = tmp_path / "m.sdec"
+    sdec.write_sdec(p, c, t, version)
+    m = sdec.load_sdec(p)
+    try:
+        assert m.config["version"] == version and m.config["n_kv_heads"] == c["n_kv_heads"]
+        torch.cuda.synchronize()
+        for name, dev in m.globals().items():
+            assert dev.data_ptr() % 256 == 0
+            assert np.array_equal(dev.cpu().numpy().view(np.uint16), t[name].view(np.uint16)), name
+        for l in range(c["n_layers"]):
+            for name, dev in m.layer(l).items():
+                key = f"L{l}.{name}"
+                if key not in t:
+                    assert dev is None, key   # biases of a file without them
+                    continue
+                assert dev.data_ptr() % 256 == 0
+                assert np.array_equal(dev.cpu().numpy().view(np.uint16), t[key].view(np.uint16)), key
+    finally:
+        m.free()
+
+
+def test_larger_than_a_staging_buffer(gpu, tmp_path):
+    """Tensors bigger than one 32 MiB staging buffer and many small ones in
+    one file (the double-buffered stream path)."""
+    case_banner("sdec large")
+    c = dict(n_layers=2, d_model=2048, n_heads=16, n_kv_heads=4, d_ff=5632, vocab_size=9000,
+             rope_theta=10000.0, has_qkv_bias=1)
+    t = random_tensors(c, 9)
+    p = tmp_path / "big.sdec"
+    sdec.write_sdec(p, c, t, 5)
+    m = sdec.load_sdec(p)
+    try:
+        for name, dev in m.globals().items():
+            assert np.array_equal(dev.cpu().numpy().view(np.uint16), t[name].view(np.uint16)), name
+        for l in range(2):
+            for name, dev in m.layer(l).items():
+                assert np.array_equal(dev.cpu().numpy().view(np.uint16),
+                                      t[f"L{l}.{name}"].view(np.uint16)), name
+    finally:
+        m.free()
+
+
+def test_bad_counts_and_truncation_are_rejected(gpu, tmp_path):
+    case_banner("sdec errors")
+    c = cfg_for(5)
+    t = random_tensors(c, 2)
+    p = tmp_path / "m.sdec"
+    sdec.write_sdec(p, c, t, 5)
+    raw = p.read_bytes()
+    hdr = 4 + 4 * 12
+    bad = bytearray(raw)
+    bad[hdr:hdr + 4] = (40 * 64 + 1).to_bytes(4, "little")   # token_embedding count
+    (tmp_path / "count.sdec").write_bytes(bytes(bad))
+    (tmp_path / "short.sdec").write_bytes(raw[:-10])
+    lib = N.load()
+    for name, want in (("count.sdec", N.SDE_ERR_FORMAT), ("short.sdec", N.SDE_ERR_IO)):
+        h = ctypes.c_void_p(1234)
+        cfg = N.ModelConfig()
+        st = lib.sde_model_load(str(tmp_path / name).encode(), ctypes.byref(h), ctypes.byref(cfg))
+        assert st == want and not h.value, name
+        with pytest.raises(SDEError):
+            sdec.load_sdec(tmp_path / name)
+    m = sdec.load_sdec(p)   # a good file still loads afterwards
+    m.free()
+
+
+def test_loaded_wo_drives_the_projection(gpu, oracle, tmp_path):
+    case_banner("sdec + matvec")
+    c = dict(n_layers=1, d_model=512, n_heads=8, n_kv_heads=2, d_ff=1024, vocab_size=64,
+             has_qkv_bias=0)
+    t = random_tensors(c, 4)
+    for k in t:
+        t[k] = (t[k].astype(np.float32) * 0.05).astype(np.float16)
+    p = tmp_path / "wo.sdec"
+    sdec.write_sdec(p, c, t, 5)
+    m = sdec.load_sdec(p)
+    try:
+        Wo = m.layer(0)["Wo"]
+        x = np.random.default_rng(1).standard_normal((1, 512)).astype(np.float32)
+        hidden0 = np.random.default_rng(2).standard_normal((1, 512)).astype(np.float32)
+        hidden = torch.from_numpy(hidden0.copy()).cuda()
+        matvec(torch.from_numpy(x).cuda(), Wo, out=hidden, accumulate=True)
+        torch.cuda.synchronize()
+        y, mag = oracle.matvec_f64(x, t["L0.Wo"].view(np.uint16), hidden0)
+        assert np.all(np.abs(hidden.cpu().numpy() - y) <= 1e-5 * mag)
+    finally:
+        m.free()
