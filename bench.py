@@ -291,6 +291,48 @@ def bench_matvec(torch, steps, warmup):
     return out
 
 
+def bench_sdec_load(torch, layers=2):
+    """Seconds and GB/s of sde_model_load for a Llama-3-8B-shaped SDEC v5
+    file of `layers` layers (d 4096, 8 KV heads, d_ff 14336, vocab 32000:
+    ~0.83 GB per two layers + 0.52 GB of embeddings), written to a
+    temporary file first, so the read comes from the page cache: the time
+    is the staged host-to-device path, not the disk."""
+    import shutil
+    import tempfile
+    from speculative_decode_engine_amd import sdec
+    cfg = dict(n_layers=layers, d_model=4096, n_heads=32, n_kv_heads=8, d_ff=14336,
+               vocab_size=32000, rope_theta=500000.0, has_qkv_bias=0)
+    tmp = tempfile.mkdtemp(prefix="sde_sdec_")
+    try:
+        path = os.path.join(tmp, "llama_like.sdec")
+        shapes = sdec.tensor_shapes(cfg)
+        # Same bytes for every tensor (a repeated pattern): the loader's work
+        # does not depend on the values.
+        pattern = (np.arange(1 << 20, dtype=np.float32) % 97 * 1e-3).astype(np.float16)
+        with open(path, "wb") as f:
+            import struct
+            f.write(b"SDEC" + struct.pack("<IIIIIIIfifii", 5, layers, 4096, 32, 8, 14336, 32000,
+                                          500000.0, 0, 1.0, 0, 0))
+            for name, shape in shapes.items():
+                n = int(np.prod(shape))
+                f.write(struct.pack("<I", n))
+                for off in range(0, n, pattern.size):
+                    f.write(pattern[:min(pattern.size, n - off)].tobytes())
+        nbytes = os.path.getsize(path)
+        times = []
+        for _ in range(3):
+            torch.cuda.synchronize()
+            t = time.perf_counter()
+            m = sdec.load_sdec(path)
+            times.append(time.perf_counter() - t)
+            m.free()
+        best = min(times)
+        return dict(file_bytes=nbytes, seconds=round(best, 4), gbps=round(nbytes / best / 1e9, 2),
+                    layers=layers, source="page cache (file written just before)")
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+
+
 def cpu_baseline(W, w, seconds):
     """The CPU oracle's tile restatement of attention.h (OpenMP over
     (query, head) pairs) on one 32K-key layer-step of the same shape, run
@@ -356,7 +398,8 @@ def main():
     torch.cuda.set_device(0)
     steps, warmup = args.steps, args.warmup
     if args.only_matvec:
-        print(json.dumps({"matvec": bench_matvec(torch, steps, warmup)}), flush=True)
+        print(json.dumps({"matvec": bench_matvec(torch, steps, warmup),
+                          "sdec_load": bench_sdec_load(torch)}), flush=True)
         return
 
     w = W.CONFIGS[HEADLINE]
@@ -393,6 +436,8 @@ def main():
         log("[bench] accept", json.dumps(extra["accept_us"]))
         extra["matvec"] = bench_matvec(torch, steps, warmup)
         log("[bench] matvec", json.dumps(extra["matvec"]))
+        extra["sdec_load"] = bench_sdec_load(torch)
+        log("[bench] sdec load", json.dumps(extra["sdec_load"]))
         for k_, v_ in configs.items():
             log(f"[bench] {k_}: {v_['us_per_layer_step']} us/layer-step, {v_['gbps']} GB/s")
 
