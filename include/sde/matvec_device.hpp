@@ -553,6 +553,8 @@ __device__ inline int device_matvec_grid(const float* x, const uint16_t* W, floa
   if (workspace_bytes < mv_workspace_size(d_in, d_out, M)) return SDE_ERR_WORKSPACE;
   const bool w8 = blockDim.x >= 512;
   const MvPlan p = mv_plan(d_in, d_out, gridDim.x * gridDim.y * gridDim.z, w8 ? 8 : 4, M);
+  // A row range is addressed with 32-bit byte offsets.
+  if ((size_t)p.rows_per_split * d_out * 2 >= ((size_t)1 << 31)) return SDE_ERR_UNSUPPORTED;
   MvArgs a;
   a.x = x;
   a.W = W;

@@ -308,8 +308,8 @@ size_t sde_matvec_workspace_size(int d_in, int d_out, int n_rows);
  * verify window's Wo (utils.h:248-280, model.cu:717: n_rows = B <= 9,
  * accumulate = 0) and the multi-kernel path's Wo GEMM + residual add
  * (kernels.cu:1069-1075, here with fp32 activations).  1 <= n_rows <= 16;
- * d_out_dim a multiple of 8 and W 16-byte aligned (SDE_ERR_UNSUPPORTED
- * otherwise).  d_workspace holds sde_matvec_workspace_size(...) bytes
+ * d_out_dim a multiple of 8, W 16-byte aligned, and one row range of W
+ * (d_in split over the CUs) under 2 GiB (SDE_ERR_UNSUPPORTED otherwise).  d_workspace holds sde_matvec_workspace_size(...) bytes
  * (SDE_ERR_WORKSPACE when smaller); calls sharing a workspace must be
  * ordered on one stream.  Deterministic: the sum order does not depend on
  * scheduling. */

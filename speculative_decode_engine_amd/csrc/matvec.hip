@@ -69,6 +69,8 @@ int sde_matvec(const float* d_x, const uint16_t* d_W, float* d_out, int d_in, in
   const int n_cus = current_cus(&st);
   if (st != SDE_OK) return st;
   const MvPlan p = mv_plan(d_in, d_out_dim, n_cus, kWaves, M);
+  // A row range is addressed with 32-bit byte offsets.
+  if ((size_t)p.rows_per_split * d_out_dim * 2 >= ((size_t)1 << 31)) return SDE_ERR_UNSUPPORTED;
   MvArgs a;
   a.x = d_x;
   a.W = d_W;
