@@ -59,6 +59,8 @@ def parse_args():
     p.add_argument("--only-headline", action="store_true")
     p.add_argument("--only-matvec", action="store_true",
                    help="time only the output projection (sde_matvec) and print its JSON")
+    p.add_argument("--matvec-shape", default=None,
+                   help="with --only-matvec: one shape name (e.g. llama3_8b_wo) and no load timing")
     p.add_argument("--calibrate-copy", type=int, default=0, metavar="MiB",
                    help="after the benchmark, copy a MiB-sized buffer 5 times")
     return p.parse_args()
@@ -239,7 +241,7 @@ def bench_accept(torch, steps=200, k=4, vocab=128256):
     return out
 
 
-def bench_matvec(torch, steps, warmup):
+def bench_matvec(torch, steps, warmup, only=None):
     """The output projection after attention (sde_matvec): us per call and
     algorithmic GB/s (fp16 weights once + fp32 x, out read when accumulating,
     out written) at the reference models' Wo / W_down shapes, graph-replayed
@@ -254,6 +256,8 @@ def bench_matvec(torch, steps, warmup):
     g = torch.Generator(device="cuda")
     g.manual_seed(21)
     for name, M, d_in, d_out, acc in shapes:
+        if only and name != only:
+            continue
         wbytes = d_in * d_out * 2
         n_mats = max(4, -(-(512 << 20) // wbytes))
         Ws = [(torch.randn(d_in, d_out, device="cuda", generator=g) * 0.02).half()
@@ -270,6 +274,8 @@ def bench_matvec(torch, steps, warmup):
                          frac_of_hbm_peak=round(gbps / HBM_PEAK_GBPS, 4))
         del Ws
         torch.cuda.empty_cache()
+    if only:
+        return out
     try:
         from oracle import paged_kv as O
         O.lib()
@@ -398,8 +404,19 @@ def main():
     torch.cuda.set_device(0)
     steps, warmup = args.steps, args.warmup
     if args.only_matvec:
-        print(json.dumps({"matvec": bench_matvec(torch, steps, warmup),
-                          "sdec_load": bench_sdec_load(torch)}), flush=True)
+        if args.matvec_shape:
+            print(json.dumps({"matvec": bench_matvec(torch, steps, warmup, args.matvec_shape)}),
+                  flush=True)
+        else:
+            print(json.dumps({"matvec": bench_matvec(torch, steps, warmup),
+                              "sdec_load": bench_sdec_load(torch)}), flush=True)
+        if args.calibrate_copy:
+            n = args.calibrate_copy * 2 ** 20 // 4
+            src = torch.ones(n, device="cuda")
+            dst = torch.empty_like(src)
+            for _ in range(5):
+                dst.copy_(src)
+            torch.cuda.synchronize()
         return
 
     w = W.CONFIGS[HEADLINE]

@@ -1,5 +1,5 @@
 """SDEC loading onto the GPU (sde_model_load, model.cu:83-260): every
-tensor of files of versions 1, 3 and 5 arrives bit-exact at its device
+tensor of files of every version (1-5) arrives bit-exact at its device
 address, 256-byte aligned; count mismatches and truncated data are
 rejected with nothing left allocated; and a loaded layer's Wo feeds the
 output projection (sde_matvec) to the float64 product."""
@@ -18,7 +18,7 @@ from test_sdec import cfg_for, random_tensors
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("version", [1, 3, 5])
+@pytest.mark.parametrize("version", [1, 2, 3, 4, 5])
 def test_load_is_bit_exact(gpu, tmp_path, version):
     case_banner("sdec load", version)
     c = cfg_for(version)
