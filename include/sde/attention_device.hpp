@@ -528,7 +528,7 @@ __device__ __forceinline__ void wave_attend(const TileSource& src, int kvh, int 
                                             float qscale, const float2 (&q_raw)[RPW][4],
                                             float& m_run, float& l_run, float (&acc)[RPW][8],
                                             const float2* rope_cs = nullptr, int r0 = 0,
-                                            int G = 1, int R = 1) {
+                                            int G = 1, int R = 1, bool balance = false) {
   using Sh = StreamShape<DPH, RPW>;
   constexpr int CH = Sh::CH, SL = Sh::SL, NLD = Sh::NLD;
   const int lane = threadIdx.x & 63;
@@ -597,6 +597,13 @@ __device__ __forceinline__ void wave_attend(const TileSource& src, int kvh, int 
       }
       // A slot past the wave's last tile: every token masked (no-op).
       const int ts_mask = t <= last ? t * kTile : INT_MAX / 2;
+      // Balanced issue: the first half of every chunk's tiles runs at raised
+      // wave priority, so a wave past its midpoint, or in its epilogue,
+      // yields VALU issue to the other wave of its SIMD that is behind.
+      if (balance) {
+        if (2 * i < CHUNK) __builtin_amdgcn_s_setprio(1);
+        else __builtin_amdgcn_s_setprio(0);
+      }
       stream_qk<DPH, RPW, 0>(ts_mask, sl, c, min_lim, my_lim, my_jp, qr, kbuf[b], m_run, l_run,
                              al, pk);
       if (i + 1 < CHUNK) {
@@ -608,6 +615,7 @@ __device__ __forceinline__ void wave_attend(const TileSource& src, int kvh, int 
       stream_pv<DPH, RPW, 0>(sl, al, pk, vbuf[b], acc);
     }
   }
+  if (balance) __builtin_amdgcn_s_setprio(0);
 }
 
 // Totals over the four 16-lane rows of four values at once: afterwards lanes
@@ -964,9 +972,13 @@ __device__ __forceinline__ void stream_item(const AttnArgs& a, int part, int kvh
     for (int r = 0; r < RPW; r++)
 #pragma unroll
       for (int e = 0; e < 8; e++) acc[r][e] = 0.f;
+    // Several row groups per KV head make the step VALU-bound per SIMD
+    // (each K/V byte serves several workgroups from L2): balance the waves
+    // of a SIMD (4K 5-query window 14.9 -> 14.5 us; a long one-group decode
+    // is HBM-bound and measured 0.3 us slower with it).
     wave_attend<DPH, RPW, CHUNK, ROPE>(a.src, kvh, tb + wave, te, WAVES, nrows, min_lim, my_lim,
                                        a.qscale, q_raw, m_run, l_run, acc, rope_cs, r0, a.G,
-                                       a.R);
+                                       a.R, a.row_groups > 1);
 
     // ---- merge the slot states of this wave; record per row -------------
     float m_row, l_row, o[2 * RPW];
