@@ -42,7 +42,7 @@ typedef enum sde_status {
   SDE_ERR_RANGE = 3,            /* table entry outside pool, bad rollback    */
   SDE_ERR_UNSUPPORTED = 4,      /* attention type / head_dim / block_size    */
   SDE_ERR_WORKSPACE = 5,        /* caller workspace smaller than required    */
-  SDE_ERR_HIP = 6,              /* a HIP runtime call failed                 */
+  SDE_ERR_HIP = 6,              /* a HIP call or a host allocation failed    */
   SDE_ERR_NO_DEVICE = 7,        /* no usable gfx950 device                   */
   SDE_ERR_IO = 8,               /* weight file cannot be opened / short read */
   SDE_ERR_FORMAT = 9            /* weight file header or tensor count bad    */

@@ -12,6 +12,7 @@
 
 #include <cstdio>
 #include <cstring>
+#include <new>
 #include <vector>
 
 #include "sde_paged_kv.h"
@@ -202,9 +203,13 @@ int sde_model_read_header(const char* path, sde_model_config* cfg) {
 
 size_t sde_model_weights_bytes(const sde_model_config* cfg) {
   if (!valid_config(cfg)) return 0;
-  sde_model m;
-  m.cfg = *cfg;
-  return arena_bytes_of(tensor_plan(&m));
+  try {  // no C++ exception crosses the C-ABI
+    sde_model m;
+    m.cfg = *cfg;
+    return arena_bytes_of(tensor_plan(&m));
+  } catch (...) {
+    return 0;
+  }
 }
 
 int sde_model_load(const char* path, sde_model** out, sde_model_config* cfg_out) {
@@ -212,7 +217,8 @@ int sde_model_load(const char* path, sde_model** out, sde_model_config* cfg_out)
   *out = nullptr;
   File file(path);
   if (!file.f) return SDE_ERR_IO;
-  sde_model* m = new sde_model();
+  sde_model* m = new (std::nothrow) sde_model();
+  if (!m) return SDE_ERR_HIP;
   int st = parse_header(file, &m->cfg);
   if (st != SDE_OK) {
     delete m;
@@ -222,7 +228,13 @@ int sde_model_load(const char* path, sde_model** out, sde_model_config* cfg_out)
     delete m;
     return SDE_ERR_NO_DEVICE;
   }
-  const std::vector<TensorSlot> plan = tensor_plan(m);
+  std::vector<TensorSlot> plan;
+  try {  // host allocation failure: no C++ exception crosses the C-ABI
+    plan = tensor_plan(m);
+  } catch (...) {
+    delete m;
+    return SDE_ERR_HIP;
+  }
   m->arena_bytes = arena_bytes_of(plan);
   if (m->arena_bytes > 0 && hipMalloc(&m->arena, m->arena_bytes) != hipSuccess) {
     delete m;
