@@ -41,7 +41,7 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E spec sheet
 HEADLINE = "llama3_8b_32k"
-KERNEL = "attn_stream_kernel"  # the headline (1-query, GQA 4) path
+KERNEL = "attn_mfma_kernel"  # the headline (1-query, GQA 4) path
 
 
 def log(*a):

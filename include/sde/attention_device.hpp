@@ -760,84 +760,72 @@ __device__ __forceinline__ float4 load_dev16(const float* base, uint32_t bytes,
 // is issued unconditionally (indices past P re-read partition P-1, then
 // weigh 0), so they all travel in one round trip: a load under `if (p < P)`
 // gets a wait of its own at the join.
-template <int DPH, int PMAX>
-__device__ __forceinline__ void combine_quarter(const float* ml, const float* acc_all,
-                                                uint32_t acc_bytes, uint32_t acc_off, int P,
-                                                int sub, float& mx, float& l, float4& o) {
-  float2 e[PMAX];
-  float4 v[PMAX];
-#pragma unroll
-  for (int i = 0; i < PMAX; i++) {
-    const int p = min(sub + i * 4, P - 1);
-    v[i] = load_dev16(acc_all, acc_bytes, acc_off + (uint32_t)p * (DPH * 4));
-  }
-  // (max, sum) of partition p is loaded once per wave, by lane p (every
-  // lane of a wave serves one row), and read across lanes.
-  const int lane = threadIdx.x & 63;
-  const float2 mine = load_dev2(ml + (size_t)min(lane, P - 1) * 2);
-#pragma unroll
-  for (int i = 0; i < PMAX; i++) {
-    e[i].x = __shfl(mine.x, sub + i * 4);
-    e[i].y = __shfl(mine.y, sub + i * 4);
-  }
-#pragma unroll
-  for (int i = 0; i < PMAX; i++) {
-    if (sub + i * 4 >= P) {
-      e[i] = make_float2(-INFINITY, 0.f);
-      v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-  }
-  mx = -INFINITY;
-#pragma unroll
-  for (int i = 0; i < PMAX; i++) mx = fmaxf(mx, e[i].x);
-  mx = fmaxf(mx, dpp_f(mx, 0));
-  mx = fmaxf(mx, dpp_f(mx, 1));
-  l = 0.f;
-  o = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-  for (int i = 0; i < PMAX; i++) {
-    const float w = e[i].x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(e[i].x - mx);
-    l += e[i].y * w;
-    o.x += w * v[i].x;
-    o.y += w * v[i].y;
-    o.z += w * v[i].z;
-    o.w += w * v[i].w;
-  }
-}
-
-// Partition combine, run by the last workgroup of a (KV head, row group) to
-// finish: thread (row r, float4 column c4, quarter sub) loads (max, sum,
-// acc[c4]) of partitions sub, sub+4, ... -- every partial in one round trip,
-// no LDS -- weights them by exp2(m_p - max) and the four quarters of a (row,
-// column) (adjacent lanes) reduce through DPP in a fixed order, so the
-// result does not depend on arrival order.  Workgroups of fewer than
-// RPW*DPH threads take the (row, column, quarter) triples in turns.
-template <int DPH, int RPW, int WAVES>
-__device__ __forceinline__ void stream_combine(const AttnArgs& a, int kvh, int r0, int nrows) {
+// One pass of the partition combine over NIT row slices: thread
+// (row, float4 column c4, quarter sub) of slice it loads (max, sum, acc[c4])
+// of partitions sub, sub+4, ... for all of its slices first -- every
+// partial of the pass in one round trip, no LDS -- then weights them by
+// exp2(m_p - max), and the four quarters of a (row, column) (adjacent
+// lanes) reduce through DPP in a fixed order, so the result does not
+// depend on arrival order.  (max, sum) of partition p is loaded once per
+// wave, by lane p (a wave's lanes serve one row), and read across lanes.
+template <int DPH, int PMAX, int NIT, int WAVES>
+__device__ __forceinline__ void combine_pass(const AttnArgs& a, int kvh, int r0, int nrows,
+                                             int it0) {
   constexpr int C4 = DPH / 4;
   constexpr int SUB = 4;
-  static_assert(kStreamMaxParts == 16 * SUB && kStreamMaxParts <= 64, "combine_quarter buckets");
-  static_assert((SUB * C4) % 64 == 0, "each wave's lanes serve one row");
+  constexpr int NT = 64 * WAVES;
   const int P = a.n_parts;
-  if ((int)threadIdx.x >= 64 * WAVES) return;  // waves past WAVES idle
-  for (int tid = threadIdx.x; tid < RPW * C4 * SUB; tid += 64 * WAVES) {
-    const int sub = tid & (SUB - 1);
-    const int col4 = (tid / SUB) % C4;
-    const int r = tid / (SUB * C4);  // uniform per wave
+  const int lane = threadIdx.x & 63;
+  const int sub = threadIdx.x & (SUB - 1);
+  const int col4 = (threadIdx.x / SUB) % C4;
+  const size_t acc_floats = (size_t)a.nkv * a.R * P * DPH;
+  const uint32_t acc_bytes = (uint32_t)(acc_floats * 4);
+  float4 v[NIT][PMAX];
+  float2 mine[NIT];
+#pragma unroll
+  for (int it = 0; it < NIT; it++) {
+    const int r = (threadIdx.x + (it0 + it) * NT) / (SUB * C4);  // uniform per wave
+    if (r < nrows) {
+      const size_t row = (size_t)kvh * a.R + r0 + r;
+      const uint32_t acc_off = (uint32_t)((row * P * DPH + 4 * col4) * 4);
+#pragma unroll
+      for (int i = 0; i < PMAX; i++) {
+        const int p = min(sub + i * SUB, P - 1);
+        v[it][i] = load_dev16(a.partials, acc_bytes, acc_off + (uint32_t)p * (DPH * 4));
+      }
+      mine[it] = load_dev2(a.partials + acc_floats + row * P * 2 + (size_t)min(lane, P - 1) * 2);
+    }
+  }
+#pragma unroll
+  for (int it = 0; it < NIT; it++) {
+    const int r = (threadIdx.x + (it0 + it) * NT) / (SUB * C4);
     if (r >= nrows) break;
-    const size_t row = (size_t)kvh * a.R + r0 + r;
-    const size_t acc_floats = (size_t)a.nkv * a.R * P * DPH;
-    const float* ml = a.partials + acc_floats + row * P * 2;
-    const uint32_t acc_bytes = (uint32_t)(acc_floats * 4);
-    const uint32_t acc_off = (uint32_t)((row * P * DPH + 4 * col4) * 4);
-    float mx, l;
-    float4 o;
-    if (P <= 4 * SUB)
-      combine_quarter<DPH, 4>(ml, a.partials, acc_bytes, acc_off, P, sub, mx, l, o);
-    else if (P <= 8 * SUB)
-      combine_quarter<DPH, 8>(ml, a.partials, acc_bytes, acc_off, P, sub, mx, l, o);
-    else
-      combine_quarter<DPH, 16>(ml, a.partials, acc_bytes, acc_off, P, sub, mx, l, o);
+    float2 e[PMAX];
+#pragma unroll
+    for (int i = 0; i < PMAX; i++) {
+      e[i].x = __shfl(mine[it].x, sub + i * SUB);
+      e[i].y = __shfl(mine[it].y, sub + i * SUB);
+      if (sub + i * SUB >= P) {
+        e[i] = make_float2(-INFINITY, 0.f);
+        v[it][i] = make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < PMAX; i++) mx = fmaxf(mx, e[i].x);
+    mx = fmaxf(mx, dpp_f(mx, 0));
+    mx = fmaxf(mx, dpp_f(mx, 1));
+    float l = 0.f;
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int i = 0; i < PMAX; i++) {
+      const float w = e[i].x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(e[i].x - mx);
+      l += e[i].y * w;
+      o.x += w * v[it][i].x;
+      o.y += w * v[it][i].y;
+      o.z += w * v[it][i].z;
+      o.w += w * v[it][i].w;
+    }
 #pragma unroll
     for (int k = 0; k < 2; k++) {
       l += dpp_f(l, k);
@@ -857,6 +845,33 @@ __device__ __forceinline__ void stream_combine(const AttnArgs& a, int kvh, int r
       dst[1] = make_float2(o.z * inv, o.w * inv);
     }
   }
+}
+
+// Passes of up to 32 in-flight partial loads per thread.
+template <int DPH, int RPW, int PMAX, int WAVES>
+__device__ __forceinline__ void combine_rows(const AttnArgs& a, int kvh, int r0, int nrows) {
+  constexpr int SLICES = (RPW * DPH + 64 * WAVES - 1) / (64 * WAVES);  // RPW*C4*SUB / threads
+  constexpr int CAP = 32 / PMAX;
+  constexpr int NIT = SLICES < CAP ? SLICES : CAP;
+#pragma unroll
+  for (int it0 = 0; it0 < SLICES; it0 += NIT)
+    combine_pass<DPH, PMAX, NIT, WAVES>(a, kvh, r0, nrows, it0);
+}
+
+// Partition combine, run by the last workgroup of a (KV head, row group) to
+// finish (the rows r0 .. r0+nrows-1 of KV head kvh).
+template <int DPH, int RPW, int WAVES>
+__device__ __forceinline__ void stream_combine(const AttnArgs& a, int kvh, int r0, int nrows) {
+  static_assert(kStreamMaxParts == 64, "combine buckets");
+  static_assert((4 * (DPH / 4)) % 64 == 0, "each wave's lanes serve one row");
+  if ((int)threadIdx.x >= 64 * WAVES) return;  // waves past WAVES idle
+  const int P = a.n_parts;
+  if (P <= 16)
+    combine_rows<DPH, RPW, 4, WAVES>(a, kvh, r0, nrows);
+  else if (P <= 32)
+    combine_rows<DPH, RPW, 8, WAVES>(a, kvh, r0, nrows);
+  else
+    combine_rows<DPH, RPW, 16, WAVES>(a, kvh, r0, nrows);
 }
 
 // The window's rows (positions pos_base .. pos_base+M-1) of KV head kvh:
@@ -897,6 +912,205 @@ __device__ __forceinline__ void rope_append_slice(const AttnArgs& a, const RopeA
   __syncthreads();
 }
 
+// ---- MFMA tile path (v_mfma_f32_16x16x32_f16, up to 16 rows per wave) ----
+//
+// K and V stream in with the same loads as the VALU path (a token's slice
+// read by CH lanes, 16 bytes each) and are staged per wave in LDS, row-major
+// by token with the 16-byte units of row t stored at unit u ^ (t % UNITS),
+// which keeps both the stores and the operand reads below free of bank
+// conflicts.  Per tile of 32 tokens:
+//  * logits S^T[token][row] = K . Q^T: A = K read from LDS in the operand
+//    layout (lane l: token l%16 of a 16-token block, features
+//    32ks + 8(l/16) .. +7), B = Q^T (row l%16, the same features).  The C
+//    layout leaves lane l the logits of row l%16 for tokens 4(l/16) + i and
+//    16 + 4(l/16) + i (i < 4), so the online softmax is lane-local per row:
+//    one cross-group max per tile (two lane swaps), sums reduced once.
+//  * O^T[feature][row] += V^T . P^T: B = P^T straight from the logits'
+//    registers (k order: tokens 4(l/16)+i, then 16+4(l/16)+i), A = V^T read
+//    with ds_read_b64_tr_b16: in each 16-lane group lane 4b+t receives
+//    element t of the 8-byte pieces addressed by lanes b, b+4, b+8, b+12, so
+//    lane m' addressing token base + m'/4, features 16db + 4(m'%4) gives
+//    lane m feature 16db + m of tokens base..base+3 (the A layout).
+// The output C layout holds features 16db + 4(l/16) + i of row l%16 in lane
+// l, so the rescale by the row's exp2(m_old - m_new) is lane-local too.
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+typedef short s4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s4_t lds_s4_t;
+
+template <int DPH>
+struct MfmaShape {
+  static constexpr int KS = DPH / 32;         // k-steps of the logits product
+  static constexpr int DB = DPH / 16;         // 16-feature blocks of the output
+  static constexpr int UNITS = DPH / 8;       // 16-byte units per token row
+  static constexpr int ROWB = 2 * DPH;        // bytes per staged row
+  static constexpr int TILEB = kTile * ROWB;  // bytes of one staged K or V tile
+  static constexpr int WAVEB = 2 * TILEB;     // LDS bytes per wave (K and V)
+};
+
+__device__ __forceinline__ float groups_max(float x) {
+  const int v = __builtin_bit_cast(int, x);
+  const auto h = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  x = fmaxf(__builtin_bit_cast(float, (int)h[0]), __builtin_bit_cast(float, (int)h[1]));
+  const int w = __builtin_bit_cast(int, x);
+  const auto r = __builtin_amdgcn_permlane16_swap(w, w, false, false);
+  return fmaxf(__builtin_bit_cast(float, (int)r[0]), __builtin_bit_cast(float, (int)r[1]));
+}
+
+__device__ __forceinline__ float groups_sum(float x) {
+  x = half_pair_total(x, x);
+  const float2 p = row_pair(x);
+  return p.x + p.y;
+}
+
+// Byte offset of 16-byte unit u of token row t in a staged tile.
+template <int DPH>
+__device__ __forceinline__ int staged(int t, int u) {
+  using Sh = MfmaShape<DPH>;
+  return t * Sh::ROWB + 16 * (u ^ (t & (Sh::UNITS - 1)));
+}
+
+// Stores a tile held in the load layout (load j: token j*SL + sl, unit c).
+template <int DPH>
+__device__ __forceinline__ void stage_tile(char* st, int sl, int c,
+                                           const uint4 (&x)[kTile / (512 / DPH)]) {
+  constexpr int SL = 512 / DPH;
+#pragma unroll
+  for (int j = 0; j < kTile / SL; j++)
+    *reinterpret_cast<uint4*>(st + staged<DPH>(j * SL + sl, c)) = x[j];
+}
+
+// Logits of a tile, masking (token position > lim), the online softmax
+// update and the rescale of o; returns P^T as the output product's B.
+// kst: this wave's staged K tile.
+template <int DPH>
+__device__ __forceinline__ h8_t mfma_logits(int ts, int q, int l16, int lim,
+                                            const h8_t (&qb)[MfmaShape<DPH>::KS],
+                                            const char* kst, float& m_run, float& l_run,
+                                            f4_t (&o)[MfmaShape<DPH>::DB]) {
+  using Sh = MfmaShape<DPH>;
+  f4_t s[2];
+#pragma unroll
+  for (int tb = 0; tb < 2; tb++) {
+    s[tb] = f4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < Sh::KS; ks++) {
+      const uint4 kx =
+          *reinterpret_cast<const uint4*>(kst + staged<DPH>(16 * tb + l16, 4 * ks + q));
+      s[tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, kx), qb[ks], s[tb],
+                                                     0, 0, 0);
+    }
+  }
+  float mx = -INFINITY;
+#pragma unroll
+  for (int tb = 0; tb < 2; tb++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const float x = ts + 16 * tb + 4 * q + i <= lim ? s[tb][i] : -INFINITY;
+      s[tb][i] = x;
+      mx = fmaxf(mx, x);
+    }
+  const float m_new = fmaxf(m_run, groups_max(mx));
+  const float m_use = m_new == -INFINITY ? 0.f : m_new;
+  const float al = __builtin_amdgcn_exp2f(m_run - m_use);
+  m_run = m_new;
+  float p[8];
+  float ps = 0.f;
+#pragma unroll
+  for (int tb = 0; tb < 2; tb++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      p[4 * tb + i] = __builtin_amdgcn_exp2f(s[tb][i] - m_use);
+      ps += p[4 * tb + i];
+    }
+  l_run = l_run * al + ps;
+#pragma unroll
+  for (int db = 0; db < Sh::DB; db++) o[db] *= al;
+  return h8_t{(_Float16)p[0], (_Float16)p[1], (_Float16)p[2], (_Float16)p[3],
+              (_Float16)p[4], (_Float16)p[5], (_Float16)p[6], (_Float16)p[7]};
+}
+
+// o += V^T . P^T for a tile; vst: this wave's staged V tile.
+template <int DPH>
+__device__ __forceinline__ void mfma_pv(int q, int l16, const h8_t pb, const char* vst,
+                                        f4_t (&o)[MfmaShape<DPH>::DB]) {
+  using Sh = MfmaShape<DPH>;
+  const int t0 = 4 * q + (l16 >> 2);   // token of this lane's piece (first half)
+  const int sub = 8 * (l16 & 1);       // byte within the 16-byte unit
+  const int u0 = (l16 & 3) >> 1;       // unit within the 32 bytes of a feature block
+#pragma unroll
+  for (int db = 0; db < Sh::DB; db++) {
+    const s4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_s4_t*)(vst + staged<DPH>(t0, 2 * db + u0) + sub));
+    const s4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_s4_t*)(vst + staged<DPH>(t0 + 16, 2 * db + u0) + sub));
+    const s4_t both[2] = {lo, hi};
+    o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, both), pb, o[db], 0,
+                                                   0, 0);
+  }
+}
+
+// A wave's tiles first, first+stride, ... < te of KV head kvh on the MFMA
+// path, with wave_attend's loads and pipeline (a tile ahead).  lim: last
+// visible position of this lane's row (-1: a padding row).  st: this wave's
+// LDS (K tile, then V tile).
+template <int DPH, int CHUNK>
+__device__ __forceinline__ void mfma_attend(const TileSource& src, int kvh, int first, int te,
+                                            int stride, int lim,
+                                            const h8_t (&qb)[MfmaShape<DPH>::KS], char* st,
+                                            float& m_run, float& l_run,
+                                            f4_t (&o)[MfmaShape<DPH>::DB], bool balance) {
+  constexpr int CH = DPH / 8, SL = 512 / DPH, NLD = kTile / SL;
+  const int lane = threadIdx.x & 63;
+  const int l16 = lane & 15, q = lane >> 4;
+  const int sl = lane / CH, c = lane % CH;
+  const const_table_t table = const_table(src);
+  const char* head_base = reinterpret_cast<const char*>(src.pool) + (size_t)kvh * DPH * 2u;
+  const uint32_t lane_off = (uint32_t)sl * 2u * (uint32_t)src.kv_dim + 16u * c;
+  const uint32_t chunk_off = 16u * c;
+  char* kst = st;
+  char* vst = st + MfmaShape<DPH>::TILEB;
+  if (first >= te) return;
+  const int last = first + ((te - 1 - first) / stride) * stride;
+  for (int c0 = first; c0 < te; c0 += CHUNK * stride) {
+    uint4 kbuf[2][NLD], vbuf[2][NLD];
+    int blk[2][NLD], slot[2][NLD];
+    tile_groups<NLD, SL>(src, table, min(c0, last) * kTile, blk[0], slot[0]);
+    stream_load<DPH>(src, head_base, min(c0, last) * kTile, sl, lane_off, chunk_off, false,
+                     blk[0], slot[0], kbuf[0]);
+    stream_load<DPH>(src, head_base, min(c0, last) * kTile, sl, lane_off, chunk_off, true,
+                     blk[0], slot[0], vbuf[0]);
+    if (CHUNK > 1)
+      tile_groups<NLD, SL>(src, table, min(c0 + stride, last) * kTile, blk[1], slot[1]);
+#pragma unroll
+    for (int i = 0; i < CHUNK; i++) {
+      const int t = c0 + i * stride;
+      const int b = i & 1, nb = b ^ 1;
+      const int tn = min(t + stride, last);
+      if (i + 1 < CHUNK)
+        stream_load<DPH>(src, head_base, tn * kTile, sl, lane_off, chunk_off, false, blk[nb],
+                         slot[nb], kbuf[nb]);
+      if (balance) {
+        if (2 * i < CHUNK) __builtin_amdgcn_s_setprio(1);
+        else __builtin_amdgcn_s_setprio(0);
+      }
+      // A slot past the wave's last tile: every token masked (no-op).
+      const int ts_mask = t <= last ? t * kTile : INT_MAX / 2;
+      stage_tile<DPH>(kst, sl, c, kbuf[b]);
+      const h8_t pb = mfma_logits<DPH>(ts_mask, q, l16, lim, qb, kst, m_run, l_run, o);
+      if (i + 1 < CHUNK) {
+        stream_load<DPH>(src, head_base, tn * kTile, sl, lane_off, chunk_off, true, blk[nb],
+                         slot[nb], vbuf[nb]);
+        if (i + 2 < CHUNK)
+          tile_groups<NLD, SL>(src, table, min(t + 2 * stride, last) * kTile, blk[b], slot[b]);
+      }
+      stage_tile<DPH>(vst, sl, c, vbuf[b]);
+      mfma_pv<DPH>(q, l16, pb, vst, o);
+    }
+  }
+  if (balance) __builtin_amdgcn_s_setprio(0);
+}
+
 // LDS of stream_item: per-wave records of every row, acc[DPH] and
 // (max, sum).
 template <int DPH, int RPW, int WAVES>
@@ -904,6 +1118,25 @@ struct StreamLds {
   float acc[WAVES * RPW * DPH] __attribute__((aligned(16)));
   float2 ml[WAVES * RPW];
   int last;
+  __device__ float* acc_at(int w, int r) { return acc + (w * RPW + r) * DPH; }
+  __device__ float2& ml_at(int w, int r) { return ml[w * RPW + r]; }
+};
+
+// LDS of the MFMA tile path: per wave, its staged K and V tiles; once the
+// wave's tiles are done the same bytes hold its records (up to 16 rows).
+template <int DPH, int WAVES>
+struct MfmaLds {
+  static constexpr int kRows = 16;
+  static_assert(kRows * (DPH + 2) * 4 <= MfmaShape<DPH>::WAVEB, "records fit the staging area");
+  char st[WAVES * MfmaShape<DPH>::WAVEB] __attribute__((aligned(16)));
+  int last;
+  __device__ char* staging(int w) { return st + w * MfmaShape<DPH>::WAVEB; }
+  __device__ float* acc_at(int w, int r) {
+    return reinterpret_cast<float*>(staging(w)) + r * DPH;
+  }
+  __device__ float2& ml_at(int w, int r) {
+    return reinterpret_cast<float2*>(staging(w) + kRows * DPH * 4)[r];
+  }
 };
 
 // Partition `part` of (KV head kvh, row group rg) on the calling workgroup:
@@ -911,14 +1144,14 @@ struct StreamLds {
 // merge their states through LDS, and either write the normalised output
 // (one partition) or publish a partial and count the arrival; the last
 // arrival combines all partitions.  Every thread of the workgroup calls it.
-template <int DPH, int RPW, int CHUNK, int WAVES, bool ROPE = false>
+template <int DPH, int RPW, int CHUNK, int WAVES, bool ROPE = false, bool MF = false,
+          class Lds>
 __device__ __forceinline__ void stream_item(const AttnArgs& a, int part, int kvh, int rg,
-                                            StreamLds<DPH, RPW, WAVES>& lds,
-                                            const RopeArgs* rp = nullptr,
+                                            Lds& lds, const RopeArgs* rp = nullptr,
                                             float2* rope_cs = nullptr) {
   static_assert(DPH == 64 || DPH == 128, "head_dim");
-  static_assert(RPW == 2 || RPW == 4, "rows per wave");
-  static_assert(RPW * (DPH / 2) <= 64 * WAVES, "one merge thread per (row, feature pair)");
+  static_assert(!(MF && ROPE), "the MFMA tile path has no fused RoPE");
+  static_assert(RPW == 2 || RPW == 4 || (MF && (RPW == 8 || RPW == 16)), "rows per wave");
   constexpr int CH = DPH / 8;
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -931,9 +1164,6 @@ __device__ __forceinline__ void stream_item(const AttnArgs& a, int part, int kvh
   const int tb = part * a.tiles_per_part;
   const int te = min(n_tiles, tb + a.tiles_per_part);
 
-  using Sh = StreamShape<DPH, RPW>;
-  const int my_r = (c >> (Sh::S - Sh::T)) >> (Sh::T - Sh::RB);
-
   if constexpr (ROPE) {
     rope_table<DPH>(*rp, a.pos_base, a.R / a.G, rope_cs);
     // A partition that reads window positions first writes the window's K
@@ -943,7 +1173,48 @@ __device__ __forceinline__ void stream_item(const AttnArgs& a, int part, int kvh
     if (te * kTile > a.pos_base) rope_append_slice<DPH>(a, *rp, rope_cs, kvh);
   }
 
-  if (wave < WAVES) {
+  if constexpr (MF) {
+    if (wave < WAVES) {
+      // MFMA tile path: lane l serves row r0 + l%16 (rows past nrows are
+      // padding: zero q, nothing visible).
+      using Mh = MfmaShape<DPH>;
+      const int l16 = lane & 15, grp = lane >> 4;
+      const bool real = l16 < nrows;
+      const int gr = min(r0 + l16, a.R - 1);
+      const int m = gr / a.G;
+      const int h = kvh * a.G + (gr - m * a.G);
+      const float2* qp = reinterpret_cast<const float2*>(a.q + (size_t)m * a.nh * DPH +
+                                                         (size_t)h * DPH + 8 * grp);
+      const float sc = real ? a.qscale : 0.f;
+      h8_t qb[Mh::KS];
+#pragma unroll
+      for (int ks = 0; ks < Mh::KS; ks++)
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+          const float2 x = qp[16 * ks + w];
+          qb[ks][2 * w] = (_Float16)(x.x * sc);
+          qb[ks][2 * w + 1] = (_Float16)(x.y * sc);
+        }
+      const int lim = real ? a.pos_base + (r0 + l16) / a.G : -1;
+      float m_run = -INFINITY, l_run = 0.f;
+      f4_t o[Mh::DB];
+#pragma unroll
+      for (int db = 0; db < Mh::DB; db++) o[db] = f4_t{0.f, 0.f, 0.f, 0.f};
+      mfma_attend<DPH, CHUNK>(a.src, kvh, tb + wave, te, WAVES, lim, qb, lds.staging(wave),
+                              m_run, l_run, o, a.row_groups > 1);
+      const float l_row = groups_sum(l_run);
+      // The staged tiles are dead: records go over them (DS operations of a
+      // wave complete in order).
+      if (real) {
+#pragma unroll
+        for (int db = 0; db < Mh::DB; db++)
+          *reinterpret_cast<f4_t*>(lds.acc_at(wave, l16) + 16 * db + 4 * grp) = o[db];
+        if (grp == 0) lds.ml_at(wave, l16) = make_float2(m_run, l_row);
+      }
+    }
+  } else if (wave < WAVES) {
+    using Sh = StreamShape<DPH, RPW>;
+    const int my_r = (c >> (Sh::S - Sh::T)) >> (Sh::T - Sh::RB);
     // This lane's q chunk (features 8c..8c+7) of every row, loaded before
     // any K/V load so that waiting for it never waits for tile data.
     float2 q_raw[RPW][4];
@@ -983,10 +1254,10 @@ __device__ __forceinline__ void stream_item(const AttnArgs& a, int part, int kvh
     // ---- merge the slot states of this wave; record per row -------------
     float m_row, l_row, o[2 * RPW];
     wave_merge_slots<DPH, RPW>(m_run, l_run, acc, m_row, l_row, o);
-    if (sl == 0 && c == Sh::owner(my_r, 0)) lds.ml[wave * RPW + my_r] = make_float2(m_row, l_row);
+    if (sl == 0 && c == Sh::owner(my_r, 0)) lds.ml_at(wave, my_r) = make_float2(m_row, l_row);
     const int j = lane >> 4;
     if (DPH == 128 || (lane & 8) == 0) {
-      float4* dst = reinterpret_cast<float4*>(lds.acc + (wave * RPW + merged_row<RPW>(j)) * DPH +
+      float4* dst = reinterpret_cast<float4*>(lds.acc_at(wave, merged_row<RPW>(j)) +
                                               8 * c + merged_col<RPW>(j));
       dst[0] = make_float4(o[0], o[1], o[2], o[3]);
       if constexpr (RPW == 4) dst[1] = make_float4(o[4], o[5], o[6], o[7]);
@@ -996,19 +1267,19 @@ __device__ __forceinline__ void stream_item(const AttnArgs& a, int part, int kvh
 
   // ---- workgroup merge: thread (row, feature pair) over the waves --------
   constexpr int DP = DPH / 2;
-  if ((int)threadIdx.x < nrows * DP) {
-    const int r = threadIdx.x / DP;
-    const int dcol = 2 * (threadIdx.x - r * DP);
+  for (int idx = threadIdx.x; idx < nrows * DP; idx += blockDim.x) {
+    const int r = idx / DP;
+    const int dcol = 2 * (idx - r * DP);
     float mx = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < WAVES; w++) mx = fmaxf(mx, lds.ml[w * RPW + r].x);
+    for (int w = 0; w < WAVES; w++) mx = fmaxf(mx, lds.ml_at(w, r).x);
     float l = 0.f, o0 = 0.f, o1 = 0.f;
 #pragma unroll
     for (int w = 0; w < WAVES; w++) {
-      const float2 ml = lds.ml[w * RPW + r];
+      const float2 ml = lds.ml_at(w, r);
       const float wt = ml.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ml.x - mx);
       l += ml.y * wt;
-      const float2 x = *reinterpret_cast<const float2*>(lds.acc + (w * RPW + r) * DPH + dcol);
+      const float2 x = *reinterpret_cast<const float2*>(lds.acc_at(w, r) + dcol);
       o0 += x.x * wt;
       o1 += x.y * wt;
     }
@@ -1052,9 +1323,13 @@ __device__ __forceinline__ void stream_item(const AttnArgs& a, int part, int kvh
 // kStreamMaxParts, at least one tile per wave), then the fewest tiles per
 // wave that cover the context.  A wave takes its tiles in chunks of `chunk`
 // (1 to max_chunk, unrolled at compile time), several chunks when it has
-// more than max_chunk tiles.
+// more than max_chunk tiles.  (Cutting the context evenly instead, with
+// masked slots for the waves past a partition's last tile, measured slower
+// on short contexts: the masked slots are not free.)  Rows per group:
+// `rows`, or (0) 2 for windows of at most 2 rows and kStreamMaxRows
+// otherwise.
 struct StreamPlan {
-  int rpw;             // rows per wave (2 or kStreamMaxRows)
+  int rpw;             // rows per group
   int row_groups;
   int chunk;
   int tiles_per_part;
@@ -1062,9 +1337,9 @@ struct StreamPlan {
 };
 
 __host__ __device__ inline StreamPlan stream_plan(int L_max, int nkv, int R, int blocks,
-                                                  int waves, int max_chunk) {
+                                                  int waves, int max_chunk, int rows = 0) {
   StreamPlan p;
-  p.rpw = R <= 2 ? 2 : kStreamMaxRows;
+  p.rpw = rows > 0 ? rows : R <= 2 ? 2 : kStreamMaxRows;
   p.row_groups = (R + p.rpw - 1) / p.rpw;
   const int n_tiles = (L_max + kTile - 1) / kTile;
   const int64_t units = (int64_t)nkv * p.row_groups;

@@ -5,25 +5,26 @@
 // out[m][h] = softmax(q[m][h] . K[0..pos_base+m]^T * dph^-1/2) V, with query
 // head h reading KV head h*nkv/nh, keys gathered through the block table.
 //
-// No MFMA: decode and small-k verify are GEMV-shaped and HBM-bound.  The
-// "rows" of a KV head are its (query, head-in-group) pairs; a row group of up
-// to four rows shares every K/V byte it loads.  The context of each (KV
-// head, row group) is split into partitions, one 8-wave workgroup each
-// (about one per CU); a single-partition context writes the normalised
-// output directly, otherwise per-row partials go to the workspace and the
-// last workgroup of a (KV head, row group) to finish -- found with one
-// arrival counter per pair -- merges all partitions with a log-sum-exp
-// combine in partition order, so the result does not depend on arrival
-// order and one call is one launch.
+// The "rows" of a KV head are its (query, head-in-group) pairs; a row group
+// (up to 16 rows, or 4 on the fused RoPE path) shares every K/V byte it
+// loads.  The context of each (KV head, row group) is split into
+// partitions, one 8-wave workgroup each (about one per CU); a
+// single-partition context writes the normalised output directly,
+// otherwise per-row partials go to the workspace and the last workgroup of
+// a (KV head, row group) to finish -- found with one arrival counter per
+// pair -- merges all partitions with a log-sum-exp combine in partition
+// order, so the result does not depend on arrival order and one call is
+// one launch.
 //
-// attn_stream_kernel: K and V stream from HBM straight into VGPRs in the
-// coalesced load layout (lane = token slot x 16-byte feature chunk),
-// software-pipelined a tile (32 tokens) ahead; logits are reduced across
-// the lanes of a token with a transposing DPP butterfly that leaves each
-// lane one (row, token pair), so the online softmax is a handful of scalar
-// ops per lane; P.V dot2-accumulates fp16 probability pairs against
-// byte-permuted V pairs.  Row groups of a larger verify window are separate
-// workgroups reading the same K/V (the repeats are L2 hits).
+// attn_mfma_kernel: K and V stream from HBM into VGPRs in the coalesced
+// load layout (lane = token slot x 16-byte feature chunk), software-
+// pipelined a tile (32 tokens) ahead, and are staged per wave in LDS; the
+// logits (K . Q^T) and the output (V^T . P^T, V read transposed with
+// ds_read_b64_tr_b16) are 16x16x32 fp16 MFMA products with fp32
+// accumulation, and the online softmax is lane-local per row.
+// attn_rope_kernel (the fused RoPE + append + attention step) keeps the
+// VALU tile path: fp16 dot2 products reduced by a transposing DPP
+// butterfly.
 #include <hip/hip_runtime.h>
 
 #include <climits>
@@ -52,24 +53,15 @@ __device__ __forceinline__ int3 stream_coords() {
   }
 }
 
+// Decode and verify steps on the MFMA tile path.
 template <int DPH, int RPW, int CHUNK>
-__global__ __launch_bounds__(64 * kStreamWaves) void attn_stream_kernel(AttnArgs a) {
-  __shared__ StreamLds<DPH, RPW, kStreamWaves> lds;
+__global__ __launch_bounds__(64 * kStreamWaves) void attn_mfma_kernel(AttnArgs a) {
+  __shared__ MfmaLds<DPH, kStreamWaves> lds;
   const int3 w = stream_coords<CHUNK>();
-  stream_item<DPH, RPW, CHUNK, kStreamWaves>(a, w.x, w.y, w.z, lds);
+  stream_item<DPH, RPW, CHUNK, kStreamWaves, false, true>(a, w.x, w.y, w.z, lds);
 }
 
-// Verify windows whose 8-wave plan leaves long serial tile chains per wave
-// (more than four tiles): 4-wave workgroups, one tile per chunk (136 VGPRs,
-// so three workgroups -- three waves per SIMD -- share a CU and hide each
-// other's load latency).
-template <int DPH, int RPW>
-__global__ __launch_bounds__(256) void attn_stream4_kernel(AttnArgs a) {
-  __shared__ StreamLds<DPH, RPW, 4> lds;
-  stream_item<DPH, RPW, 1, 4>(a, blockIdx.x, blockIdx.y, blockIdx.z, lds);
-}
-
-// attn_stream_kernel with RoPE of q and of the window's k, and the window's
+// The VALU tile path with RoPE of q and of the window's k, and the window's
 // append, fused in (sde_rope_append_attention).
 template <int DPH, int RPW, int CHUNK>
 __global__ __launch_bounds__(64 * kStreamWaves) void attn_rope_kernel(AttnArgs a, RopeArgs rp) {
@@ -86,24 +78,33 @@ namespace {
 
 using namespace sde::attn;
 
-constexpr int kVerifyWaves = 4;  // waves per workgroup of attn_stream4_kernel
 
 // Upper bound of the plans' n_parts over every L <= max_total_len: a
-// partition holds at least one tile per wave (four waves at least) and
-// there are at most kStreamMaxParts of them.
+// partition holds at least one tile per wave and there are at most
+// kStreamMaxParts of them.
 int parts_bound(int max_total_len) {
   const int n_tiles = (max_total_len + kTile - 1) / kTile;
-  const int by_len = (n_tiles + kVerifyWaves - 1) / kVerifyWaves;
+  const int by_len = (n_tiles + kStreamWaves - 1) / kStreamWaves;
   return by_len < kStreamMaxParts ? by_len : kStreamMaxParts;
 }
 
-// The plan of a call: 8-wave workgroups, one per CU; or, for windows of
-// more than four rows per KV head whose waves would walk more than four
-// tiles each, 4-wave single-tile-chunk workgroups, three per CU.
-StreamPlan plan_for(int L_max, int nkv, int R, int n_cus, bool fused, bool* four_waves) {
-  const StreamPlan p8 = stream_plan(L_max, nkv, R, n_cus, kStreamWaves, 4);
-  *four_waves = !fused && R > 4 && p8.tiles_per_part > 4 * kStreamWaves;
-  return *four_waves ? stream_plan(L_max, nkv, R, 3 * n_cus, kVerifyWaves, 1) : p8;
+// Rows per group on the MFMA path (an MFMA tile holds 16; measured on
+// MI355X): up to 8 rows (decode) in groups of 4, so a KV head's rows keep
+// twice the workgroups pulling K/V; verify windows of up to 48 rows over
+// contexts up to 16K in groups of 8, whose repeated K/V reads are cache
+// hits; larger windows and longer contexts in groups of 16, the fewest
+// repeated reads.
+int mfma_rows(int R, int L_max) {
+  if (R <= 2) return 2;
+  if (R <= 8) return 4;
+  if (R <= 48 && L_max <= 16384) return 8;
+  return 16;
+}
+
+// The plan of a call: 8-wave workgroups, one per CU.
+StreamPlan plan_for(int L_max, int nkv, int R, int n_cus, bool fused) {
+  return stream_plan(L_max, nkv, R, n_cus, kStreamWaves, 4,
+                     fused ? (R <= 2 ? 2 : kStreamMaxRows) : mfma_rows(R, L_max));
 }
 
 size_t partial_bytes(int nkv, int R, int n_parts, int dph) {
@@ -112,31 +113,45 @@ size_t partial_bytes(int nkv, int R, int n_parts, int dph) {
 
 template <int DPH>
 int launch(const StreamPlan& p, const AttnArgs& a, int nkv, hipStream_t s,
-           const RopeArgs* rope, bool four_waves) {
+           const RopeArgs* rope) {
   const dim3 grid(p.n_parts, nkv, p.row_groups);
   const dim3 block(64 * kStreamWaves);
-  if (four_waves) {
-    if (p.rpw != 4 || p.chunk != 1) return SDE_ERR_UNSUPPORTED;
-    attn_stream4_kernel<DPH, 4><<<grid, dim3(64 * kVerifyWaves), 0, s>>>(a);
-    return sde::launch_status();
-  }
-#define SDE_STREAM(R, C)                                              \
-  if (p.rpw == R && p.chunk == C) {                                   \
-    if (rope)                                                         \
-      attn_rope_kernel<DPH, R, C><<<grid, block, 0, s>>>(a, *rope);   \
-    else                                                              \
-      attn_stream_kernel<DPH, R, C><<<grid, block, 0, s>>>(a);        \
+#define SDE_MFMA(R, C)                                                \
+  if (!rope && p.rpw == R && p.chunk == C) {                          \
+    attn_mfma_kernel<DPH, R, C><<<grid, block, 0, s>>>(a);            \
     return sde::launch_status();                                      \
   }
-  SDE_STREAM(2, 1)
-  SDE_STREAM(2, 2)
-  SDE_STREAM(2, 3)
-  SDE_STREAM(2, 4)
-  SDE_STREAM(4, 1)
-  SDE_STREAM(4, 2)
-  SDE_STREAM(4, 3)
-  SDE_STREAM(4, 4)
-#undef SDE_STREAM
+#define SDE_ROPE(R, C)                                                \
+  if (rope && p.rpw == R && p.chunk == C) {                           \
+    attn_rope_kernel<DPH, R, C><<<grid, block, 0, s>>>(a, *rope);     \
+    return sde::launch_status();                                      \
+  }
+  SDE_MFMA(2, 1)
+  SDE_MFMA(2, 2)
+  SDE_MFMA(2, 3)
+  SDE_MFMA(2, 4)
+  SDE_MFMA(4, 1)
+  SDE_MFMA(4, 2)
+  SDE_MFMA(4, 3)
+  SDE_MFMA(4, 4)
+  SDE_MFMA(8, 1)
+  SDE_MFMA(8, 2)
+  SDE_MFMA(8, 3)
+  SDE_MFMA(8, 4)
+  SDE_MFMA(16, 1)
+  SDE_MFMA(16, 2)
+  SDE_MFMA(16, 3)
+  SDE_MFMA(16, 4)
+  SDE_ROPE(2, 1)
+  SDE_ROPE(2, 2)
+  SDE_ROPE(2, 3)
+  SDE_ROPE(2, 4)
+  SDE_ROPE(4, 1)
+  SDE_ROPE(4, 2)
+  SDE_ROPE(4, 3)
+  SDE_ROPE(4, 4)
+#undef SDE_MFMA
+#undef SDE_ROPE
   return SDE_ERR_UNSUPPORTED;
 }
 
@@ -187,8 +202,7 @@ int run_attention(sde_kv_cache* cache, int layer, const float* d_q, float* d_out
   const int G = nh / nkv;
   const int R = n_queries * G;
   const int L_max = pos_base + n_queries;
-  bool four_waves = false;
-  const StreamPlan plan = plan_for(L_max, nkv, R, cache->n_cus, rope != nullptr, &four_waves);
+  const StreamPlan plan = plan_for(L_max, nkv, R, cache->n_cus, rope != nullptr);
   if ((int64_t)nkv * plan.row_groups > sde::kMaxAttnCounters) return SDE_ERR_UNSUPPORTED;
   const size_t need = partial_bytes(nkv, R, plan.n_parts, dph);
   float* partials = nullptr;
@@ -233,8 +247,7 @@ int run_attention(sde_kv_cache* cache, int layer, const float* d_q, float* d_out
   a.qscale = (float)(kLog2e / std::sqrt((double)dph));
 
   const hipStream_t s = (hipStream_t)stream;
-  return dph == 128 ? launch<128>(plan, a, nkv, s, rope, four_waves)
-                    : launch<64>(plan, a, nkv, s, rope, four_waves);
+  return dph == 128 ? launch<128>(plan, a, nkv, s, rope) : launch<64>(plan, a, nkv, s, rope);
 }
 
 }  // namespace
