@@ -1050,64 +1050,132 @@ __device__ __forceinline__ void mfma_pv(int q, int l16, const h8_t pb, const cha
   }
 }
 
+// This lane's q operand (row l%16, features 32ks + 8(l/16) + e) from its
+// raw fp32 values: rotated by RoPE when cs (the row's (cos, sin) table
+// entries, feature-pair-indexed) is given -- the partner of feature f is
+// f +- dph/2, k-step ks +- KS/2 of the same lane -- then scaled into the
+// exp2 domain and rounded to fp16.
+template <int DPH>
+__device__ __forceinline__ void mfma_pack_q(const float2 (&qr)[MfmaShape<DPH>::KS][4], float sc,
+                                            const float2* cs, int grp,
+                                            h8_t (&qb)[MfmaShape<DPH>::KS]) {
+  constexpr int KS = MfmaShape<DPH>::KS;
+  float x[KS][8];
+#pragma unroll
+  for (int ks = 0; ks < KS; ks++)
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+      x[ks][2 * w] = qr[ks][w].x;
+      x[ks][2 * w + 1] = qr[ks][w].y;
+    }
+  if (cs) {
+#pragma unroll
+    for (int ks = 0; ks < KS / 2; ks++)
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const float2 k = cs[32 * ks + 8 * grp + e];
+        const float a = x[ks][e], b = x[ks + KS / 2][e];
+        x[ks][e] = a * k.x - b * k.y;
+        x[ks + KS / 2][e] = a * k.y + b * k.x;
+      }
+  }
+#pragma unroll
+  for (int ks = 0; ks < KS; ks++)
+#pragma unroll
+    for (int e = 0; e < 8; e++) qb[ks][e] = (_Float16)(x[ks][e] * sc);
+}
+
+// Per-wave constants of the MFMA tile loop.
+struct MfmaWave {
+  const char* head_base;  // this KV head's slice in the pool
+  const_table_t table;
+  uint32_t lane_off, chunk_off;
+  int sl, c, l16, q;      // load role (slot, chunk) and operand role (row, group)
+  int last, stride, lim;
+  char* kst;              // staged K tile; the V tile follows
+};
+
+// One chunk of a wave's tiles, starting at tile c0, pipelined a tile ahead
+// like wave_attend.  FIRST: the wave's first chunk, which packs q once its
+// first loads are in flight (q was loaded before them, so this waits for no
+// tile data); the raw q registers are dead after it.
+template <int DPH, int CHUNK, bool FIRST>
+__device__ __forceinline__ void mfma_chunk(const TileSource& src, const MfmaWave& w, int c0,
+                                           const float2 (&qr)[MfmaShape<DPH>::KS][4], float qsc,
+                                           const float2* cs, h8_t (&qb)[MfmaShape<DPH>::KS],
+                                           float& m_run, float& l_run,
+                                           f4_t (&o)[MfmaShape<DPH>::DB], bool balance) {
+  constexpr int SL = 512 / DPH, NLD = kTile / SL;
+  char* vst = w.kst + MfmaShape<DPH>::TILEB;
+  uint4 kbuf[2][NLD], vbuf[2][NLD];
+  int blk[2][NLD], slot[2][NLD];
+  tile_groups<NLD, SL>(src, w.table, min(c0, w.last) * kTile, blk[0], slot[0]);
+  stream_load<DPH>(src, w.head_base, min(c0, w.last) * kTile, w.sl, w.lane_off, w.chunk_off,
+                   false, blk[0], slot[0], kbuf[0]);
+  stream_load<DPH>(src, w.head_base, min(c0, w.last) * kTile, w.sl, w.lane_off, w.chunk_off,
+                   true, blk[0], slot[0], vbuf[0]);
+  if (CHUNK > 1)
+    tile_groups<NLD, SL>(src, w.table, min(c0 + w.stride, w.last) * kTile, blk[1], slot[1]);
+#pragma unroll
+  for (int i = 0; i < CHUNK; i++) {
+    const int t = c0 + i * w.stride;
+    const int b = i & 1, nb = b ^ 1;
+    const int tn = min(t + w.stride, w.last);
+    if (i + 1 < CHUNK)
+      stream_load<DPH>(src, w.head_base, tn * kTile, w.sl, w.lane_off, w.chunk_off, false,
+                       blk[nb], slot[nb], kbuf[nb]);
+    if (FIRST && i == 0) mfma_pack_q<DPH>(qr, qsc, cs, w.q, qb);
+    if (balance) {
+      if (2 * i < CHUNK) __builtin_amdgcn_s_setprio(1);
+      else __builtin_amdgcn_s_setprio(0);
+    }
+    // A slot past the wave's last tile: every token masked (no-op).
+    const int ts_mask = t <= w.last ? t * kTile : INT_MAX / 2;
+    stage_tile<DPH>(w.kst, w.sl, w.c, kbuf[b]);
+    const h8_t pb = mfma_logits<DPH>(ts_mask, w.q, w.l16, w.lim, qb, w.kst, m_run, l_run, o);
+    if (i + 1 < CHUNK) {
+      stream_load<DPH>(src, w.head_base, tn * kTile, w.sl, w.lane_off, w.chunk_off, true,
+                       blk[nb], slot[nb], vbuf[nb]);
+      if (i + 2 < CHUNK)
+        tile_groups<NLD, SL>(src, w.table, min(t + 2 * w.stride, w.last) * kTile, blk[b],
+                             slot[b]);
+    }
+    stage_tile<DPH>(vst, w.sl, w.c, vbuf[b]);
+    mfma_pv<DPH>(w.q, w.l16, pb, vst, o);
+  }
+}
+
 // A wave's tiles first, first+stride, ... < te of KV head kvh on the MFMA
-// path, with wave_attend's loads and pipeline (a tile ahead).  lim: last
-// visible position of this lane's row (-1: a padding row).  st: this wave's
-// LDS (K tile, then V tile).
+// path.  lim: last visible position of this lane's row (-1: a padding
+// row).  qr, qsc, cs: the lane's raw q values, their scale and RoPE table
+// (mfma_pack_q).  st: this wave's LDS (K tile, then V tile).
 template <int DPH, int CHUNK>
 __device__ __forceinline__ void mfma_attend(const TileSource& src, int kvh, int first, int te,
                                             int stride, int lim,
-                                            const h8_t (&qb)[MfmaShape<DPH>::KS], char* st,
-                                            float& m_run, float& l_run,
-                                            f4_t (&o)[MfmaShape<DPH>::DB], bool balance) {
-  constexpr int CH = DPH / 8, SL = 512 / DPH, NLD = kTile / SL;
-  const int lane = threadIdx.x & 63;
-  const int l16 = lane & 15, q = lane >> 4;
-  const int sl = lane / CH, c = lane % CH;
-  const const_table_t table = const_table(src);
-  const char* head_base = reinterpret_cast<const char*>(src.pool) + (size_t)kvh * DPH * 2u;
-  const uint32_t lane_off = (uint32_t)sl * 2u * (uint32_t)src.kv_dim + 16u * c;
-  const uint32_t chunk_off = 16u * c;
-  char* kst = st;
-  char* vst = st + MfmaShape<DPH>::TILEB;
+                                            const float2 (&qr)[MfmaShape<DPH>::KS][4], float qsc,
+                                            const float2* cs, char* st, float& m_run,
+                                            float& l_run, f4_t (&o)[MfmaShape<DPH>::DB],
+                                            bool balance) {
+  constexpr int CH = DPH / 8;
   if (first >= te) return;
-  const int last = first + ((te - 1 - first) / stride) * stride;
-  for (int c0 = first; c0 < te; c0 += CHUNK * stride) {
-    uint4 kbuf[2][NLD], vbuf[2][NLD];
-    int blk[2][NLD], slot[2][NLD];
-    tile_groups<NLD, SL>(src, table, min(c0, last) * kTile, blk[0], slot[0]);
-    stream_load<DPH>(src, head_base, min(c0, last) * kTile, sl, lane_off, chunk_off, false,
-                     blk[0], slot[0], kbuf[0]);
-    stream_load<DPH>(src, head_base, min(c0, last) * kTile, sl, lane_off, chunk_off, true,
-                     blk[0], slot[0], vbuf[0]);
-    if (CHUNK > 1)
-      tile_groups<NLD, SL>(src, table, min(c0 + stride, last) * kTile, blk[1], slot[1]);
-#pragma unroll
-    for (int i = 0; i < CHUNK; i++) {
-      const int t = c0 + i * stride;
-      const int b = i & 1, nb = b ^ 1;
-      const int tn = min(t + stride, last);
-      if (i + 1 < CHUNK)
-        stream_load<DPH>(src, head_base, tn * kTile, sl, lane_off, chunk_off, false, blk[nb],
-                         slot[nb], kbuf[nb]);
-      if (balance) {
-        if (2 * i < CHUNK) __builtin_amdgcn_s_setprio(1);
-        else __builtin_amdgcn_s_setprio(0);
-      }
-      // A slot past the wave's last tile: every token masked (no-op).
-      const int ts_mask = t <= last ? t * kTile : INT_MAX / 2;
-      stage_tile<DPH>(kst, sl, c, kbuf[b]);
-      const h8_t pb = mfma_logits<DPH>(ts_mask, q, l16, lim, qb, kst, m_run, l_run, o);
-      if (i + 1 < CHUNK) {
-        stream_load<DPH>(src, head_base, tn * kTile, sl, lane_off, chunk_off, true, blk[nb],
-                         slot[nb], vbuf[nb]);
-        if (i + 2 < CHUNK)
-          tile_groups<NLD, SL>(src, table, min(t + 2 * stride, last) * kTile, blk[b], slot[b]);
-      }
-      stage_tile<DPH>(vst, sl, c, vbuf[b]);
-      mfma_pv<DPH>(q, l16, pb, vst, o);
-    }
-  }
+  const int lane = threadIdx.x & 63;
+  MfmaWave w;
+  w.sl = lane / CH;
+  w.c = lane % CH;
+  w.l16 = lane & 15;
+  w.q = lane >> 4;
+  w.table = const_table(src);
+  w.head_base = reinterpret_cast<const char*>(src.pool) + (size_t)kvh * DPH * 2u;
+  w.lane_off = (uint32_t)w.sl * 2u * (uint32_t)src.kv_dim + 16u * w.c;
+  w.chunk_off = 16u * w.c;
+  w.last = first + ((te - 1 - first) / stride) * stride;
+  w.stride = stride;
+  w.lim = lim;
+  w.kst = st;
+  h8_t qb[MfmaShape<DPH>::KS];
+  mfma_chunk<DPH, CHUNK, true>(src, w, first, qr, qsc, cs, qb, m_run, l_run, o, balance);
+  for (int c0 = first + CHUNK * stride; c0 < te; c0 += CHUNK * stride)
+    mfma_chunk<DPH, CHUNK, false>(src, w, c0, qr, qsc, cs, qb, m_run, l_run, o, balance);
   if (balance) __builtin_amdgcn_s_setprio(0);
 }
 
@@ -1150,7 +1218,6 @@ __device__ __forceinline__ void stream_item(const AttnArgs& a, int part, int kvh
                                             Lds& lds, const RopeArgs* rp = nullptr,
                                             float2* rope_cs = nullptr) {
   static_assert(DPH == 64 || DPH == 128, "head_dim");
-  static_assert(!(MF && ROPE), "the MFMA tile path has no fused RoPE");
   static_assert(RPW == 2 || RPW == 4 || (MF && (RPW == 8 || RPW == 16)), "rows per wave");
   constexpr int CH = DPH / 8;
 
@@ -1185,23 +1252,21 @@ __device__ __forceinline__ void stream_item(const AttnArgs& a, int part, int kvh
       const int h = kvh * a.G + (gr - m * a.G);
       const float2* qp = reinterpret_cast<const float2*>(a.q + (size_t)m * a.nh * DPH +
                                                          (size_t)h * DPH + 8 * grp);
-      const float sc = real ? a.qscale : 0.f;
-      h8_t qb[Mh::KS];
+      float2 qr[Mh::KS][4];
 #pragma unroll
       for (int ks = 0; ks < Mh::KS; ks++)
 #pragma unroll
-        for (int w = 0; w < 4; w++) {
-          const float2 x = qp[16 * ks + w];
-          qb[ks][2 * w] = (_Float16)(x.x * sc);
-          qb[ks][2 * w + 1] = (_Float16)(x.y * sc);
-        }
+        for (int w = 0; w < 4; w++) qr[ks][w] = qp[16 * ks + w];
+      const float2* cs = nullptr;
+      if constexpr (ROPE) cs = rope_cs + m * (DPH / 2);
       const int lim = real ? a.pos_base + (r0 + l16) / a.G : -1;
       float m_run = -INFINITY, l_run = 0.f;
       f4_t o[Mh::DB];
 #pragma unroll
       for (int db = 0; db < Mh::DB; db++) o[db] = f4_t{0.f, 0.f, 0.f, 0.f};
-      mfma_attend<DPH, CHUNK>(a.src, kvh, tb + wave, te, WAVES, lim, qb, lds.staging(wave),
-                              m_run, l_run, o, a.row_groups > 1);
+      mfma_attend<DPH, CHUNK>(a.src, kvh, tb + wave, te, WAVES, lim, qr,
+                              real ? a.qscale : 0.f, cs, lds.staging(wave), m_run, l_run, o,
+                              a.row_groups > 1);
       const float l_row = groups_sum(l_run);
       // The staged tiles are dead: records go over them (DS operations of a
       // wave complete in order).

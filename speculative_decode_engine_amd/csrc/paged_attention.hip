@@ -61,14 +61,14 @@ __global__ __launch_bounds__(64 * kStreamWaves) void attn_mfma_kernel(AttnArgs a
   stream_item<DPH, RPW, CHUNK, kStreamWaves, false, true>(a, w.x, w.y, w.z, lds);
 }
 
-// The VALU tile path with RoPE of q and of the window's k, and the window's
+// attn_mfma_kernel with RoPE of q and of the window's k, and the window's
 // append, fused in (sde_rope_append_attention).
 template <int DPH, int RPW, int CHUNK>
 __global__ __launch_bounds__(64 * kStreamWaves) void attn_rope_kernel(AttnArgs a, RopeArgs rp) {
-  __shared__ StreamLds<DPH, RPW, kStreamWaves> lds;
+  __shared__ MfmaLds<DPH, kStreamWaves> lds;
   __shared__ float2 rope_cs[kRopeMaxQueries * (DPH / 2)];
   const int3 w = stream_coords<CHUNK>();
-  stream_item<DPH, RPW, CHUNK, kStreamWaves, true>(a, w.x, w.y, w.z, lds, &rp, rope_cs);
+  stream_item<DPH, RPW, CHUNK, kStreamWaves, true, true>(a, w.x, w.y, w.z, lds, &rp, rope_cs);
 }
 
 }  // namespace attn
@@ -102,9 +102,8 @@ int mfma_rows(int R, int L_max) {
 }
 
 // The plan of a call: 8-wave workgroups, one per CU.
-StreamPlan plan_for(int L_max, int nkv, int R, int n_cus, bool fused) {
-  return stream_plan(L_max, nkv, R, n_cus, kStreamWaves, 4,
-                     fused ? (R <= 2 ? 2 : kStreamMaxRows) : mfma_rows(R, L_max));
+StreamPlan plan_for(int L_max, int nkv, int R, int n_cus) {
+  return stream_plan(L_max, nkv, R, n_cus, kStreamWaves, 4, mfma_rows(R, L_max));
 }
 
 size_t partial_bytes(int nkv, int R, int n_parts, int dph) {
@@ -150,6 +149,14 @@ int launch(const StreamPlan& p, const AttnArgs& a, int nkv, hipStream_t s,
   SDE_ROPE(4, 2)
   SDE_ROPE(4, 3)
   SDE_ROPE(4, 4)
+  SDE_ROPE(8, 1)
+  SDE_ROPE(8, 2)
+  SDE_ROPE(8, 3)
+  SDE_ROPE(8, 4)
+  SDE_ROPE(16, 1)
+  SDE_ROPE(16, 2)
+  SDE_ROPE(16, 3)
+  SDE_ROPE(16, 4)
 #undef SDE_MFMA
 #undef SDE_ROPE
   return SDE_ERR_UNSUPPORTED;
@@ -202,7 +209,7 @@ int run_attention(sde_kv_cache* cache, int layer, const float* d_q, float* d_out
   const int G = nh / nkv;
   const int R = n_queries * G;
   const int L_max = pos_base + n_queries;
-  const StreamPlan plan = plan_for(L_max, nkv, R, cache->n_cus, rope != nullptr);
+  const StreamPlan plan = plan_for(L_max, nkv, R, cache->n_cus);
   if ((int64_t)nkv * plan.row_groups > sde::kMaxAttnCounters) return SDE_ERR_UNSUPPORTED;
   const size_t need = partial_bytes(nkv, R, plan.n_parts, dph);
   float* partials = nullptr;
