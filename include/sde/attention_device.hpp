@@ -460,35 +460,6 @@ __device__ __forceinline__ void rope_table(const RopeArgs& rp, int pos_base, int
   __syncthreads();
 }
 
-// RoPE of the lane's eight q features (8c..8c+7) of every row, in place,
-// with the window's (cos, sin) table; the partner feature (j + dph/2 or
-// j - dph/2) lives in lane c ^ CH/2 of the same token slot.
-template <int DPH, int RPW>
-__device__ __forceinline__ void rope_q_rows(const float2* cs_tab, float2 (&q)[RPW][4], int r0,
-                                            int G, int R) {
-  constexpr int CH = DPH / 8;
-  constexpr int HALF = DPH / 2;
-  const int c = (threadIdx.x & 63) % CH;
-  const bool first_half = c < CH / 2;
-  const int j0 = (8 * c) % HALF;
-#pragma unroll
-  for (int r = 0; r < RPW; r++) {
-    // rows past R (masked later) reuse the last row's query
-    const float2* t = cs_tab + (min(r0 + r, R - 1) / G) * HALF + j0;
-    float x[8] = {q[r][0].x, q[r][0].y, q[r][1].x, q[r][1].y,
-                  q[r][2].x, q[r][2].y, q[r][3].x, q[r][3].y};
-    float y[8];
-#pragma unroll
-    for (int e = 0; e < 8; e++) {
-      const float2 k = t[e];
-      const float partner = __shfl_xor(x[e], CH / 2);
-      y[e] = first_half ? x[e] * k.x - partner * k.y : partner * k.y + x[e] * k.x;
-    }
-#pragma unroll
-    for (int w = 0; w < 4; w++) q[r][w] = make_float2(y[2 * w], y[2 * w + 1]);
-  }
-}
-
 // The lane's row permutation for stream_qk's select-free butterfly steps:
 // bit (RB-1-kk) of the flip is bit (S-1-kk) of the chunk index c, for the
 // first SF steps.  A step can go select-free only if its partner lanes
@@ -522,13 +493,12 @@ __device__ __forceinline__ void permute_rows(uint4 (&qr)[RPW], int flip) {
   }
 }
 
-template <int DPH, int RPW, int CHUNK, bool ROPE = false>
+template <int DPH, int RPW, int CHUNK>
 __device__ __forceinline__ void wave_attend(const TileSource& src, int kvh, int first, int te,
                                             int stride, int nrows, int min_lim, int my_lim,
                                             float qscale, const float2 (&q_raw)[RPW][4],
                                             float& m_run, float& l_run, float (&acc)[RPW][8],
-                                            const float2* rope_cs = nullptr, int r0 = 0,
-                                            int G = 1, int R = 1, bool balance = false) {
+                                            bool balance = false) {
   using Sh = StreamShape<DPH, RPW>;
   constexpr int CH = Sh::CH, SL = Sh::SL, NLD = Sh::NLD;
   const int lane = threadIdx.x & 63;
@@ -562,26 +532,7 @@ __device__ __forceinline__ void wave_attend(const TileSource& src, int kvh, int 
       if (i + 1 < CHUNK)
         stream_load<DPH>(src, head_base, tn * kTile, sl, lane_off, chunk_off, false, blk[nb],
                          slot[nb], kbuf[nb]);
-      if constexpr (ROPE) {
-        if (i == 0 && c0 == first) {
-          // q rotated by RoPE, then packed like below (once).
-          float2 qv[RPW][4];
-#pragma unroll
-          for (int r = 0; r < RPW; r++)
-#pragma unroll
-            for (int w = 0; w < 4; w++) qv[r][w] = q_raw[r][w];
-          rope_q_rows<DPH, RPW>(rope_cs, qv, r0, G, R);
-#pragma unroll
-          for (int r = 0; r < RPW; r++) {
-            const float sc = r < nrows ? qscale : 0.f;
-            qr[r] = make_uint4(pack_h2(qv[r][0].x * sc, qv[r][0].y * sc),
-                               pack_h2(qv[r][1].x * sc, qv[r][1].y * sc),
-                               pack_h2(qv[r][2].x * sc, qv[r][2].y * sc),
-                               pack_h2(qv[r][3].x * sc, qv[r][3].y * sc));
-          }
-          permute_rows<RPW>(qr, q_row_flip<DPH, RPW>(c));
-        }
-      } else if (i == 0) {
+      if (i == 0) {
         // q is scaled into the exp2 domain and rounded to fp16 pairs once
         // this chunk's loads are in flight (q was loaded before them, so
         // this waits for no tile data).
@@ -1219,6 +1170,7 @@ __device__ __forceinline__ void stream_item(const AttnArgs& a, int part, int kvh
                                             float2* rope_cs = nullptr) {
   static_assert(DPH == 64 || DPH == 128, "head_dim");
   static_assert(RPW == 2 || RPW == 4 || (MF && (RPW == 8 || RPW == 16)), "rows per wave");
+  static_assert(MF || !ROPE, "fused RoPE runs on the MFMA tile path");
   constexpr int CH = DPH / 8;
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1312,9 +1264,8 @@ __device__ __forceinline__ void stream_item(const AttnArgs& a, int part, int kvh
     // (each K/V byte serves several workgroups from L2): balance the waves
     // of a SIMD (4K 5-query window 14.9 -> 14.5 us; a long one-group decode
     // is HBM-bound and measured 0.3 us slower with it).
-    wave_attend<DPH, RPW, CHUNK, ROPE>(a.src, kvh, tb + wave, te, WAVES, nrows, min_lim, my_lim,
-                                       a.qscale, q_raw, m_run, l_run, acc, rope_cs, r0, a.G,
-                                       a.R, a.row_groups > 1);
+    wave_attend<DPH, RPW, CHUNK>(a.src, kvh, tb + wave, te, WAVES, nrows, min_lim, my_lim,
+                                 a.qscale, q_raw, m_run, l_run, acc, a.row_groups > 1);
 
     // ---- merge the slot states of this wave; record per row -------------
     float m_row, l_row, o[2 * RPW];
