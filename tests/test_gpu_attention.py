@@ -156,6 +156,17 @@ def test_head_groupings_and_windows(gpu, oracle, nh, nkv, M, dph):
     run_case(oracle, nh, nkv, dph, 16, 300, M, 60, nh * 7 + M + dph, f"{nh}/{nkv} M{M}")
 
 
+@pytest.mark.parametrize("nh,nkv,dph,M", [(32, 8, 128, 5), (32, 4, 64, 5), (32, 8, 128, 2)])
+def test_long_context_windows(gpu, oracle, nh, nkv, dph, M):
+    """Windows over a context past 16K keys: 20 and 40 rows per KV head go
+    to 16-row groups there (8-row groups below), 8 rows to 4-row groups;
+    several chunks of tiles per wave."""
+    case_banner("long window", nh, nkv, dph, M)
+    ctx = 17000
+    run_case(oracle, nh, nkv, dph, 16, ctx, M, -(-(ctx + M) // 16) + 3, 7 * M + dph,
+             f"long {nh}/{nkv} dph{dph} M{M}")
+
+
 @pytest.mark.parametrize("bs", [8, 16, 32, 64, 128])
 def test_block_sizes(gpu, oracle, bs):
     case_banner("bs", bs)

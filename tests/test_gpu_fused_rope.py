@@ -58,6 +58,7 @@ CASES = [
     (28, 4, 128, 32, 777, 3, 3, 2.0, 0.0),         # YaRN scaling, default theta
     (8, 8, 128, 8, 30, 4, 0, 1.0, 10000.0),        # window across a tile boundary
     (8, 2, 64, 16, 0, 32, 0, 1.0, 10000.0),        # empty context, 32-row window
+    (32, 8, 128, 16, 17000, 5, 0, 1.0, 500000.0),  # window past 16K keys: 16-row groups
 ]
 
 
