@@ -62,20 +62,23 @@ struct MvPlan {
 
 // Row ranges so that col_tiles * splits fills `blocks` workgroups, each wave
 // keeping at least kUnroll rows (one full batch of loads in flight).
-// Rows of x of a pass rounded up to its unrolled instantiation (1, 2, 4, 8).
+// Rows of x of a pass as unrolled (every count 1..kChunkRows has its own
+// instantiation: the multiply-adds are the streaming loop's issue cost, so
+// a 5-row verify window must not pay for 8).
 __host__ __device__ inline int mv_row_bucket(int rows) {
-  return rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : 8;
+  return rows <= 1 ? 1 : rows >= kChunkRows ? kChunkRows : rows;
 }
 
-// splits * bucket <= kMaxSplit: the combining workgroup then holds every
-// partial of its columns in registers (one round trip).
+// splits <= 4 * (kMaxSplit / 4 / bucket): the combining workgroup then holds
+// every partial of its columns in registers (one round trip; four quarters
+// of kMaxSplit / 4 / bucket loads per row of x).
 __host__ __device__ inline MvPlan mv_plan(int d_in, int d_out, int blocks, int waves, int M) {
   MvPlan p;
   p.col_tiles = (d_out + kCols - 1) / kCols;
   int s = blocks / p.col_tiles;
   const int by_rows = d_in / (waves * kUnroll * kRowPhases);
   if (s > by_rows) s = by_rows;
-  const int cap = kMaxSplit / mv_row_bucket(M < kChunkRows ? M : kChunkRows);
+  const int cap = 4 * (kMaxSplit / 4 / mv_row_bucket(M < kChunkRows ? M : kChunkRows));
   if (s > cap) s = cap;
   if (s < 1) s = 1;
   p.rows_per_split = (d_in + s - 1) / s;
@@ -436,14 +439,16 @@ __device__ __forceinline__ void mv_item(const MvArgs& a, int ct, int ks, MvLds<W
 // Rows of x rounded up to an unrolled instantiation.
 template <int WAVES>
 __device__ __forceinline__ void mv_item_any(const MvArgs& a, int ct, int ks, MvLds<WAVES>& lds) {
-  if (a.M <= 1)
-    mv_item<1, WAVES>(a, ct, ks, lds);
-  else if (a.M <= 2)
-    mv_item<2, WAVES>(a, ct, ks, lds);
-  else if (a.M <= 4)
-    mv_item<4, WAVES>(a, ct, ks, lds);
-  else
-    mv_item<8, WAVES>(a, ct, ks, lds);
+  switch (mv_row_bucket(a.M)) {
+    case 1: mv_item<1, WAVES>(a, ct, ks, lds); break;
+    case 2: mv_item<2, WAVES>(a, ct, ks, lds); break;
+    case 3: mv_item<3, WAVES>(a, ct, ks, lds); break;
+    case 4: mv_item<4, WAVES>(a, ct, ks, lds); break;
+    case 5: mv_item<5, WAVES>(a, ct, ks, lds); break;
+    case 6: mv_item<6, WAVES>(a, ct, ks, lds); break;
+    case 7: mv_item<7, WAVES>(a, ct, ks, lds); break;
+    default: mv_item<8, WAVES>(a, ct, ks, lds); break;
+  }
 }
 
 }  // namespace mv

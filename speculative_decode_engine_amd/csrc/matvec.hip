@@ -93,15 +93,16 @@ int sde_matvec(const float* d_x, const uint16_t* d_W, float* d_out, int d_in, in
   const dim3 grid(p.col_tiles, p.splits, mv_passes(M));
   const dim3 block(64 * kWaves);
   const hipStream_t s = (hipStream_t)stream;
-  const int rows = mv_pass_rows(M);
-  if (rows <= 1)
-    sde::mv::matvec_kernel<1><<<grid, block, 0, s>>>(a);
-  else if (rows <= 2)
-    sde::mv::matvec_kernel<2><<<grid, block, 0, s>>>(a);
-  else if (rows <= 4)
-    sde::mv::matvec_kernel<4><<<grid, block, 0, s>>>(a);
-  else
-    sde::mv::matvec_kernel<8><<<grid, block, 0, s>>>(a);
+  switch (mv_row_bucket(mv_pass_rows(M))) {
+    case 1: sde::mv::matvec_kernel<1><<<grid, block, 0, s>>>(a); break;
+    case 2: sde::mv::matvec_kernel<2><<<grid, block, 0, s>>>(a); break;
+    case 3: sde::mv::matvec_kernel<3><<<grid, block, 0, s>>>(a); break;
+    case 4: sde::mv::matvec_kernel<4><<<grid, block, 0, s>>>(a); break;
+    case 5: sde::mv::matvec_kernel<5><<<grid, block, 0, s>>>(a); break;
+    case 6: sde::mv::matvec_kernel<6><<<grid, block, 0, s>>>(a); break;
+    case 7: sde::mv::matvec_kernel<7><<<grid, block, 0, s>>>(a); break;
+    default: sde::mv::matvec_kernel<8><<<grid, block, 0, s>>>(a); break;
+  }
   return sde::launch_status();
 }
 

@@ -50,6 +50,11 @@ SHAPES = [
     (3, 1000, 1032),     # ragged: rows not a multiple of the tiling, partial column tile
     (1, 7, 8),           # fewer rows than one wave's batch
     (16, 640, 520),      # the largest row count
+    (2, 4096, 1024),     # every row count has its own unrolled instantiation:
+    (3, 14336, 1024),    #   3 rows split 20 ways (the combine's quarters hold 5 each)
+    (4, 2048, 2048),
+    (6, 8192, 512),      #   6 and 7 rows: 8 row ranges at most
+    (7, 8192, 512),
 ]
 
 
