@@ -103,6 +103,23 @@ __device__ float block_sum(float x, float* lds) {
   return t;
 }
 
+// Two block sums at once, each in block_sum's order (the same bits).
+__device__ float2 block_sum2(float x, float y, float2* lds) {
+  for (int off = 32; off > 0; off >>= 1) {
+    x += __shfl_xor(x, off);
+    y += __shfl_xor(y, off);
+  }
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = make_float2(x, y);
+  __syncthreads();
+  float2 t = make_float2(0.f, 0.f);
+  for (int i = 0; i < kWaves; i++) {
+    t.x += lds[i].x;
+    t.y += lds[i].y;
+  }
+  return t;
+}
+
 // Exclusive prefix of x over the threads in thread order.
 __device__ float block_exclusive_scan(float x, float* lds) {
   const int lane = threadIdx.x & 63;
@@ -132,6 +149,30 @@ struct RowWeights {
     return fmaxf(pi - qi, 0.f);
   }
   __device__ __forceinline__ float operator()(int i) const { return of(p[i], q ? q[i] : 0.f); }
+  // This thread's sums of the residual max(0, p - q) and of p over tokens
+  // lo + tid, lo + tid + 1024, ... below hi in one pass (q non-null); each
+  // sum in thread_sum's order.
+  __device__ __forceinline__ float2 thread_sums(int tid, int lo, int hi) const {
+    float cr = 0.f, cp = 0.f;
+    for (int i0 = lo + tid; i0 < hi; i0 += kThreads * kUnroll) {
+      float xp[kUnroll], xq[kUnroll];
+#pragma unroll
+      for (int u = 0; u < kUnroll; u++) {
+        const int i = i0 + u * kThreads;
+        xp[u] = i < hi ? p[i] : -INFINITY;
+        xq[u] = i < hi ? q[i] : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < kUnroll; u++)
+        if (i0 + u * kThreads < hi) {
+          const float pi = __expf(xp[u] * inv_tt - mp) * inv_sp;
+          const float qi = __expf(xq[u] * inv_td - mq) * inv_sq;
+          cr += fmaxf(pi - qi, 0.f);
+          cp += pi;
+        }
+    }
+    return make_float2(cr, cp);
+  }
   // Sum of this thread's weights over tokens lo + tid, lo + tid + 1024, ...
   // below hi, loads batched.
   __device__ __forceinline__ float thread_sum(int tid, int lo, int hi) const {
@@ -222,6 +263,7 @@ __global__ __launch_bounds__(kThreads) void spec_slice_stats_kernel(StochArgs a)
 // token; the last row to arrive decides and rewinds.
 __global__ __launch_bounds__(kThreads) void spec_slice_sample_kernel(StochArgs a) {
   __shared__ float red[kWaves];
+  __shared__ float2 red2[kWaves];
   __shared__ int s_pick, s_last_pos, s_token, s_last_slice;
   __shared__ float s_before;
   const int s = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
@@ -269,12 +311,14 @@ __global__ __launch_bounds__(kThreads) void spec_slice_sample_kernel(StochArgs a
   // This slice's totals of the residual max(0, p - q) and of p.
   const int lo = s * a.L, hi = min(V, lo + a.L);
   RowWeights w{p, q, mp, 1.f / sp, mq, q ? 1.f / sq : 0.f, a.inv_tt, a.inv_td};
-  const float tr = block_sum(w.thread_sum(tid, lo, hi), red);
-  float tp = tr;
+  float tr, tp;
   if (q) {
-    RowWeights wp = w;
-    wp.q = nullptr;
-    tp = block_sum(wp.thread_sum(tid, lo, hi), red);
+    const float2 ts = w.thread_sums(tid, lo, hi);
+    const float2 t = block_sum2(ts.x, ts.y, red2);
+    tr = t.x;
+    tp = t.y;
+  } else {
+    tr = tp = block_sum(w.thread_sum(tid, lo, hi), red);
   }
   if (tid == 0) {
     st_dev(sc.totals(b, s), tr);
