@@ -168,9 +168,10 @@ def test_long_context_windows(gpu, oracle, nh, nkv, dph, M):
 
 
 @pytest.mark.parametrize("bs", [8, 16, 32, 64, 128])
-def test_block_sizes(gpu, oracle, bs):
-    case_banner("bs", bs)
-    run_case(oracle, 16, 4, 128, bs, 700, 4, 4 * (-(-704 // bs)), bs, f"bs{bs}")
+@pytest.mark.parametrize("dph", [64, 128])
+def test_block_sizes(gpu, oracle, bs, dph):
+    case_banner("bs", bs, dph)
+    run_case(oracle, 16, 4, dph, bs, 700, 4, 4 * (-(-704 // bs)), bs + dph, f"bs{bs} dph{dph}")
 
 
 def test_verify_window_equals_single_query_calls(gpu, oracle):
