@@ -206,9 +206,21 @@ __device__ __forceinline__ void mv_fma_batch(const struct MvArgs& a, int r, int 
       for (int p = 0; p < kRowPhases; p++)
         xs[u][p] = a.x[min(r + u * WAVES * kRowPhases + p, a.d_in - 1)];
   }
+  // LDS-staged x: the values of UP row blocks are read up front, so their
+  // LDS round trips overlap instead of sitting in the multiply-add chain
+  // (UP = U unless that would need more than 48 registers).
+  constexpr int UP = MB * U <= 48 ? U : U / 2;
+  float xpre[UP][MB];
 #pragma unroll
   for (int u = 0; u < U; u++) {
     const int rb = r + u * WAVES * kRowPhases;
+    if (xl && u % UP == 0) {
+#pragma unroll
+      for (int v = 0; v < UP; v++)
+#pragma unroll
+        for (int m = 0; m < MB; m++)
+          xpre[v][m] = xl[m * rows + min(rb + v * WAVES * kRowPhases + rp, r1 - 1) - r0];
+    }
     const bool live = FULL || rb + rp < r1;
     const uint32_t wd[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
 #pragma unroll
@@ -216,7 +228,7 @@ __device__ __forceinline__ void mv_fma_batch(const struct MvArgs& a, int r, int 
       if (m < a.M) {
         float xv;
         if (xl) {
-          xv = xl[m * rows + min(rb + rp, r1 - 1) - r0];
+          xv = xpre[u % UP][m];
         } else if (MB == 1) {
           xv = xs[u][0];
 #pragma unroll
