@@ -705,12 +705,6 @@ __device__ __forceinline__ float4 load_dev16(const float* base, uint32_t bytes,
   return make_float4(v.x, v.y, v.z, v.w);
 }
 
-// One (row, float4 column, quarter `sub`) of the partition combine: loads
-// (max, sum, acc[c4]) of partitions sub, sub+4, ... (PMAX of them, P real),
-// returns this quarter's weighted sum and its (max) in l, o, mx.  Every load
-// is issued unconditionally (indices past P re-read partition P-1, then
-// weigh 0), so they all travel in one round trip: a load under `if (p < P)`
-// gets a wait of its own at the join.
 // One pass of the partition combine over NIT row slices: thread
 // (row, float4 column c4, quarter sub) of slice it loads (max, sum, acc[c4])
 // of partitions sub, sub+4, ... for all of its slices first -- every
@@ -719,6 +713,9 @@ __device__ __forceinline__ float4 load_dev16(const float* base, uint32_t bytes,
 // lanes) reduce through DPP in a fixed order, so the result does not
 // depend on arrival order.  (max, sum) of partition p is loaded once per
 // wave, by lane p (a wave's lanes serve one row), and read across lanes.
+// Within a live slice every load is issued unconditionally (indices past
+// P re-read partition P-1, then weigh 0), so they all travel in one round
+// trip: a load under `if (p < P)` would get a wait of its own at the join.
 template <int DPH, int PMAX, int NIT, int WAVES>
 __device__ __forceinline__ void combine_pass(const AttnArgs& a, int kvh, int r0, int nrows,
                                              int it0) {
