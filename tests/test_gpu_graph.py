@@ -72,3 +72,38 @@ def test_matvec_graph_replays_match_eager(gpu, M, d_in, d_out):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, ref), f"replay {rep}"
+
+
+@pytest.mark.parametrize("nh,nkv,dph,ctx,M", [(32, 8, 128, 3000, 5), (32, 4, 64, 2047, 1)])
+def test_fused_rope_graph_replays_match_eager(gpu, nh, nkv, dph, ctx, M):
+    """The fused step appends the window itself: every replay rewrites the
+    same rotated K and V and must give the eager output again."""
+    case_banner("graph fused", nh, nkv, dph, ctx, M)
+    cache, _, _, rng = build_layer(nh, nkv, dph, 16, ctx, M, -(-(ctx + M) // 16) + 8, ctx + 3 * M)
+    kv_dim = nkv * dph
+    q = torch.from_numpy(rng.standard_normal((M, nh * dph), dtype=np.float32)).cuda()
+    k = torch.from_numpy(rng.standard_normal((M, kv_dim), dtype=np.float32)).cuda()
+    v = torch.from_numpy(rng.standard_normal((M, kv_dim), dtype=np.float32)).cuda()
+    q_other = torch.from_numpy(rng.standard_normal((1, nh * dph), dtype=np.float32)).cuda()
+    ws_bytes = cache.workspace_size(nh, nkv, dph, M, ctx + M)
+    ws = torch.zeros(max(1, -(-ws_bytes // 4)), dtype=torch.float32, device="cuda")
+    ref = cache.rope_append_attention(0, q, k, v, nh, nkv, dph, ctx, theta=500000.0, workspace=ws)
+    torch.cuda.synchronize()
+    out = torch.empty_like(ref)
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        cache.rope_append_attention(0, q, k, v, nh, nkv, dph, ctx, theta=500000.0, out=out,
+                                    workspace=ws, stream=side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=side):
+        cache.rope_append_attention(0, q, k, v, nh, nkv, dph, ctx, theta=500000.0, out=out,
+                                    workspace=ws, stream=side)
+    for rep in range(4):
+        out.zero_()
+        cache.attention(0, q_other, nh, nkv, dph, ctx + M - 1, workspace=ws)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), f"replay {rep}"
+    cache.free()
