@@ -349,14 +349,19 @@ __device__ __forceinline__ void mv_item(const MvArgs& a, int ct, int ks, MvLds<W
 
   // ---- waves -> one partial per (row of x, column) --------------------
   // Thread t < 128 sums 4 adjacent columns over the waves; a partial is one
-  // 16-byte device-scope store.
+  // 16-byte device-scope store.  Rows alternate between two LDS buffers
+  // (the x staging area is free once every wave is past the streaming
+  // loop), so one barrier per row orders its stores before the sums, and
+  // the barrier of row m+1 orders row m's sums before row m+2's stores.
+  static_assert(kXStage >= WAVES * kCols, "second reduction buffer");
   const uint32_t part_bytes = (uint32_t)((size_t)a.splits * a.M * a.d_out * sizeof(float));
 #pragma unroll
   for (int m = 0; m < MB; m++) {
     if (m >= a.M) break;
-    __syncthreads();  // the previous row's sums have been read
+    if (m == 0) __syncthreads();  // every wave is past the streaming loop
+    float* red = (m & 1) ? lds.xs : lds.red;
     if (wave < WAVES && rp == 0) {
-      float4* d = reinterpret_cast<float4*>(lds.red + wave * kCols + lc * 8);
+      float4* d = reinterpret_cast<float4*>(red + wave * kCols + lc * 8);
       d[0] = make_float4(acc[m][0], acc[m][1], acc[m][2], acc[m][3]);
       d[1] = make_float4(acc[m][4], acc[m][5], acc[m][6], acc[m][7]);
     }
@@ -367,7 +372,7 @@ __device__ __forceinline__ void mv_item(const MvArgs& a, int ct, int ks, MvLds<W
       float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
       for (int w = 0; w < WAVES; w++) {
-        const float4 r = *reinterpret_cast<const float4*>(lds.red + w * kCols + 4 * t);
+        const float4 r = *reinterpret_cast<const float4*>(red + w * kCols + 4 * t);
         v.x += r.x;
         v.y += r.y;
         v.z += r.z;
