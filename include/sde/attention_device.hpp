@@ -9,12 +9,23 @@
  *   cuda/include/attention.h:21-29    device_flash_attention_gqa
  *   cuda/include/attention.h:140-150  device_attention_dispatch
  * with the cache passed as the POD sde_kv_view (sde_kv_get_view), whose pool
- * and table layout is the reference's (kv_cache.h:5-18).
+ * and table layout is the reference's (kv_cache.h:5-18).  Both attention
+ * functions also come with the reference's full argument list (the caller's
+ * shared-memory scratch `blk_logits` and the five shared scalars), so a call
+ * site of the reference compiles unchanged once its cache type is
+ * sde_kv_view.
  *
  * The functions in namespace sde are block-cooperative like the reference's:
  * every thread of the calling block calls them with the same arguments
- * (blockDim.x a multiple of 64).  They need no caller scratch.  Building
- * blocks of the streaming attention live in namespace sde::attn.
+ * (blockDim.x a multiple of 64).  Their own staging lives in static LDS (see
+ * each function).  Building blocks of the streaming attention live in
+ * namespace sde::attn.
+ *
+ * Arithmetic: K and V are the cache's fp16 values.  q and the softmax
+ * weights P enter the matrix cores as fp16 hi + lo pairs (x = hi + lo with
+ * hi = fp16(x), lo = fp16(x - hi)), so each product carries ~22 bits of the
+ * fp32 operand, as in the reference's fp32 q.K and P.V (attention.h:61-62,
+ * 103-112); products and sums are fp32.
  */
 #pragma once
 
@@ -28,10 +39,7 @@
 namespace sde {
 namespace attn {
 
-typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
-
-constexpr int kTile = 32;          // tokens per tile
-constexpr int kStreamMaxRows = 4;  // rows (query, q head) per wave
+constexpr int kTile = 32;  // tokens per tile
 constexpr double kLog2e = 1.4426950408889634;
 
 // Where a (layer, context) of the paged cache lives: the pool, that layer's
@@ -45,38 +53,19 @@ struct TileSource {
   int L_max;
 };
 
-__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
-  return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, a),
-                                __builtin_bit_cast(half2_t, b), c, false);
-}
-
-// dot2(a, b, 0) as one VOP3P instruction with an inline-constant addend (the
-// builtin with a 0 addend becomes a register move plus the accumulating
-// VOP2 form).
-__device__ __forceinline__ float dot2_0(uint32_t a, uint32_t b) {
-  float r;
-  asm("v_dot2_f32_f16 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
-  return r;
-}
-
 // Cross-lane moves (gfx950 lane semantics):
-//  * DPP quad_perm [1,0,3,2] / [2,3,0,1] exchange lanes i^1 / i^2, and
-//    row_ror:4 / row_ror:8 rotate each 16-lane row, so four steps reduce
-//    every row of 16 lanes;
-//  * v_permlane16_swap(x, x) returns rows {0,0,2,2} and {1,1,3,3}: one more
-//    step reduces each 32-lane half without mixing the halves;
+//  * DPP quad_perm [1,0,3,2] / [2,3,0,1] exchange lanes i^1 / i^2;
+//  * v_permlane16_swap(x, x) returns rows {0,0,2,2} and {1,1,3,3} of the
+//    four 16-lane rows;
 //  * v_permlane32_swap(a, b) returns [a.lo | b.lo] and [a.hi | b.hi], so
 //    their sum holds a's half-sum in lanes 0-31 and b's in lanes 32-63.
 __device__ __forceinline__ float dpp_f(float x, int ctrl_sel) {
   const int v = __builtin_bit_cast(int, x);
   int r;
-  switch (ctrl_sel) {
-    case 0: r = __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xf, 0xf, true); break;   // i^1
-    case 1: r = __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xf, 0xf, true); break;   // i^2
-    case 2: r = __builtin_amdgcn_update_dpp(0, v, 0x124, 0xf, 0xf, true); break;  // ror 4
-    case 3: r = __builtin_amdgcn_update_dpp(0, v, 0x128, 0xf, 0xf, true); break;  // ror 8
-    default: r = __builtin_amdgcn_update_dpp(0, v, 0x141, 0xf, 0xf, true); break; // i^7 in 8
-  }
+  if (ctrl_sel == 0)
+    r = __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xf, 0xf, true);  // i^1
+  else
+    r = __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xf, 0xf, true);  // i^2
   return __builtin_bit_cast(float, r);
 }
 
@@ -87,8 +76,6 @@ __device__ __forceinline__ float2 row_pair(float x) {
   return make_float2(__builtin_bit_cast(float, (int)p[0]), __builtin_bit_cast(float, (int)p[1]));
 }
 
-
-
 // Sums a (partial over lanes 0-31 and 32-63) and b likewise: lanes 0-31
 // get a's total, lanes 32-63 b's total.
 __device__ __forceinline__ float half_pair_total(float a, float b) {
@@ -96,7 +83,6 @@ __device__ __forceinline__ float half_pair_total(float a, float b) {
                                                   __builtin_bit_cast(int, b), false, false);
   return __builtin_bit_cast(float, (int)p[0]) + __builtin_bit_cast(float, (int)p[1]);
 }
-
 
 typedef const __attribute__((address_space(4))) int32_t* const_table_t;
 
@@ -107,31 +93,17 @@ __device__ __forceinline__ const_table_t const_table(const TileSource& a) {
   return (const_table_t)a.table;
 }
 
-__device__ __forceinline__ uint32_t pack_h2(float x, float y) {
-  const half2_t h = {(_Float16)x, (_Float16)y};
-  return __builtin_bit_cast(uint32_t, h);
-}
-
-// All-reduce over the token slots (lanes with the same chunk c).
-template <int DPH>
-__device__ __forceinline__ float slot_sum(float x) {
-  if constexpr (DPH == 64) x += dpp_f(x, 3);  // slots 2k, 2k+1 share a 16-lane row
-  const float2 p = row_pair(x);
-  x = p.x + p.y;
-  return half_pair_total(x, x);
-}
-
-template <int DPH>
-__device__ __forceinline__ float slot_max(float x) {
-  if constexpr (DPH == 64) x = fmaxf(x, dpp_f(x, 3));
-  const float2 p = row_pair(x);
-  x = fmaxf(p.x, p.y);
-  const auto q = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, x),
-                                                  __builtin_bit_cast(int, x), false, false);
-  return fmaxf(__builtin_bit_cast(float, (int)q[0]), __builtin_bit_cast(float, (int)q[1]));
-}
-
 __device__ __forceinline__ uint4 ld16(const char* p) { return *reinterpret_cast<const uint4*>(p); }
+
+// threadIdx.x through an opaque (volatile) move, taken once per work item:
+// values derived from it (lane roles, LDS and load offsets) are then
+// computed per item instead of being hoisted out of a caller's loop over
+// items and kept live across the partition combine, which would spill.
+__device__ __forceinline__ int item_tid() {
+  int t = threadIdx.x;
+  asm volatile("" : "+v"(t));
+  return t;
+}
 
 // Physical block and in-block slot of the first token of each load group of
 // tile ts (SL tokens per group, SL divides block_size).  Groups at or past
@@ -194,236 +166,6 @@ __device__ __forceinline__ void stream_load(const TileSource& a, const char* hea
   __builtin_amdgcn_sched_barrier(0);
 }
 
-// Marks the point where a tile's registers are first consumed: the empty
-// asm redefines them, so no use of the tile (and hence no wait for its
-// loads) is hoisted above this point into the previous tile's work.  SITE
-// makes the asm text differ per call site, so identical pins at the heads of
-// two branches are not merged and hoisted into their common predecessor.
-template <int NLD, int SITE>
-__device__ __forceinline__ void pin_arrival(const uint4 (&x)[NLD]) {
-  uint4(&y)[NLD] = const_cast<uint4(&)[NLD]>(x);
-#pragma unroll
-  for (int j = 0; j < NLD; j++) {
-    if constexpr (SITE == 0) asm volatile("; tile 0" : "+v"(y[j].x), "+v"(y[j].y), "+v"(y[j].z), "+v"(y[j].w));
-    else if constexpr (SITE == 1) asm volatile("; tile 1" : "+v"(y[j].x), "+v"(y[j].y), "+v"(y[j].z), "+v"(y[j].w));
-    else if constexpr (SITE == 2) asm volatile("; tile 2" : "+v"(y[j].x), "+v"(y[j].y), "+v"(y[j].z), "+v"(y[j].w));
-    else asm volatile("; tile 3" : "+v"(y[j].x), "+v"(y[j].y), "+v"(y[j].z), "+v"(y[j].w));
-  }
-}
-
-// Lane roles of the streaming attention.  Load role: lane = (slot sl, chunk c),
-// c = lane % CH.  After the transposing reduction of the logits a lane owns
-// one (row r, token pair jp) of its slot: the NV = RPW*NLD partial logits of
-// a lane are halved once per butterfly step (the lane keeps the half named
-// by one bit of c and adds its partner's copy of that half), so after
-// log2(NV)-1 steps a lane holds the full logits of tokens 2jp and 2jp+1 of
-// row r, and the softmax does per-lane scalar work.
-template <int DPH, int RPW>
-struct StreamShape {
-  static constexpr int CH = DPH / 8;                  // lanes per token
-  static constexpr int S = CH == 16 ? 4 : 3;          // butterfly steps over CH lanes
-  static constexpr int SL = 64 / CH;                  // slots
-  static constexpr int NLD = kTile / SL;              // loads per tile (K and V each)
-  static constexpr int NV = RPW * NLD;                // partial logits per lane
-  static constexpr int T = (NV == 32 ? 5 : NV == 16 ? 4 : NV == 8 ? 3 : 2) - 1;  // halving steps
-  static constexpr int RB = RPW == 4 ? 2 : 1;         // bits of r
-  static constexpr int SF = CH == 16 ? RB : 1;        // select-free butterfly steps
-  static_assert(T <= S, "more logits than lanes to spread them over");
-  // chunk index of the lane owning (row r, pair jp) (its redundant bits 0)
-  static constexpr int owner(int r, int jp) { return ((r << (T - RB)) | jp) << (S - T); }
-};
-
-// Butterfly step k over the CH lanes of a token: partner lane = c ^ mask,
-// masks {8, 7, 2, 1} (dph 128) or {7, 2, 1} (dph 64) -- row_ror:8,
-// row_half_mirror, quad_perm [2,3,0,1], quad_perm [1,0,3,2]; step k splits on
-// bit S-1-k of c, which the later masks leave unchanged.
-template <int CH>
-__device__ __forceinline__ float bfly(float x, int k) {
-  const int v = __builtin_bit_cast(int, x);
-  int r;
-  switch (CH == 16 ? k : k + 1) {
-    case 0: r = __builtin_amdgcn_update_dpp(0, v, 0x128, 0xf, 0xf, true); break;
-    case 1: r = __builtin_amdgcn_update_dpp(0, v, 0x141, 0xf, 0xf, true); break;
-    case 2: r = __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xf, 0xf, true); break;
-    default: r = __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xf, 0xf, true); break;
-  }
-  return __builtin_bit_cast(float, r);
-}
-
-// Value of lane n of this lane's 16-lane row (DPP row_newbcast:n).
-__device__ __forceinline__ int row_bcast(int v, int n) {
-  switch (n) {
-    case 0: return __builtin_amdgcn_update_dpp(0, v, 0x150, 0xf, 0xf, true);
-    case 1: return __builtin_amdgcn_update_dpp(0, v, 0x151, 0xf, 0xf, true);
-    case 2: return __builtin_amdgcn_update_dpp(0, v, 0x152, 0xf, 0xf, true);
-    case 3: return __builtin_amdgcn_update_dpp(0, v, 0x153, 0xf, 0xf, true);
-    case 4: return __builtin_amdgcn_update_dpp(0, v, 0x154, 0xf, 0xf, true);
-    case 5: return __builtin_amdgcn_update_dpp(0, v, 0x155, 0xf, 0xf, true);
-    case 6: return __builtin_amdgcn_update_dpp(0, v, 0x156, 0xf, 0xf, true);
-    case 7: return __builtin_amdgcn_update_dpp(0, v, 0x157, 0xf, 0xf, true);
-    case 8: return __builtin_amdgcn_update_dpp(0, v, 0x158, 0xf, 0xf, true);
-    case 9: return __builtin_amdgcn_update_dpp(0, v, 0x159, 0xf, 0xf, true);
-    case 10: return __builtin_amdgcn_update_dpp(0, v, 0x15A, 0xf, 0xf, true);
-    case 11: return __builtin_amdgcn_update_dpp(0, v, 0x15B, 0xf, 0xf, true);
-    case 12: return __builtin_amdgcn_update_dpp(0, v, 0x15C, 0xf, 0xf, true);
-    case 13: return __builtin_amdgcn_update_dpp(0, v, 0x15D, 0xf, 0xf, true);
-    case 14: return __builtin_amdgcn_update_dpp(0, v, 0x15E, 0xf, 0xf, true);
-    default: return __builtin_amdgcn_update_dpp(0, v, 0x15F, 0xf, 0xf, true);
-  }
-}
-
-// Value held by the owner of (row r, pair jp) in this lane's slot.  With
-// dph 64 a 16-lane row holds two slots (lane bit 3 = odd slot).
-template <int DPH, int RPW>
-__device__ __forceinline__ uint32_t from_owner(uint32_t x, int r, int jp, bool odd_slot) {
-  using Sh = StreamShape<DPH, RPW>;
-  const int n = Sh::owner(r, jp);
-  const int v = (int)x;
-  if constexpr (DPH == 128) {
-    return (uint32_t)row_bcast(v, n);
-  } else {
-    const int lo = row_bcast(v, n);
-    const int hi = row_bcast(v, n + 8);
-    return (uint32_t)(odd_slot ? hi : lo);
-  }
-}
-
-template <int DPH, int RPW>
-__device__ __forceinline__ float from_owner_f(float x, int r, int jp, bool odd_slot) {
-  return __builtin_bit_cast(
-      float, from_owner<DPH, RPW>(__builtin_bit_cast(uint32_t, x), r, jp, odd_slot));
-}
-
-// Logits of one tile (transposing reduction) and the online-softmax update
-// of the lane's (row, pair): m_run / l_run are the lane's (row, slot) state
-// (l_run a partial sum over the lane's token pairs).  Returns the rescale
-// factor in al_out and the pair's probabilities as fp16x2 in pk_out.
-template <int DPH, int RPW, int SITE>
-__device__ __forceinline__ void stream_qk(int ts, int sl, int c, int min_lim, int my_lim,
-                                          int my_jp, const uint4 (&qr)[RPW],
-                                          const uint4 (&k)[kTile / (512 / DPH)], float& m_run,
-                                          float& l_run, float& al_out, uint32_t& pk_out) {
-  using Sh = StreamShape<DPH, RPW>;
-  constexpr int CH = Sh::CH, S = Sh::S, SL = Sh::SL, NLD = Sh::NLD, NV = Sh::NV, T = Sh::T;
-  pin_arrival<NLD, SITE>(k);
-  float x[NV];
-#pragma unroll
-  for (int r = 0; r < RPW; r++) {
-    const uint4 q4 = qr[r];
-#pragma unroll
-    for (int j = 0; j < NLD; j++) {
-      float t = dot2_0(q4.x, k[j].x);
-      t = dot2(q4.y, k[j].y, t);
-      t = dot2(q4.z, k[j].z, t);
-      t = dot2(q4.w, k[j].w, t);
-      x[r * NLD + j] = t;
-    }
-  }
-  // Transposing butterfly: step kk keeps the half of x whose top index bit
-  // equals bit S-1-kk of c.  The first SF steps split on row bits, and the
-  // lane's q rows arrive permuted by those same lane bits (qr[r] holds row
-  // r ^ flip, see q_row_flip), so the half to keep is always the lower one
-  // there -- no per-element select.
-#pragma unroll
-  for (int kk = 0; kk < T; kk++) {
-    const bool f = (c >> (S - 1 - kk)) & 1;
-    const int h = NV >> (kk + 1);
-#pragma unroll
-    for (int i = 0; i < (NV >> 1); i++) {
-      if (i < h) {
-        if (kk < Sh::SF) {
-          x[i] += bfly<CH>(x[i + h], kk);
-        } else {
-          const float a = x[i], b = x[i + h];
-          const float send = f ? a : b;
-          const float keep = f ? b : a;
-          x[i] = keep + bfly<CH>(send, kk);
-        }
-      }
-    }
-  }
-#pragma unroll
-  for (int kk = T; kk < S; kk++) {
-    x[0] += bfly<CH>(x[0], kk);
-    x[1] += bfly<CH>(x[1], kk);
-  }
-  float s0 = x[0], s1 = x[1];
-  // Causal / length mask: token g is visible to the lane's row iff g <= my_lim.
-  if (ts + kTile - 1 > min_lim) {
-    const int g0 = ts + 2 * my_jp * SL + sl;
-    if (g0 > my_lim) s0 = -INFINITY;
-    if (g0 + SL > my_lim) s1 = -INFINITY;
-  }
-  float tmax = fmaxf(s0, s1);
-#pragma unroll
-  for (int kk = Sh::RB; kk < S; kk++) tmax = fmaxf(tmax, bfly<CH>(tmax, kk));
-  const float m_new = fmaxf(m_run, tmax);
-  // Nothing visible yet: base 0 makes every weight exp2(-inf) = 0.
-  const float base = m_new == -INFINITY ? 0.f : m_new;
-  const float al = __builtin_amdgcn_exp2f(m_run - base);
-  const float p0 = __builtin_amdgcn_exp2f(s0 - base);
-  const float p1 = __builtin_amdgcn_exp2f(s1 - base);
-  l_run = l_run * al + (p0 + p1);
-  m_run = m_new;
-  al_out = al;
-  pk_out = pack_h2(p0, p1);
-  // Finish this tile's logits here, in program order (see pin_arrival).
-  asm volatile("" : "+v"(m_run), "+v"(l_run), "+v"(al_out), "+v"(pk_out));
-}
-
-// P.V of one tile: rescales acc by each row's factor and accumulates the
-// probability pairs (from their owners) against the byte-permuted V pairs.
-template <int DPH, int RPW, int SITE>
-__device__ __forceinline__ void stream_pv(int sl, float al, uint32_t pk,
-                                          const uint4 (&v)[kTile / (512 / DPH)],
-                                          float (&acc)[RPW][8]) {
-  constexpr int NLD = StreamShape<DPH, RPW>::NLD;
-  pin_arrival<NLD, SITE>(v);
-  const bool odd_slot = sl & 1;
-#pragma unroll
-  for (int r = 0; r < RPW; r++) {
-    const float a_r = from_owner_f<DPH, RPW>(al, r, 0, odd_slot);
-#pragma unroll
-    for (int e = 0; e < 8; e++) acc[r][e] *= a_r;
-  }
-#pragma unroll
-  for (int jp = 0; jp < NLD / 2; jp++) {
-    uint32_t pp[RPW];
-#pragma unroll
-    for (int r = 0; r < RPW; r++) pp[r] = from_owner<DPH, RPW>(pk, r, jp, odd_slot);
-    const uint32_t v0[4] = {v[2 * jp].x, v[2 * jp].y, v[2 * jp].z, v[2 * jp].w};
-    const uint32_t v1[4] = {v[2 * jp + 1].x, v[2 * jp + 1].y, v[2 * jp + 1].z, v[2 * jp + 1].w};
-#pragma unroll
-    for (int w = 0; w < 4; w++) {
-      const uint32_t lo = __builtin_amdgcn_perm(v1[w], v0[w], 0x05040100u);
-      const uint32_t hi = __builtin_amdgcn_perm(v1[w], v0[w], 0x07060302u);
-#pragma unroll
-      for (int r = 0; r < RPW; r++) {
-        acc[r][2 * w] = dot2(pp[r], lo, acc[r][2 * w]);
-        acc[r][2 * w + 1] = dot2(pp[r], hi, acc[r][2 * w + 1]);
-      }
-    }
-  }
-  // Finish this tile's P.V here, in program order, so it is not sunk past
-  // the following tiles' work (which would keep its V registers live).
-#pragma unroll
-  for (int r = 0; r < RPW; r++)
-    asm volatile("" : "+v"(acc[r][0]), "+v"(acc[r][1]), "+v"(acc[r][2]), "+v"(acc[r][3]),
-                 "+v"(acc[r][4]), "+v"(acc[r][5]), "+v"(acc[r][6]), "+v"(acc[r][7]));
-}
-
-
-// Streams the tiles first, first+stride, ... (< te) of KV head kvh through
-// this wave: the online softmax of the wave's rows (q_raw: this lane's
-// chunk, features 8c..8c+7, of each row in fp32) accumulates into
-// (m_run, l_run, acc).  Rows r >= nrows and positions past each row's limit
-// (my_lim for the lane's own row, min_lim the smallest over rows) are
-// masked.  Tiles are taken in chunks of CHUNK, unrolled at compile time:
-// K of tile i+1 is issued before tile i's logits and V of tile i+1 before
-// tile i's P.V, so a tile of loads stays in flight while the wave computes,
-// and no in-flight register is carried across a loop edge (the compiler
-// would copy it, which waits for it).  Chunk slots past the wave's last tile
-// re-read that tile (an L2 hit) and are fully masked.
 // Fused RoPE + append (sde_rope_append_attention): the window's k and v
 // rows before RoPE, and the rotate-half RoPE of rope_apply_inplace
 // (model.cu:281-323): pair (j, j + dph/2) of a head rotates by angle
@@ -460,186 +202,6 @@ __device__ __forceinline__ void rope_table(const RopeArgs& rp, int pos_base, int
   __syncthreads();
 }
 
-// The lane's row permutation for stream_qk's select-free butterfly steps:
-// bit (RB-1-kk) of the flip is bit (S-1-kk) of the chunk index c, for the
-// first SF steps.  A step can go select-free only if its partner lanes
-// differ in its own flip bit and agree on the earlier ones: with 16 lanes
-// per token the first two partners are c^8 and the 8-lane mirror (both row
-// bits); with 8 lanes the first partner is the 8-lane mirror, which also
-// flips the second bit, so only the first step qualifies.
-template <int DPH, int RPW>
-__device__ __forceinline__ int q_row_flip(int c) {
-  using Sh = StreamShape<DPH, RPW>;
-  int flip = 0;
-#pragma unroll
-  for (int kk = 0; kk < Sh::SF; kk++) flip |= ((c >> (Sh::S - 1 - kk)) & 1) << (Sh::RB - 1 - kk);
-  return flip;
-}
-
-// qr[r] <- packed row r ^ flip (selects on whole rows, once per packing).
-template <int RPW>
-__device__ __forceinline__ void permute_rows(uint4 (&qr)[RPW], int flip) {
-#pragma unroll
-  for (int bit = RPW / 2; bit >= 1; bit >>= 1) {
-    const bool f = flip & bit;
-    uint4 t[RPW];
-#pragma unroll
-    for (int r = 0; r < RPW; r++) {
-      const uint4 a = qr[r], b = qr[r ^ bit];
-      t[r] = make_uint4(f ? b.x : a.x, f ? b.y : a.y, f ? b.z : a.z, f ? b.w : a.w);
-    }
-#pragma unroll
-    for (int r = 0; r < RPW; r++) qr[r] = t[r];
-  }
-}
-
-template <int DPH, int RPW, int CHUNK>
-__device__ __forceinline__ void wave_attend(const TileSource& src, int kvh, int first, int te,
-                                            int stride, int nrows, int min_lim, int my_lim,
-                                            float qscale, const float2 (&q_raw)[RPW][4],
-                                            float& m_run, float& l_run, float (&acc)[RPW][8],
-                                            bool balance = false) {
-  using Sh = StreamShape<DPH, RPW>;
-  constexpr int CH = Sh::CH, SL = Sh::SL, NLD = Sh::NLD;
-  const int lane = threadIdx.x & 63;
-  const int sl = lane / CH;
-  const int c = lane % CH;
-  const int my_jp = (c >> (Sh::S - Sh::T)) & ((1 << (Sh::T - Sh::RB)) - 1);
-  const const_table_t table = const_table(src);
-  const char* head_base = reinterpret_cast<const char*>(src.pool) + (size_t)kvh * DPH * 2u;
-  const uint32_t lane_off = (uint32_t)sl * 2u * (uint32_t)src.kv_dim + 16u * c;
-  const uint32_t chunk_off = 16u * c;
-  if (first >= te) return;
-  const int last = first + ((te - 1 - first) / stride) * stride;
-  uint4 qr[RPW];
-  for (int c0 = first; c0 < te; c0 += CHUNK * stride) {
-    uint4 kbuf[2][NLD], vbuf[2][NLD];
-    int blk[2][NLD], slot[2][NLD];
-    float al;
-    uint32_t pk;
-    tile_groups<NLD, SL>(src, table, min(c0, last) * kTile, blk[0], slot[0]);
-    stream_load<DPH>(src, head_base, min(c0, last) * kTile, sl, lane_off, chunk_off, false,
-                     blk[0], slot[0], kbuf[0]);
-    stream_load<DPH>(src, head_base, min(c0, last) * kTile, sl, lane_off, chunk_off, true,
-                     blk[0], slot[0], vbuf[0]);
-    if (CHUNK > 1)
-      tile_groups<NLD, SL>(src, table, min(c0 + stride, last) * kTile, blk[1], slot[1]);
-#pragma unroll
-    for (int i = 0; i < CHUNK; i++) {
-      const int t = c0 + i * stride;
-      const int b = i & 1, nb = b ^ 1;
-      const int tn = min(t + stride, last);
-      if (i + 1 < CHUNK)
-        stream_load<DPH>(src, head_base, tn * kTile, sl, lane_off, chunk_off, false, blk[nb],
-                         slot[nb], kbuf[nb]);
-      if (i == 0) {
-        // q is scaled into the exp2 domain and rounded to fp16 pairs once
-        // this chunk's loads are in flight (q was loaded before them, so
-        // this waits for no tile data).
-#pragma unroll
-        for (int r = 0; r < RPW; r++) {
-          const float sc = r < nrows ? qscale : 0.f;
-          qr[r] = make_uint4(pack_h2(q_raw[r][0].x * sc, q_raw[r][0].y * sc),
-                             pack_h2(q_raw[r][1].x * sc, q_raw[r][1].y * sc),
-                             pack_h2(q_raw[r][2].x * sc, q_raw[r][2].y * sc),
-                             pack_h2(q_raw[r][3].x * sc, q_raw[r][3].y * sc));
-        }
-        permute_rows<RPW>(qr, q_row_flip<DPH, RPW>(c));
-      }
-      // A slot past the wave's last tile: every token masked (no-op).
-      const int ts_mask = t <= last ? t * kTile : INT_MAX / 2;
-      // Balanced issue: the first half of every chunk's tiles runs at raised
-      // wave priority, so a wave past its midpoint, or in its epilogue,
-      // yields VALU issue to the other wave of its SIMD that is behind.
-      if (balance) {
-        if (2 * i < CHUNK) __builtin_amdgcn_s_setprio(1);
-        else __builtin_amdgcn_s_setprio(0);
-      }
-      stream_qk<DPH, RPW, 0>(ts_mask, sl, c, min_lim, my_lim, my_jp, qr, kbuf[b], m_run, l_run,
-                             al, pk);
-      if (i + 1 < CHUNK) {
-        stream_load<DPH>(src, head_base, tn * kTile, sl, lane_off, chunk_off, true, blk[nb],
-                         slot[nb], vbuf[nb]);
-        if (i + 2 < CHUNK)
-          tile_groups<NLD, SL>(src, table, min(t + 2 * stride, last) * kTile, blk[b], slot[b]);
-      }
-      stream_pv<DPH, RPW, 0>(sl, al, pk, vbuf[b], acc);
-    }
-  }
-  if (balance) __builtin_amdgcn_s_setprio(0);
-}
-
-// Totals over the four 16-lane rows of four values at once: afterwards lanes
-// of row j hold the total of v[j] (per column).  permlane16_swap exchanges
-// the odd rows of its first operand with the even rows of its second,
-// permlane32_swap the upper half of its first with the lower half of its
-// second, so two row-pair sums and one half-pair sum leave each row with the
-// total of one of the four.
-__device__ __forceinline__ float rows_total4(float v0, float v1, float v2, float v3) {
-  const auto p = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(int, v0),
-                                                  __builtin_bit_cast(int, v1), false, false);
-  const auto q = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(int, v2),
-                                                  __builtin_bit_cast(int, v3), false, false);
-  const float s01 = __builtin_bit_cast(float, (int)p[0]) + __builtin_bit_cast(float, (int)p[1]);
-  const float s23 = __builtin_bit_cast(float, (int)q[0]) + __builtin_bit_cast(float, (int)q[1]);
-  return half_pair_total(s01, s23);
-}
-
-// Where wave_merge_slots leaves the slot totals: 16-lane row j holds row
-// merged_row(j) of the record, features 8c + merged_col(j) + e for
-// e < 2*RPW.
-template <int RPW>
-__device__ __forceinline__ int merged_row(int j) { return RPW == 4 ? j : (j & 1); }
-template <int RPW>
-__device__ __forceinline__ int merged_col(int j) { return RPW == 4 ? 0 : 4 * (j >> 1); }
-
-// Merges the token slots' softmax states of this wave.  Every lane gets
-// m_row / l_row, the max and sum of its own row my_r over all slots, and
-// out[e] (e < 2*RPW), the accumulators rescaled to that max and summed over
-// the slots, spread over the 16-lane rows j = lane/16: row j holds row
-// merged_row(j), features 8c + merged_col(j) + e (c = lane % CH; with
-// dph 64 both halves of a 16-lane row hold the same values).  Four values
-// share each pair of row swaps, so the merge costs a quarter of the
-// cross-lane moves of one all-reduce per value.
-template <int DPH, int RPW>
-__device__ __forceinline__ void wave_merge_slots(float m_run, float l_run,
-                                                 const float (&acc)[RPW][8], float& m_row,
-                                                 float& l_row, float (&out)[2 * RPW]) {
-  using Sh = StreamShape<DPH, RPW>;
-  constexpr int CH = Sh::CH;
-  const int lane = threadIdx.x & 63;
-  const int c = lane % CH;
-  const bool odd_slot = (lane / CH) & 1;
-  // Lanes of one chunk c share the row my_r, so the slot max of m_run is
-  // the row's max and f_own rescales this lane's (row, slot) state to it.
-  m_row = slot_max<DPH>(m_run);
-  const float f_own = m_row == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run - m_row);
-  // l of (row, slot): sum over the row's token-pair owners (redundant lanes
-  // hold copies and contribute 0).
-  const bool redundant = (c & ((1 << (Sh::S - Sh::T)) - 1)) != 0;
-  float lsum = redundant ? 0.f : l_run;
-#pragma unroll
-  for (int kk = Sh::RB; kk < Sh::S; kk++) lsum += bfly<CH>(lsum, kk);
-  l_row = slot_sum<DPH>(lsum * f_own);
-  float x[RPW][8];
-#pragma unroll
-  for (int r = 0; r < RPW; r++) {
-    const float f = from_owner_f<DPH, RPW>(f_own, r, 0, odd_slot);
-#pragma unroll
-    for (int e = 0; e < 8; e++) {
-      x[r][e] = acc[r][e] * f;
-      if constexpr (DPH == 64) x[r][e] += dpp_f(x[r][e], 3);  // slots 2k, 2k+1 of a row
-    }
-  }
-#pragma unroll
-  for (int e = 0; e < 2 * RPW; e++) {
-    if constexpr (RPW == 4)
-      out[e] = rows_total4(x[0][e], x[1][e], x[2][e], x[3][e]);
-    else
-      out[e] = rows_total4(x[0][e], x[1][e], x[0][e + 4], x[1][e + 4]);
-  }
-}
-
 // attention.h:120-126: normalise unless the sum is tiny or not finite.
 __device__ __forceinline__ float finish_scale(float l) {
   return (l > 1e-20f && isfinite(l)) ? 1.f / l : 0.f;
@@ -660,7 +222,7 @@ struct AttnArgs {
   int nkv;
   int G;           // query heads per KV head
   int R;           // rows per KV head = M * G
-  int row_groups;  // ceil(R / rows per wave)
+  int row_groups;  // ceil(R / rows per group)
   int pos_base;    // query m sees positions [0, pos_base+m]
   int n_parts;
   int tiles_per_part;
@@ -670,10 +232,19 @@ struct AttnArgs {
 constexpr int kStreamWaves = 8;      // waves per workgroup of libsde_paged's kernel
 constexpr int kStreamMaxParts = 64;  // partitions per (KV head, row group)
 
-// Device-scope (agent) relaxed atomic accesses for the partition partials:
-// the stores write through to the device coherence point and the loads do
-// not hit stale lines of another XCD's L2, so publishing partials needs no
-// L2 writeback/invalidate fence (those cost microseconds per workgroup).
+// Device-scope (agent) relaxed atomic accesses for the partition partials.
+// Memory-ordering argument (gfx950): an agent-scope relaxed store is a
+// global store with the sc1 cache policy, which writes through the issuing
+// XCD's L2 to the device coherence point (MALL / HBM); an agent-scope
+// relaxed load (sc1) misses in the reader's L2 and reads that point.  The
+// publisher issues its partial stores, waits for them (s_waitcnt vmcnt(0):
+// a store's counter drops once it is acknowledged at the coherence point),
+// then increments the arrival counter with an agent-scope atomic, which
+// itself executes at that point.  The combiner observes the final count
+// from the same atomic, so every publisher's stores were acknowledged
+// before it, and its sc1 loads cannot hit a stale L2 line.  No L2
+// writeback/invalidate fence is needed (those cost microseconds per
+// workgroup here).
 __device__ __forceinline__ void store_dev2(float* p, float x, float y) {
   const uint64_t bits = (uint64_t)__builtin_bit_cast(uint32_t, x) |
                         ((uint64_t)__builtin_bit_cast(uint32_t, y) << 32);
@@ -717,22 +288,22 @@ __device__ __forceinline__ float4 load_dev16(const float* base, uint32_t bytes,
 // P re-read partition P-1, then weigh 0), so they all travel in one round
 // trip: a load under `if (p < P)` would get a wait of its own at the join.
 template <int DPH, int PMAX, int NIT, int WAVES>
-__device__ __forceinline__ void combine_pass(const AttnArgs& a, int kvh, int r0, int nrows,
-                                             int it0) {
+__device__ __forceinline__ void combine_pass(const AttnArgs& a, int tid, int kvh, int r0,
+                                             int nrows, int it0) {
   constexpr int C4 = DPH / 4;
   constexpr int SUB = 4;
   constexpr int NT = 64 * WAVES;
   const int P = a.n_parts;
-  const int lane = threadIdx.x & 63;
-  const int sub = threadIdx.x & (SUB - 1);
-  const int col4 = (threadIdx.x / SUB) % C4;
+  const int lane = tid & 63;
+  const int sub = tid & (SUB - 1);
+  const int col4 = (tid / SUB) % C4;
   const size_t acc_floats = (size_t)a.nkv * a.R * P * DPH;
   const uint32_t acc_bytes = (uint32_t)(acc_floats * 4);
   float4 v[NIT][PMAX];
   float2 mine[NIT];
 #pragma unroll
   for (int it = 0; it < NIT; it++) {
-    const int r = (threadIdx.x + (it0 + it) * NT) / (SUB * C4);  // uniform per wave
+    const int r = (tid + (it0 + it) * NT) / (SUB * C4);  // uniform per wave
     if (r < nrows) {
       const size_t row = (size_t)kvh * a.R + r0 + r;
       const uint32_t acc_off = (uint32_t)((row * P * DPH + 4 * col4) * 4);
@@ -746,7 +317,7 @@ __device__ __forceinline__ void combine_pass(const AttnArgs& a, int kvh, int r0,
   }
 #pragma unroll
   for (int it = 0; it < NIT; it++) {
-    const int r = (threadIdx.x + (it0 + it) * NT) / (SUB * C4);
+    const int r = (tid + (it0 + it) * NT) / (SUB * C4);
     if (r >= nrows) break;
     float2 e[PMAX];
 #pragma unroll
@@ -797,29 +368,31 @@ __device__ __forceinline__ void combine_pass(const AttnArgs& a, int kvh, int r0,
 
 // Passes of up to 32 in-flight partial loads per thread.
 template <int DPH, int RPW, int PMAX, int WAVES>
-__device__ __forceinline__ void combine_rows(const AttnArgs& a, int kvh, int r0, int nrows) {
+__device__ __forceinline__ void combine_rows(const AttnArgs& a, int tid, int kvh, int r0,
+                                             int nrows) {
   constexpr int SLICES = (RPW * DPH + 64 * WAVES - 1) / (64 * WAVES);  // RPW*C4*SUB / threads
   constexpr int CAP = 32 / PMAX;
   constexpr int NIT = SLICES < CAP ? SLICES : CAP;
 #pragma unroll
   for (int it0 = 0; it0 < SLICES; it0 += NIT)
-    combine_pass<DPH, PMAX, NIT, WAVES>(a, kvh, r0, nrows, it0);
+    combine_pass<DPH, PMAX, NIT, WAVES>(a, tid, kvh, r0, nrows, it0);
 }
 
 // Partition combine, run by the last workgroup of a (KV head, row group) to
 // finish (the rows r0 .. r0+nrows-1 of KV head kvh).
 template <int DPH, int RPW, int WAVES>
-__device__ __forceinline__ void stream_combine(const AttnArgs& a, int kvh, int r0, int nrows) {
+__device__ __forceinline__ void stream_combine(const AttnArgs& a, int tid, int kvh, int r0,
+                                               int nrows) {
   static_assert(kStreamMaxParts == 64, "combine buckets");
   static_assert((4 * (DPH / 4)) % 64 == 0, "each wave's lanes serve one row");
-  if ((int)threadIdx.x >= 64 * WAVES) return;  // waves past WAVES idle
+  if (tid >= 64 * WAVES) return;  // waves past WAVES idle
   const int P = a.n_parts;
   if (P <= 16)
-    combine_rows<DPH, RPW, 4, WAVES>(a, kvh, r0, nrows);
+    combine_rows<DPH, RPW, 4, WAVES>(a, tid, kvh, r0, nrows);
   else if (P <= 32)
-    combine_rows<DPH, RPW, 8, WAVES>(a, kvh, r0, nrows);
+    combine_rows<DPH, RPW, 8, WAVES>(a, tid, kvh, r0, nrows);
   else
-    combine_rows<DPH, RPW, 16, WAVES>(a, kvh, r0, nrows);
+    combine_rows<DPH, RPW, 16, WAVES>(a, tid, kvh, r0, nrows);
 }
 
 // The window's rows (positions pos_base .. pos_base+M-1) of KV head kvh:
@@ -862,23 +435,25 @@ __device__ __forceinline__ void rope_append_slice(const AttnArgs& a, const RopeA
 
 // ---- MFMA tile path (v_mfma_f32_16x16x32_f16, up to 16 rows per wave) ----
 //
-// K and V stream in with the same loads as the VALU path (a token's slice
-// read by CH lanes, 16 bytes each) and are staged per wave in LDS, row-major
-// by token with the 16-byte units of row t stored at unit u ^ (t % UNITS),
-// which keeps both the stores and the operand reads below free of bank
+// K and V stream in with coalesced loads (a token's slice read by dph/8
+// lanes, 16 bytes each) and are staged per wave in LDS, row-major by token
+// with the 16-byte units of row t stored at unit u ^ (t % UNITS), which
+// keeps both the stores and the operand reads below free of bank
 // conflicts.  Per tile of 32 tokens:
 //  * logits S^T[token][row] = K . Q^T: A = K read from LDS in the operand
 //    layout (lane l: token l%16 of a 16-token block, features
-//    32ks + 8(l/16) .. +7), B = Q^T (row l%16, the same features).  The C
-//    layout leaves lane l the logits of row l%16 for tokens 4(l/16) + i and
-//    16 + 4(l/16) + i (i < 4), so the online softmax is lane-local per row:
-//    one cross-group max per tile (two lane swaps), sums reduced once.
+//    32ks + 8(l/16) .. +7), B = Q^T (row l%16, the same features), once
+//    with q's hi part and once with its lo part.  The C layout leaves lane
+//    l the logits of row l%16 for tokens 4(l/16) + i and 16 + 4(l/16) + i
+//    (i < 4), so the online softmax is lane-local per row: one cross-group
+//    max per tile (two lane swaps), sums reduced once.
 //  * O^T[feature][row] += V^T . P^T: B = P^T straight from the logits'
-//    registers (k order: tokens 4(l/16)+i, then 16+4(l/16)+i), A = V^T read
-//    with ds_read_b64_tr_b16: in each 16-lane group lane 4b+t receives
-//    element t of the 8-byte pieces addressed by lanes b, b+4, b+8, b+12, so
-//    lane m' addressing token base + m'/4, features 16db + 4(m'%4) gives
-//    lane m feature 16db + m of tokens base..base+3 (the A layout).
+//    registers as fp16 hi and lo parts (k order: tokens 4(l/16)+i, then
+//    16+4(l/16)+i), A = V^T read with ds_read_b64_tr_b16: in each 16-lane
+//    group lane 4b+t receives element t of the 8-byte pieces addressed by
+//    lanes b, b+4, b+8, b+12, so lane m' addressing token base + m'/4,
+//    features 16db + 4(m'%4) gives lane m feature 16db + m of tokens
+//    base..base+3 (the A layout).
 // The output C layout holds features 16db + 4(l/16) + i of row l%16 in lane
 // l, so the rescale by the row's exp2(m_old - m_new) is lane-local too.
 typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
@@ -911,6 +486,24 @@ __device__ __forceinline__ float groups_sum(float x) {
   return p.x + p.y;
 }
 
+// x = hi + lo to ~22 bits: hi = fp16(x), lo = fp16(x - hi) (the difference
+// is exact in fp32).  x is pinned as a rounded fp32 register first: when x
+// is a product, the compiler would otherwise form the hi it subtracts with
+// a fused multiply-convert (v_fma_mixlo_f16: one rounding of the exact
+// product) but the hi it stores with v_mul_f32 + v_cvt_pk_f16_f32 (two
+// roundings), and where the fp32 product lands on an fp16 tie the two
+// differ by one fp16 ulp, which hi + lo would then carry.
+__device__ __forceinline__ void split_h8(const float (&x)[8], h8_t& hi, h8_t& lo) {
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    float v = x[e];
+    asm("" : "+v"(v));
+    const _Float16 h = (_Float16)v;
+    hi[e] = h;
+    lo[e] = (_Float16)(v - (float)h);
+  }
+}
+
 // Byte offset of 16-byte unit u of token row t in a staged tile.
 template <int DPH>
 __device__ __forceinline__ int staged(int t, int u) {
@@ -929,24 +522,26 @@ __device__ __forceinline__ void stage_tile(char* st, int sl, int c,
 }
 
 // Logits of a tile, masking (token position > lim), the online softmax
-// update and the rescale of o; returns P^T as the output product's B.
-// kst: this wave's staged K tile.
+// update and the rescale of o; p receives the tile's probabilities in the
+// C layout (p[4tb + i]: token 16tb + 4(l/16) + i of row l%16).  kst: this
+// wave's staged K tile.
 template <int DPH>
-__device__ __forceinline__ h8_t mfma_logits(int ts, int q, int l16, int lim,
-                                            const h8_t (&qb)[MfmaShape<DPH>::KS],
-                                            const char* kst, float& m_run, float& l_run,
-                                            f4_t (&o)[MfmaShape<DPH>::DB]) {
+__device__ __forceinline__ void mfma_logits(int ts, int lane, int q, int l16, int lim,
+                                            const h8_t* qop, const char* kst, float& m_run,
+                                            float& l_run, f4_t (&o)[MfmaShape<DPH>::DB],
+                                            float (&p)[8]) {
   using Sh = MfmaShape<DPH>;
-  f4_t s[2];
+  f4_t s[2] = {f4_t{0.f, 0.f, 0.f, 0.f}, f4_t{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-  for (int tb = 0; tb < 2; tb++) {
-    s[tb] = f4_t{0.f, 0.f, 0.f, 0.f};
+  for (int ks = 0; ks < Sh::KS; ks++) {
+    const h8_t qh = qop[ks * 64 + lane];
+    const h8_t ql = qop[(Sh::KS + ks) * 64 + lane];
 #pragma unroll
-    for (int ks = 0; ks < Sh::KS; ks++) {
-      const uint4 kx =
-          *reinterpret_cast<const uint4*>(kst + staged<DPH>(16 * tb + l16, 4 * ks + q));
-      s[tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, kx), qb[ks], s[tb],
-                                                     0, 0, 0);
+    for (int tb = 0; tb < 2; tb++) {
+      const h8_t kx = __builtin_bit_cast(
+          h8_t, *reinterpret_cast<const uint4*>(kst + staged<DPH>(16 * tb + l16, 4 * ks + q)));
+      s[tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kx, qh, s[tb], 0, 0, 0);
+      s[tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kx, ql, s[tb], 0, 0, 0);
     }
   }
   float mx = -INFINITY;
@@ -962,7 +557,6 @@ __device__ __forceinline__ h8_t mfma_logits(int ts, int q, int l16, int lim,
   const float m_use = m_new == -INFINITY ? 0.f : m_new;
   const float al = __builtin_amdgcn_exp2f(m_run - m_use);
   m_run = m_new;
-  float p[8];
   float ps = 0.f;
 #pragma unroll
   for (int tb = 0; tb < 2; tb++)
@@ -974,14 +568,13 @@ __device__ __forceinline__ h8_t mfma_logits(int ts, int q, int l16, int lim,
   l_run = l_run * al + ps;
 #pragma unroll
   for (int db = 0; db < Sh::DB; db++) o[db] *= al;
-  return h8_t{(_Float16)p[0], (_Float16)p[1], (_Float16)p[2], (_Float16)p[3],
-              (_Float16)p[4], (_Float16)p[5], (_Float16)p[6], (_Float16)p[7]};
 }
 
-// o += V^T . P^T for a tile; vst: this wave's staged V tile.
+// o += V^T . P^T for a tile (P as hi + lo parts); vst: this wave's staged
+// V tile.
 template <int DPH>
-__device__ __forceinline__ void mfma_pv(int q, int l16, const h8_t pb, const char* vst,
-                                        f4_t (&o)[MfmaShape<DPH>::DB]) {
+__device__ __forceinline__ void mfma_pv(int q, int l16, const h8_t ph, const h8_t pl,
+                                        const char* vst, f4_t (&o)[MfmaShape<DPH>::DB]) {
   using Sh = MfmaShape<DPH>;
   const int t0 = 4 * q + (l16 >> 2);   // token of this lane's piece (first half)
   const int sub = 8 * (l16 & 1);       // byte within the 16-byte unit
@@ -993,8 +586,72 @@ __device__ __forceinline__ void mfma_pv(int q, int l16, const h8_t pb, const cha
     const s4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
         (lds_s4_t*)(vst + staged<DPH>(t0 + 16, 2 * db + u0) + sub));
     const s4_t both[2] = {lo, hi};
-    o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, both), pb, o[db], 0,
-                                                   0, 0);
+    const h8_t a = __builtin_bit_cast(h8_t, both);
+    o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ph, o[db], 0, 0, 0);
+    o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pl, o[db], 0, 0, 0);
+  }
+}
+
+// Bits 15 / 31 set where the low / high fp16 of x has an all-ones exponent
+// (Inf or NaN): adding 1 to the 5-bit exponent field carries into the bit
+// above it only from 31, and the low field's carry stops at bit 15.
+__device__ __forceinline__ uint32_t nonfinite_h2(uint32_t x) {
+  return ((x & 0x7C007C00u) + 0x04000400u) & 0x80008000u;
+}
+
+// Whether any lane holds a non-finite V element in a slot of tile ts that
+// some real row of the wave may not see (position > wmin, the smallest
+// limit over the real rows; this includes slots past L_max, which hold a
+// copy of another token, and the fully masked slots past a wave's last
+// tile).  Those slots have zero weight for such rows, and the matrix
+// product would turn 0 x Inf into NaN there; the reference never reads
+// them (attention.h:98-115).  Wave-uniform.
+template <int DPH>
+__device__ __forceinline__ bool hidden_nonfinite(int ts, int sl, int wmin,
+                                                 const uint4 (&v)[kTile / (512 / DPH)]) {
+  constexpr int SL = 512 / DPH;
+  uint32_t bad = 0;
+#pragma unroll
+  for (int j = 0; j < kTile / SL; j++) {
+    const uint32_t nf = nonfinite_h2(v[j].x) | nonfinite_h2(v[j].y) | nonfinite_h2(v[j].z) |
+                        nonfinite_h2(v[j].w);
+    if (ts + j * SL + sl > wmin) bad |= nf;
+  }
+  return __builtin_amdgcn_ballot_w64(bad != 0) != 0;
+}
+
+// o += P . V for a tile over the tokens each row sees, skipping the rest
+// (the reference's loop, attention.h:98-115): the exact-semantics path of
+// a tile for which hidden_nonfinite holds.  The tile's probabilities go
+// over the wave's staged K tile (dead after the logits; a wave's LDS
+// operations complete in order), then each lane accumulates its row's
+// visible tokens against its features of the staged V rows in fp32.
+template <int DPH>
+__device__ __forceinline__ void masked_pv(int ts, int q, int l16, int lim, const float (&p)[8],
+                                          char* kst, const char* vst,
+                                          f4_t (&o)[MfmaShape<DPH>::DB]) {
+  using Sh = MfmaShape<DPH>;
+  float* pt = reinterpret_cast<float*>(kst);
+#pragma unroll
+  for (int tb = 0; tb < 2; tb++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) pt[l16 * kTile + 16 * tb + 4 * q + i] = p[4 * tb + i];
+#pragma unroll 1
+  for (int t = 0; t < kTile; t++) {
+    const float w = pt[l16 * kTile + t];
+    const bool vis = ts + t <= lim;
+#pragma unroll
+    for (int db = 0; db < Sh::DB; db++) {
+      // features 16db + 4q .. +3: unit 2db + q/2, byte 8(q%2) of it
+      const uint2 v =
+          *reinterpret_cast<const uint2*>(vst + staged<DPH>(t, 2 * db + (q >> 1)) + 8 * (q & 1));
+      const float x[4] = {(float)__builtin_bit_cast(_Float16, (uint16_t)(v.x & 0xffffu)),
+                          (float)__builtin_bit_cast(_Float16, (uint16_t)(v.x >> 16)),
+                          (float)__builtin_bit_cast(_Float16, (uint16_t)(v.y & 0xffffu)),
+                          (float)__builtin_bit_cast(_Float16, (uint16_t)(v.y >> 16))};
+#pragma unroll
+      for (int i = 0; i < 4; i++) o[db][i] = vis ? fmaf(w, x[i], o[db][i]) : o[db][i];
+    }
   }
 }
 
@@ -1002,11 +659,16 @@ __device__ __forceinline__ void mfma_pv(int q, int l16, const h8_t pb, const cha
 // raw fp32 values: rotated by RoPE when cs (the row's (cos, sin) table
 // entries, feature-pair-indexed) is given -- the partner of feature f is
 // f +- dph/2, k-step ks +- KS/2 of the same lane -- then scaled into the
-// exp2 domain and rounded to fp16.
+// exp2 domain and split into fp16 hi and lo parts, stored to the
+// workgroup's q operand area: hi of k-step ks at qop[ks*64 + lane], lo at
+// qop[(KS + ks)*64 + lane].  Every wave of a workgroup serves the same rows
+// and stores the same bytes, so a wave reads back what it wrote (a wave's
+// LDS operations complete in order) whatever the other waves do: no
+// barrier.
 template <int DPH>
 __device__ __forceinline__ void mfma_pack_q(const float2 (&qr)[MfmaShape<DPH>::KS][4], float sc,
-                                            const float2* cs, int grp,
-                                            h8_t (&qb)[MfmaShape<DPH>::KS]) {
+                                            const float2* cs, int lane, h8_t* qop) {
+  const int grp = lane >> 4;
   constexpr int KS = MfmaShape<DPH>::KS;
   float x[KS][8];
 #pragma unroll
@@ -1028,9 +690,14 @@ __device__ __forceinline__ void mfma_pack_q(const float2 (&qr)[MfmaShape<DPH>::K
       }
   }
 #pragma unroll
-  for (int ks = 0; ks < KS; ks++)
+  for (int ks = 0; ks < KS; ks++) {
 #pragma unroll
-    for (int e = 0; e < 8; e++) qb[ks][e] = (_Float16)(x[ks][e] * sc);
+    for (int e = 0; e < 8; e++) x[ks][e] *= sc;
+    h8_t hi, lo;
+    split_h8(x[ks], hi, lo);
+    qop[ks * 64 + lane] = hi;
+    qop[(KS + ks) * 64 + lane] = lo;
+  }
 }
 
 // Per-wave constants of the MFMA tile loop.
@@ -1038,20 +705,27 @@ struct MfmaWave {
   const char* head_base;  // this KV head's slice in the pool
   const_table_t table;
   uint32_t lane_off, chunk_off;
+  int lane;
   int sl, c, l16, q;      // load role (slot, chunk) and operand role (row, group)
   int last, stride, lim;
+  int wmin;               // smallest lim over the wave's real rows
   char* kst;              // staged K tile; the V tile follows
+  h8_t* qop;              // the workgroup's packed q operand (mfma_pack_q)
 };
 
-// One chunk of a wave's tiles, starting at tile c0, pipelined a tile ahead
-// like wave_attend.  FIRST: the wave's first chunk, which packs q once its
-// first loads are in flight (q was loaded before them, so this waits for no
-// tile data); the raw q registers are dead after it.
+// One chunk of a wave's tiles, starting at tile c0, pipelined a tile ahead:
+// K of tile i+1 is issued before tile i's logits and V of tile i+1 before
+// tile i's output product, so a tile of loads stays in flight while the
+// wave computes, and no in-flight register is carried across a loop edge
+// (the compiler would copy it, which waits for it).  Chunk slots past the
+// wave's last tile re-read that tile (an L2 hit) and are fully masked.
+// FIRST: the wave's first chunk, which packs q once its first loads are in
+// flight (q was loaded before them, so this waits for no tile data); the
+// raw q registers are dead after it.
 template <int DPH, int CHUNK, bool FIRST>
 __device__ __forceinline__ void mfma_chunk(const TileSource& src, const MfmaWave& w, int c0,
                                            const float2 (&qr)[MfmaShape<DPH>::KS][4], float qsc,
-                                           const float2* cs, h8_t (&qb)[MfmaShape<DPH>::KS],
-                                           float& m_run, float& l_run,
+                                           const float2* cs, float& m_run, float& l_run,
                                            f4_t (&o)[MfmaShape<DPH>::DB], bool balance) {
   constexpr int SL = 512 / DPH, NLD = kTile / SL;
   char* vst = w.kst + MfmaShape<DPH>::TILEB;
@@ -1072,7 +746,7 @@ __device__ __forceinline__ void mfma_chunk(const TileSource& src, const MfmaWave
     if (i + 1 < CHUNK)
       stream_load<DPH>(src, w.head_base, tn * kTile, w.sl, w.lane_off, w.chunk_off, false,
                        blk[nb], slot[nb], kbuf[nb]);
-    if (FIRST && i == 0) mfma_pack_q<DPH>(qr, qsc, cs, w.q, qb);
+    if (FIRST && i == 0) mfma_pack_q<DPH>(qr, qsc, cs, w.lane, w.qop);
     if (balance) {
       if (2 * i < CHUNK) __builtin_amdgcn_s_setprio(1);
       else __builtin_amdgcn_s_setprio(0);
@@ -1080,7 +754,8 @@ __device__ __forceinline__ void mfma_chunk(const TileSource& src, const MfmaWave
     // A slot past the wave's last tile: every token masked (no-op).
     const int ts_mask = t <= w.last ? t * kTile : INT_MAX / 2;
     stage_tile<DPH>(w.kst, w.sl, w.c, kbuf[b]);
-    const h8_t pb = mfma_logits<DPH>(ts_mask, w.q, w.l16, w.lim, qb, w.kst, m_run, l_run, o);
+    float p[8];
+    mfma_logits<DPH>(ts_mask, w.lane, w.q, w.l16, w.lim, w.qop, w.kst, m_run, l_run, o, p);
     if (i + 1 < CHUNK) {
       stream_load<DPH>(src, w.head_base, tn * kTile, w.sl, w.lane_off, w.chunk_off, true,
                        blk[nb], slot[nb], vbuf[nb]);
@@ -1088,26 +763,37 @@ __device__ __forceinline__ void mfma_chunk(const TileSource& src, const MfmaWave
         tile_groups<NLD, SL>(src, w.table, min(t + 2 * w.stride, w.last) * kTile, blk[b],
                              slot[b]);
     }
+    // Tiles reaching a position some real row cannot see get the non-finite
+    // check (wave-uniform condition: the window's tail and the context end).
+    const bool exact = ts_mask + kTile - 1 > w.wmin &&
+                       hidden_nonfinite<DPH>(ts_mask, w.sl, w.wmin, vbuf[b]);
     stage_tile<DPH>(vst, w.sl, w.c, vbuf[b]);
-    mfma_pv<DPH>(w.q, w.l16, pb, vst, o);
+    if (exact) {
+      masked_pv<DPH>(ts_mask, w.q, w.l16, w.lim, p, w.kst, vst, o);
+    } else {
+      h8_t ph, pl;
+      split_h8(p, ph, pl);
+      mfma_pv<DPH>(w.q, w.l16, ph, pl, vst, o);
+    }
   }
 }
 
 // A wave's tiles first, first+stride, ... < te of KV head kvh on the MFMA
 // path.  lim: last visible position of this lane's row (-1: a padding
-// row).  qr, qsc, cs: the lane's raw q values, their scale and RoPE table
-// (mfma_pack_q).  st: this wave's LDS (K tile, then V tile).
+// row); wmin: the smallest lim over the wave's real rows.  qr, qsc, cs: the
+// lane's raw q values, their scale and RoPE table (mfma_pack_q); qop: the
+// workgroup's q operand area.  st: this wave's LDS (K tile, then V tile).
 template <int DPH, int CHUNK>
-__device__ __forceinline__ void mfma_attend(const TileSource& src, int kvh, int first, int te,
-                                            int stride, int lim,
+__device__ __forceinline__ void mfma_attend(const TileSource& src, int lane, int kvh, int first,
+                                            int te, int stride, int lim, int wmin,
                                             const float2 (&qr)[MfmaShape<DPH>::KS][4], float qsc,
-                                            const float2* cs, char* st, float& m_run,
+                                            const float2* cs, char* st, h8_t* qop, float& m_run,
                                             float& l_run, f4_t (&o)[MfmaShape<DPH>::DB],
                                             bool balance) {
   constexpr int CH = DPH / 8;
   if (first >= te) return;
-  const int lane = threadIdx.x & 63;
   MfmaWave w;
+  w.lane = lane;
   w.sl = lane / CH;
   w.c = lane % CH;
   w.l16 = lane & 15;
@@ -1119,32 +805,25 @@ __device__ __forceinline__ void mfma_attend(const TileSource& src, int kvh, int 
   w.last = first + ((te - 1 - first) / stride) * stride;
   w.stride = stride;
   w.lim = lim;
+  w.wmin = wmin;
   w.kst = st;
-  h8_t qb[MfmaShape<DPH>::KS];
-  mfma_chunk<DPH, CHUNK, true>(src, w, first, qr, qsc, cs, qb, m_run, l_run, o, balance);
+  w.qop = qop;
+  mfma_chunk<DPH, CHUNK, true>(src, w, first, qr, qsc, cs, m_run, l_run, o, balance);
   for (int c0 = first + CHUNK * stride; c0 < te; c0 += CHUNK * stride)
-    mfma_chunk<DPH, CHUNK, false>(src, w, c0, qr, qsc, cs, qb, m_run, l_run, o, balance);
+    mfma_chunk<DPH, CHUNK, false>(src, w, c0, qr, qsc, cs, m_run, l_run, o, balance);
   if (balance) __builtin_amdgcn_s_setprio(0);
 }
 
-// LDS of stream_item: per-wave records of every row, acc[DPH] and
-// (max, sum).
-template <int DPH, int RPW, int WAVES>
-struct StreamLds {
-  float acc[WAVES * RPW * DPH] __attribute__((aligned(16)));
-  float2 ml[WAVES * RPW];
-  int last;
-  __device__ float* acc_at(int w, int r) { return acc + (w * RPW + r) * DPH; }
-  __device__ float2& ml_at(int w, int r) { return ml[w * RPW + r]; }
-};
-
 // LDS of the MFMA tile path: per wave, its staged K and V tiles; once the
 // wave's tiles are done the same bytes hold its records (up to 16 rows).
+// Then the workgroup's packed q operand (hi and lo parts, 16 rows).
 template <int DPH, int WAVES>
 struct MfmaLds {
   static constexpr int kRows = 16;
   static_assert(kRows * (DPH + 2) * 4 <= MfmaShape<DPH>::WAVEB, "records fit the staging area");
+  static_assert(kRows * kTile * 4 <= MfmaShape<DPH>::TILEB, "probabilities fit a K tile");
   char st[WAVES * MfmaShape<DPH>::WAVEB] __attribute__((aligned(16)));
+  h8_t qop[2 * MfmaShape<DPH>::KS * 64];
   int last;
   __device__ char* staging(int w) { return st + w * MfmaShape<DPH>::WAVEB; }
   __device__ float* acc_at(int w, int r) {
@@ -1156,24 +835,23 @@ struct MfmaLds {
 };
 
 // Partition `part` of (KV head kvh, row group rg) on the calling workgroup:
-// waves 0..WAVES-1 take tiles tb+w, tb+w+WAVES, ... (further waves idle),
-// merge their states through LDS, and either write the normalised output
-// (one partition) or publish a partial and count the arrival; the last
-// arrival combines all partitions.  Every thread of the workgroup calls it.
-template <int DPH, int RPW, int CHUNK, int WAVES, bool ROPE = false, bool MF = false,
-          class Lds>
+// waves 0..nwaves-1 (nwaves <= WAVES) take tiles tb+w, tb+w+nwaves, ...
+// (further waves idle), merge their states through LDS, and either write
+// the normalised output (one partition) or publish a partial and count the
+// arrival; the last arrival combines all partitions (with WAVES waves).
+// Every thread of the workgroup calls it.
+template <int DPH, int RPW, int CHUNK, int WAVES, bool ROPE = false, class Lds>
 __device__ __forceinline__ void stream_item(const AttnArgs& a, int part, int kvh, int rg,
-                                            Lds& lds, const RopeArgs* rp = nullptr,
+                                            Lds& lds, int nwaves = WAVES,
+                                            const RopeArgs* rp = nullptr,
                                             float2* rope_cs = nullptr) {
   static_assert(DPH == 64 || DPH == 128, "head_dim");
-  static_assert(RPW == 2 || RPW == 4 || (MF && (RPW == 8 || RPW == 16)), "rows per wave");
-  static_assert(MF || !ROPE, "fused RoPE runs on the MFMA tile path");
-  constexpr int CH = DPH / 8;
+  static_assert(RPW == 2 || RPW == 4 || RPW == 8 || RPW == 16, "rows per group");
+  using Mh = MfmaShape<DPH>;
 
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  const int sl = lane / CH;
-  const int c = lane % CH;
+  const int tid = item_tid();
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
   const int r0 = rg * RPW;
   const int nrows = min(RPW, a.R - r0);
   const int n_tiles = (a.src.L_max + kTile - 1) / kTile;
@@ -1189,106 +867,56 @@ __device__ __forceinline__ void stream_item(const AttnArgs& a, int part, int kvh
     if (te * kTile > a.pos_base) rope_append_slice<DPH>(a, *rp, rope_cs, kvh);
   }
 
-  if constexpr (MF) {
-    if (wave < WAVES) {
-      // MFMA tile path: lane l serves row r0 + l%16 (rows past nrows are
-      // padding: zero q, nothing visible).
-      using Mh = MfmaShape<DPH>;
-      const int l16 = lane & 15, grp = lane >> 4;
-      const bool real = l16 < nrows;
-      const int gr = min(r0 + l16, a.R - 1);
-      const int m = gr / a.G;
-      const int h = kvh * a.G + (gr - m * a.G);
-      const float2* qp = reinterpret_cast<const float2*>(a.q + (size_t)m * a.nh * DPH +
-                                                         (size_t)h * DPH + 8 * grp);
-      float2 qr[Mh::KS][4];
+  if (wave < nwaves) {
+    // Lane l serves row r0 + l%16 (rows past nrows are padding: zero q,
+    // nothing visible).
+    const int l16 = lane & 15, grp = lane >> 4;
+    const bool real = l16 < nrows;
+    const int gr = min(r0 + l16, a.R - 1);
+    const int m = gr / a.G;
+    const int h = kvh * a.G + (gr - m * a.G);
+    const float2* qp = reinterpret_cast<const float2*>(a.q + (size_t)m * a.nh * DPH +
+                                                       (size_t)h * DPH + 8 * grp);
+    float2 qr[Mh::KS][4];
 #pragma unroll
-      for (int ks = 0; ks < Mh::KS; ks++)
+    for (int ks = 0; ks < Mh::KS; ks++)
 #pragma unroll
-        for (int w = 0; w < 4; w++) qr[ks][w] = qp[16 * ks + w];
-      const float2* cs = nullptr;
-      if constexpr (ROPE) cs = rope_cs + m * (DPH / 2);
-      const int lim = real ? a.pos_base + (r0 + l16) / a.G : -1;
-      float m_run = -INFINITY, l_run = 0.f;
-      f4_t o[Mh::DB];
+      for (int w = 0; w < 4; w++) qr[ks][w] = qp[16 * ks + w];
+    const float2* cs = nullptr;
+    if constexpr (ROPE) cs = rope_cs + m * (DPH / 2);
+    const int lim = real ? a.pos_base + (r0 + l16) / a.G : -1;
+    const int wmin = a.pos_base + r0 / a.G;  // row r0 is the group's first query
+    float m_run = -INFINITY, l_run = 0.f;
+    f4_t o[Mh::DB];
 #pragma unroll
-      for (int db = 0; db < Mh::DB; db++) o[db] = f4_t{0.f, 0.f, 0.f, 0.f};
-      mfma_attend<DPH, CHUNK>(a.src, kvh, tb + wave, te, WAVES, lim, qr,
-                              real ? a.qscale : 0.f, cs, lds.staging(wave), m_run, l_run, o,
-                              a.row_groups > 1);
-      const float l_row = groups_sum(l_run);
-      // The staged tiles are dead: records go over them (DS operations of a
-      // wave complete in order).
-      if (real) {
+    for (int db = 0; db < Mh::DB; db++) o[db] = f4_t{0.f, 0.f, 0.f, 0.f};
+    // Several row groups per KV head: the first half of every chunk's tiles
+    // runs at raised wave priority, so a wave past its midpoint yields issue
+    // to the other wave of its SIMD that is behind.
+    mfma_attend<DPH, CHUNK>(a.src, lane, kvh, tb + wave, te, nwaves, lim, wmin, qr,
+                            real ? a.qscale : 0.f, cs, lds.staging(wave), lds.qop, m_run, l_run,
+                            o, a.row_groups > 1);
+    const float l_row = groups_sum(l_run);
+    // The staged tiles are dead: records go over them (DS operations of a
+    // wave complete in order).
+    if (real) {
 #pragma unroll
-        for (int db = 0; db < Mh::DB; db++)
-          *reinterpret_cast<f4_t*>(lds.acc_at(wave, l16) + 16 * db + 4 * grp) = o[db];
-        if (grp == 0) lds.ml_at(wave, l16) = make_float2(m_run, l_row);
-      }
-    }
-  } else if (wave < WAVES) {
-    using Sh = StreamShape<DPH, RPW>;
-    const int my_r = (c >> (Sh::S - Sh::T)) >> (Sh::T - Sh::RB);
-    // This lane's q chunk (features 8c..8c+7) of every row, loaded before
-    // any K/V load so that waiting for it never waits for tile data.
-    float2 q_raw[RPW][4];
-#pragma unroll
-    for (int r = 0; r < RPW; r++) {
-      const int gr = min(r0 + r, a.R - 1);  // rows past nrows: zeroed by wave_attend
-      const int m = gr / a.G;
-      const int h = kvh * a.G + (gr - m * a.G);
-      const float2* qp = reinterpret_cast<const float2*>(a.q + (size_t)m * a.nh * DPH +
-                                                         (size_t)h * DPH + 8 * c);
-#pragma unroll
-      for (int w = 0; w < 4; w++) q_raw[r][w] = qp[w];
-    }
-    // Last visible position of each row (query m sees pos_base + m); rows
-    // past nrows see nothing.
-    int min_lim = INT_MAX, my_lim = -1;
-#pragma unroll
-    for (int r = 0; r < RPW; r++) {
-      const int lim = r < nrows ? a.pos_base + (r0 + r) / a.G : -1;
-      min_lim = min(min_lim, lim);
-      if (r == my_r) my_lim = lim;
-    }
-
-    float m_run = -INFINITY, l_run = 0.f, acc[RPW][8];
-#pragma unroll
-    for (int r = 0; r < RPW; r++)
-#pragma unroll
-      for (int e = 0; e < 8; e++) acc[r][e] = 0.f;
-    // Several row groups per KV head make the step VALU-bound per SIMD
-    // (each K/V byte serves several workgroups from L2): balance the waves
-    // of a SIMD (4K 5-query window 14.9 -> 14.5 us; a long one-group decode
-    // is HBM-bound and measured 0.3 us slower with it).
-    wave_attend<DPH, RPW, CHUNK>(a.src, kvh, tb + wave, te, WAVES, nrows, min_lim, my_lim,
-                                 a.qscale, q_raw, m_run, l_run, acc, a.row_groups > 1);
-
-    // ---- merge the slot states of this wave; record per row -------------
-    float m_row, l_row, o[2 * RPW];
-    wave_merge_slots<DPH, RPW>(m_run, l_run, acc, m_row, l_row, o);
-    if (sl == 0 && c == Sh::owner(my_r, 0)) lds.ml_at(wave, my_r) = make_float2(m_row, l_row);
-    const int j = lane >> 4;
-    if (DPH == 128 || (lane & 8) == 0) {
-      float4* dst = reinterpret_cast<float4*>(lds.acc_at(wave, merged_row<RPW>(j)) +
-                                              8 * c + merged_col<RPW>(j));
-      dst[0] = make_float4(o[0], o[1], o[2], o[3]);
-      if constexpr (RPW == 4) dst[1] = make_float4(o[4], o[5], o[6], o[7]);
+      for (int db = 0; db < Mh::DB; db++)
+        *reinterpret_cast<f4_t*>(lds.acc_at(wave, l16) + 16 * db + 4 * grp) = o[db];
+      if (grp == 0) lds.ml_at(wave, l16) = make_float2(m_run, l_row);
     }
   }
   __syncthreads();
 
   // ---- workgroup merge: thread (row, feature pair) over the waves --------
   constexpr int DP = DPH / 2;
-  for (int idx = threadIdx.x; idx < nrows * DP; idx += blockDim.x) {
+  for (int idx = tid; idx < nrows * DP; idx += blockDim.x) {
     const int r = idx / DP;
     const int dcol = 2 * (idx - r * DP);
     float mx = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < WAVES; w++) mx = fmaxf(mx, lds.ml_at(w, r).x);
+    for (int w = 0; w < nwaves; w++) mx = fmaxf(mx, lds.ml_at(w, r).x);
     float l = 0.f, o0 = 0.f, o1 = 0.f;
-#pragma unroll
-    for (int w = 0; w < WAVES; w++) {
+    for (int w = 0; w < nwaves; w++) {
       const float2 ml = lds.ml_at(w, r);
       const float wt = ml.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ml.x - mx);
       l += ml.y * wt;
@@ -1314,10 +942,10 @@ __device__ __forceinline__ void stream_item(const AttnArgs& a, int part, int kvh
 
   // ---- the last workgroup of (KV head, row group) combines --------------
   // Partials are device-scope stores; waiting for them (vmcnt) before the
-  // arrival increment orders them before it.
+  // arrival increment orders them before it (see store_dev2).
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (threadIdx.x == 0) {
+  if (tid == 0) {
     uint32_t* ctr = a.counters + (size_t)kvh * a.row_groups + rg;
     const uint32_t prev =
         __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1327,7 +955,7 @@ __device__ __forceinline__ void stream_item(const AttnArgs& a, int part, int kvh
   }
   __syncthreads();
   if (!lds.last) return;
-  stream_combine<DPH, RPW, WAVES>(a, kvh, r0, nrows);
+  stream_combine<DPH, RPW, WAVES>(a, tid, kvh, r0, nrows);
 }
 
 // Partition sizing shared by libsde_paged and the grid API: at most
@@ -1339,8 +967,7 @@ __device__ __forceinline__ void stream_item(const AttnArgs& a, int part, int kvh
 // more than max_chunk tiles.  (Cutting the context evenly instead, with
 // masked slots for the waves past a partition's last tile, measured slower
 // on short contexts: the masked slots are not free.)  Rows per group:
-// `rows`, or (0) 2 for windows of at most 2 rows and kStreamMaxRows
-// otherwise.
+// `rows` (2, 4, 8 or 16).
 struct StreamPlan {
   int rpw;             // rows per group
   int row_groups;
@@ -1350,9 +977,9 @@ struct StreamPlan {
 };
 
 __host__ __device__ inline StreamPlan stream_plan(int L_max, int nkv, int R, int blocks,
-                                                  int waves, int max_chunk, int rows = 0) {
+                                                  int waves, int max_chunk, int rows) {
   StreamPlan p;
-  p.rpw = rows > 0 ? rows : R <= 2 ? 2 : kStreamMaxRows;
+  p.rpw = rows;
   p.row_groups = (R + p.rpw - 1) / p.rpw;
   const int n_tiles = (L_max + kTile - 1) / kTile;
   const int64_t units = (int64_t)nkv * p.row_groups;
@@ -1369,65 +996,59 @@ __host__ __device__ inline StreamPlan stream_plan(int L_max, int nkv, int R, int
   return p;
 }
 
-// One query, all heads, all of [0, total_len) on one block (no split):
-// wave w takes the (KV head, group of up to four q heads) units w, w+nw, ...
-template <int DPH>
-__device__ __forceinline__ void block_attend(const float* q_all, float* out, const sde_kv_view& kv,
-                                             int layer, int nh, int nkv, int total_len) {
-  constexpr int RPW = kStreamMaxRows;
-  constexpr int CH = DPH / 8;
-  const int G = nh / nkv;
-  const int groups = (G + RPW - 1) / RPW;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int nw = blockDim.x >> 6;
-  const int lane = threadIdx.x & 63;
-  const int c = lane % CH;
-  const TileSource src{kv.pool, kv.block_tables + (size_t)layer * kv.max_blocks_per_layer,
-                       kv.kv_dim, kv.block_size, total_len};
-  const int n_tiles = (total_len + kTile - 1) / kTile;
-  const float qscale = (float)(kLog2e / __builtin_sqrt((double)DPH));
-  using Sh = StreamShape<DPH, RPW>;
-  const int my_r = (c >> (Sh::S - Sh::T)) >> (Sh::T - Sh::RB);
-  for (int u = wave; u < nkv * groups; u += nw) {
-    const int kvh = u / groups;
-    const int h0 = kvh * G + (u - kvh * groups) * RPW;
-    const int nrows = min(RPW, kvh * G + G - h0);
-    float2 q_raw[RPW][4];
-#pragma unroll
-    for (int r = 0; r < RPW; r++) {
-      const float2* qp = reinterpret_cast<const float2*>(q_all + (size_t)min(h0 + r, nh - 1) * DPH +
-                                                         8 * c);
-#pragma unroll
-      for (int w = 0; w < 4; w++) q_raw[r][w] = qp[w];
-    }
-    const int min_lim = nrows < RPW ? -1 : total_len - 1;
-    const int my_lim = my_r < nrows ? total_len - 1 : -1;
-    float m_run = -INFINITY, l_run = 0.f, acc[RPW][8];
-#pragma unroll
-    for (int r = 0; r < RPW; r++)
-#pragma unroll
-      for (int e = 0; e < 8; e++) acc[r][e] = 0.f;
-    wave_attend<DPH, RPW, 2>(src, kvh, 0, n_tiles, 1, nrows, min_lim, my_lim, qscale, q_raw,
-                             m_run, l_run, acc);
-    float m_row, l_row, o[2 * RPW];
-    wave_merge_slots<DPH, RPW>(m_run, l_run, acc, m_row, l_row, o);
-    // 16-lane row j holds row rr of the output; its sum sits in the lanes
-    // of chunk owner(rr, 0).
-    const int j = lane >> 4;
-    const int rr = merged_row<RPW>(j);
-    float l_mine = 0.f;
-#pragma unroll
-    for (int r = 0; r < RPW; r++) {
-      const float lr = from_owner_f<DPH, RPW>(l_row, r, 0, false);
-      if (r == rr) l_mine = lr;
-    }
-    if (rr < nrows && (DPH == 128 || (lane & 8) == 0)) {
-      const float inv = finish_scale(l_mine);
-      float4* dst = reinterpret_cast<float4*>(out + (size_t)(h0 + rr) * DPH + 8 * c +
-                                              merged_col<RPW>(j));
-      dst[0] = make_float4(o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv);
-      if constexpr (RPW == 4) dst[1] = make_float4(o[4] * inv, o[5] * inv, o[6] * inv, o[7] * inv);
-    }
+// Rows per group of the device functions: 4 (decode of up to 4 q heads per
+// KV head) or 16 (everything larger) -- the MFMA computes 16 rows either
+// way; fewer rows per group give a KV head more workgroups.
+__host__ __device__ inline int device_rows(int R) { return R <= 4 ? 4 : 16; }
+
+// Static LDS shared by the device functions of one kernel (a function-scope
+// __shared__ array is one allocation per kernel, whichever caller uses
+// it): MaxWaves waves' staging at head_dim 128.
+template <int MaxWaves>
+__device__ __forceinline__ char* device_lds() {
+  __shared__ __attribute__((aligned(16))) char buf[sizeof(MfmaLds<128, MaxWaves>)];
+  return buf;
+}
+
+// The units (KV head, row group) of a call on the calling block alone, the
+// whole context per unit (one partition: the output is written directly),
+// its tiles spread over `nwaves` waves and merged through LDS.
+template <int DPH, int RPW, int MaxWaves>
+__device__ __forceinline__ void block_units(const AttnArgs& a, int nwaves) {
+  auto& lds = *reinterpret_cast<MfmaLds<DPH, MaxWaves>*>(device_lds<MaxWaves>());
+  for (int u = 0; u < a.nkv * a.row_groups; u++) {
+    __syncthreads();  // the previous unit's readers of lds are done
+    stream_item<DPH, RPW, 2, MaxWaves>(a, 0, u % a.nkv, u / a.nkv, lds, nwaves);
+  }
+}
+
+template <int DPH, int RPW, int WAVES, int MaxWaves>
+__device__ __forceinline__ void grid_items(const AttnArgs& a) {
+  auto& lds = *reinterpret_cast<MfmaLds<DPH, MaxWaves>*>(device_lds<MaxWaves>());
+  const int n_blocks = gridDim.x * gridDim.y * gridDim.z;
+  const int block = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+  const int items = a.nkv * a.row_groups * a.n_parts;
+  for (int it = block; it < items; it += n_blocks) {
+    const int part = it % a.n_parts;
+    const int unit = it / a.n_parts;
+    __syncthreads();  // the previous item's readers of lds are done
+    stream_item<DPH, RPW, 2, WAVES>(a, part, unit % a.nkv, unit / a.nkv, lds);
+  }
+}
+
+template <int WAVES, int MaxWaves>
+__device__ __forceinline__ void grid_dispatch(const AttnArgs& a, int dph, int rpw) {
+  static_assert(WAVES <= MaxWaves, "staging for every wave");
+  if (dph == 128) {
+    if (rpw == 4)
+      grid_items<128, 4, WAVES, MaxWaves>(a);
+    else
+      grid_items<128, 16, WAVES, MaxWaves>(a);
+  } else {
+    if (rpw == 4)
+      grid_items<64, 4, WAVES, MaxWaves>(a);
+    else
+      grid_items<64, 16, WAVES, MaxWaves>(a);
   }
 }
 
@@ -1481,68 +1102,130 @@ __device__ inline void kv_cache_rollback(const sde_kv_view& kv, int target_len) 
 }
 
 // attention.h:21-127: attention of one query (q_all fp32 [nh*dph], RoPE
-// applied) over positions [0, total_len) of `layer`: q head h reads KV head
-// h*nkv/nh, scale dph^-1/2; attn_out fp32 [nh*dph] is fully written
-// (zeros when total_len is 0).  head_dim 64 or 128, block_size a multiple
-// of 8, nkv | nh; returns SDE_ERR_UNSUPPORTED (writing nothing) otherwise.
-__device__ inline int device_flash_attention_gqa(const float* q_all, float* attn_out,
-                                                 const sde_kv_view& kv, int layer, int nh, int nkv,
-                                                 int dph, int total_len) {
-  if (nkv < 1 || nh % nkv != 0 || kv.block_size % 8 != 0 || total_len < 0) return SDE_ERR_UNSUPPORTED;
-  if (dph == 128)
-    attn::block_attend<128>(q_all, attn_out, kv, layer, nh, nkv, total_len);
-  else if (dph == 64)
-    attn::block_attend<64>(q_all, attn_out, kv, layer, nh, nkv, total_len);
-  else
+// applied; global or shared memory) over positions [0, total_len) of
+// `layer`, by the calling block: q head h reads KV head h*nkv/nh, scale
+// dph^-1/2; attn_out fp32 [nh*dph] (global or shared) is fully written
+// (zeros when total_len is 0), so the caller need not zero it.  The units
+// (KV head, up to 16 q heads) run one after another, each spread over
+// min(blockDim.x/64, MaxWaves) waves that split its context and merge
+// through LDS.  Uses sizeof(attn::MfmaLds<128, MaxWaves>) bytes of static
+// LDS (64 KiB for the default 4 waves), shared with the grid function.
+// Inlined into the caller; its tile loop needs up to ~240 VGPRs per lane,
+// so the calling kernel should be declared __launch_bounds__(512) or
+// smaller (two waves per SIMD), else the compiler spills.
+// head_dim 64 or 128, block_size a multiple of 8, nkv | nh; returns
+// SDE_ERR_UNSUPPORTED (writing nothing) otherwise.
+template <int MaxWaves = 4>
+__device__ __forceinline__ int device_flash_attention_gqa(const float* q_all, float* attn_out,
+                                                          const sde_kv_view& kv, int layer, int nh,
+                                                          int nkv, int dph, int total_len) {
+  using namespace attn;
+  static_assert(MaxWaves == 1 || MaxWaves == 2 || MaxWaves == 4 || MaxWaves == 8, "waves");
+  if (nkv < 1 || nh % nkv != 0 || kv.block_size % 8 != 0 || total_len < 0 ||
+      (dph != 64 && dph != 128) || blockDim.x % 64 != 0)
     return SDE_ERR_UNSUPPORTED;
+  const int G = nh / nkv;
+  const int rows = device_rows(G);
+  AttnArgs a;
+  a.src = TileSource{kv.pool, kv.block_tables + (size_t)layer * kv.max_blocks_per_layer,
+                     kv.kv_dim, kv.block_size, total_len};
+  a.q = q_all;
+  a.out = attn_out;
+  a.partials = nullptr;
+  a.counters = nullptr;
+  a.nh = nh;
+  a.nkv = nkv;
+  a.G = G;
+  a.R = G;
+  a.row_groups = (G + rows - 1) / rows;
+  a.pos_base = total_len - 1;  // one query seeing [0, total_len)
+  a.n_parts = 1;
+  a.tiles_per_part = (total_len + kTile - 1) / kTile;
+  a.qscale = (float)(kLog2e / __builtin_sqrt((double)dph));
+  const int nw = min((int)(blockDim.x >> 6), MaxWaves);
+  if (total_len == 0) {
+    for (int i = threadIdx.x; i < nh * dph; i += blockDim.x) attn_out[i] = 0.f;
+  } else if (dph == 128) {
+    rows == 4 ? block_units<128, 4, MaxWaves>(a, nw) : block_units<128, 16, MaxWaves>(a, nw);
+  } else {
+    rows == 4 ? block_units<64, 4, MaxWaves>(a, nw) : block_units<64, 16, MaxWaves>(a, nw);
+  }
   __syncthreads();
   return SDE_OK;
 }
 
+// attention.h:21-29 with the reference's full argument list: blk_logits
+// (KV_BLOCK_SIZE floats of the caller's shared scratch) and the five shared
+// scalars are accepted for call-site compatibility and left untouched (this
+// function keeps its state in registers and its own LDS).
+template <int MaxWaves = 4>
+__device__ __forceinline__ int device_flash_attention_gqa(const float* q_all, float* attn_out,
+                                                          const sde_kv_view& kv, int layer, int nh,
+                                                          int nkv, int dph, int total_len,
+                                                          float* blk_logits, float& s_m, float& s_l,
+                                                          float& s_tm, float& s_alpha,
+                                                          float& s_inv) {
+  (void)blk_logits;
+  (void)s_m;
+  (void)s_l;
+  (void)s_tm;
+  (void)s_alpha;
+  (void)s_inv;
+  return device_flash_attention_gqa<MaxWaves>(q_all, attn_out, kv, layer, nh, nkv, dph,
+                                              total_len);
+}
+
 // attention.h:140-164: SDE_ATTN_SOFTMAX runs device_flash_attention_gqa; the
 // types the reference reserves (and traps on) return SDE_ERR_UNSUPPORTED.
-__device__ inline int device_attention_dispatch(int attn_type, const float* q_all, float* attn_out,
-                                                const sde_kv_view& kv, int layer, int nh, int nkv,
-                                                int dph, int total_len) {
+// attn_type takes the reference's AttentionType enum (config.h:51-56) or an
+// sde_attention_type.
+template <int MaxWaves = 4>
+__device__ __forceinline__ int device_attention_dispatch(int attn_type, const float* q_all,
+                                                         float* attn_out, const sde_kv_view& kv,
+                                                         int layer, int nh, int nkv, int dph,
+                                                         int total_len) {
   if (attn_type != SDE_ATTN_SOFTMAX) return SDE_ERR_UNSUPPORTED;
-  return device_flash_attention_gqa(q_all, attn_out, kv, layer, nh, nkv, dph, total_len);
+  return device_flash_attention_gqa<MaxWaves>(q_all, attn_out, kv, layer, nh, nkv, dph,
+                                              total_len);
+}
+
+// attention.h:140-150 with the reference's full argument list.
+template <int MaxWaves = 4>
+__device__ __forceinline__ int device_attention_dispatch(int attn_type, const float* q_all,
+                                                         float* attn_out, const sde_kv_view& kv,
+                                                         int layer, int nh, int nkv, int dph,
+                                                         int total_len, float* blk_logits,
+                                                         float& s_m, float& s_l, float& s_tm,
+                                                         float& s_alpha, float& s_inv) {
+  if (attn_type != SDE_ATTN_SOFTMAX) return SDE_ERR_UNSUPPORTED;
+  return device_flash_attention_gqa<MaxWaves>(q_all, attn_out, kv, layer, nh, nkv, dph,
+                                              total_len, blk_logits, s_m, s_l, s_tm, s_alpha,
+                                              s_inv);
 }
 
 // ---- grid-cooperative split-context attention (persistent kernels) -------
 
+// Arrival counters at the head of the grid function's workspace: a fixed
+// area, so calls of different shapes sharing one workspace never find
+// partial data where another shape keeps its counters.
+constexpr int kGridCounters = 4096;
+constexpr size_t kGridCounterBytes = kGridCounters * sizeof(uint32_t);
+
 // Bytes of the workspace of device_flash_attention_gqa_grid for windows of
 // up to n_queries queries over up to max_total_len positions: the arrival
-// counters (one per (KV head, row group), padded to 256 bytes; zero-fill
-// them once before the first call, each call leaves them zero) followed by
-// the partials of at most kStreamMaxParts partitions.
+// counters (zero-fill them once before the first call; each call leaves
+// them zero) followed by the partials of at most kStreamMaxParts
+// partitions.
 __host__ __device__ inline size_t grid_attention_workspace_size(int nh, int nkv, int dph,
                                                                 int n_queries, int max_total_len) {
   if (nh < 1 || nkv < 1 || nh % nkv != 0 || dph < 1 || n_queries < 1 || max_total_len < 1)
     return 0;
   const int R = n_queries * (nh / nkv);
-  const int rpw = R <= 2 ? 2 : attn::kStreamMaxRows;
-  const size_t counters = ((size_t)nkv * ((R + rpw - 1) / rpw) * 4 + 255) / 256 * 256;
   const int n_tiles = (max_total_len + attn::kTile - 1) / attn::kTile;
   const int by_len = (n_tiles + 3) / 4;  // 4-wave workgroups hold at least 4 tiles
   const int parts = by_len < attn::kStreamMaxParts ? by_len : attn::kStreamMaxParts;
-  return counters + (size_t)nkv * R * parts * (size_t)(dph + 2) * sizeof(float);
+  return kGridCounterBytes + (size_t)nkv * R * parts * (size_t)(dph + 2) * sizeof(float);
 }
-
-namespace attn {
-template <int DPH, int RPW, int WAVES>
-__device__ __forceinline__ void grid_items(const AttnArgs& a, int units_rg, void* lds_raw) {
-  auto& lds = *reinterpret_cast<StreamLds<DPH, RPW, WAVES>*>(lds_raw);
-  const int n_blocks = gridDim.x * gridDim.y * gridDim.z;
-  const int block = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
-  const int items = a.nkv * units_rg * a.n_parts;
-  for (int it = block; it < items; it += n_blocks) {
-    const int part = it % a.n_parts;
-    const int unit = it / a.n_parts;
-    __syncthreads();  // the previous item's readers of lds are done
-    stream_item<DPH, RPW, 2, WAVES>(a, part, unit % a.nkv, unit / a.nkv, lds);
-  }
-}
-}  // namespace attn
 
 // Grid-cooperative form of cublas_attention_kernel (kernels.cu:904-940) for
 // persistent (megakernel) decode loops, where the reference runs
@@ -1558,16 +1241,24 @@ __device__ __forceinline__ void grid_items(const AttnArgs& a, int units_rg, void
 // that share a workspace need a grid barrier between them.  `workspace`
 // (device memory of grid_attention_workspace_size(...) bytes or more)
 // starts with arrival counters that must be zero before the first call.
-// Uses 17 KiB of LDS.  Returns the same status in every thread: SDE_OK,
-// SDE_ERR_UNSUPPORTED (dph not 64/128, block_size not a multiple of 8,
-// blockDim.x < 256), SDE_ERR_INVALID_ARGUMENT, SDE_ERR_CAPACITY (window past
+// Blocks run 8 waves when MaxWaves is 8 and blockDim.x >= 512, else 4;
+// static LDS sizeof(attn::MfmaLds<128, MaxWaves>) (64 KiB by default),
+// shared with device_flash_attention_gqa.  Like it, the caller's kernel
+// should be declared __launch_bounds__(512) or smaller.  Returns the same
+// status in every thread: SDE_OK, SDE_ERR_UNSUPPORTED (dph not 64/128, block_size not a
+// multiple of 8, blockDim.x < 256, more than kGridCounters (KV head, row
+// group) pairs), SDE_ERR_INVALID_ARGUMENT, SDE_ERR_CAPACITY (window past
 // the layer's table) or SDE_ERR_WORKSPACE; nothing is written on error.
-__device__ inline int device_flash_attention_gqa_grid(const float* q_all, float* attn_out,
-                                                      const sde_kv_view& kv, int layer, int nh,
-                                                      int nkv, int dph, int pos_base,
-                                                      int n_queries, void* workspace,
-                                                      size_t workspace_bytes) {
+template <int MaxWaves = 4>
+__device__ __forceinline__ int device_flash_attention_gqa_grid(const float* q_all,
+                                                               float* attn_out,
+                                                               const sde_kv_view& kv, int layer,
+                                                               int nh, int nkv, int dph,
+                                                               int pos_base, int n_queries,
+                                                               void* workspace,
+                                                               size_t workspace_bytes) {
   using namespace attn;
+  static_assert(MaxWaves == 4 || MaxWaves == 8, "grid workgroups of 4 or 8 waves");
   if (blockDim.x < 256 || blockDim.x % 64 != 0) return SDE_ERR_UNSUPPORTED;
   if ((dph != 64 && dph != 128) || kv.block_size % 8 != 0) return SDE_ERR_UNSUPPORTED;
   if (nh < 1 || nkv < 1 || nh % nkv != 0 || nkv * dph != kv.kv_dim || layer < 0 ||
@@ -1578,19 +1269,19 @@ __device__ inline int device_flash_attention_gqa_grid(const float* q_all, float*
   if (workspace_bytes < grid_attention_workspace_size(nh, nkv, dph, n_queries, L_max))
     return SDE_ERR_WORKSPACE;
 
-  const int waves = blockDim.x >= 512 ? kStreamWaves : 4;
+  const int waves = (MaxWaves == 8 && blockDim.x >= 512) ? 8 : 4;
   const int G = nh / nkv;
   const int R = n_queries * G;
-  const StreamPlan p =
-      stream_plan(L_max, nkv, R, gridDim.x * gridDim.y * gridDim.z, waves, 2);
+  const StreamPlan p = stream_plan(L_max, nkv, R, gridDim.x * gridDim.y * gridDim.z, waves, 2,
+                                   device_rows(R));
+  if ((int64_t)nkv * p.row_groups > kGridCounters) return SDE_ERR_UNSUPPORTED;
   AttnArgs a;
   a.src = TileSource{kv.pool, kv.block_tables + (size_t)layer * kv.max_blocks_per_layer,
                      kv.kv_dim, kv.block_size, L_max};
   a.q = q_all;
   a.out = attn_out;
   a.counters = static_cast<uint32_t*>(workspace);
-  a.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) +
-                                        ((size_t)nkv * p.row_groups * 4 + 255) / 256 * 256);
+  a.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + kGridCounterBytes);
   a.nh = nh;
   a.nkv = nkv;
   a.G = G;
@@ -1601,23 +1292,14 @@ __device__ inline int device_flash_attention_gqa_grid(const float* q_all, float*
   a.tiles_per_part = p.tiles_per_part;
   a.qscale = (float)(kLog2e / __builtin_sqrt((double)dph));
 
-  __shared__ __attribute__((aligned(16))) char lds[sizeof(StreamLds<128, 4, kStreamWaves>)];
-  const bool w8 = waves == kStreamWaves;
-  if (dph == 128) {
-    if (p.rpw == 2)
-      w8 ? grid_items<128, 2, kStreamWaves>(a, p.row_groups, lds)
-         : grid_items<128, 2, 4>(a, p.row_groups, lds);
-    else
-      w8 ? grid_items<128, 4, kStreamWaves>(a, p.row_groups, lds)
-         : grid_items<128, 4, 4>(a, p.row_groups, lds);
-  } else {
-    if (p.rpw == 2)
-      w8 ? grid_items<64, 2, kStreamWaves>(a, p.row_groups, lds)
-         : grid_items<64, 2, 4>(a, p.row_groups, lds);
-    else
-      w8 ? grid_items<64, 4, kStreamWaves>(a, p.row_groups, lds)
-         : grid_items<64, 4, 4>(a, p.row_groups, lds);
+  if constexpr (MaxWaves == 8) {
+    if (waves == 8) {
+      attn::grid_dispatch<8, MaxWaves>(a, dph, p.rpw);
+      __syncthreads();
+      return SDE_OK;
+    }
   }
+  attn::grid_dispatch<4, MaxWaves>(a, dph, p.rpw);
   __syncthreads();
   return SDE_OK;
 }

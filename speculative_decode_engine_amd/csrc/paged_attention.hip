@@ -6,25 +6,24 @@
 // head h reading KV head h*nkv/nh, keys gathered through the block table.
 //
 // The "rows" of a KV head are its (query, head-in-group) pairs; a row group
-// (up to 16 rows, or 4 on the fused RoPE path) shares every K/V byte it
-// loads.  The context of each (KV head, row group) is split into
-// partitions, one 8-wave workgroup each (about one per CU); a
-// single-partition context writes the normalised output directly,
-// otherwise per-row partials go to the workspace and the last workgroup of
-// a (KV head, row group) to finish -- found with one arrival counter per
-// pair -- merges all partitions with a log-sum-exp combine in partition
-// order, so the result does not depend on arrival order and one call is
-// one launch.
+// (2 to 16 rows) shares every K/V byte it loads.  The context of each (KV
+// head, row group) is split into partitions, one 8-wave workgroup each
+// (about one per CU); a single-partition context writes the normalised
+// output directly, otherwise per-row partials go to the workspace and the
+// last workgroup of a (KV head, row group) to finish -- found with one
+// arrival counter per pair -- merges all partitions with a log-sum-exp
+// combine in partition order, so the result does not depend on arrival
+// order and one call is one launch.
 //
-// attn_mfma_kernel: K and V stream from HBM into VGPRs in the coalesced
-// load layout (lane = token slot x 16-byte feature chunk), software-
-// pipelined a tile (32 tokens) ahead, and are staged per wave in LDS; the
-// logits (K . Q^T) and the output (V^T . P^T, V read transposed with
-// ds_read_b64_tr_b16) are 16x16x32 fp16 MFMA products with fp32
-// accumulation, and the online softmax is lane-local per row.
-// attn_rope_kernel (the fused RoPE + append + attention step) keeps the
-// VALU tile path: fp16 dot2 products reduced by a transposing DPP
-// butterfly.
+// Both kernels (attn_mfma_kernel, and attn_rope_kernel for the fused RoPE +
+// append + attention step) run the MFMA tile path of
+// sde/attention_device.hpp: K and V stream from HBM into VGPRs in the
+// coalesced load layout (lane = token slot x 16-byte feature chunk),
+// software-pipelined a tile (32 tokens) ahead, and are staged per wave in
+// LDS; the logits (K . Q^T) and the output (V^T . P^T, V read transposed
+// with ds_read_b64_tr_b16) are 16x16x32 fp16 MFMA products with fp32
+// accumulation, q and P entering as fp16 hi + lo parts, and the online
+// softmax is lane-local per row.
 #include <hip/hip_runtime.h>
 
 #include <climits>
@@ -58,7 +57,7 @@ template <int DPH, int RPW, int CHUNK>
 __global__ __launch_bounds__(64 * kStreamWaves) void attn_mfma_kernel(AttnArgs a) {
   __shared__ MfmaLds<DPH, kStreamWaves> lds;
   const int3 w = stream_coords<CHUNK>();
-  stream_item<DPH, RPW, CHUNK, kStreamWaves, false, true>(a, w.x, w.y, w.z, lds);
+  stream_item<DPH, RPW, CHUNK, kStreamWaves>(a, w.x, w.y, w.z, lds);
 }
 
 // attn_mfma_kernel with RoPE of q and of the window's k, and the window's
@@ -68,7 +67,8 @@ __global__ __launch_bounds__(64 * kStreamWaves) void attn_rope_kernel(AttnArgs a
   __shared__ MfmaLds<DPH, kStreamWaves> lds;
   __shared__ float2 rope_cs[kRopeMaxQueries * (DPH / 2)];
   const int3 w = stream_coords<CHUNK>();
-  stream_item<DPH, RPW, CHUNK, kStreamWaves, true, true>(a, w.x, w.y, w.z, lds, &rp, rope_cs);
+  stream_item<DPH, RPW, CHUNK, kStreamWaves, true>(a, w.x, w.y, w.z, lds, kStreamWaves, &rp,
+                                                  rope_cs);
 }
 
 }  // namespace attn

@@ -14,9 +14,13 @@
 namespace {
 
 // One block per query, like cublas_attention_kernel (kernels.cu:904-940):
-// query m sees positions [0, pos_base + m].
-__global__ void attention_kernel(sde_kv_view kv, int layer, const float* q, float* out, int nh,
-                                 int nkv, int dph, int pos_base, int attn_type, int* status) {
+// query m sees positions [0, pos_base + m].  The device attention wants up
+// to ~240 VGPRs per lane, so its callers are declared with at most 512
+// threads per block.
+__global__ __launch_bounds__(512) void attention_kernel(sde_kv_view kv, int layer, const float* q,
+                                                        float* out, int nh, int nkv, int dph,
+                                                        int pos_base, int attn_type,
+                                                        int* status) {
   const int m = blockIdx.x;
   const size_t d = (size_t)nh * dph;
   const int st = sde::device_attention_dispatch(attn_type, q + m * d, out + m * d, kv, layer, nh,
@@ -39,12 +43,77 @@ __global__ void read_kernel(sde_kv_view kv, int layer, int pos, float* k, float*
 
 __global__ void rollback_kernel(sde_kv_view kv, int target) { sde::kv_cache_rollback(kv, target); }
 
-// Every block of an arbitrary grid calls the grid-cooperative attention.
-__global__ void grid_attention_kernel(sde_kv_view kv, int layer, const float* q, float* out,
-                                      int nh, int nkv, int dph, int pos_base, int n_queries,
-                                      void* ws, size_t ws_bytes, int* status) {
-  const int st = sde::device_flash_attention_gqa_grid(q, out, kv, layer, nh, nkv, dph, pos_base,
-                                                      n_queries, ws, ws_bytes);
+// The reference's layer attention (model.cu:400-432) with its own argument
+// list: q_all and attn_out live in the caller's dynamic shared memory
+// (smem[d..2d) and smem[0..d)), blk_logits in its scratch, the five
+// scalars are __shared__; only the cache's type differs (sde_kv_view for
+// KVCache).  One block per query m, total_len = pos_base + m + 1.
+__global__ __launch_bounds__(512) void ref_layer_attention_kernel(sde_kv_view kv, int layer,
+                                                                  const float* q, float* out,
+                                                                  int nh, int nkv, int dph,
+                                                                  int pos_base, int attn_type,
+                                                                  int* status) {
+  extern __shared__ float smem[];
+  const int d = nh * dph;
+  const int kd = nkv * dph;
+  const int tid = threadIdx.x;
+  const int m = blockIdx.x;
+  float* q_all = smem + d;
+  float* attn_out = smem;
+  float* scratch = smem + 2 * d + 2 * kd;
+  float* blk_logits = scratch;
+  __shared__ float s_attn_m;
+  __shared__ float s_attn_l;
+  __shared__ float s_tile_m_new;
+  __shared__ float s_attn_alpha;
+  __shared__ float s_attn_inv_den;
+  for (int i = tid; i < d; i += blockDim.x) q_all[i] = q[(size_t)m * d + i];
+  const int total_len = pos_base + m + 1;
+  for (int i = tid; i < d; i += blockDim.x) attn_out[i] = 0.0f;
+  __syncthreads();
+  const int st = sde::device_attention_dispatch(
+      attn_type, q_all, attn_out, kv, layer, nh, nkv, dph, total_len, blk_logits, s_attn_m,
+      s_attn_l, s_tile_m_new, s_attn_alpha, s_attn_inv_den);
+  for (int i = tid; i < d; i += blockDim.x) out[(size_t)m * d + i] = attn_out[i];
+  if (tid == 0) status[m] = st;
+}
+
+// The megakernel's RoPE'd-input step on block 0 (kernels.cu:2727-2739):
+// kv_cache_append of the token at `seq`, zero g_attn, then
+// device_attention_dispatch over seq + 1 positions with __shared__ scalars
+// and scratch, the reference's argument lists.
+__global__ __launch_bounds__(256) void ref_megakernel_step_kernel(sde_kv_view kv, int l,
+                                                                  const float* g_k,
+                                                                  const float* g_v,
+                                                                  const float* g_q, float* g_attn,
+                                                                  int nh, int nkv, int dph,
+                                                                  int seq, int attn_type,
+                                                                  int* status) {
+  const int tid = threadIdx.x;
+  const int d = nh * dph;
+  __shared__ float s_scratch[64];
+  if (blockIdx.x == 0) {
+    sde::kv_cache_append(kv, l, g_k, g_v, seq);
+    for (int i = tid; i < d; i += blockDim.x) g_attn[i] = 0.f;
+    __syncthreads();
+    __shared__ float s_m, s_l, s_tm, s_al, s_iv;
+    const int st = sde::device_attention_dispatch(attn_type, g_q, g_attn, kv, l, nh, nkv, dph,
+                                                  seq + 1, s_scratch, s_m, s_l, s_tm, s_al,
+                                                  s_iv);
+    if (tid == 0) status[0] = st;
+  }
+}
+
+// Every block of an arbitrary grid calls the grid-cooperative attention
+// (4-wave staging: 64 KiB of LDS, or 8 waves: 128 KiB).
+template <int MaxWaves>
+__global__ __launch_bounds__(512) void grid_attention_kernel(sde_kv_view kv, int layer,
+                                                             const float* q, float* out, int nh,
+                                                             int nkv, int dph, int pos_base,
+                                                             int n_queries, void* ws,
+                                                             size_t ws_bytes, int* status) {
+  const int st = sde::device_flash_attention_gqa_grid<MaxWaves>(
+      q, out, kv, layer, nh, nkv, dph, pos_base, n_queries, ws, ws_bytes);
   if (threadIdx.x == 0) status[blockIdx.x] = st;
 }
 
@@ -121,18 +190,47 @@ extern "C" {
 int sdet_attention(const sde_kv_view* kv, int layer, const float* q, float* out, int nh, int nkv,
                    int dph, int pos_base, int n_queries, int threads, int attn_type, int* status,
                    void* stream) {
-  if (!kv || threads < 64 || threads % 64 != 0 || threads > 1024 || n_queries < 1) return 1;
+  if (!kv || threads < 64 || threads % 64 != 0 || threads > 512 || n_queries < 1) return 1;
   attention_kernel<<<n_queries, threads, 0, (hipStream_t)stream>>>(*kv, layer, q, out, nh, nkv, dph,
                                                                    pos_base, attn_type, status);
   return status_of(hipGetLastError());
 }
 
+// ref_layer_attention_kernel: one block per query; dynamic shared memory
+// (2d + 2kd + 16) floats as model.cu sizes it.
+int sdet_ref_layer_attention(const sde_kv_view* kv, int layer, const float* q, float* out, int nh,
+                             int nkv, int dph, int pos_base, int n_queries, int threads,
+                             int attn_type, int* status, void* stream) {
+  if (!kv || threads < 64 || threads % 64 != 0 || threads > 512 || n_queries < 1) return 1;
+  const size_t smem = (size_t)(2 * nh * dph + 2 * nkv * dph + 16) * sizeof(float);
+  if (smem > 64 * 1024) return 1;
+  ref_layer_attention_kernel<<<n_queries, threads, smem, (hipStream_t)stream>>>(
+      *kv, layer, q, out, nh, nkv, dph, pos_base, attn_type, status);
+  return status_of(hipGetLastError());
+}
+
+int sdet_ref_megakernel_step(const sde_kv_view* kv, int layer, const float* k, const float* v,
+                             const float* q, float* attn, int nh, int nkv, int dph, int seq,
+                             int blocks, int attn_type, int* status, void* stream) {
+  if (!kv || blocks < 1) return 1;
+  ref_megakernel_step_kernel<<<blocks, 256, 0, (hipStream_t)stream>>>(
+      *kv, layer, k, v, q, attn, nh, nkv, dph, seq, attn_type, status);
+  return status_of(hipGetLastError());
+}
+
+// max_waves 4 or 8: the grid function's staging variant.
 int sdet_grid_attention(const sde_kv_view* kv, int layer, const float* q, float* out, int nh,
                         int nkv, int dph, int pos_base, int n_queries, int blocks, int threads,
-                        void* ws, size_t ws_bytes, int* status, void* stream) {
-  if (!kv || blocks < 1 || threads < 64 || threads % 64 != 0 || threads > 1024) return 1;
-  grid_attention_kernel<<<blocks, threads, 0, (hipStream_t)stream>>>(
-      *kv, layer, q, out, nh, nkv, dph, pos_base, n_queries, ws, ws_bytes, status);
+                        int max_waves, void* ws, size_t ws_bytes, int* status, void* stream) {
+  if (!kv || blocks < 1 || threads < 64 || threads % 64 != 0 || threads > 512) return 1;
+  if (max_waves == 8)
+    grid_attention_kernel<8><<<blocks, threads, 0, (hipStream_t)stream>>>(
+        *kv, layer, q, out, nh, nkv, dph, pos_base, n_queries, ws, ws_bytes, status);
+  else if (max_waves == 4)
+    grid_attention_kernel<4><<<blocks, threads, 0, (hipStream_t)stream>>>(
+        *kv, layer, q, out, nh, nkv, dph, pos_base, n_queries, ws, ws_bytes, status);
+  else
+    return 1;
   return status_of(hipGetLastError());
 }
 

@@ -23,10 +23,11 @@ ATOL, RTOL = 2e-3, 1e-2
 
 def assert_close(got, ref, what=""):
     """The contract (north_star: |err| <= 2e-3 + 1e-2 |ref|), and a tighter
-    regression guard on the kernels' own precision: fp16 q and fp16
-    probabilities keep the error below 2e-3 of the output's scale (measured
-    ~2.5e-4 of it), so a lost partition or a mis-weighted tile, which the
-    contract's absolute term can hide when outputs are ~1e-2, fails here."""
+    regression guard on the kernels' own precision: q and the weights enter
+    the matrix cores as fp16 hi + lo pairs (fp32-level products), so the
+    error stays far below 2e-3 of the output's scale, and a lost partition
+    or a mis-weighted tile, which the contract's absolute term can hide when
+    outputs are ~1e-2, fails here."""
     got = np.asarray(got, np.float64)
     ref = np.asarray(ref, np.float64)
     err = np.abs(got - ref)

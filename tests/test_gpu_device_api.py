@@ -80,7 +80,7 @@ def test_device_attention_matches_oracle(dev, oracle, nh, nkv, dph, bs, ctx, M):
     cache.free()
 
 
-@pytest.mark.parametrize("threads", [64, 192, 512, 1024])
+@pytest.mark.parametrize("threads", [64, 192, 256, 512])
 def test_device_attention_any_block_size(dev, oracle, threads):
     case_banner("device attention threads", threads)
     nh, nkv, dph, ctx = 32, 8, 128, 700
@@ -90,6 +90,85 @@ def test_device_attention_any_block_size(dev, oracle, threads):
                                    threads=threads)
     assert (status == 0).all()
     assert_close(out.cpu().numpy(), oracle.attention_f64_np(q, K, V, nh, nkv, dph, ctx), "threads")
+    cache.free()
+
+
+def _ref_fns(dev):
+    vp, i = ctypes.c_void_p, ctypes.c_int
+    view_p = ctypes.POINTER(N.KVView)
+    dev.sdet_ref_layer_attention.argtypes = [view_p, i, vp, vp, i, i, i, i, i, i, i, vp, vp]
+    dev.sdet_ref_megakernel_step.argtypes = [view_p, i, vp, vp, vp, vp, i, i, i, i, i, i, vp,
+                                             vp]
+    dev.sdet_ref_layer_attention.restype = i
+    dev.sdet_ref_megakernel_step.restype = i
+
+
+@pytest.mark.parametrize("nh,nkv,dph,bs,ctx,M,threads", [
+    (32, 8, 128, 16, 3000, 5, 256),    # Llama-3-8B, the reference's 256-thread blocks
+    (28, 4, 128, 32, 1000, 2, 512),    # Qwen2.5-7B (G = 7)
+    (32, 4, 64, 16, 2048, 1, 256),     # TinyLlama
+])
+def test_reference_signature_layer_attention(dev, oracle, nh, nkv, dph, bs, ctx, M, threads):
+    """model.cu:400-432's call, verbatim but for the cache type: q_all and
+    attn_out in the caller's dynamic shared memory, blk_logits and the five
+    __shared__ scalars passed through device_attention_dispatch's
+    reference argument list."""
+    case_banner("reference-signature layer attention", nh, nkv, dph, bs, ctx, M, threads)
+    _ref_fns(dev)
+    nblk = -(-(ctx + M) // bs)
+    cache, K, V, rng = build_layer(nh, nkv, dph, bs, ctx, M, nblk + 11, 5 * nh + ctx)
+    q = W.queries(rng, M, nh, dph)
+    qd = torch.from_numpy(q).cuda()
+    out = torch.full((M, nh * dph), float("nan"), device="cuda")
+    status = torch.full((M,), -1, dtype=torch.int32, device="cuda")
+    view = cache.view()
+    assert dev.sdet_ref_layer_attention(ctypes.byref(view), 0, qd.data_ptr(), out.data_ptr(), nh,
+                                        nkv, dph, ctx, M, threads, 0, status.data_ptr(),
+                                        _stream()) == 0
+    torch.cuda.synchronize()
+    assert (status.cpu().numpy() == 0).all()
+    ref = oracle.attention_f64_np(q, K, V, nh, nkv, dph, ctx)
+    assert_close(out.cpu().numpy(), ref, "reference-signature dispatch")
+    cache.free()
+
+
+def test_reference_signature_megakernel_step(dev, oracle):
+    """kernels.cu:2727-2739 on block 0 of a 256-thread grid: append the
+    token at seq, zero g_attn, dispatch over seq + 1 positions with the
+    reference's arguments (s_scratch, five __shared__ scalars); the pool
+    bytes are the oracle's and the output matches its attention."""
+    case_banner("reference-signature megakernel step")
+    _ref_fns(dev)
+    nh, nkv, dph, bs, ctx = 32, 8, 128, 16, 1200
+    kv_dim = nkv * dph
+    nblk = -(-(ctx + 1) // bs)
+    rng = np.random.default_rng(2739)
+    tables = W.make_tables(rng, 2, nblk, 2 * nblk + 5)
+    cache = KVCache(2, kv_dim, nblk, bs, 2 * nblk + 5)
+    model = oracle.PagedKVModel(2, kv_dim, nblk, bs, 2 * nblk + 5)
+    kc, vc = W.context_kv(rng, ctx, kv_dim)
+    for l in range(2):
+        cache.set_block_table(l, tables[l])
+        model.set_block_table(l, tables[l])
+    cache.write_fp16(1, torch.from_numpy(kc.view(np.int16)).cuda(),
+                     torch.from_numpy(vc.view(np.int16)).cuda(), 0)
+    model.write_fp16(1, kc, vc, 0)
+    k, v = W.new_kv(rng, 1, kv_dim)
+    q = W.queries(rng, 1, nh, dph)
+    kd, vd, qd = (torch.from_numpy(x).cuda() for x in (k, v, q))
+    attn = torch.full((nh * dph,), float("nan"), device="cuda")
+    status = torch.full((1,), -1, dtype=torch.int32, device="cuda")
+    view = cache.view()
+    assert dev.sdet_ref_megakernel_step(ctypes.byref(view), 1, kd.data_ptr(), vd.data_ptr(),
+                                        qd.data_ptr(), attn.data_ptr(), nh, nkv, dph, ctx, 4, 0,
+                                        status.data_ptr(), _stream()) == 0
+    torch.cuda.synchronize()
+    assert status.item() == 0
+    model.append(1, k, v, ctx)
+    pool = cache.pool.cpu().numpy().view(np.uint16).reshape(model.pool.shape)
+    assert np.array_equal(pool, model.pool)
+    ref = model.attention(1, q, nh, nkv, dph, ctx, mode="f64")
+    assert_close(attn.cpu().numpy()[None], ref, "megakernel step")
     cache.free()
 
 
@@ -225,7 +304,8 @@ def _grid_ws(nh, nkv, dph, M, L):
     return torch.zeros(n // 4 + 1, dtype=torch.int32, device="cuda")
 
 
-def grid_attention(dev, cache, q, nh, nkv, dph, pos_base, blocks, threads, ws, layer=0):
+def grid_attention(dev, cache, q, nh, nkv, dph, pos_base, blocks, threads, ws, layer=0,
+                   max_waves=4):
     M = q.shape[0]
     out = torch.full((M, nh * dph), float("nan"), device="cuda")
     status = torch.full((blocks,), -1, dtype=torch.int32, device="cuda")
@@ -233,25 +313,27 @@ def grid_attention(dev, cache, q, nh, nkv, dph, pos_base, blocks, threads, ws, l
     f = dev.sdet_grid_attention
     f.restype = ctypes.c_int
     vp, i = ctypes.c_void_p, ctypes.c_int
-    f.argtypes = [ctypes.POINTER(N.KVView), i, vp, vp, i, i, i, i, i, i, i, vp, ctypes.c_size_t,
-                  vp, vp]
+    f.argtypes = [ctypes.POINTER(N.KVView), i, vp, vp, i, i, i, i, i, i, i, i, vp,
+                  ctypes.c_size_t, vp, vp]
     assert f(ctypes.byref(view), layer, q.data_ptr(), out.data_ptr(), nh, nkv, dph, pos_base, M,
-             blocks, threads, ws.data_ptr(), ws.numel() * 4, status.data_ptr(), _stream()) == 0
+             blocks, threads, max_waves, ws.data_ptr(), ws.numel() * 4, status.data_ptr(),
+             _stream()) == 0
     torch.cuda.synchronize()
     return out, status.cpu().numpy()
 
 
-@pytest.mark.parametrize("nh,nkv,dph,bs,ctx,M,blocks,threads", [
-    (32, 8, 128, 16, 32767, 1, 256, 512),   # Llama-3-8B 32K decode, one block per CU
-    (32, 8, 128, 16, 4096, 5, 300, 256),    # verify window, 4-wave blocks
-    (28, 4, 128, 32, 8192, 9, 64, 1024),    # Qwen2.5-7B verify, fewer blocks than items
-    (32, 4, 64, 16, 2048, 1, 37, 320),      # TinyLlama, odd grid, a wave past the four
-    (4, 2, 64, 16, 128, 1, 1, 256),         # config 1 shape on a single block
-    (8, 8, 128, 8, 77, 2, 512, 512),        # ragged last tile, more blocks than work
+@pytest.mark.parametrize("nh,nkv,dph,bs,ctx,M,blocks,threads,max_waves", [
+    (32, 8, 128, 16, 32767, 1, 256, 512, 8),   # Llama-3-8B 32K decode, one block per CU
+    (32, 8, 128, 16, 32767, 1, 256, 512, 4),   # the same with 4-wave staging
+    (32, 8, 128, 16, 4096, 5, 300, 256, 4),    # verify window, 4-wave blocks
+    (28, 4, 128, 32, 8192, 9, 64, 512, 8),     # Qwen2.5-7B verify, fewer blocks than items
+    (32, 4, 64, 16, 2048, 1, 37, 320, 4),      # TinyLlama, odd grid, a wave past the four
+    (4, 2, 64, 16, 128, 1, 1, 256, 4),         # config 1 shape on a single block
+    (8, 8, 128, 8, 77, 2, 512, 512, 8),        # ragged last tile, more blocks than work
 ])
 def test_grid_attention_matches_oracle_and_host_entry(dev, oracle, nh, nkv, dph, bs, ctx, M,
-                                                      blocks, threads):
-    case_banner("grid attention", nh, nkv, dph, bs, ctx, M, blocks, threads)
+                                                      blocks, threads, max_waves):
+    case_banner("grid attention", nh, nkv, dph, bs, ctx, M, blocks, threads, max_waves)
     nblk = -(-(ctx + M) // bs)
     cache, K, V, rng = build_layer(nh, nkv, dph, bs, ctx, M, nblk + 40, nh + ctx + M)
     q = W.queries(rng, M, nh, dph)
@@ -262,7 +344,8 @@ def test_grid_attention_matches_oracle_and_host_entry(dev, oracle, nh, nkv, dph,
     torch.cuda.synchronize()
     first = None
     for call in range(2):   # the second call finds the counters the first left at zero
-        out, status = grid_attention(dev, cache, qd, nh, nkv, dph, ctx, blocks, threads, ws)
+        out, status = grid_attention(dev, cache, qd, nh, nkv, dph, ctx, blocks, threads, ws,
+                                     max_waves=max_waves)
         assert (status == 0).all()
         assert_close(out.cpu().numpy(), ref, f"grid call {call}")
         assert_close(out.cpu().numpy(), host.cpu().numpy().astype(np.float64), "grid vs host")
@@ -270,8 +353,36 @@ def test_grid_attention_matches_oracle_and_host_entry(dev, oracle, nh, nkv, dph,
             first = out
         else:
             assert torch.equal(out, first)   # deterministic
-    nc = (nkv * -(-(M * nh // nkv) // (2 if M * nh // nkv <= 2 else 4)))
-    assert torch.count_nonzero(ws[:nc]).item() == 0   # counters back at zero
+    assert torch.count_nonzero(ws[:4096]).item() == 0   # counters back at zero
+    cache.free()
+
+
+def test_grid_attention_nonfinite_window_rows_stay_hidden(dev, oracle):
+    """Rows 2-4 of a 5-query window hold Inf/NaN V: on the grid-cooperative
+    path too, queries 0-1 match the oracle and later queries are non-finite
+    exactly where the reference's restatement is."""
+    from test_gpu_precision import _cache_with_context, check_poisoned, poisoned_window
+    case_banner("grid attention non-finite window")
+    nh, nkv, dph, bs, ctx, M = 32, 8, 128, 16, 4096, 5
+    kv_dim = nkv * dph
+    cache, table, pool_blocks, kc, vc, rng = _cache_with_context(nh, nkv, dph, bs, ctx, M, 404)
+    k, v = poisoned_window(rng, M, kv_dim, False)
+    cache.append(0, torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(), ctx)
+    K = np.concatenate([kc.astype(np.float32), k.astype(np.float16).astype(np.float32)])
+    V = np.concatenate([vc.astype(np.float32), v.astype(np.float16).astype(np.float32)])
+    q = W.queries(rng, M, nh, dph)
+    ws = _grid_ws(nh, nkv, dph, M, ctx + M)
+    out, status = grid_attention(dev, cache, torch.from_numpy(q).cuda(), nh, nkv, dph, ctx, 256,
+                                 512, ws, max_waves=8)
+    assert (status == 0).all()
+    model = oracle.PagedKVModel(1, kv_dim, len(table), bs, pool_blocks)
+    model.set_block_table(0, table)
+    model.write_fp16(0, kc, vc, 0)
+    model.append(0, k, v, ctx)
+    with np.errstate(invalid="ignore", over="ignore"):
+        f64 = oracle.attention_f64_np(q, K, V, nh, nkv, dph, ctx)
+        tiled = model.attention(0, q, nh, nkv, dph, ctx, mode="tiled")
+    check_poisoned(out.cpu().numpy(), f64, tiled, "grid window")
     cache.free()
 
 
