@@ -11,11 +11,12 @@
 //                                projection (the step after attention)
 //
 // Layout of the work (libsde_paged's sde_matvec and device_matvec_grid):
-// the columns are cut into tiles of 512 (a wave's 64 lanes x 8 fp16, one
-// 16-byte load per lane covers 1 KiB of a row) and the rows into `splits`
-// ranges, one workgroup per (column tile, row range).  Its waves stream
-// rows w, w+WAVES, ... of the range, two batches of eight 16-byte loads in
-// flight per lane; x[m][r] is wave-uniform (scalar loads).  The waves' sums meet in
+// the columns are cut into tiles of kCols = 256 (32 lanes x 8 fp16: a
+// wave's 16-byte loads cover two rows of 512 B, lane groups of 32 taking
+// the two row phases) and the rows into `splits` ranges, one workgroup per
+// (column tile, row range).  Its waves stream rows of the range, two
+// batches of eight 16-byte loads in flight per lane; x[m][r] is
+// wave-uniform per row phase (scalar loads).  The waves' sums meet in
 // LDS; each row range publishes a partial per column, and the last
 // workgroup of a column tile to finish (one arrival counter per tile) adds
 // the partials in row-range order, so the result does not depend on
@@ -348,8 +349,8 @@ __device__ __forceinline__ void mv_item(const MvArgs& a, int ct, int ks, MvLds<W
   }
 
   // ---- waves -> one partial per (row of x, column) --------------------
-  // Thread t < 128 sums 4 adjacent columns over the waves; a partial is one
-  // 16-byte device-scope store.  Rows alternate between two LDS buffers
+  // Thread t < kCols/4 (64) sums 4 adjacent columns over the waves; a
+  // partial is one 16-byte device-scope store.  Rows alternate between two LDS buffers
   // (the x staging area is free once every wave is past the streaming
   // loop), so one barrier per row orders its stores before the sums, and
   // the barrier of row m+1 orders row m's sums before row m+2's stores.

@@ -162,6 +162,7 @@ void release(sde_kv_cache* c) {
   if (c->d_tables) (void)hipFree(c->d_tables);
   if (c->d_seq_len) (void)hipFree(c->d_seq_len);
   if (c->workspace) (void)hipFree(c->workspace);
+  for (void* w : c->retired_workspaces) (void)hipFree(w);
   if (c->d_counters) (void)hipFree(c->d_counters);
   delete c;
 }

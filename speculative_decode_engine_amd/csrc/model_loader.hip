@@ -10,6 +10,8 @@
 // next chunk of the file is read into the other.
 #include <hip/hip_runtime.h>
 
+#include <climits>
+#include <cstdint>
 #include <cstdio>
 #include <cstring>
 #include <new>
@@ -131,10 +133,20 @@ std::vector<TensorSlot> tensor_plan(sde_model* m) {
   return t;
 }
 
-size_t arena_bytes_of(const std::vector<TensorSlot>& t) {
+// Arena bytes of a plan.  SDE_ERR_FORMAT when a tensor has more elements
+// than the file's uint32 count can state (no file can match it) or the sum
+// would wrap: the header bounds (each dimension up to 2^30) allow both, and
+// the arena is allocated from this sum before any tensor is read.
+int arena_bytes_of(const std::vector<TensorSlot>& t, size_t* bytes) {
   size_t b = 0;
-  for (const auto& s : t) b += align_up(s.n * 2);
-  return b;
+  for (const auto& s : t) {
+    if (s.n > (size_t)UINT32_MAX) return SDE_ERR_FORMAT;
+    const size_t add = align_up(s.n * 2);
+    if (add > SIZE_MAX - b) return SDE_ERR_FORMAT;
+    b += add;
+  }
+  *bytes = b;
+  return SDE_OK;
 }
 
 // Two pinned buffers and a stream: chunk i is read while chunk i-1 copies.
@@ -206,7 +218,8 @@ size_t sde_model_weights_bytes(const sde_model_config* cfg) {
   try {  // no C++ exception crosses the C-ABI
     sde_model m;
     m.cfg = *cfg;
-    return arena_bytes_of(tensor_plan(&m));
+    size_t bytes = 0;
+    return arena_bytes_of(tensor_plan(&m), &bytes) == SDE_OK ? bytes : 0;
   } catch (...) {
     return 0;
   }
@@ -235,7 +248,11 @@ int sde_model_load(const char* path, sde_model** out, sde_model_config* cfg_out)
     delete m;
     return SDE_ERR_HIP;
   }
-  m->arena_bytes = arena_bytes_of(plan);
+  st = arena_bytes_of(plan, &m->arena_bytes);
+  if (st != SDE_OK) {
+    delete m;
+    return st;
+  }
   if (m->arena_bytes > 0 && hipMalloc(&m->arena, m->arena_bytes) != hipSuccess) {
     delete m;
     return SDE_ERR_HIP;

@@ -219,14 +219,17 @@ int run_attention(sde_kv_cache* cache, int layer, const float* d_q, float* d_out
       partials = static_cast<float*>(d_workspace);
     } else {
       if (cache->workspace_bytes < need) {
-        // Grow the cache-owned workspace (not for use under graph capture).
-        if (cache->workspace) {
-          if (hipDeviceSynchronize() != hipSuccess) return SDE_ERR_HIP;
-          (void)hipFree(cache->workspace);
-          cache->workspace = nullptr;
-          cache->workspace_bytes = 0;
-        }
-        if (hipMalloc(&cache->workspace, need) != hipSuccess) return SDE_ERR_HIP;
+        // Grow the cache-owned workspace.  Not while the stream is being
+        // captured: the allocation cannot be recorded, and a graph would
+        // keep its address.  The old buffer stays allocated (queued work
+        // or an earlier graph may still use it) until the cache is freed.
+        hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing((hipStream_t)stream, &cap) != hipSuccess) return SDE_ERR_HIP;
+        if (cap != hipStreamCaptureStatusNone) return SDE_ERR_WORKSPACE;
+        void* grown = nullptr;
+        if (hipMalloc(&grown, need) != hipSuccess) return SDE_ERR_HIP;
+        if (cache->workspace) cache->retired_workspaces.push_back(cache->workspace);
+        cache->workspace = grown;
         cache->workspace_bytes = need;
       }
       partials = static_cast<float*>(cache->workspace);
@@ -317,3 +320,4 @@ int sde_attention_dispatch(int attn_type, sde_kv_cache* cache, int layer,
 }
 
 }  // extern "C"
+

@@ -26,6 +26,10 @@ struct sde_kv_cache {
   bool seq_len_on_device = false;       // *d_seq_len was set by a device-side rewind
   void* workspace = nullptr;            // internal attention workspace
   size_t workspace_bytes = 0;
+  // Workspaces outgrown by a larger call: kept until the cache is
+  // destroyed, because work already queued, or a graph captured earlier,
+  // may still use them.
+  std::vector<void*> retired_workspaces;
   // Arrival counters of the fused partition combine, one per (KV head, row
   // group) of a call; zero at rest (the last arriving workgroup resets its
   // counter), so calls on one cache must be stream-ordered.

@@ -14,6 +14,7 @@ from ._native import check
 from .kv_cache import _stream_handle
 
 _WORKSPACES: dict = {}
+_RETIRED: list = []
 
 
 def matvec_workspace(d_in: int, d_out: int, n_rows: int, device) -> torch.Tensor:
@@ -26,12 +27,18 @@ def matvec_workspace(d_in: int, d_out: int, n_rows: int, device) -> torch.Tensor
     return torch.zeros(n, dtype=torch.uint8, device=device)
 
 
-def _cached_workspace(d_in: int, d_out: int, n_rows: int, device) -> torch.Tensor:
+def _cached_workspace(d_in: int, d_out: int, n_rows: int, device, stream) -> torch.Tensor:
+    """One workspace per (device, stream): calls on one stream are ordered,
+    so they may share its arrival counters; calls on different streams get
+    different workspaces.  An outgrown workspace is kept alive (queued work
+    or a captured graph may still use it)."""
     lib = _native.load()
     need = int(lib.sde_matvec_workspace_size(d_in, d_out, n_rows))
-    key = torch.device(device)
+    key = (torch.device(device), _stream_handle(stream).value or 0)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < need:
+        if ws is not None:
+            _RETIRED.append(ws)
         ws = torch.zeros(need, dtype=torch.uint8, device=device)
         _WORKSPACES[key] = ws
     return ws
@@ -45,8 +52,7 @@ def matvec(x: torch.Tensor, W: torch.Tensor, out: Optional[torch.Tensor] = None,
     x: CUDA float32 [M][d_in] or [d_in]; W: CUDA float16 [d_in][d_out]
     (row-major, the reference's weight layout); out: CUDA float32
     [M][d_out] (allocated when None; required when accumulate).  The
-    workspace defaults to one cached per device (calls sharing it must be
-    ordered on one stream)."""
+    workspace defaults to one cached per (device, stream)."""
     squeeze = x.dim() == 1
     x2 = x.unsqueeze(0) if squeeze else x
     if x2.device.type != "cuda" or x2.dtype != torch.float32 or not x2.is_contiguous():
@@ -66,7 +72,7 @@ def matvec(x: torch.Tensor, W: torch.Tensor, out: Optional[torch.Tensor] = None,
             or out.numel() != M * d_out:
         raise TypeError(f"out must be a contiguous CUDA float32 tensor of {M}x{d_out}")
     if workspace is None:
-        workspace = _cached_workspace(d_in, d_out, M, x.device)
+        workspace = _cached_workspace(d_in, d_out, M, x.device, stream)
     lib = _native.load()
     check(lib.sde_matvec(ctypes.c_void_p(x2.data_ptr()), ctypes.c_void_p(W.data_ptr()),
                          ctypes.c_void_p(out.data_ptr()), d_in, d_out, M, int(bool(accumulate)),

@@ -55,6 +55,9 @@ SHAPES = [
     (4, 2048, 2048),
     (6, 8192, 512),      #   6 and 7 rows: 8 row ranges at most
     (7, 8192, 512),
+    (2, 200, 264),       # d_in < 256: one row range, so 2/4/8 rows take the direct
+    (4, 120, 512),       #   single-split write, odd rows through the second LDS
+    (8, 255, 1032),      #   reduction buffer
 ]
 
 
@@ -222,6 +225,9 @@ def _grid_mv(mvdev, gpu, xt, Wt, ot, M, d_in, d_out, acc, blocks, threads, ws, w
     (9, 3584, 3584, 0, 300, 256),     # Qwen verify window, 4-wave blocks, two row passes
     (16, 640, 520, 1, 7, 1024),       # the largest row count, fewer blocks than items
     (1, 7, 8, 0, 3, 320),             # fewer rows than one batch
+    (2, 200, 2048, 1, 3, 512),        # d_in < 256 (single split): 2, 4 and 8 rows, odd
+    (4, 120, 1032, 0, 2, 256),        #   rows through the second reduction buffer, blocks
+    (8, 255, 4096, 1, 5, 512),        #   taking several column tiles each
 ])
 def test_grid_matvec(gpu, mvdev, oracle, M, d_in, d_out, acc, blocks, threads):
     case_banner("grid matvec", M, d_in, d_out, acc, blocks, threads)

@@ -99,3 +99,7 @@ def test_weights_bytes_is_the_aligned_sum():
         want = sum(-(-int(np.prod(s)) * 2 // 256) * 256 for s in sdec.tensor_shapes(c).values())
         assert sdec.weights_bytes(dict(c, version=v)) == want
     assert sdec.weights_bytes(dict(CFG, n_heads=0)) == 0
+    # A 2^30 x 2^30 embedding has more elements than the file's uint32 count
+    # can state: rejected before any arena is sized from it.
+    huge = dict(CFG, d_model=1 << 30, n_heads=1, n_kv_heads=1, vocab_size=1 << 30)
+    assert sdec.weights_bytes(huge) == 0
