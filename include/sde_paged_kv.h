@@ -198,6 +198,29 @@ int sde_paged_attention(sde_kv_cache* cache, int layer, const float* d_q,
                         int n_queries, void* d_workspace,
                         size_t workspace_bytes, sde_stream_t stream);
 
+/* Bytes of the static device array sde_paged_attention_noalloc keeps its
+ * partials in (one per device).  A call's partials are at most
+ * (CUs x 16 rows) x (dph + 2) x 4 bytes: 2.1 MB on MI355X's 256 CUs, so
+ * every plan there fits. */
+#define SDE_NOALLOC_SCRATCH_BYTES ((size_t)4 << 20)
+
+/* sde_paged_attention without a workspace, allocating nothing: the
+ * split-context partials go to a static device array of the library
+ * (SDE_NOALLOC_SCRATCH_BYTES per device, held until the process ends) and
+ * the arrival counters are the cache's.  No counterpart in the reference:
+ * it is for callers that cannot allocate device memory during the call --
+ * code under HIP graph capture, tight serving loops, harnesses that forbid
+ * allocation.  Same arguments, results and errors as sde_paged_attention
+ * (minus the workspace), plus SDE_ERR_WORKSPACE for a call whose partials
+ * would exceed the array.  The first call on a device looks up the array's
+ * address there (with the cache's device current).  Every call on one GPU
+ * shares that GPU's array: calls that overlap on one GPU (on different
+ * streams, or on different caches used concurrently) race on it and must
+ * be ordered by the caller. */
+int sde_paged_attention_noalloc(sde_kv_cache* cache, int layer, const float* d_q,
+                                float* d_out, int nh, int nkv, int dph, int pos_base,
+                                int n_queries, sde_stream_t stream);
+
 /* Greedy acceptance + O(1) rewind of speculative decoding on the device,
  * with no host round trip (the reference's host loop kernels.cu:2428-2466
  * copies the tokens back and rewinds from the host; its megakernel does it

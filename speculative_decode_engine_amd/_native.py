@@ -27,6 +27,9 @@ SDE_ERR_NO_DEVICE = 7
 SDE_ERR_IO = 8
 SDE_ERR_FORMAT = 9
 
+# SDE_NOALLOC_SCRATCH_BYTES: sde_paged_attention_noalloc's static partials array
+NOALLOC_SCRATCH_BYTES = 4 << 20
+
 SDE_ATTN_SOFTMAX = 0
 SDE_ATTN_SLIDING_WINDOW = 1
 SDE_ATTN_KDA = 2
@@ -132,6 +135,8 @@ PROTOTYPES = {
     "sde_grid_attention_workspace_size": (_sz, [_c_int, _c_int, _c_int, _c_int, _c_int]),
     "sde_paged_attention": (_c_int, [_vp, _c_int, _vp, _vp, _c_int, _c_int, _c_int, _c_int,
                                      _c_int, _vp, _sz, _vp]),
+    "sde_paged_attention_noalloc": (_c_int, [_vp, _c_int, _vp, _vp, _c_int, _c_int, _c_int,
+                                             _c_int, _c_int, _vp]),
     "sde_spec_accept_stochastic": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int,
                                             ctypes.c_float, ctypes.c_float, ctypes.c_uint64, _vp,
                                             _c_int, _c_int, _vp, _vp]),

@@ -26,9 +26,11 @@
 // softmax is lane-local per row.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <climits>
 #include <cmath>
 #include <cstdlib>
+#include <mutex>
 
 #include "sde/attention_device.hpp"
 #include "sde_internal.hpp"
@@ -309,6 +311,10 @@ int sde_rope_append_attention(sde_kv_cache* cache, int layer, const float* d_q,
                        d_workspace, workspace_bytes, stream, &rp);
 }
 
+int sde_paged_attention_noalloc(sde_kv_cache* cache, int layer, const float* d_q,
+                                float* d_out, int nh, int nkv, int dph, int pos_base,
+                                int n_queries, sde_stream_t stream);
+
 int sde_attention_dispatch(int attn_type, sde_kv_cache* cache, int layer,
                            const float* d_q, float* d_out, int nh, int nkv,
                            int dph, int pos_base, int n_queries,
@@ -321,3 +327,54 @@ int sde_attention_dispatch(int attn_type, sde_kv_cache* cache, int layer,
 
 }  // extern "C"
 
+// ---- sde_paged_attention_noalloc: partials in a static device array -------
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+
+// The split-context partials of sde_paged_attention_noalloc, one copy per
+// device (each GPU the library runs on holds it until the process ends).
+// In host code this name is a host-side stand-in, not a device address:
+// host code uses only the address hipGetSymbolAddress returns for the
+// current device (scratch_address).  No part of it must start at zero
+// (each call writes every partial it later reads).
+static __device__ __align__(256) char scratch[SDE_NOALLOC_SCRATCH_BYTES];
+
+std::mutex g_scratch_mutex;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+
+// The device address of `scratch` on `device`, which must be current:
+// looked up on the first call on that device, then kept.
+int scratch_address(int device, void** out) {
+  if (device < 0 || device >= kMaxDevices) return SDE_ERR_UNSUPPORTED;
+  void* p = g_scratch_ptr[device].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    p = g_scratch_ptr[device].load(std::memory_order_relaxed);
+    if (!p) {
+      if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return SDE_ERR_HIP;
+      g_scratch_ptr[device].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return SDE_OK;
+}
+
+}  // namespace
+
+extern "C" int sde_paged_attention_noalloc(sde_kv_cache* cache, int layer, const float* d_q,
+                                           float* d_out, int nh, int nkv, int dph, int pos_base,
+                                           int n_queries, sde_stream_t stream) {
+  const int st = check_attention(cache, layer, d_q, d_out, nh, nkv, dph, pos_base, n_queries);
+  if (st != SDE_OK) return st;
+  sde::DeviceGuard guard(cache->device);
+  if (!guard.ok()) return SDE_ERR_HIP;
+  void* ws = nullptr;
+  const int sst = scratch_address(cache->device, &ws);
+  if (sst != SDE_OK) return sst;
+  // A plan whose partials exceed the array gets SDE_ERR_WORKSPACE from
+  // run_attention, before any launch; nothing here allocates.
+  return run_attention(cache, layer, d_q, d_out, nh, nkv, dph, pos_base, n_queries, ws,
+                       SDE_NOALLOC_SCRATCH_BYTES, stream, nullptr);
+}

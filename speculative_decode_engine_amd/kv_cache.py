@@ -234,6 +234,22 @@ class KVCache:
             "paged_attention")
         return out
 
+    def attention_noalloc(self, layer: int, q: torch.Tensor, nh: int, nkv: int, dph: int,
+                          pos_base: int, out: Optional[torch.Tensor] = None,
+                          stream=None) -> torch.Tensor:
+        """attention() through sde_paged_attention_noalloc: the partials go
+        to the library's static per-device array, so the call allocates no
+        device memory (out must then be given by the caller)."""
+        M = q.shape[0] if q.dim() == 2 else 1
+        q = _dev_f32(q.reshape(M, nh * dph), "q", (M, nh * dph))
+        if out is None:
+            out = torch.empty(M, nh * dph, dtype=torch.float32, device=self.device)
+        _dev_f32(out, "out", (M, nh * dph))
+        check(self._lib.sde_paged_attention_noalloc(
+            self.handle, layer, ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(out.data_ptr()),
+            nh, nkv, dph, pos_base, M, _stream_handle(stream)), "paged_attention_noalloc")
+        return out
+
     def rope_append_attention(self, layer: int, q: torch.Tensor, k: torch.Tensor,
                               v: torch.Tensor, nh: int, nkv: int, dph: int, pos_base: int,
                               theta: float = 10000.0, scaling_type: int = 0,

@@ -100,3 +100,9 @@ def test_reserved_attention_types_unsupported(lib):
 def test_workspace_size_query_is_host_only(lib):
     null = ctypes.c_void_p()
     assert lib.sde_paged_attention_workspace_size(null, 32, 8, 128, 1, 32768) == 0
+
+
+def test_noalloc_scratch_size_matches_the_header():
+    text = N.HEADER_PATH.read_text()
+    assert "#define SDE_NOALLOC_SCRATCH_BYTES ((size_t)4 << 20)" in text
+    assert N.NOALLOC_SCRATCH_BYTES == 4 << 20
