@@ -416,6 +416,55 @@ int sde_model_get_globals(const sde_model* model, sde_model_globals* out);
 /* model_free (model.cu:54-65). */
 int sde_model_free(sde_model* model);
 
+/* ---- persistent speculative decoding loop --------------------------------
+ * megakernel_speculative (kernels.cu:2864-3106, host launcher
+ * kernels.cu:3593-3755): the whole draft / verify / accept / rewind loop in
+ * one cooperative launch, self-speculative over one cache (model.cu:838-890:
+ * layers [0, n_draft) draft, layers [n_draft, n_layers) verify the k+1-token
+ * window from the prefix layers' outputs).  The reference's loop runs its
+ * transformer; this one runs the paged-KV path's model: layer l of token t
+ * has q, k, v rows emb_q/emb_k/emb_v[l][t], q adding the previous layer's
+ * attention output of the same row, and `head` (fp16, row-major [in][out] as
+ * the reference stores weights, model.h:19) maps the last layer's attention
+ * output to logits.  Every block of the grid runs the attention
+ * (sde::device_flash_attention_gqa_grid) and the head
+ * (sde::device_matvec_grid); each round drafts k tokens by greedy argmax,
+ * verifies them, accepts the leading matches plus the target's next token
+ * (sde::spec_accept_greedy) and rewinds seq_len to save + n_accepted + 1; the
+ * next round starts at the device seq_len.  k = 0 is plain greedy decoding
+ * through all layers (one token per round). */
+typedef struct sde_loop_model {
+  const float* emb_q;   /* [n_layers][vocab][n_heads*head_dim]                  */
+  const float* emb_k;   /* [n_layers][vocab][kv_dim]                            */
+  const float* emb_v;   /* [n_layers][vocab][kv_dim]                            */
+  const uint16_t* head; /* fp16 bits [n_heads*head_dim][vocab], 16-byte aligned */
+  int32_t vocab;        /* a multiple of 8                                      */
+  int32_t n_heads;
+  int32_t n_kv_heads;
+  int32_t head_dim;     /* 64 or 128; n_kv_heads*head_dim == the cache's kv_dim */
+} sde_loop_model;
+
+/* Workspace bytes of sde_spec_loop_greedy for this cache, model and k; 0 for
+ * invalid shapes.  No initialisation needed (the loop zeroes what it uses). */
+size_t sde_spec_loop_workspace_size(const sde_kv_cache* cache, const sde_loop_model* model,
+                                    int k);
+
+/* Runs rounds until max_new tokens are emitted.  The cache holds the
+ * context at positions [0, seq_len) (the device seq_len word at launch);
+ * d_state int32[8]: in [0] the last emitted token (not yet in the cache);
+ * out [0] the last emitted token, [1] tokens emitted (max_new .. max_new+k-1),
+ * [2] rounds, [3] status (SDE_OK, or SDE_ERR_CAPACITY when a window would
+ * pass the layers' mapped blocks), [4] drafts proposed, [5] accepted.
+ * d_emitted int32[max_new + k], d_accepted int32[max_new] (per round).
+ * 0 <= k <= 15; 1 <= n_draft < n_layers when k > 0.  d_workspace: 256-byte
+ * aligned, sde_spec_loop_workspace_size bytes.  One block per CU, all
+ * resident (a cooperative launch); the cache's seq_len is then on the device
+ * (sde_kv_device_seq_len). */
+int sde_spec_loop_greedy(sde_kv_cache* cache, const sde_loop_model* model, int k, int n_draft,
+                         int max_new, int32_t* d_state, int32_t* d_emitted,
+                         int32_t* d_accepted, void* d_workspace, size_t workspace_bytes,
+                         sde_stream_t stream);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif

@@ -231,6 +231,65 @@ def spec_accept_greedy(draft_tokens, target_tokens, k: int, target_save: int,
     return n, int(target_tokens[n]), target_seq, draft_seq, emitted
 
 
+def spec_loop_greedy(model: PagedKVModel, emb_q, emb_k, emb_v, head_bits, nh: int, nkv: int,
+                     dph: int, anchor: int, k: int, n_draft: int, max_new: int,
+                     shift_rewind: int = 0):
+    """The persistent self-speculative greedy loop (megakernel_speculative,
+    kernels.cu:2864-3106; self-speculative verify model.cu:838-890) over the
+    byte model, with the loop model of sde_spec_loop_greedy: layer l of token
+    t has q, k, v rows emb_q/emb_k/emb_v[l][t] (fp32), q adds the previous
+    layer's attention output (rounded to fp32, as the device keeps it), and
+    the logits are that output of the last layer (fp64) times head (fp16
+    bits [nh*dph][V], widened exactly), argmax taking the lowest index.
+
+    Each round from P = model.seq_len: for i = 0..k (k > 0) the prefix layers
+    [0, n_draft) append window token i at P+i and attend (one query); the
+    first k of them propose window token i+1 from their head logits.  Then
+    layers [n_draft, n_layers) (all layers when k = 0) append the window
+    [anchor, drafts] at P.. and attend it causally; the target's tokens are
+    the argmaxes of every row; spec_accept_greedy emits the accepted drafts
+    and the bonus and seq_len <- P + n + 1 (kernels.cu:3050-3072).
+    `shift_rewind` plants a rewind mistake (for the tests that must catch
+    one).  Returns (tokens, accepted per round, rounds)."""
+    L = model.n_layers
+    d = nh * dph
+    head = f16_bits_to_f32(np.asarray(head_bits, dtype=np.uint16)).astype(np.float64)
+    M = k + 1
+    tokens_out, accepted = [], []
+    cur = int(anchor)
+    while len(tokens_out) < max_new:
+        P = model.seq_len
+        window = [cur] + [0] * k
+        h = np.zeros((M, d), dtype=np.float32)
+
+        def layers(lo, hi, r0, n):
+            for l in range(lo, hi):
+                toks = window[r0:r0 + n]
+                model.append(l, emb_k[l][toks], emb_v[l][toks], P + r0)
+                q = emb_q[l][toks].astype(np.float32)
+                if l > 0:
+                    q = q + h[r0:r0 + n]
+                out = model.attention(l, q, nh, nkv, dph, P + r0, mode="f64")
+                h[r0:r0 + n] = out.astype(np.float32)
+            return h[r0:r0 + n].astype(np.float64) @ head
+
+        lo = 0
+        if k > 0:
+            for i in range(M):
+                logits = layers(0, n_draft, i, 1)
+                if i < k:
+                    window[i + 1] = int(np.argmax(logits[0]))
+            lo = n_draft
+        logits = layers(lo, L, 0, M)
+        target = [int(np.argmax(logits[m])) for m in range(M)]
+        n, bonus, t_seq, _, emitted = spec_accept_greedy(window[1:], target, k, P, P, True)
+        tokens_out += emitted
+        accepted.append(n)
+        model.seq_len = t_seq + shift_rewind
+        cur = bonus
+    return tokens_out, accepted, len(accepted)
+
+
 _PHILOX_M = (0xD2511F53, 0xCD9E8D57)   # Salmon et al., SC'11 (Philox4x32)
 _PHILOX_W = (0x9E3779B9, 0xBB67AE85)
 

@@ -96,6 +96,20 @@ LAYER_TENSORS = ("rms_attn_weight", "Wq", "Wk", "Wv", "Wo", "rms_mlp_weight", "W
 GLOBAL_TENSORS = ("token_embedding", "rms_final_weight", "output_proj")
 
 
+class LoopModel(ctypes.Structure):
+    """sde_loop_model: the persistent loop's embedding tables and head."""
+    _fields_ = [
+        ("emb_q", ctypes.c_void_p),
+        ("emb_k", ctypes.c_void_p),
+        ("emb_v", ctypes.c_void_p),
+        ("head", ctypes.c_void_p),
+        ("vocab", ctypes.c_int32),
+        ("n_heads", ctypes.c_int32),
+        ("n_kv_heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+    ]
+
+
 class LayerWeights(ctypes.Structure):
     """sde_layer_weights: device pointers (model.h:32-47)."""
     _fields_ = [(n, ctypes.c_void_p) for n in LAYER_TENSORS]
@@ -154,6 +168,9 @@ PROTOTYPES = {
     "sde_model_get_globals": (_c_int, [_vp, ctypes.POINTER(ModelGlobals)]),
     "sde_model_free": (_c_int, [_vp]),
     "sde_matvec": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _sz, _vp]),
+    "sde_spec_loop_workspace_size": (_sz, [_vp, ctypes.POINTER(LoopModel), _c_int]),
+    "sde_spec_loop_greedy": (_c_int, [_vp, ctypes.POINTER(LoopModel), _c_int, _c_int, _c_int,
+                                      _vp, _vp, _vp, _vp, _sz, _vp]),
 }
 
 _LIB = None

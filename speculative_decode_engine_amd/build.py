@@ -23,7 +23,7 @@ LIB_PATH = PKG_DIR / LIB_NAME
 OFFLOAD_ARCH = "gfx950"
 
 SOURCES = ["kv_cache.hip", "paged_attention.hip", "spec_accept.hip", "matvec.hip",
-           "model_loader.hip"]
+           "model_loader.hip", "spec_loop.hip"]
 
 # Test infrastructure: kernels that call the device-side API of
 # include/sde/attention_device.hpp from inside a caller's kernel.

@@ -1,0 +1,371 @@
+// The persistent speculative decoding loop on gfx950: one cooperative
+// launch runs round after round of self-speculative greedy decoding over a
+// paged KV cache, with every token decision and every rewind made on the
+// device.
+//
+// Reference (arkhamHack/speculative_decode_engine):
+//   cuda/src/kernels.cu:2864-3106  megakernel_speculative_kernel: draft k
+//                                  tokens, verify the window [last, drafts]
+//                                  in one batched pass, greedy accept,
+//                                  rewind target / draft seq_len
+//   cuda/src/model.cu:838-890      self-speculative verify: layers
+//                                  [n_draft, n_layers) over the saved
+//                                  hiddens of the prefix layers
+//   cuda/src/kernels.cu:2727-2739  the megakernel's attention (block 0)
+//
+// What differs from the reference by design: attention runs on every block
+// (device_flash_attention_gqa_grid) instead of block 0, the output head on
+// every block (device_matvec_grid), and the window's appends and argmaxes on
+// one block per window row.  The model is the paged-KV path's own: layer l
+// of token t reads q, k, v rows from per-layer embedding tables, q adds the
+// previous layer's attention output (a residual stream through the
+// attention), and fp16 head weights map the last layer's attention output to
+// logits.  K/V bytes therefore depend on (token, position) alone, so greedy
+// speculation must leave exactly the greedy decoder's bytes below seq_len.
+#include <hip/hip_runtime.h>
+#include <hip/hip_cooperative_groups.h>
+
+#include <cstdint>
+
+#include "sde/attention_device.hpp"
+#include "sde/matvec_device.hpp"
+#include "sde/spec_device.hpp"
+#include "sde_internal.hpp"
+
+namespace sde {
+namespace loop {
+
+namespace cg = cooperative_groups;
+
+constexpr int kThreads = 512;
+constexpr int kMaxWindow = 16;  // k + 1 rows (device_matvec_grid's limit)
+
+// Words of d_state.
+enum : int {
+  kAnchor = 0,    // in: the last emitted token (not yet in the cache); out: updated
+  kEmitted = 1,   // tokens written to d_emitted
+  kRounds = 2,    // rounds run
+  kStatus = 3,    // first error (SDE_OK when none)
+  kProposed = 4,  // drafts proposed
+  kAccepted = 5,  // drafts accepted
+  kStateWords = 8
+};
+
+struct LoopArgs {
+  sde_kv_view kv;
+  sde_loop_model m;
+  int d;  // n_heads * head_dim
+  int k;
+  int n_draft;
+  int max_new;
+  int cap;  // positions the layer tables map
+  int32_t* state;
+  int32_t* emitted;   // [max_new + k]
+  int32_t* accepted;  // [max_new], per round
+  float* q_buf;       // [k+1][d]
+  float* h_buf;       // [k+1][d]
+  float* logits;      // [k+1][vocab]
+  int32_t* tokens;    // [2(k+1)]: window tokens, then the target's tokens
+  void* attn_ws;
+  size_t attn_ws_bytes;
+  void* mv_ws;
+  size_t mv_ws_bytes;
+};
+
+// Workspace layout: attention workspace (counters first), projection
+// workspace (counters first), then the loop's buffers, each 256-byte
+// aligned.
+struct Layout {
+  size_t attn, mv, q, h, logits, tokens, total;
+};
+
+inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+inline Layout layout(int nh, int nkv, int dph, int vocab, int k, int cap) {
+  Layout l;
+  const int M = k + 1;
+  const size_t d = (size_t)nh * dph;
+  l.attn = 0;
+  l.mv = align256(grid_attention_workspace_size(nh, nkv, dph, M, cap));
+  l.q = l.mv + align256(mv::mv_workspace_size((int)d, vocab, M));
+  l.h = l.q + align256(M * d * sizeof(float));
+  l.logits = l.h + align256(M * d * sizeof(float));
+  l.tokens = l.logits + align256((size_t)M * vocab * sizeof(float));
+  l.total = l.tokens + align256(2 * M * sizeof(int32_t));
+  return l;
+}
+
+// Stores of one phase reach the device coherence point and the next
+// phase's loads miss stale lines of their XCD's L2: a device-scope fence on
+// both sides of the grid barrier.
+__device__ __forceinline__ void barrier(cg::grid_group& g) {
+  __threadfence();
+  g.sync();
+  __threadfence();
+}
+
+__device__ __forceinline__ int load_word(const int32_t* p) {
+  return __builtin_amdgcn_readfirstlane(
+      __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+
+__device__ __forceinline__ void note_error(const LoopArgs& a, int st) {
+  if (st != SDE_OK && threadIdx.x == 0)
+    atomicCAS(reinterpret_cast<int*>(a.state + kStatus), SDE_OK, st);
+}
+
+// q rows [r0, r0+n) of layer l: the token's embedding, plus the previous
+// layer's attention output of the row (residual), by the whole grid.
+__device__ void build_q(const LoopArgs& a, int l, int r0, int n, bool residual) {
+  const int d = a.d, V = a.m.vocab;
+  const int total = n * d;
+  for (int i = blockIdx.x * blockDim.x + attn::item_tid(); i < total;
+       i += gridDim.x * blockDim.x) {
+    const int m = r0 + i / d, e = i - (i / d) * d;
+    const int tok = a.tokens[m];
+    float x = a.m.emb_q[((size_t)l * V + tok) * d + e];
+    if (residual) x += a.h_buf[(size_t)m * d + e];
+    a.q_buf[(size_t)m * d + e] = x;
+  }
+}
+
+// Window rows [r0, r0+n) of layer l appended at pos0 + row, one block per
+// row: kv_cache_append (kv_cache.cu:70-93), fp32 -> fp16 round to nearest
+// even.  The host checked that every position the loop reaches is mapped.
+// (Thread indices here and below come through attn::item_tid(), so the
+// compiler cannot keep them live across the attention's register-heavy
+// tile loop.)
+__device__ void append_rows(const LoopArgs& a, int l, int r0, int n, int pos0) {
+  const int kvd = a.kv.kv_dim, V = a.m.vocab;
+  for (int r = r0 + blockIdx.x; r < r0 + n; r += gridDim.x) {
+    const int tok = a.tokens[r];
+    const float* k = a.m.emb_k + ((size_t)l * V + tok) * kvd;
+    const float* v = a.m.emb_v + ((size_t)l * V + tok) * kvd;
+    const int pos = pos0 + r;
+    const int lb = pos / a.kv.block_size;
+    const int pb = a.kv.block_tables[(size_t)l * a.kv.max_blocks_per_layer + lb];
+    uint16_t* kd = a.kv.pool + ((size_t)pb * 2u * a.kv.block_size + (pos - lb * a.kv.block_size)) *
+                                   (size_t)kvd;
+    uint16_t* vd = kd + (size_t)a.kv.block_size * kvd;
+    for (int i = attn::item_tid(); i < kvd; i += blockDim.x) {
+      kd[i] = __builtin_bit_cast(uint16_t, (_Float16)k[i]);
+      vd[i] = __builtin_bit_cast(uint16_t, (_Float16)v[i]);
+    }
+  }
+}
+
+// argmax of logits row r (the lowest index among equal maxima; NaN never
+// wins) into tokens[dst + r], one block per row.
+__device__ void argmax_rows(const LoopArgs& a, int n, int dst) {
+  __shared__ float s_val[kThreads / 64];
+  __shared__ int s_idx[kThreads / 64];
+  const int V = a.m.vocab;
+  for (int r = blockIdx.x; r < n; r += gridDim.x) {
+    const float* x = a.logits + (size_t)r * V;
+    const int tid = attn::item_tid();
+    float best = -INFINITY;
+    int bi = V;
+    for (int i = tid; i < V; i += blockDim.x) {
+      const float v = x[i];
+      if (v > best) {  // ascending i per thread: the first maximum stays
+        best = v;
+        bi = i;
+      }
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+      const float ov = __shfl_xor(best, off);
+      const int oi = __shfl_xor(bi, off);
+      if (ov > best || (ov == best && oi < bi)) {
+        best = ov;
+        bi = oi;
+      }
+    }
+    const int w = tid >> 6;
+    if ((tid & 63) == 0) {
+      s_val[w] = best;
+      s_idx[w] = bi;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      for (int i = 1; i < (int)(blockDim.x >> 6); i++)
+        if (s_val[i] > best || (s_val[i] == best && s_idx[i] < bi)) {
+          best = s_val[i];
+          bi = s_idx[i];
+        }
+      a.tokens[dst + r] = bi < V ? bi : 0;  // all NaN: token 0
+    }
+    __syncthreads();
+  }
+}
+
+// Layers [lo, hi) on window rows [r0, r0+n) at positions pos0 + row:
+// append, q, grid attention; h_buf rows hold the last layer's output.
+__device__ void run_layers(const LoopArgs& a, cg::grid_group& g, int lo, int hi, int r0, int n,
+                           int pos0) {
+  for (int l = lo; l < hi; l++) {
+    append_rows(a, l, r0, n, pos0);
+    build_q(a, l, r0, n, l > 0);
+    barrier(g);
+    const int st = device_flash_attention_gqa_grid<4>(
+        a.q_buf + (size_t)r0 * a.d, a.h_buf + (size_t)r0 * a.d, a.kv, l, a.m.n_heads,
+        a.m.n_kv_heads, a.m.head_dim, pos0 + r0, n, a.attn_ws, a.attn_ws_bytes);
+    note_error(a, st);
+    barrier(g);
+  }
+}
+
+// Logits of window rows [r0, r0+n) from their h_buf rows, then their
+// argmaxes into tokens[dst + row].
+__device__ void decide(const LoopArgs& a, cg::grid_group& g, int r0, int n, int dst) {
+  const int st = device_matvec_grid(a.h_buf + (size_t)r0 * a.d, a.m.head, a.logits, a.d,
+                                    a.m.vocab, n, 0, a.mv_ws, a.mv_ws_bytes);
+  note_error(a, st);
+  barrier(g);
+  argmax_rows(a, n, dst);
+  barrier(g);
+}
+
+__global__ __launch_bounds__(kThreads) void spec_loop_kernel(LoopArgs a) {
+  cg::grid_group g = cg::this_grid();
+  const int M = a.k + 1;
+  const int n_layers = a.kv.n_layers;
+  // The device functions' arrival counters start at zero.
+  if (blockIdx.x == 0) {
+    uint32_t* c = static_cast<uint32_t*>(a.attn_ws);
+    for (int i = threadIdx.x; i < kGridCounters; i += blockDim.x) c[i] = 0u;
+    uint32_t* mc = static_cast<uint32_t*>(a.mv_ws);
+    const int nmc = (int)(mv::mv_counter_bytes(a.m.vocab, M) / sizeof(uint32_t));
+    for (int i = threadIdx.x; i < nmc; i += blockDim.x) mc[i] = 0u;
+    if (threadIdx.x == 0) {
+      a.tokens[0] = a.state[kAnchor];
+      for (int i = kEmitted; i < kStateWords; i++) a.state[i] = 0;
+    }
+  }
+  barrier(g);
+
+  for (int round = 0;; round++) {
+    // Every block reads the same words after the barrier: the loop's exits
+    // are uniform over the grid, so every block meets every barrier.
+    const int P = load_word(a.kv.seq_len);
+    if (load_word(a.state + kEmitted) >= a.max_new || load_word(a.state + kStatus) != SDE_OK)
+      break;
+    if (P < 0 || P + M > a.cap) {
+      if (blockIdx.x == 0 && threadIdx.x == 0) a.state[kStatus] = SDE_ERR_CAPACITY;
+      break;
+    }
+    if (a.k > 0) {
+      // Draft (kernels.cu:2960-3006): the prefix layers for window token i
+      // at P+i, one token at a time; the first k outputs propose window
+      // token i+1.
+      for (int i = 0; i < M; i++) {
+        run_layers(a, g, 0, a.n_draft, i, 1, P);
+        if (i < a.k) decide(a, g, i, 1, i + 1);
+      }
+    }
+    // Verify (model.cu:838-890): the remaining layers over the whole
+    // window, then the target's token for every row.
+    run_layers(a, g, a.n_draft, n_layers, 0, M, P);
+    decide(a, g, 0, M, M);
+    // Greedy accept and O(1) rewind (kernels.cu:3050-3072).
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+      const int E = a.state[kEmitted];
+      const SpecAccept r = spec_accept_greedy(a.tokens + 1, a.tokens + M, a.k, P, P, a.kv,
+                                              nullptr, a.emitted + E);
+      a.state[kEmitted] = E + r.n_accepted + 1;
+      a.state[kAnchor] = r.bonus;
+      a.state[kRounds] = round + 1;
+      a.state[kProposed] += a.k;
+      a.state[kAccepted] += r.n_accepted;
+      a.accepted[round] = r.n_accepted;
+      a.tokens[0] = r.bonus;
+    }
+    barrier(g);
+  }
+}
+
+}  // namespace loop
+}  // namespace sde
+
+extern "C" {
+
+size_t sde_spec_loop_workspace_size(const sde_kv_cache* cache, const sde_loop_model* model,
+                                    int k) {
+  if (!cache || !model || k < 0 || k + 1 > sde::loop::kMaxWindow) return 0;
+  if (model->n_heads < 1 || model->n_kv_heads < 1 || model->head_dim < 1 || model->vocab < 1)
+    return 0;
+  const int cap = cache->cfg.max_blocks_per_layer * cache->cfg.block_size;
+  return sde::loop::layout(model->n_heads, model->n_kv_heads, model->head_dim, model->vocab, k,
+                           cap)
+      .total;
+}
+
+int sde_spec_loop_greedy(sde_kv_cache* cache, const sde_loop_model* model, int k, int n_draft,
+                         int max_new, int32_t* d_state, int32_t* d_emitted,
+                         int32_t* d_accepted, void* d_workspace, size_t workspace_bytes,
+                         sde_stream_t stream) {
+  using namespace sde::loop;
+  if (!cache || !model || !d_state || !d_emitted || !d_accepted || !d_workspace)
+    return SDE_ERR_INVALID_ARGUMENT;
+  const sde_loop_model& m = *model;
+  if (!m.emb_q || !m.emb_k || !m.emb_v || !m.head) return SDE_ERR_INVALID_ARGUMENT;
+  if (m.n_heads < 1 || m.n_kv_heads < 1 || m.n_heads % m.n_kv_heads != 0 ||
+      m.n_kv_heads * m.head_dim != cache->cfg.kv_dim || m.vocab < 8 || max_new < 1)
+    return SDE_ERR_INVALID_ARGUMENT;
+  if (m.head_dim != 64 && m.head_dim != 128) return SDE_ERR_UNSUPPORTED;
+  if (cache->cfg.block_size % 8 != 0 || m.vocab % 8 != 0 ||
+      (reinterpret_cast<uintptr_t>(m.head) & 15u) != 0)
+    return SDE_ERR_UNSUPPORTED;
+  if (k < 0 || k + 1 > kMaxWindow) return SDE_ERR_RANGE;
+  const int n_layers = cache->cfg.n_layers;
+  if (k > 0 && (n_draft < 1 || n_draft >= n_layers)) return SDE_ERR_INVALID_ARGUMENT;
+  // Every position the loop can reach must have a physical block.
+  int cap = cache->cfg.max_blocks_per_layer * cache->cfg.block_size;
+  for (int l = 0; l < n_layers; l++) {
+    const int mapped = (int)sde::mapped_tokens(cache, l);
+    if (mapped < cap) cap = mapped;
+  }
+  const Layout lay = layout(m.n_heads, m.n_kv_heads, m.head_dim, m.vocab, k,
+                            cache->cfg.max_blocks_per_layer * cache->cfg.block_size);
+  if (workspace_bytes < lay.total) return SDE_ERR_WORKSPACE;
+  if ((reinterpret_cast<uintptr_t>(d_workspace) & 255u) != 0) return SDE_ERR_INVALID_ARGUMENT;
+
+  sde::DeviceGuard guard(cache->device);
+  if (!guard.ok()) return SDE_ERR_HIP;
+  int coop = 0, per_cu = 0;
+  if (hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, cache->device) !=
+          hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, spec_loop_kernel, kThreads, 0) !=
+          hipSuccess)
+    return SDE_ERR_HIP;
+  if (!coop || per_cu < 1) return SDE_ERR_UNSUPPORTED;
+
+  LoopArgs a;
+  if (sde_kv_get_view(cache, &a.kv) != SDE_OK) return SDE_ERR_INVALID_ARGUMENT;
+  a.m = m;
+  a.d = m.n_heads * m.head_dim;
+  a.k = k;
+  a.n_draft = k > 0 ? n_draft : 0;
+  a.max_new = max_new;
+  a.cap = cap;
+  a.state = d_state;
+  a.emitted = d_emitted;
+  a.accepted = d_accepted;
+  char* ws = static_cast<char*>(d_workspace);
+  a.attn_ws = ws + lay.attn;
+  a.attn_ws_bytes = lay.mv - lay.attn;
+  a.mv_ws = ws + lay.mv;
+  a.mv_ws_bytes = lay.q - lay.mv;
+  a.q_buf = reinterpret_cast<float*>(ws + lay.q);
+  a.h_buf = reinterpret_cast<float*>(ws + lay.h);
+  a.logits = reinterpret_cast<float*>(ws + lay.logits);
+  a.tokens = reinterpret_cast<int32_t*>(ws + lay.tokens);
+  void* args[] = {&a};
+  const hipError_t e = hipLaunchCooperativeKernel(
+      reinterpret_cast<const void*>(spec_loop_kernel), dim3(cache->n_cus), dim3(kThreads), args,
+      0, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return SDE_ERR_HIP;
+  cache->seq_len_on_device = true;
+  return SDE_OK;
+}
+
+}  // extern "C"

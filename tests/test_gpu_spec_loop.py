@@ -1,0 +1,146 @@
+"""The persistent speculative loop (sde_spec_loop_greedy) against its CPU
+restatement (oracle.spec_loop_greedy), through the C-ABI.
+
+One cooperative launch runs every round on the device (megakernel_speculative,
+kernels.cu:2864-3106): drafting with the prefix layers, the window's verify
+(model.cu:838-890), greedy acceptance on device tokens and the O(1) rewind;
+each round starts at the device seq_len the previous one wrote.  Checked:
+  * emitted tokens, per-round acceptances, the final device seq_len and the
+    SHA-256 of the whole pool (stale rejected drafts included) equal the
+    oracle's, for greedy decoding (k = 0) and self-speculation;
+  * speculation emits the greedy tokens (the reference's invariant,
+    main.cu:311-337) and leaves the greedy run's K/V bytes below seq_len;
+  * a window past the mapped blocks stops the loop with SDE_ERR_CAPACITY
+    after the rounds that fit; bad arguments are rejected before any work.
+"""
+import hashlib
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import case_banner
+from loop_model import make_loop_model, prefill, prompt_tokens
+from speculative_decode_engine_amd import KVCache, SDEError
+from speculative_decode_engine_amd.spec_loop import SpecLoopModel, spec_loop_greedy
+
+pytestmark = pytest.mark.gpu
+
+
+class DeviceKV:
+    """prefill()'s cache interface over a KVCache."""
+
+    def __init__(self, cache):
+        self.c = cache
+
+    def append(self, layer, k, v, pos):
+        self.c.append(layer, torch.from_numpy(np.ascontiguousarray(k)).cuda(),
+                      torch.from_numpy(np.ascontiguousarray(v)).cuda(), pos)
+
+    def set_seq_len(self, n):
+        self.c.set_seq_len(n)
+
+
+def device_model(m):
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    return SpecLoopModel(t(m.emb_q), t(m.emb_k), t(m.emb_v), t(m.head.view(np.float16)),
+                         m.nh, m.nkv, m.dph)
+
+
+def run_both(oracle, m, k, n_draft, max_new, seed, P0, nblk=None):
+    nblk = nblk or -(-(P0 + max_new + k + 1) // 16)
+    kvd = m.nkv * m.dph
+    cache = KVCache(m.n_layers, kvd, nblk, 16, m.n_layers * nblk)
+    model = oracle.PagedKVModel(m.n_layers, kvd, nblk, 16, m.n_layers * nblk)
+    prompt = prompt_tokens(seed, P0, m.vocab)
+    prefill(DeviceKV(cache), m, prompt)
+    prefill(model, m, prompt)
+    anchor = int(np.random.default_rng(seed).integers(0, m.vocab))
+    res = spec_loop_greedy(cache, device_model(m), anchor, k, n_draft, max_new)
+    return res, cache, model, anchor
+
+
+def pool_sha(cache):
+    torch.cuda.synchronize()
+    return hashlib.sha256(cache.pool.cpu().numpy().tobytes()).hexdigest()
+
+
+CASES = [
+    # seed, (L, nh, nkv, dph, V), P0, k, n_draft
+    (3, (4, 4, 2, 64, 256), 40, 4, 2),
+    (6, (4, 4, 2, 64, 256), 40, 7, 1),
+    (5, (3, 8, 2, 128, 512), 700, 4, 1),
+    (9, (2, 32, 8, 128, 1024), 2000, 5, 1),   # Llama-3-8B heads, multi-partition windows
+]
+
+
+@pytest.mark.parametrize("seed,shape,P0,k,n_draft", CASES)
+def test_spec_loop_matches_oracle_and_greedy(gpu, oracle, seed, shape, P0, k, n_draft):
+    L, nh, nkv, dph, V = shape
+    case_banner("spec loop", seed, shape, P0, k, n_draft)
+    m = make_loop_model(seed, n_layers=L, nh=nh, nkv=nkv, dph=dph, vocab=V, noise=0.1,
+                        q_scale=2.0)
+    max_new = 32
+    greedy, gcache, gmodel, anchor = run_both(oracle, m, 0, 0, max_new, seed, P0,
+                                              nblk=-(-(P0 + max_new + k + 1) // 16))
+    g_toks, g_acc, _ = oracle.spec_loop_greedy(gmodel, m.emb_q, m.emb_k, m.emb_v, m.head, nh,
+                                               nkv, dph, anchor, 0, 0, max_new)
+    assert greedy.status == 0
+    assert greedy.tokens == g_toks and greedy.accepted == g_acc == [0] * max_new
+    assert greedy.seq_len == gmodel.seq_len == P0 + max_new
+    assert pool_sha(gcache) == gmodel.pool_sha256()
+
+    spec, scache, smodel, _ = run_both(oracle, m, k, n_draft, max_new, seed, P0)
+    s_toks, s_acc, _ = oracle.spec_loop_greedy(smodel, m.emb_q, m.emb_k, m.emb_v, m.head, nh,
+                                               nkv, dph, anchor, k, n_draft, max_new)
+    assert spec.status == 0
+    assert spec.tokens == s_toks and spec.accepted == s_acc
+    assert spec.seq_len == smodel.seq_len == P0 + len(spec.tokens)
+    assert pool_sha(scache) == smodel.pool_sha256()
+    # the reference's invariant, on the device: speculation emits the greedy
+    # tokens and keeps the greedy run's K/V bytes below seq_len
+    assert spec.tokens[:max_new] == greedy.tokens
+    assert spec.rounds < max_new and any(a > 0 for a in spec.accepted)
+    n = P0 + max_new
+    for l in range(L):
+        gk, gv = gcache.read(l, 0, n)
+        sk, sv = scache.read(l, 0, n)
+        assert torch.equal(gk, sk) and torch.equal(gv, sv)
+    gcache.free()
+    scache.free()
+
+
+def test_spec_loop_stops_at_capacity(gpu, oracle):
+    case_banner("spec loop capacity")
+    m = make_loop_model(3, noise=0.1, q_scale=2.0)
+    P0, k = 40, 4
+    # 4 blocks = 64 positions: rounds run while P + k + 1 <= 64
+    res, cache, model, anchor = run_both(oracle, m, k, 2, 64, 3, P0, nblk=4)
+    assert res.status == 2  # SDE_ERR_CAPACITY
+    assert res.seq_len + k + 1 > 64 and res.seq_len <= 64
+    toks, acc, _ = oracle.spec_loop_greedy(model, m.emb_q, m.emb_k, m.emb_v, m.head, m.nh, m.nkv,
+                                           m.dph, anchor, k, 2, len(res.tokens))
+    assert res.tokens == toks[:len(res.tokens)] and res.accepted == acc[:len(res.accepted)]
+    cache.free()
+
+
+def test_spec_loop_rejects_bad_arguments(gpu):
+    case_banner("spec loop errors")
+    m = make_loop_model(3, noise=0.1, q_scale=2.0)
+    cache = KVCache(m.n_layers, m.nkv * m.dph, 8, 16, m.n_layers * 8)
+    cache.set_seq_len(10)
+    dm = device_model(m)
+    before = cache.pool.clone()
+    for k, n_draft, status in ((16, 1, 3), (4, 0, 1), (4, m.n_layers, 1), (-1, 1, 3)):
+        with pytest.raises(SDEError) as e:
+            spec_loop_greedy(cache, dm, 5, k, n_draft, 8)
+        assert e.value.status == status
+    odd = SpecLoopModel(dm.emb_q[:, :250].contiguous(), dm.emb_k[:, :250].contiguous(),
+                        dm.emb_v[:, :250].contiguous(), dm.head[:, :250].contiguous(),
+                        m.nh, m.nkv, m.dph)
+    with pytest.raises(SDEError) as e:
+        spec_loop_greedy(cache, odd, 5, 2, 1, 8)
+    assert e.value.status == 4  # vocab not a multiple of 8
+    torch.cuda.synchronize()
+    assert torch.equal(cache.pool, before) and cache.device_seq_len() == 10
+    cache.free()

@@ -178,3 +178,45 @@ def test_speculative_sampling_special_cases(oracle):
     for off in range(50):
         r = oracle.spec_accept_stochastic(tl0, tl[:1], [3], 1, 1.0, 1.0, 3, off, 4, 4, False)
         assert r["n_accepted"] == 0 and r["token"] != 3 and r["draft_seq"] == 4
+
+
+# ---- the persistent loop's restatement (oracle.spec_loop_greedy) ------------
+# sde_spec_loop_greedy's algorithm on the CPU byte model: self-speculation
+# over one cache must emit the greedy tokens (k = 0) and leave the greedy
+# run's K/V bytes below seq_len; a rewind one position off either way breaks
+# it, so the check is sharp.
+
+def loop_run(oracle, m, k, n_draft, max_new, seed, P0=40, shift=0):
+    from loop_model import prefill, prompt_tokens
+    nblk = -(-(P0 + 2 * max_new + k + 1) // 16)
+    model = oracle.PagedKVModel(m.n_layers, m.nkv * m.dph, nblk, 16, m.n_layers * nblk)
+    prefill(model, m, prompt_tokens(seed, P0, m.vocab))
+    anchor = int(np.random.default_rng(seed).integers(0, m.vocab))
+    toks, acc, _ = oracle.spec_loop_greedy(model, m.emb_q, m.emb_k, m.emb_v, m.head, m.nh,
+                                           m.nkv, m.dph, anchor, k, n_draft, max_new, shift)
+    return toks, acc, model
+
+
+@pytest.mark.parametrize("seed,k,n_draft", [(3, 4, 2), (6, 7, 1), (5, 4, 3)])
+def test_loop_restatement_speculation_emits_greedy_tokens(oracle, seed, k, n_draft):
+    from loop_model import make_loop_model
+    m = make_loop_model(seed, noise=0.1, q_scale=2.0)
+    base, base_acc, bm = loop_run(oracle, m, 0, 0, 40, seed)
+    assert base_acc == [0] * 40 and bm.seq_len == 80
+    spec, acc, sm = loop_run(oracle, m, k, n_draft, 40, seed)
+    assert spec[:40] == base
+    assert any(a > 0 for a in acc) and any(a < k for a in acc)  # both rewind paths
+    assert sm.seq_len == 40 + sum(a + 1 for a in acc) == 40 + len(spec)
+    for l in range(m.n_layers):
+        kb, vb = bm.gather(l, 0, 80)
+        ks, vs = sm.gather(l, 0, 80)
+        assert np.array_equal(kb, ks) and np.array_equal(vb, vs)
+
+
+@pytest.mark.parametrize("shift", [-1, 1])
+def test_loop_restatement_planted_rewind_mistake(oracle, shift):
+    from loop_model import make_loop_model
+    m = make_loop_model(3, noise=0.1, q_scale=2.0)
+    base, _, _ = loop_run(oracle, m, 0, 0, 40, 3)
+    spec, _, _ = loop_run(oracle, m, 4, 2, 40, 3, shift=shift)
+    assert spec[:40] != base
