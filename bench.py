@@ -6,18 +6,23 @@ peak) at 4K/32K context, verify k=4.  The headline `value` is the achieved
 algorithmic HBM throughput (GB/s) of a Llama-3-8B-shaped 32K-context decode
 layer-step (attention of one query over 32768 keys, 32 q / 8 KV heads,
 head_dim 128, block_size 16, fragmented 131072-block pool).  A step is one
-such layer-step; steps rotate over the 32 layers of the model (4 GiB of K/V)
-so the 256 MB Infinity Cache cannot hold the working set.
+such layer-step; steps rotate over 16 layers of 128 MiB of K/V each (2 GiB,
+eight times the 256 MB Infinity Cache), every other config over >= 2 GiB
+too when its steps reach that many layers.
 
 Timing: the K timed steps are captured once into a HIP graph (rotating over
 the layers) and replayed between two HIP events on the launch stream, so a
 step costs its kernels plus the graph's inter-kernel gaps, without Python or
 launch overhead; eager per-launch event durations are reported beside it.
 
-Also reported: us per layer-step for all five BASELINE configs, the verify
-(k=4) / single-query step ratio at 4K, the cost of an O(1) rollback, the
-roofline of the dominant kernel, and the CPU oracle (oracle/sde_oracle.c,
-OpenMP) timed on a bounded sample.
+Also reported: us per layer-step for all five BASELINE configs, each beside
+the CPU oracle's time for the same layer-step (oracle/sde_oracle.c, OpenMP,
+a bounded sample), the verify (k=4) / single-query step ratio at 4K, the cost
+of an O(1) rollback, the grid-cooperative device function
+(sde::device_flash_attention_gqa_grid, through its test kernel) at the 4K
+verify and 32K shapes, the roofline of the dominant kernel against both the
+8 TB/s peak and a device copy measured in the same process, and the
+persistent speculative loop's time per round.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
        [--calibrate-copy MiB]  (adds plain device copies of known size, the
@@ -40,7 +45,18 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E spec sheet
+ROTATE_BYTES = 2 << 30  # K/V bytes the timed steps rotate over (8x the Infinity Cache)
+DTYPE = ("fp16 K/V; q and the softmax weights enter the MFMA as fp16 hi+lo pairs "
+         "(fp32-level products), fp32 accumulate")
 HEADLINE = "llama3_8b_32k"
+# configs entries named differently from their workload
+CONFIG_WORKLOAD = {"llama3_8b_4k_decode": "llama3_8b_verify",
+                   "llama3_8b_4k_attn": "llama3_8b_verify",
+                   "llama3_8b_verify_fused": "llama3_8b_verify",
+                   "llama3_8b_4k_decode_fused": "llama3_8b_verify",
+                   "qwen25_7b_selfspec_verify": "qwen25_7b_selfspec",
+                   "qwen25_7b_selfspec_draft": "qwen25_7b_selfspec",
+                   "qwen25_7b_selfspec_verify_fused": "qwen25_7b_selfspec"}
 KERNEL = "attn_mfma_kernel"  # the headline (1-query, GQA 4) path
 
 
@@ -149,9 +165,9 @@ def bench_config(torch, W, w, steps, warmup, mode):
     n_app = 0 if mode == "attn" else n_q
     pos_base = w.ctx if mode != "attn" else w.l_max - 1
     l_max = pos_base + n_q
-    # rotate over enough layers to exceed the Infinity Cache (>= 512 MiB)
+    # rotate over distinct layers holding ROTATE_BYTES of K/V in all
     per_layer = 4 * w.kv_dim * l_max
-    n_layers = max(1, min(w.n_layers, math.ceil(512 * 2 ** 20 / per_layer)))
+    n_layers = max(1, min(4096, math.ceil(ROTATE_BYTES / per_layer)))
     nblk = -(-l_max // w.block_size)
     pool_blocks = max(w.pool_blocks, n_layers * nblk)
     cache = make_rotation_cache(torch, W, w, n_layers, l_max, pool_blocks, w.seed)
@@ -339,12 +355,180 @@ def bench_sdec_load(torch, layers=2):
         shutil.rmtree(tmp, ignore_errors=True)
 
 
+def measured_hbm(torch, nbytes=2 << 30, reps=5):
+    """Same-process reference points for the HBM roofline: the best of
+    `reps` device-to-device copies of an nbytes buffer (read + write bytes
+    over the time) and the best of `reps` fp32 sums over it (read bytes over
+    the time), each between HIP events on the current stream."""
+    src = torch.ones(nbytes // 4, device="cuda")
+    dst = torch.empty_like(src)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def best(fn):
+        fn()
+        torch.cuda.synchronize()
+        t = []
+        for _ in range(reps):
+            e0.record()
+            fn()
+            e1.record()
+            torch.cuda.synchronize()
+            t.append(e0.elapsed_time(e1) * 1e-3)
+        return min(t)
+    t_copy = best(lambda: dst.copy_(src))
+    t_read = best(lambda: src.sum())
+    del src, dst
+    torch.cuda.empty_cache()
+    return dict(copy_gbps=round(2 * nbytes / t_copy / 1e9, 1),
+                read_gbps=round(nbytes / t_read / 1e9, 1), bytes=nbytes,
+                how="best of 5: torch copy_ of a 2 GiB fp32 buffer (read+write bytes), "
+                    "torch sum over it (read bytes)")
+
+
+def cpu_threads():
+    return int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
+
+
+def cpu_config(W, w, mode, seconds):
+    """The CPU oracle on one layer-step of `mode` (bench_config's modes) at
+    workload w's shape: the append of the window (fp32 -> fp16) and the
+    literal fp32 tile restatement of attention.h (OpenMP over (query, head)
+    pairs), repeated for about `seconds`.  Fused modes time the same two
+    steps (the oracle has no fused form; RoPE is excluded)."""
+    from oracle import paged_kv as O
+    threads = cpu_threads()
+    n_q = 1 if mode.startswith(("attn", "decode")) else w.n_queries
+    n_app = 0 if mode == "attn" else n_q
+    pos_base = w.ctx if mode != "attn" else w.l_max - 1
+    l_max = pos_base + n_q
+    rng = np.random.default_rng(w.seed)
+    nblk = -(-l_max // w.block_size)
+    pool = 2 * nblk
+    m = O.PagedKVModel(1, w.kv_dim, nblk, w.block_size, pool)
+    m.set_block_table(0, rng.permutation(pool)[:nblk])
+    m.pool[...] = (rng.standard_normal(m.pool.shape, dtype=np.float32)
+                   .astype(np.float16).view(np.uint16))
+    q = W.queries(rng, n_q, w.nh, w.dph)
+    k, v = W.new_kv(rng, max(n_app, 1), w.kv_dim)
+    reps = 0
+    t0 = time.perf_counter()
+    while True:
+        if n_app:
+            m.append(0, k[:n_app], v[:n_app], pos_base)
+        m.attention(0, q, w.nh, w.nkv, w.dph, pos_base, mode="tiled", threads=threads)
+        reps += 1
+        if time.perf_counter() - t0 >= seconds:
+            break
+    dt = (time.perf_counter() - t0) / reps
+    nbytes = w.algorithmic_bytes(l_max=l_max, n_app=n_app, n_queries=n_q)
+    return dict(us_per_layer_step=round(dt * 1e6, 1), gbps=round(nbytes / dt / 1e9, 3),
+                reps=reps, cores=threads)
+
+
+def bench_grid_device_fn(torch, W, steps, warmup):
+    """sde::device_flash_attention_gqa_grid as a persistent kernel would
+    call it (every block of a one-block-per-CU grid of 512 threads; 8-wave
+    staging), launched by the device-API test library's grid_attention
+    kernel, at the 4K verify window (5 queries over 4101 keys) and the 32K
+    decode (1 query over 32768 keys), graph-replayed over >= 2 GiB like the
+    library's kernel."""
+    import ctypes
+    from speculative_decode_engine_amd import _native
+    lib_path = ROOT / "tests" / "device" / "libsde_device_test.so"
+    if not lib_path.exists():
+        return dict(error=f"{lib_path} not built")
+    lib = ctypes.CDLL(str(lib_path))
+    fn = lib.sdet_grid_attention
+    fn.restype = ctypes.c_int
+    n_cus = torch.cuda.get_device_properties(0).multi_processor_count
+    out = {}
+    for name, mode in (("llama3_8b_verify", "verify"), ("llama3_8b_32k", "attn")):
+        w = W.CONFIGS[name]
+        n_q = 1 if mode == "attn" else w.n_queries
+        pos_base = w.ctx if mode != "attn" else w.l_max - 1
+        l_max = pos_base + n_q
+        per_layer = 4 * w.kv_dim * l_max
+        n_layers = max(1, min(4096, math.ceil(ROTATE_BYTES / per_layer)))
+        nblk = -(-l_max // w.block_size)
+        cache = make_rotation_cache(torch, W, w, n_layers, l_max,
+                                    max(w.pool_blocks, n_layers * nblk), w.seed)
+        view = cache.view()
+        gen = torch.Generator(device="cuda")
+        gen.manual_seed(w.seed + 200)
+        q = torch.randn(n_layers, n_q, w.nh * w.dph, device="cuda", generator=gen)
+        o = torch.empty(n_q, w.nh * w.dph, device="cuda")
+        ws_bytes = int(_native.load().sde_grid_attention_workspace_size(w.nh, w.nkv, w.dph, n_q,
+                                                                        l_max))
+        ws = torch.zeros(ws_bytes // 4 + 1, dtype=torch.int32, device="cuda")
+        status = torch.zeros(n_cus, dtype=torch.int32, device="cuda")
+
+        def step(i):
+            l = i % n_layers
+            s = torch.cuda.current_stream().cuda_stream
+            rc = fn(ctypes.byref(view), l, ctypes.c_void_p(q[l].data_ptr()),
+                    ctypes.c_void_p(o.data_ptr()), w.nh, w.nkv, w.dph, pos_base, n_q, n_cus, 512,
+                    8, ctypes.c_void_p(ws.data_ptr()), ctypes.c_size_t(ws_bytes),
+                    ctypes.c_void_p(status.data_ptr()), ctypes.c_void_p(s))
+            if rc != 0:
+                raise RuntimeError(f"sdet_grid_attention: {rc}")
+        ms = graph_step_ms(torch, step, steps, warmup)
+        torch.cuda.synchronize()
+        st = int(status.abs().max().item())
+        nbytes = w.algorithmic_bytes(l_max=l_max, n_app=0, n_queries=n_q)
+        out[f"{name}_{mode}"] = dict(us=round(ms * 1e3, 3), queries=n_q, keys=l_max,
+                                     gbps=round(nbytes / (ms * 1e-3) / 1e9, 1), blocks=n_cus,
+                                     threads=512, status=st)
+        cache.free()
+    return out
+
+
+def bench_spec_loop(torch, max_new=64):
+    """The persistent speculative loop (sde_spec_loop_greedy, one cooperative
+    launch): us per round and per emitted token at a Llama-3-8B head shape
+    (32 q / 8 KV heads, dph 128), 4 layers, 4K context, vocabulary 4096,
+    greedy (k = 0) and self-speculative (k = 4, one draft layer)."""
+    from speculative_decode_engine_amd import KVCache
+    from speculative_decode_engine_amd.spec_loop import SpecLoopModel, spec_loop_greedy
+    L, nh, nkv, dph, V, P0 = 4, 32, 8, 128, 4096, 4096
+    g = torch.Generator(device="cuda")
+    g.manual_seed(31)
+    base_q = torch.randn(V, nh * dph, device="cuda", generator=g) * 2.0
+    base_k = torch.randn(V, nkv * dph, device="cuda", generator=g)
+    base_v = torch.randn(V, nkv * dph, device="cuda", generator=g)
+    mk = lambda b: (b[None] + 0.1 * b.abs().mean() * torch.randn(L, *b.shape, device="cuda",
+                                                                   generator=g)).contiguous()
+    model = SpecLoopModel(mk(base_q), mk(base_k), mk(base_v),
+                          (torch.randn(nh * dph, V, device="cuda", generator=g) /
+                           math.sqrt(nh * dph)).half(), nh, nkv, dph)
+    out = {}
+    for k in (0, 4):
+        nblk = -(-(P0 + max_new + k + 1) // 16)
+        cache = KVCache(L, nkv * dph, nblk, 16, L * nblk)
+        toks = torch.randint(0, V, (P0,), device="cuda", generator=g)
+        for l in range(L):
+            cache.append(l, model.emb_k[l][toks].contiguous(), model.emb_v[l][toks].contiguous(),
+                         0)
+        cache.set_seq_len(P0)
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        res = spec_loop_greedy(cache, model, 7, k, 1 if k else 0, max_new)
+        dt = time.perf_counter() - t
+        out[f"k{k}"] = dict(rounds=res.rounds, tokens=len(res.tokens),
+                            accepted=sum(res.accepted), status=res.status,
+                            us_per_round=round(dt / max(res.rounds, 1) * 1e6, 1),
+                            us_per_token=round(dt / max(len(res.tokens), 1) * 1e6, 1))
+        cache.free()
+    out["shape"] = dict(layers=L, nh=nh, nkv=nkv, dph=dph, vocab=V, context=P0,
+                        n_draft=1, note="wall time of one launch incl. launch and sync")
+    return out
+
+
 def cpu_baseline(W, w, seconds):
     """The CPU oracle's tile restatement of attention.h (OpenMP over
     (query, head) pairs) on one 32K-key layer-step of the same shape, run
     repeatedly for about `seconds`."""
     from oracle import paged_kv as O
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
+    threads = cpu_threads()
     rng = np.random.default_rng(w.seed)
     l_max = w.l_max
     nblk = l_max // w.block_size
@@ -455,6 +639,10 @@ def main():
         log("[bench] matvec", json.dumps(extra["matvec"]))
         extra["sdec_load"] = bench_sdec_load(torch)
         log("[bench] sdec load", json.dumps(extra["sdec_load"]))
+        extra["grid_device_fn"] = bench_grid_device_fn(torch, W, steps, warmup)
+        log("[bench] grid device fn", json.dumps(extra["grid_device_fn"]))
+        extra["spec_loop"] = bench_spec_loop(torch)
+        log("[bench] spec loop", json.dumps(extra["spec_loop"]))
         for k_, v_ in configs.items():
             log(f"[bench] {k_}: {v_['us_per_layer_step']} us/layer-step, {v_['gbps']} GB/s")
 
@@ -463,17 +651,31 @@ def main():
     kernel_us = head["us_per_layer_step"]
     nbytes = head["algorithmic_bytes"]
     achieved = nbytes / (kernel_us * 1e-6) / 1e9
+    hbm = measured_hbm(torch)
+    log("[bench] hbm", json.dumps(hbm))
     roofline = dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBPS, unit="GB/s",
                     frac=round(achieved / HBM_PEAK_GBPS, 4),
                     traffic=measured_traffic(HEADLINE), kernel=KERNEL,
                     bytes_per_launch=nbytes, kernel_us=kernel_us,
-                    kernel_us_eager_events=head.get("kernel_us_events"))
+                    kernel_us_eager_events=head.get("kernel_us_events"),
+                    measured_copy_gbps=hbm["copy_gbps"], measured_read_gbps=hbm["read_gbps"],
+                    frac_of_measured_copy=round(achieved / hbm["copy_gbps"], 4),
+                    frac_of_measured_read=round(achieved / hbm["read_gbps"], 4))
 
     cpu = None
     if not args.no_cpu:
         log("[bench] cpu baseline ...")
         cpu = cpu_baseline(W, w, args.cpu_seconds)
         log("[bench] cpu", json.dumps(cpu))
+        # every other config's layer-step on the CPU oracle too (bounded samples)
+        for name, res in configs.items():
+            if name == HEADLINE:
+                continue
+            wl = W.CONFIGS[CONFIG_WORKLOAD.get(name, name)]
+            c = cpu_config(W, wl, res["mode"], min(3.0, args.cpu_seconds))
+            res["cpu"] = c
+            res["gpu_over_cpu"] = round(c["us_per_layer_step"] / res["us_per_layer_step"], 1)
+            log(f"[bench] cpu {name}: {c['us_per_layer_step']} us")
 
     line = {
         "metric": "paged decode-attn us/layer + HBM GB/s (% peak) at ctx 4K/32K, verify k=4",
@@ -486,7 +688,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16 K/V, f32 q/accumulate",
+        "dtype": DTYPE,
         "data": "synthetic: N(0,1) fp16 K/V filling the pool, N(0,1) fp32 q, seeded "
                 "fragmented block tables",
         "config": {"workload": HEADLINE, "keys": head["keys"], "nh": w.nh, "nkv": w.nkv,

@@ -23,7 +23,6 @@
 // logits.  K/V bytes therefore depend on (token, position) alone, so greedy
 // speculation must leave exactly the greedy decoder's bytes below seq_len.
 #include <hip/hip_runtime.h>
-#include <hip/hip_cooperative_groups.h>
 
 #include <cstdint>
 
@@ -35,9 +34,8 @@
 namespace sde {
 namespace loop {
 
-namespace cg = cooperative_groups;
-
 constexpr int kThreads = 512;
+constexpr uint32_t kSpinLimit = 1u << 18;  // polls of a grid barrier before it gives up
 constexpr int kMaxWindow = 16;  // k + 1 rows (device_matvec_grid's limit)
 
 // Words of d_state.
@@ -70,13 +68,14 @@ struct LoopArgs {
   size_t attn_ws_bytes;
   void* mv_ws;
   size_t mv_ws_bytes;
+  uint32_t* bar;  // [0] arrivals (zero at rest), [1] generation
 };
 
 // Workspace layout: attention workspace (counters first), projection
 // workspace (counters first), then the loop's buffers, each 256-byte
 // aligned.
 struct Layout {
-  size_t attn, mv, q, h, logits, tokens, total;
+  size_t attn, mv, q, h, logits, tokens, bar, total;
 };
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -91,22 +90,57 @@ inline Layout layout(int nh, int nkv, int dph, int vocab, int k, int cap) {
   l.h = l.q + align256(M * d * sizeof(float));
   l.logits = l.h + align256(M * d * sizeof(float));
   l.tokens = l.logits + align256((size_t)M * vocab * sizeof(float));
-  l.total = l.tokens + align256(2 * M * sizeof(int32_t));
+  l.bar = l.tokens + align256(2 * M * sizeof(int32_t));
+  l.total = l.bar + 256;
   return l;
 }
 
-// Stores of one phase reach the device coherence point and the next
-// phase's loads miss stale lines of their XCD's L2: a device-scope fence on
-// both sides of the grid barrier.
-__device__ __forceinline__ void barrier(cg::grid_group& g) {
-  __threadfence();
-  g.sync();
-  __threadfence();
+// Grid barrier between the loop's phases.  One thread per block: a
+// device-scope release fence (its XCD's L2 written back, so the block's
+// stores of the phase reach the coherence point), an arrival on a counter,
+// a wait for the generation word to move, and an acquire fence (stale lines
+// of the XCD's L2 and the CU's L1 dropped); the block's own barriers order
+// its other waves around that thread.  The last arrival resets the counter
+// and moves the generation.  A wait gives up after kSpinLimit polls and
+// records SDE_ERR_HIP, so a broken barrier ends the launch instead of
+// hanging it (every later round check sees the status and exits).
+__device__ __forceinline__ void barrier(const LoopArgs& a) {
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's stores have reached its XCD's L2
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t gen = __hip_atomic_load(a.bar + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    const uint32_t prev =
+        __hip_atomic_fetch_add(a.bar, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (prev == gridDim.x - 1) {
+      __hip_atomic_store(a.bar, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(a.bar + 1, gen + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+      uint32_t polls = 0;
+      while (__hip_atomic_load(a.bar + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gen) {
+        if (++polls == kSpinLimit) {
+          atomicCAS(reinterpret_cast<int*>(a.state + kStatus), SDE_OK, SDE_ERR_HIP);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  }
+  __syncthreads();
 }
 
+// The loop's control words (seq_len, tokens emitted, status) are written
+// and read with device-scope atomics, so every block takes the same exits
+// whatever the caches hold: a block that left the loop early would leave the
+// others waiting at a grid barrier.
 __device__ __forceinline__ int load_word(const int32_t* p) {
   return __builtin_amdgcn_readfirstlane(
       __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+
+__device__ __forceinline__ void store_word(int32_t* p, int x) {
+  __hip_atomic_store(p, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ __forceinline__ void note_error(const LoopArgs& a, int st) {
@@ -200,48 +234,51 @@ __device__ void argmax_rows(const LoopArgs& a, int n, int dst) {
 
 // Layers [lo, hi) on window rows [r0, r0+n) at positions pos0 + row:
 // append, q, grid attention; h_buf rows hold the last layer's output.
-__device__ void run_layers(const LoopArgs& a, cg::grid_group& g, int lo, int hi, int r0, int n,
+__device__ void run_layers(const LoopArgs& a, int lo, int hi, int r0, int n,
                            int pos0) {
   for (int l = lo; l < hi; l++) {
     append_rows(a, l, r0, n, pos0);
     build_q(a, l, r0, n, l > 0);
-    barrier(g);
+    barrier(a);
     const int st = device_flash_attention_gqa_grid<4>(
         a.q_buf + (size_t)r0 * a.d, a.h_buf + (size_t)r0 * a.d, a.kv, l, a.m.n_heads,
         a.m.n_kv_heads, a.m.head_dim, pos0 + r0, n, a.attn_ws, a.attn_ws_bytes);
     note_error(a, st);
-    barrier(g);
+    barrier(a);
   }
 }
 
 // Logits of window rows [r0, r0+n) from their h_buf rows, then their
 // argmaxes into tokens[dst + row].
-__device__ void decide(const LoopArgs& a, cg::grid_group& g, int r0, int n, int dst) {
+__device__ void decide(const LoopArgs& a, int r0, int n, int dst) {
   const int st = device_matvec_grid(a.h_buf + (size_t)r0 * a.d, a.m.head, a.logits, a.d,
                                     a.m.vocab, n, 0, a.mv_ws, a.mv_ws_bytes);
   note_error(a, st);
-  barrier(g);
+  barrier(a);
   argmax_rows(a, n, dst);
-  barrier(g);
+  barrier(a);
+}
+
+// Before the loop (the launch before it on the stream): the device
+// functions' arrival counters and the barrier's arrivals at zero, the state
+// words cleared, window token 0 = the anchor.
+__global__ void spec_loop_init_kernel(LoopArgs a) {
+  uint32_t* c = static_cast<uint32_t*>(a.attn_ws);
+  for (int i = threadIdx.x; i < kGridCounters; i += blockDim.x) c[i] = 0u;
+  uint32_t* mc = static_cast<uint32_t*>(a.mv_ws);
+  const int nmc = (int)(mv::mv_counter_bytes(a.m.vocab, a.k + 1) / sizeof(uint32_t));
+  for (int i = threadIdx.x; i < nmc; i += blockDim.x) mc[i] = 0u;
+  if (threadIdx.x == 0) {
+    a.bar[0] = 0u;
+    a.bar[1] = 0u;
+    a.tokens[0] = a.state[kAnchor];
+    for (int i = kEmitted; i < kStateWords; i++) a.state[i] = 0;
+  }
 }
 
 __global__ __launch_bounds__(kThreads) void spec_loop_kernel(LoopArgs a) {
-  cg::grid_group g = cg::this_grid();
   const int M = a.k + 1;
   const int n_layers = a.kv.n_layers;
-  // The device functions' arrival counters start at zero.
-  if (blockIdx.x == 0) {
-    uint32_t* c = static_cast<uint32_t*>(a.attn_ws);
-    for (int i = threadIdx.x; i < kGridCounters; i += blockDim.x) c[i] = 0u;
-    uint32_t* mc = static_cast<uint32_t*>(a.mv_ws);
-    const int nmc = (int)(mv::mv_counter_bytes(a.m.vocab, M) / sizeof(uint32_t));
-    for (int i = threadIdx.x; i < nmc; i += blockDim.x) mc[i] = 0u;
-    if (threadIdx.x == 0) {
-      a.tokens[0] = a.state[kAnchor];
-      for (int i = kEmitted; i < kStateWords; i++) a.state[i] = 0;
-    }
-  }
-  barrier(g);
 
   for (int round = 0;; round++) {
     // Every block reads the same words after the barrier: the loop's exits
@@ -250,7 +287,7 @@ __global__ __launch_bounds__(kThreads) void spec_loop_kernel(LoopArgs a) {
     if (load_word(a.state + kEmitted) >= a.max_new || load_word(a.state + kStatus) != SDE_OK)
       break;
     if (P < 0 || P + M > a.cap) {
-      if (blockIdx.x == 0 && threadIdx.x == 0) a.state[kStatus] = SDE_ERR_CAPACITY;
+      if (blockIdx.x == 0 && threadIdx.x == 0) store_word(a.state + kStatus, SDE_ERR_CAPACITY);
       break;
     }
     if (a.k > 0) {
@@ -258,20 +295,21 @@ __global__ __launch_bounds__(kThreads) void spec_loop_kernel(LoopArgs a) {
       // at P+i, one token at a time; the first k outputs propose window
       // token i+1.
       for (int i = 0; i < M; i++) {
-        run_layers(a, g, 0, a.n_draft, i, 1, P);
-        if (i < a.k) decide(a, g, i, 1, i + 1);
+        run_layers(a, 0, a.n_draft, i, 1, P);
+        if (i < a.k) decide(a, i, 1, i + 1);
       }
     }
     // Verify (model.cu:838-890): the remaining layers over the whole
     // window, then the target's token for every row.
-    run_layers(a, g, a.n_draft, n_layers, 0, M, P);
-    decide(a, g, 0, M, M);
+    run_layers(a, a.n_draft, n_layers, 0, M, P);
+    decide(a, 0, M, M);
     // Greedy accept and O(1) rewind (kernels.cu:3050-3072).
     if (blockIdx.x == 0 && threadIdx.x == 0) {
       const int E = a.state[kEmitted];
       const SpecAccept r = spec_accept_greedy(a.tokens + 1, a.tokens + M, a.k, P, P, a.kv,
                                               nullptr, a.emitted + E);
-      a.state[kEmitted] = E + r.n_accepted + 1;
+      store_word(a.kv.seq_len, r.target_seq);  // (spec_accept_greedy wrote it plainly)
+      store_word(a.state + kEmitted, E + r.n_accepted + 1);
       a.state[kAnchor] = r.bonus;
       a.state[kRounds] = round + 1;
       a.state[kProposed] += a.k;
@@ -279,7 +317,7 @@ __global__ __launch_bounds__(kThreads) void spec_loop_kernel(LoopArgs a) {
       a.accepted[round] = r.n_accepted;
       a.tokens[0] = r.bonus;
     }
-    barrier(g);
+    barrier(a);
   }
 }
 
@@ -359,6 +397,11 @@ int sde_spec_loop_greedy(sde_kv_cache* cache, const sde_loop_model* model, int k
   a.h_buf = reinterpret_cast<float*>(ws + lay.h);
   a.logits = reinterpret_cast<float*>(ws + lay.logits);
   a.tokens = reinterpret_cast<int32_t*>(ws + lay.tokens);
+  a.bar = reinterpret_cast<uint32_t*>(ws + lay.bar);
+  spec_loop_init_kernel<<<1, 256, 0, static_cast<hipStream_t>(stream)>>>(a);
+  if (hipGetLastError() != hipSuccess) return SDE_ERR_HIP;
+  // A cooperative launch: every block resident at once, which the grid
+  // barrier needs.
   void* args[] = {&a};
   const hipError_t e = hipLaunchCooperativeKernel(
       reinterpret_cast<const void*>(spec_loop_kernel), dim3(cache->n_cus), dim3(kThreads), args,
