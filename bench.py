@@ -73,6 +73,9 @@ def parse_args():
     p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="approximate CPU work of the baseline sample")
     p.add_argument("--only-headline", action="store_true")
+    p.add_argument("--only", default=None, metavar="CONFIG",
+                   help="time one configs entry (e.g. llama3_8b_verify, "
+                        "qwen25_7b_selfspec_verify_fused) and print its JSON (profiling)")
     p.add_argument("--only-matvec", action="store_true",
                    help="time only the output projection (sde_matvec) and print its JSON")
     p.add_argument("--matvec-shape", default=None,
@@ -594,6 +597,25 @@ def main():
         else:
             print(json.dumps({"matvec": bench_matvec(torch, steps, warmup),
                               "sdec_load": bench_sdec_load(torch)}), flush=True)
+        if args.calibrate_copy:
+            n = args.calibrate_copy * 2 ** 20 // 4
+            src = torch.ones(n, device="cuda")
+            dst = torch.empty_like(src)
+            for _ in range(5):
+                dst.copy_(src)
+            torch.cuda.synchronize()
+        return
+
+    if args.only:
+        modes = {"llama3_8b_verify": "verify", "llama3_8b_4k_decode": "decode",
+                 "llama3_8b_4k_attn": "attn", "llama3_8b_verify_fused": "verify_fused",
+                 "llama3_8b_4k_decode_fused": "decode_fused", "tiny": "decode",
+                 "tinyllama": "decode", "qwen25_7b_selfspec_verify": "verify",
+                 "qwen25_7b_selfspec_draft": "decode",
+                 "qwen25_7b_selfspec_verify_fused": "verify_fused", HEADLINE: "attn"}
+        wl = W.CONFIGS[CONFIG_WORKLOAD.get(args.only, args.only)]
+        res = bench_config(torch, W, wl, steps, warmup, modes[args.only])
+        print(json.dumps({args.only: res}), flush=True)
         if args.calibrate_copy:
             n = args.calibrate_copy * 2 ** 20 // 4
             src = torch.ones(n, device="cuda")
