@@ -7,6 +7,7 @@
 #include <cstdint>
 #include <vector>
 
+#include "sde/spec_device.hpp"
 #include "sde_paged_kv.h"
 
 // The opaque cache handle.  Device memory: pool (owned or borrowed), the
@@ -38,13 +39,10 @@ struct sde_kv_cache {
 };
 
 namespace sde {
+// Attention arrival counters per cache; after them the stochastic
+// acceptance's scratch (kSpecScratchWords, sde/spec_device.hpp: arrival
+// counters zero at rest, per-row results and per-slice statistics).
 constexpr int kMaxAttnCounters = 4096;
-// Words after the attention counters: the stochastic acceptance's arrival
-// counters (zero at rest), per-row results and per-slice statistics of one
-// call (rows <= kSpecMaxK + 1, slices <= kSpecMaxSlices).
-constexpr int kSpecMaxK = 64;
-constexpr int kSpecMaxSlices = 64;
-constexpr int kSpecScratchWords = 1 + 3 * (kSpecMaxK + 1) + 6 * (kSpecMaxK + 1) * kSpecMaxSlices;
 }  // namespace sde
 
 namespace sde {

@@ -8,6 +8,7 @@
 #include <hip/hip_runtime.h>
 
 #include "sde/attention_device.hpp"
+#include "sde/spec_device.hpp"
 #include "sde/kv_cache.hpp"
 #include "sde/matvec_device.hpp"
 
@@ -181,6 +182,21 @@ __global__ void grid_matvec_kernel(const float* x, const uint16_t* W, float* out
   if (threadIdx.x == 0) status[blockIdx.x] = st;
 }
 
+// Every block of a cooperative grid calls the grid form of the stochastic
+// acceptance, with the cooperative-groups grid barrier between its passes.
+__global__ void stochastic_grid_kernel(const float* tl, const float* dl, const int32_t* drafts,
+                                       int k, int V, float tt, float td, uint64_t seed,
+                                       uint64_t* offset, int ts, int ds, sde_kv_view target,
+                                       sde_kv_view draft, int has_draft, int32_t* result, void* ws,
+                                       size_t ws_bytes, int* status) {
+  namespace cg = cooperative_groups;
+  cg::grid_group grid = cg::this_grid();
+  const int st = sde::device_spec_accept_stochastic_grid(
+      tl, dl, drafts, k, V, tt, td, seed, offset, ts, ds, target, has_draft ? &draft : nullptr,
+      result, ws, ws_bytes, [&] { grid.sync(); });
+  if (threadIdx.x == 0) status[blockIdx.x] = st;
+}
+
 int status_of(hipError_t e) { return e == hipSuccess ? 0 : 6; }
 
 }  // namespace
@@ -253,6 +269,30 @@ int sdet_persistent_loop(const sde_kv_view* kv, const int* d_pos, int n_steps, i
   void* args[] = {&view, (void*)&d_pos, &n_steps, &M, &nh, &nkv, &dph, (void*)&k, (void*)&v,
                   (void*)&q, &out, &ws, &ws_bytes, &status};
   return status_of(hipLaunchCooperativeKernel((const void*)persistent_loop_kernel, dim3(blocks),
+                                              dim3(threads), args, 0, (hipStream_t)stream));
+}
+
+// Cooperative launch of stochastic_grid_kernel (blocks all resident).
+int sdet_stochastic_grid(const float* tl, const float* dl, const int32_t* drafts, int k, int V,
+                         float tt, float td, uint64_t seed, uint64_t* offset, int ts, int ds,
+                         const sde_kv_view* target, const sde_kv_view* draft, int32_t* result,
+                         void* ws, size_t ws_bytes, int* status, int blocks, int threads,
+                         void* stream) {
+  if (!target || blocks < 1 || threads < 64 || threads > 1024) return 1;
+  int dev = 0, per_cu = 0, cus = 0, coop = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, stochastic_grid_kernel, threads, 0) !=
+          hipSuccess)
+    return 6;
+  if (!coop || blocks > per_cu * cus) return 2;
+  sde_kv_view t = *target;
+  sde_kv_view d = draft ? *draft : sde_kv_view{};
+  int has_draft = draft ? 1 : 0;
+  void* args[] = {(void*)&tl, (void*)&dl, (void*)&drafts, &k, &V, &tt, &td, &seed, &offset, &ts,
+                  &ds, &t, &d, &has_draft, &result, &ws, &ws_bytes, &status};
+  return status_of(hipLaunchCooperativeKernel((const void*)stochastic_grid_kernel, dim3(blocks),
                                               dim3(threads), args, 0, (hipStream_t)stream));
 }
 

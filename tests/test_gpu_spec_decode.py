@@ -228,3 +228,68 @@ def test_device_stochastic_errors(gpu):
         _stoch(tc, None, tl[:5], tl[:4], [0] * 4, 4, 28, 0, 1, off)  # past the capacity
     assert int(off.item()) == 0
     tc.free()
+
+
+# ---- the grid device function form (sde::device_spec_accept_stochastic_grid) --
+
+def _grid_lib():
+    from pathlib import Path
+    import ctypes
+    from speculative_decode_engine_amd import _native as N
+    p = Path(__file__).resolve().parent / "device" / "libsde_device_test.so"
+    if not p.exists():
+        pytest.fail(f"{p} missing: run __graft_entry__.build()")
+    lib = ctypes.CDLL(str(p))
+    vp, i, f32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_float
+    view_p = ctypes.POINTER(N.KVView)
+    lib.sdet_stochastic_grid.argtypes = [vp, vp, vp, i, i, f32, f32, ctypes.c_uint64, vp, i, i,
+                                         view_p, view_p, vp, vp, ctypes.c_size_t, vp, i, i, vp]
+    lib.sdet_stochastic_grid.restype = i
+    return lib
+
+
+@pytest.mark.parametrize("V,k,tt,td,blocks,threads", [
+    (1000, 4, 1.0, 1.0, 64, 512), (128256, 4, 1.0, 0.8, 256, 512), (128256, 8, 0.7, 1.3, 37, 256),
+    (50000, 0, 1.0, 1.0, 13, 1024), (300, 3, 1e-8, 1.0, 3, 256), (8, 1, 1.0, 1.0, 1, 512)])
+def test_grid_stochastic_equals_the_c_abi(gpu, V, k, tt, td, blocks, threads):
+    """Every block of a cooperative grid (any size, 256-1024 threads) runs the
+    grid form; its result, rewinds and call index equal sde_spec_accept_stochastic's
+    bit for bit on the same inputs, seed and offset, call after call."""
+    import ctypes
+    from speculative_decode_engine_amd import spec_accept_stochastic
+    case_banner("grid stochastic", V, k, tt, td, blocks, threads)
+    lib = _grid_lib()
+    rng = np.random.default_rng(V + 7 * k + threads)
+    tca, dca = KVCache(1, 64, 8, 16, 8), KVCache(1, 64, 8, 16, 8)
+    tcb, dcb = KVCache(1, 64, 8, 16, 8), KVCache(1, 64, 8, 16, 8)
+    off_a = torch.zeros(1, dtype=torch.int64, device="cuda")
+    off_b = torch.zeros(1, dtype=torch.int64, device="cuda")
+    ws = torch.zeros(1 << 18, dtype=torch.int32, device="cuda")
+    status = torch.full((blocks,), -1, dtype=torch.int32, device="cuda")
+    res_b = torch.empty(k + 5, dtype=torch.int32, device="cuda")
+    tv, dv = tcb.view(), dcb.view()
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for call in range(6):
+        tl = torch.from_numpy((rng.standard_normal((k + 1, V)) * 3).astype(np.float32)).cuda()
+        dl = torch.from_numpy((tl.cpu().numpy()[:k] + rng.standard_normal((k, V)).astype(
+            np.float32))).cuda() if k else torch.zeros(1, 1, device="cuda")
+        drafts = torch.from_numpy(rng.integers(0, V, size=max(k, 1)).astype(np.int32)).cuda()
+        ts, ds = 20 + call, 10 + call
+        for c, n in ((tca, ts + k + 1), (dca, ds + k), (tcb, ts + k + 1), (dcb, ds + k)):
+            c.set_seq_len(n)
+        res_a = spec_accept_stochastic(tca, dca, tl, dl if k else None, drafts, k, ts, ds, 99,
+                                       off_a, tt, td)
+        rc = lib.sdet_stochastic_grid(tl.data_ptr(), dl.data_ptr(), drafts.data_ptr(), k, V, tt,
+                                      td, 99, off_b.data_ptr(), ts, ds, ctypes.byref(tv),
+                                      ctypes.byref(dv), res_b.data_ptr(), ws.data_ptr(),
+                                      ws.numel() * 4, status.data_ptr(), blocks, threads, s)
+        assert rc == 0
+        torch.cuda.synchronize()
+        assert (status == 0).all()
+        n = int(res_a[0].item())  # entries past the emitted tokens are not written
+        assert torch.equal(res_a[:5 + n], res_b[:5 + n]), (res_a.tolist(), res_b.tolist())
+        assert int(off_a.item()) == int(off_b.item()) == call + 1
+        assert tcb.device_seq_len() == tca.device_seq_len()
+        assert dcb.device_seq_len() == dca.device_seq_len()
+    for c in (tca, dca, tcb, dcb):
+        c.free()
