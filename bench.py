@@ -269,7 +269,8 @@ def bench_matvec(torch, steps, warmup, only=None):
     (oracle_matvec, OpenMP on the host cores) timed beside the Llama-3-8B Wo."""
     from speculative_decode_engine_amd import matvec, matvec_workspace
     shapes = [("llama3_8b_wo", 1, 4096, 4096, 1), ("llama3_8b_wo_verify", 5, 4096, 4096, 0),
-              ("llama3_8b_w_down", 1, 14336, 4096, 1), ("qwen25_7b_wo", 1, 3584, 3584, 1),
+              ("llama3_8b_w_down", 1, 14336, 4096, 1), ("llama3_8b_w_down_verify", 5, 14336, 4096, 0),
+              ("qwen25_7b_wo", 1, 3584, 3584, 1),
               ("tinyllama_wo", 1, 2048, 2048, 1)]
     out = {}
     g = torch.Generator(device="cuda")

@@ -289,10 +289,83 @@ struct MvLds {
   int last;
 };
 
+// ---- matrix-core form for three or more rows of x ------------------------
+//
+// out^T[c][m] += W^T[c][r] . x^T[r][m] with v_mfma_f32_16x16x16_f16: each
+// wave stores a batch of its loads (16 rows of W x the tile's 256 columns,
+// in the load layout) into 8 KiB of its own LDS, with the 16-byte units of
+// row r at u ^ (r % 16), and reads it back transposed with
+// ds_read_b64_tr_b16: for column block cb, lane l (group g = l / 16, L =
+// l % 16) addresses row 4g + L/4, columns 16cb + 4(L%4) .. +3, and receives
+// column 16cb + L of rows 4g .. 4g+3 -- the A operand (i = column, k = row).
+// B = x^T: lane l holds x[l % 16][rows 4g .. 4g+3] as fp16 hi + lo parts
+// (two MFMAs, so the products carry x to ~2^-22 relative; the VALU form's
+// fp32 multiply-adds are exact products).  D leaves lane l columns 16cb +
+// 4g .. 4g+3 of row l % 16 of x.  Rows of a batch at or past the range end
+// load zeros (the raw buffer) and take x = 0.  Per batch and wave: 16 LDS
+// stores, 16 transposed reads and 32 MFMA, where the VALU form spends 8
+// multiply-adds per row of x and loaded 16 bytes.
+typedef _Float16 mv_h4 __attribute__((ext_vector_type(4)));
+typedef float mv_f4 __attribute__((ext_vector_type(4)));
+typedef short mv_s4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) mv_s4 mv_lds_s4;
+constexpr int kStageRows = kUnroll * kRowPhases;
+constexpr int kStageBytes = kStageRows * kCols * 2;
+constexpr int kColBlocks = kCols / 16;
+// The VALU form's LDS plus every wave's W staging area (which the
+// epilogue reuses for the rows' sums).
+template <int WAVES>
+struct MvMfmaLds {
+  MvLds<WAVES> base;
+  uint4 wst[WAVES][kStageBytes / 16];
+};
+__device__ __forceinline__ int mv_staged(int r, int u) { return r * (kCols * 2) + 16 * (u ^ (r & 15)); }
+template <int WAVES>
+__device__ __forceinline__ void mv_x_operand(const MvArgs& a, const float* xl, int xrows, int r0,
+                                             int r1, int rbase, int lane, mv_h4& xh, mv_h4& xo) {
+  const int m = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    const int lr = 4 * g + q;
+    const int row = rbase + (lr >> 1) * WAVES * kRowPhases + (lr & 1);
+    float v = 0.f;
+    if (m < a.M && row < r1) v = xl ? xl[m * xrows + row - r0] : a.x[(size_t)m * a.d_in + row];
+    asm("" : "+v"(v));  // rounded once: hi = fp16(v), lo = fp16(v - hi)
+    const _Float16 h = (_Float16)v;
+    xh[q] = h;
+    xo[q] = (_Float16)(v - (float)h);
+  }
+}
+template <int U>
+__device__ __forceinline__ void mv_stage(char* st, int rp, int lc, const uint4 (&w)[U]) {
+#pragma unroll
+  for (int u = 0; u < U; u++) *reinterpret_cast<uint4*>(st + mv_staged(2 * u + rp, lc)) = w[u];
+}
+__device__ __forceinline__ void mv_mfma_batch(const char* st, int lane, mv_h4 xh, mv_h4 xo,
+                                              mv_f4 (&c)[kColBlocks]) {
+  const int L = lane & 15, g = lane >> 4;
+  const int row = 4 * g + (L >> 2);
+  const int u0 = (L & 3) >> 1, sub = 8 * (L & 1);
+#pragma unroll
+  for (int cb = 0; cb < kColBlocks; cb++) {
+    const mv_s4 s = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (mv_lds_s4*)(st + mv_staged(row, 2 * cb + u0) + sub));
+    const mv_h4 w = __builtin_bit_cast(mv_h4, s);
+    c[cb] = __builtin_amdgcn_mfma_f32_16x16x16f16(w, xh, c[cb], 0, 0, 0);
+    c[cb] = __builtin_amdgcn_mfma_f32_16x16x16f16(w, xo, c[cb], 0, 0, 0);
+  }
+}
+
 // (column tile ct, row range ks) on the calling workgroup; every thread
 // calls it.  MB >= a.M rows of x are unrolled; waves at or past WAVES idle.
-template <int MB, int WAVES>
-__device__ __forceinline__ void mv_item(const MvArgs& a, int ct, int ks, MvLds<WAVES>& lds) {
+template <int MB, int WAVES, bool MFMA = false, class Lds>
+__device__ __forceinline__ void mv_item(const MvArgs& a, int ct, int ks, Lds& L) {
+  MvLds<WAVES>* lds_p;
+  if constexpr (MFMA)
+    lds_p = &L.base;
+  else
+    lds_p = &L;
+  MvLds<WAVES>& lds = *lds_p;
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int lane = threadIdx.x & 63;
   const int rp = lane / kLanesPerRow;  // row phase
@@ -303,10 +376,16 @@ __device__ __forceinline__ void mv_item(const MvArgs& a, int ct, int ks, MvLds<W
   const int r0 = ks * a.rows_per_split;
   const int r1 = min(a.d_in, r0 + a.rows_per_split);
   float acc[MB][8];
+  mv_f4 cm[MFMA ? kColBlocks : 1];
+  if constexpr (MFMA) {
 #pragma unroll
-  for (int m = 0; m < MB; m++)
+    for (int cb = 0; cb < kColBlocks; cb++) cm[cb] = mv_f4{0.f, 0.f, 0.f, 0.f};
+  } else {
 #pragma unroll
-    for (int j = 0; j < 8; j++) acc[m][j] = 0.f;
+    for (int m = 0; m < MB; m++)
+#pragma unroll
+      for (int j = 0; j < 8; j++) acc[m][j] = 0.f;
+  }
 
   // Several rows of x: stage the range's x in LDS when it fits.
   const int xrows = r1 - r0;
@@ -329,6 +408,23 @@ __device__ __forceinline__ void mv_item(const MvArgs& a, int ct, int ks, MvLds<W
     const int step = WAVES * U * kRowPhases;   // rows per batch of the workgroup
     const int last = (U - 1) * WAVES * kRowPhases + kRowPhases - 1;  // a batch's last row
     const int first = r0 + wave * kRowPhases;
+    if constexpr (MFMA) {
+      char* st = reinterpret_cast<char*>(L.wst[wave]);
+      for (int r = first; r < r1; r += 2 * step) {
+        uint4 wa[U], wb[U];
+        mv_load_batch<WAVES, U>(rows, r, wa);
+        mv_load_batch<WAVES, U>(rows, r + step, wb);
+        mv_h4 xh, xo;
+        mv_x_operand<WAVES>(a, xl, xrows, r0, r1, r, lane, xh, xo);
+        mv_stage<U>(st, rp, lc, wa);
+        mv_mfma_batch(st, lane, xh, xo, cm);
+        if (r + step < r1) {
+          mv_x_operand<WAVES>(a, xl, xrows, r0, r1, r + step, lane, xh, xo);
+          mv_stage<U>(st, rp, lc, wb);  // (a wave's LDS operations complete in order)
+          mv_mfma_batch(st, lane, xh, xo, cm);
+        }
+      }
+    } else {
     for (int r = first; r < r1; r += 2 * step) {
       uint4 wa[U], wb[U];
       mv_load_batch<WAVES, U>(rows, r, wa);
@@ -346,6 +442,7 @@ __device__ __forceinline__ void mv_item(const MvArgs& a, int ct, int ks, MvLds<W
     for (int m = 0; m < MB; m++)
 #pragma unroll
       for (int j = 0; j < 8; j++) acc[m][j] = mv_phase_sum(acc[m][j]);
+    }
   }
 
   // ---- waves -> one partial per (row of x, column) --------------------
@@ -356,12 +453,59 @@ __device__ __forceinline__ void mv_item(const MvArgs& a, int ct, int ks, MvLds<W
   // the barrier of row m+1 orders row m's sums before row m+2's stores.
   static_assert(kXStage >= WAVES * kCols, "second reduction buffer");
   const uint32_t part_bytes = (uint32_t)((size_t)a.splits * a.M * a.d_out * sizeof(float));
+  if constexpr (MFMA) {
+    // every row of x at once: lane l writes its columns of row l % 16 into
+    // [m][wave][kCols] over the W staging area (free once every wave is past
+    // the streaming loop), 16-byte unit u of row m at u ^ (m % 16) so the
+    // 16 rows of a store do not share banks; one barrier, then thread
+    // t < kCols/4 sums 4 columns over the waves for each row of x
+    static_assert(sizeof(L.wst) >= 8 * WAVES * kCols * sizeof(float), "row buffers");
+    float* red = reinterpret_cast<float*>(L.wst);
+    __syncthreads();
+    if (wave < WAVES && (lane & 15) < a.M) {
+#pragma unroll
+      for (int cb = 0; cb < kColBlocks; cb++)
+        *reinterpret_cast<mv_f4*>(red + ((lane & 15) * WAVES + wave) * kCols +
+                                  4 * ((4 * cb + (lane >> 4)) ^ (lane & 15))) = cm[cb];
+    }
+    __syncthreads();
+    const int t = threadIdx.x;
+    const int c = ct * kCols + 4 * t;
+    if (t < kCols / 4 && c < a.d_out) {
+#pragma unroll
+      for (int m = 0; m < MB; m++) {
+        if (m >= a.M) break;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int w = 0; w < WAVES; w++) {
+          const float4 r =
+              *reinterpret_cast<const float4*>(red + (m * WAVES + w) * kCols + 4 * (t ^ (m & 15)));
+          v.x += r.x;
+          v.y += r.y;
+          v.z += r.z;
+          v.w += r.w;
+        }
+        if (a.splits == 1)
+          mv_write_out(a, m, c, v);
+        else
+          mv_store_dev16(a.partials, part_bytes,
+                         (uint32_t)((((size_t)ks * a.M + m) * a.d_out + c) * sizeof(float)), v);
+      }
+    }
+  }
 #pragma unroll
   for (int m = 0; m < MB; m++) {
+    if constexpr (MFMA) break;
     if (m >= a.M) break;
     if (m == 0) __syncthreads();  // every wave is past the streaming loop
     float* red = (m & 1) ? lds.xs : lds.red;
-    if (wave < WAVES && rp == 0) {
+    if constexpr (MFMA) {
+      if (wave < WAVES && (lane & 15) == m) {
+#pragma unroll
+        for (int cb = 0; cb < kColBlocks; cb++)
+          *reinterpret_cast<mv_f4*>(red + wave * kCols + 16 * cb + 4 * (lane >> 4)) = cm[cb];
+      }
+    } else if (wave < WAVES && rp == 0) {
       float4* d = reinterpret_cast<float4*>(red + wave * kCols + lc * 8);
       d[0] = make_float4(acc[m][0], acc[m][1], acc[m][2], acc[m][3]);
       d[1] = make_float4(acc[m][4], acc[m][5], acc[m][6], acc[m][7]);

@@ -16,11 +16,20 @@ namespace mv {
 
 constexpr int kWaves = 8;
 
-// Workgroup (column tile x, row range y) of pass z (rows 8z.. of x).
+// Workgroup (column tile x, row range y) of pass z (rows 8z.. of x): one or
+// two rows of x on the VALU (8 or 16 multiply-adds per loaded 16 bytes keep
+// up with the loads), three or more on the matrix cores (measured: 5 rows
+// of a 4096 x 4096 projection 25.6 -> 21.6 us, 9 rows 34.4 -> 23.8, 5 rows
+// of the 14336 x 4096 W_down 103 -> 40.3; 2 rows 16.7 either way).
 template <int MB>
 __global__ __launch_bounds__(64 * kWaves) void matvec_kernel(MvArgs a) {
-  __shared__ MvLds<kWaves> lds;
-  mv_item<MB, kWaves>(mv_pass(a, blockIdx.z), blockIdx.x, blockIdx.y, lds);
+  if constexpr (MB <= 2) {
+    __shared__ MvLds<kWaves> lds;
+    mv_item<MB, kWaves>(mv_pass(a, blockIdx.z), blockIdx.x, blockIdx.y, lds);
+  } else {
+    __shared__ MvMfmaLds<kWaves> lds;
+    mv_item<MB, kWaves, true>(mv_pass(a, blockIdx.z), blockIdx.x, blockIdx.y, lds);
+  }
 }
 
 }  // namespace mv

@@ -5,9 +5,12 @@ accumulation -- device_matvec_partial(_accum) / device_matvec_batched
 
 Checked against the float64 product within 1e-5 x sum_r |x_r W_rc| (an
 fp32 summation bound; the C restatement of the reference's per-column loop
-sits within the same bound), exactly on the closed forms (identity weights,
-one-hot inputs), bit-identically across repeated calls (the partial sums
-are added in a fixed order), and at the reference's shapes: Llama-3-8B Wo
+sits within the same bound), on the closed forms (identity weights exactly
+for one or two rows of x, which run on the VALU, and within 2^-21 of x for
+three or more, which reach the matrix cores as fp16 hi + lo parts (or
+2^-25 absolute where lo is an fp16 subnormal); one-hot
+inputs exactly on both), bit-identically across repeated calls (the partial
+sums are added in a fixed order), and at the reference's shapes: Llama-3-8B Wo
 (4096 x 4096) and W_down (14336 -> 4096), Qwen2.5-7B (3584), TinyLlama
 (2048), the tiny model (256), a verify window of 9 rows."""
 import ctypes
@@ -91,12 +94,23 @@ def test_matvec_closed_forms_are_exact(gpu):
     d = 4096
     eye = np.eye(d, dtype=np.float16).view(np.uint16)
     x = rng.standard_normal((2, d)).astype(np.float32)
-    assert np.array_equal(_run(gpu, x, eye), x)
+    assert np.array_equal(_run(gpu, x, eye), x)            # VALU: exact products
+    x5 = rng.standard_normal((5, d)).astype(np.float32)
+    got5 = _run(gpu, x5, eye)                              # matrix cores: x as hi + lo
+    # |x - hi - lo| <= 2^-22 |x| for normal lo, half an fp16 subnormal step (2^-25) below
+    assert np.all(np.abs(got5 - x5) <= np.maximum(2.0 ** -21 * np.abs(x5), 2.0 ** -25))
+    assert not np.array_equal(got5, x5)  # (the lo part's rounding shows: this is the MFMA path)
     _, Wb = _case(rng, 1, 3584, 3584)
     for k in (0, 1791, 3583):
         e = np.zeros((1, 3584), np.float32)
         e[0, k] = 1.0
         assert np.array_equal(_run(gpu, e, Wb)[0], Wb[k].view(np.float16).astype(np.float32))
+    e5 = np.zeros((5, 3584), np.float32)
+    for m, k in enumerate((0, 900, 1791, 2700, 3583)):
+        e5[m, k] = 1.0
+    got = _run(gpu, e5, Wb)
+    for m, k in enumerate((0, 900, 1791, 2700, 3583)):
+        assert np.array_equal(got[m], Wb[k].view(np.float16).astype(np.float32))
 
 
 def test_matvec_is_deterministic(gpu):
