@@ -261,16 +261,18 @@ def bench_accept(torch, steps=200, k=4, vocab=128256):
 
 
 def bench_matvec(torch, steps, warmup, only=None):
-    """The output projection after attention (sde_matvec): us per call and
-    algorithmic GB/s (fp16 weights once + fp32 x, out read when accumulating,
-    out written) at the reference models' Wo / W_down shapes, graph-replayed
-    over >= 512 MiB of distinct weight matrices (beyond the 256 MB Infinity
+    """The output projection after attention: us per call and algorithmic
+    GB/s (fp16 weights once + fp32 x, out read when accumulating, out
+    written) at the reference models' Wo / W_down shapes, for W in the
+    reference's row-major layout (sde_matvec) and in the panel-packed layout
+    (sde_matvec_packed, W packed once beforehand), each graph-replayed over
+    >= 512 MiB of distinct weight matrices (beyond the 256 MB Infinity
     Cache); the C restatement of the reference's per-column loop
     (oracle_matvec, OpenMP on the host cores) timed beside the Llama-3-8B Wo."""
-    from speculative_decode_engine_amd import matvec, matvec_workspace
+    from speculative_decode_engine_amd import PackedWeight, matvec, matvec_packed, matvec_workspace
     shapes = [("llama3_8b_wo", 1, 4096, 4096, 1), ("llama3_8b_wo_verify", 5, 4096, 4096, 0),
               ("llama3_8b_w_down", 1, 14336, 4096, 1), ("llama3_8b_w_down_verify", 5, 14336, 4096, 0),
-              ("qwen25_7b_wo", 1, 3584, 3584, 1),
+              ("qwen25_7b_wo", 1, 3584, 3584, 1), ("qwen25_7b_wo_verify", 9, 3584, 3584, 0),
               ("tinyllama_wo", 1, 2048, 2048, 1)]
     out = {}
     g = torch.Generator(device="cuda")
@@ -289,10 +291,18 @@ def bench_matvec(torch, steps, warmup, only=None):
                                                     workspace=ws), steps, warmup) * 1e3
         nbytes = wbytes + M * d_in * 4 + M * d_out * 4 * (2 if acc else 1)
         gbps = nbytes / (us * 1e-6) / 1e9
+        Ps = [PackedWeight(W) for W in Ws]
+        del Ws
+        pus = graph_step_ms(torch, lambda i: matvec_packed(x, Ps[i % n_mats], out=y,
+                                                           accumulate=bool(acc)),
+                            steps, warmup) * 1e3
+        pgbps = nbytes / (pus * 1e-6) / 1e9
         out[name] = dict(n_rows=M, d_in=d_in, d_out=d_out, accumulate=acc, us=round(us, 3),
                          algorithmic_bytes=nbytes, gbps=round(gbps, 1),
-                         frac_of_hbm_peak=round(gbps / HBM_PEAK_GBPS, 4))
-        del Ws
+                         frac_of_hbm_peak=round(gbps / HBM_PEAK_GBPS, 4),
+                         packed_us=round(pus, 3), packed_gbps=round(pgbps, 1),
+                         packed_frac_of_hbm_peak=round(pgbps / HBM_PEAK_GBPS, 4))
+        del Ps
         torch.cuda.empty_cache()
     if only:
         return out

@@ -340,6 +340,30 @@ int sde_matvec(const float* d_x, const uint16_t* d_W, float* d_out, int d_in,
                int d_out_dim, int n_rows, int accumulate, void* d_workspace,
                size_t workspace_bytes, sde_stream_t stream);
 
+/* Bytes of the panel-packed copy of a d_in x d_out fp16 W that
+ * sde_matvec_packed streams (include/sde/matvec_packed.hpp gives the
+ * layout); 0 when d_in or d_out is not a positive multiple of 8. */
+size_t sde_matvec_packed_size(int d_in, int d_out_dim);
+
+/* Writes the panel-packed copy of row-major W [d_in][d_out_dim] (fp16 bits,
+ * 16-byte aligned) into d_packed (sde_matvec_packed_size bytes, 16-byte
+ * aligned; SDE_ERR_WORKSPACE when smaller), stream-ordered.  A one-time
+ * re-layout at weight-load time: the reference loads W as stored
+ * (model.cu:89-260) and has no counterpart. */
+int sde_matvec_pack(const uint16_t* d_W, int d_in, int d_out_dim, void* d_packed,
+                    size_t packed_bytes, sde_stream_t stream);
+
+/* sde_matvec's product over a packed copy: d_out[m][c] = (accumulate ?
+ * d_out[m][c] : 0) + sum_r d_x[m][r] * W[r][c], the same replacement of
+ * device_matvec_partial_accum / device_matvec_batched (utils.h:248-280,
+ * 437-452; kernels.cu:2742-2747; model.cu:717) for callers that packed W
+ * once.  One workgroup per panel of output columns, no workspace, no
+ * cross-workgroup reduction; deterministic.  1 <= n_rows <= 16, d_in and
+ * d_out_dim positive multiples of 8, d_x 16-byte aligned
+ * (SDE_ERR_UNSUPPORTED otherwise). */
+int sde_matvec_packed(const float* d_x, const void* d_packed, float* d_out, int d_in,
+                      int d_out_dim, int n_rows, int accumulate, sde_stream_t stream);
+
 /* ---- SDEC weight files (model_load_weights, model.cu:68-260) ------------ */
 
 /* ModelConfig (config.h:67-83) as read from an SDEC header, plus the file

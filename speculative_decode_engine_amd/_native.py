@@ -168,6 +168,9 @@ PROTOTYPES = {
     "sde_model_get_globals": (_c_int, [_vp, ctypes.POINTER(ModelGlobals)]),
     "sde_model_free": (_c_int, [_vp]),
     "sde_matvec": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _sz, _vp]),
+    "sde_matvec_packed_size": (_sz, [_c_int, _c_int]),
+    "sde_matvec_pack": (_c_int, [_vp, _c_int, _c_int, _vp, _sz, _vp]),
+    "sde_matvec_packed": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp]),
     "sde_spec_loop_workspace_size": (_sz, [_vp, ctypes.POINTER(LoopModel), _c_int]),
     "sde_spec_loop_greedy": (_c_int, [_vp, ctypes.POINTER(LoopModel), _c_int, _c_int, _c_int,
                                       _vp, _vp, _vp, _vp, _sz, _vp]),

@@ -5,10 +5,14 @@
 // verify window (utils.h:248-280, model.cu:717) and the multi-kernel path's
 // Wo GEMM + residual add (kernels.cu:1069-1075, with fp32 activations as in
 // the other two).  The work layout and its reduction are described in
-// include/sde/matvec_device.hpp.
+// include/sde/matvec_device.hpp.  sde_matvec_pack / sde_matvec_packed run
+// the same product over a one-time panel-packed copy of W
+// (include/sde/matvec_packed.hpp): one workgroup per panel of output
+// columns, no split reduction.
 #include <hip/hip_runtime.h>
 
 #include "sde/matvec_device.hpp"
+#include "sde/matvec_packed.hpp"
 #include "sde_internal.hpp"
 
 namespace sde {
@@ -33,6 +37,20 @@ __global__ __launch_bounds__(64 * kWaves) void matvec_kernel(MvArgs a) {
 }
 
 }  // namespace mv
+
+namespace mvp {
+
+// Workgroup (panel, pass).  One row of x takes whole batches per step (8
+// units in flight per lane and step); several rows take half batches, whose
+// multiply-adds overlap more of the streaming (measured on MI355X, 5 rows
+// of the 14336 x 4096 W_down: 24.2 vs 25.2 us) and whose doubled step
+// registers stay within 256 VGPRs up to 9 rows.
+template <int MB, int LPR>
+__global__ __launch_bounds__(64 * kWaves) void matvec_packed_kernel(PackedArgs a) {
+  packed_item<MB, LPR, (MB == 1 ? 8 : 4)>(a, blockIdx.x, blockIdx.y);
+}
+
+}  // namespace mvp
 }  // namespace sde
 
 namespace {
@@ -112,6 +130,69 @@ int sde_matvec(const float* d_x, const uint16_t* d_W, float* d_out, int d_in, in
     case 7: sde::mv::matvec_kernel<7><<<grid, block, 0, s>>>(a); break;
     default: sde::mv::matvec_kernel<8><<<grid, block, 0, s>>>(a); break;
   }
+  return sde::launch_status();
+}
+
+size_t sde_matvec_packed_size(int d_in, int d_out) {
+  return sde::mvp::packed_shape(d_in, d_out).units * 16;
+}
+
+int sde_matvec_pack(const uint16_t* d_W, int d_in, int d_out_dim, void* d_packed,
+                    size_t packed_bytes, sde_stream_t stream) {
+  if (!d_W || !d_packed || d_in < 1 || d_out_dim < 1) return SDE_ERR_INVALID_ARGUMENT;
+  const sde::mvp::PackedShape sh = sde::mvp::packed_shape(d_in, d_out_dim);
+  if (sh.panels == 0 || (reinterpret_cast<uintptr_t>(d_W) & 15u) != 0 ||
+      (reinterpret_cast<uintptr_t>(d_packed) & 15u) != 0)
+    return SDE_ERR_UNSUPPORTED;
+  if (packed_bytes < sh.units * 16) return SDE_ERR_WORKSPACE;
+  int st = SDE_OK;
+  const int n_cus = current_cus(&st);
+  if (st != SDE_OK) return st;
+  const size_t want = (sh.units + 255) / 256;
+  const int blocks = (int)(want < (size_t)n_cus * 16 ? want : (size_t)n_cus * 16);
+  sde::mvp::matvec_pack_kernel<<<blocks, 256, 0, (hipStream_t)stream>>>(
+      d_W, static_cast<uint4*>(d_packed), d_in, d_out_dim);
+  return sde::launch_status();
+}
+
+int sde_matvec_packed(const float* d_x, const void* d_packed, float* d_out, int d_in,
+                      int d_out_dim, int M, int accumulate, sde_stream_t stream) {
+  if (!d_x || !d_packed || !d_out || d_in < 1 || d_out_dim < 1 || M < 1 || M > kMaxRows)
+    return SDE_ERR_INVALID_ARGUMENT;
+  const sde::mvp::PackedShape sh = sde::mvp::packed_shape(d_in, d_out_dim);
+  if (sh.panels == 0 || (reinterpret_cast<uintptr_t>(d_x) & 15u) != 0 ||
+      (reinterpret_cast<uintptr_t>(d_packed) & 15u) != 0)
+    return SDE_ERR_UNSUPPORTED;
+  sde::mvp::PackedArgs a;
+  a.W = static_cast<const uint4*>(d_packed);
+  a.x = d_x;
+  a.out = d_out;
+  a.d_in = d_in;
+  a.d_out = d_out_dim;
+  a.M = M;
+  a.pass_rows = sde::mvp::packed_pass_rows(M);
+  a.n_batches = sh.n_batches;
+  a.accumulate = accumulate ? 1 : 0;
+  const dim3 grid(sh.panels, sde::mvp::packed_passes(M));
+  const dim3 block(64 * sde::mvp::kWaves);
+  const hipStream_t s = (hipStream_t)stream;
+#define SDE_MVP(MB)                                                                  \
+  case MB:                                                                           \
+    if (sh.lpr == 2)                                                                 \
+      sde::mvp::matvec_packed_kernel<MB, 2><<<grid, block, 0, s>>>(a);               \
+    else                                                                             \
+      sde::mvp::matvec_packed_kernel<MB, 1><<<grid, block, 0, s>>>(a);               \
+    break;
+  switch (a.pass_rows) {
+    SDE_MVP(1) SDE_MVP(2) SDE_MVP(3) SDE_MVP(4) SDE_MVP(5) SDE_MVP(6) SDE_MVP(7) SDE_MVP(8)
+    default:
+      if (sh.lpr == 2)
+        sde::mvp::matvec_packed_kernel<9, 2><<<grid, block, 0, s>>>(a);
+      else
+        sde::mvp::matvec_packed_kernel<9, 1><<<grid, block, 0, s>>>(a);
+      break;
+  }
+#undef SDE_MVP
   return sde::launch_status();
 }
 
