@@ -1,7 +1,8 @@
 """The attention half of a decoder layer composed from the library, with
 weights from an SDEC file: q, k, v = x @ Wq, Wk, Wv (sde_matvec), RoPE +
 append + causal attention in one launch (sde_rope_append_attention), then
-hidden += attn @ Wo (sde_matvec, accumulate) -- the reference's
+hidden += attn @ Wo (sde_matvec, accumulate; and sde_matvec_packed over a
+packed copy of the loaded Wo) -- the reference's
 model_layer_kv_phase + attention + Wo residual (model.cu:346-435,
 kernels.cu:2700-2747) for a decode step and a 5-row verify window.
 
@@ -15,7 +16,7 @@ import pytest
 import torch
 
 from conftest import case_banner
-from speculative_decode_engine_amd import matvec
+from speculative_decode_engine_amd import PackedWeight, matvec, matvec_packed
 from speculative_decode_engine_amd import sdec
 from test_gpu_attention import assert_close
 from test_gpu_fused_rope import build
@@ -59,6 +60,8 @@ def test_attention_sublayer_from_sdec_weights(gpu, oracle, tmp_path, d, nh, nkv,
                                            theta=model.config["rope_theta"])
         hidden = torch.from_numpy(hidden0.copy()).cuda()
         matvec(attn, lw["Wo"], out=hidden, accumulate=True)
+        hidden_p = torch.from_numpy(hidden0.copy()).cuda()
+        matvec_packed(attn, PackedWeight(lw["Wo"]), out=hidden_p, accumulate=True)
         torch.cuda.synchronize()
         pos = np.arange(ctx, ctx + M)
         gk, gv = cache.read(0, ctx, M)
@@ -70,6 +73,7 @@ def test_attention_sublayer_from_sdec_weights(gpu, oracle, tmp_path, d, nh, nkv,
         assert_close(a, ref, "attention of the projected, rotated rows")
         y, mag = oracle.matvec_f64(a, t["L0.Wo"].view(np.uint16), hidden0)
         assert np.all(np.abs(hidden.cpu().numpy() - y) <= MV_TOL * mag)
+        assert np.all(np.abs(hidden_p.cpu().numpy() - y) <= MV_TOL * mag)
     finally:
         model.free()
         cache.free()
