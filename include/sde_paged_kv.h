@@ -189,10 +189,12 @@ size_t sde_grid_attention_workspace_size(int nh, int nkv, int dph, int n_queries
  * decode step, n_queries = k+1 the speculative verify window.
  * d_workspace may be NULL (the cache then keeps its own, grown on demand);
  * otherwise it must hold sde_paged_attention_workspace_size(...) bytes.
- * Supported: dph in {64, 128}, block_size a multiple of 8, nkv | nh,
- * 1 <= n_queries <= 4096 and nkv * ceil(n_queries * nh/nkv / 4) <= 4096
- * (SDE_ERR_UNSUPPORTED otherwise).  Calls on one cache must be ordered on
- * one stream (they share the cache's arrival counters). */
+ * Any dph up to 512 and any block size, nkv | nh, 1 <= n_queries <= 4096
+ * (SDE_ERR_UNSUPPORTED for dph > 512): dph 64 / 128 with block sizes that
+ * are multiples of 8 run the matrix-core tile kernels (those also need
+ * nkv * ceil(n_queries * nh/nkv / 4) <= 4096), every other shape a plain
+ * fp32 kernel with the same semantics and workspace.  Calls on one cache
+ * must be ordered on one stream (they share the cache's arrival counters). */
 int sde_paged_attention(sde_kv_cache* cache, int layer, const float* d_q,
                         float* d_out, int nh, int nkv, int dph, int pos_base,
                         int n_queries, void* d_workspace,

@@ -22,7 +22,7 @@ LIB_NAME = "libsde_paged.so"
 LIB_PATH = PKG_DIR / LIB_NAME
 OFFLOAD_ARCH = "gfx950"
 
-SOURCES = ["kv_cache.hip", "paged_attention.hip", "spec_accept.hip", "matvec.hip",
+SOURCES = ["kv_cache.hip", "paged_attention.hip", "attention_generic.hip", "spec_accept.hip", "matvec.hip",
            "model_loader.hip", "spec_loop.hip"]
 
 # Test infrastructure: kernels that call the device-side API of

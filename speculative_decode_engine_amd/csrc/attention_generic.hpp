@@ -1,0 +1,55 @@
+// Attention for the shapes the tile kernels do not cover (head_dim other
+// than 64 / 128, block sizes not a multiple of 8): the interface between
+// paged_attention.hip's entry points and attention_generic.hip.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+namespace sde {
+namespace gen {
+
+constexpr int kMaxDph = 512;   // head_dim limit of the generic kernel (LDS for q)
+
+// The generic path serves every (dph, block size) the tile kernels do not.
+inline bool needs_generic(int dph, int block_size) {
+  return !(dph == 64 || dph == 128) || block_size % 8 != 0;
+}
+
+// Rotate-half RoPE of the fused entry point: inv_freq[j] for j < dph / 2
+// (theta already NTK-scaled, computed on the host in double precision and
+// rounded to fp32) and the linear / YaRN position divisor.
+struct GenRope {
+  const float* k_new;  // [M][kv_dim] fp32, before RoPE
+  const float* v_new;  // [M][kv_dim] fp32
+  float pos_div;
+  float inv_freq[kMaxDph / 2];
+};
+
+struct GenPlan {
+  int row_groups;
+  int n_parts;
+  int part_len;  // tokens per partition (a multiple of 64)
+};
+
+// The partition plan of a call: partitions of at least 64 tokens, at most
+// as many as parts_bound (the bound the attention workspace is sized for)
+// and about two workgroups per CU over all (KV head, row group) units.
+GenPlan generic_plan(int L_max, int nkv, int R, int n_cus, int max_parts);
+
+// Bytes of partials the plan needs (0 for one partition).
+size_t generic_partial_bytes(const GenPlan& p, int nkv, int R, int dph);
+
+// Launches the generic path on `stream`: (RoPE of k and append of k, v at
+// pos_base.. when rope != nullptr), attention with the query rows rotated
+// in-kernel when rope != nullptr, and the partition combine when the plan
+// has more than one partition.  Returns an sde status.
+int generic_attention(uint16_t* pool, const int32_t* table, int kv_dim, int block_size,
+                      const float* q, float* out, float* partials, int nh, int nkv, int dph,
+                      int pos_base, int n_queries, const GenPlan& plan,
+                      const GenRope* rope, hipStream_t stream);
+
+}  // namespace gen
+}  // namespace sde

@@ -33,6 +33,7 @@
 #include <mutex>
 
 #include "sde/attention_device.hpp"
+#include "attention_generic.hpp"
 #include "sde_internal.hpp"
 
 namespace sde {
@@ -172,8 +173,7 @@ int check_attention(const sde_kv_cache* c, int layer, const float* d_q,
   if (nh < 1 || nkv < 1 || dph < 1 || nh % nkv != 0) return SDE_ERR_INVALID_ARGUMENT;
   if ((int64_t)nkv * dph != c->cfg.kv_dim) return SDE_ERR_INVALID_ARGUMENT;
   if (pos_base < 0 || n_queries < 1 || n_queries > 4096) return SDE_ERR_INVALID_ARGUMENT;
-  if (dph != 64 && dph != 128) return SDE_ERR_UNSUPPORTED;
-  if (c->cfg.block_size % 8 != 0) return SDE_ERR_UNSUPPORTED;
+  if (dph > sde::gen::kMaxDph) return SDE_ERR_UNSUPPORTED;
   if ((((uintptr_t)d_q) & 7u) != 0 || (((uintptr_t)d_out) & 7u) != 0)
     return SDE_ERR_INVALID_ARGUMENT;
   if ((int64_t)pos_base + n_queries > sde::mapped_tokens(c, layer)) return SDE_ERR_CAPACITY;
@@ -204,16 +204,26 @@ namespace {
 
 int run_attention(sde_kv_cache* cache, int layer, const float* d_q, float* d_out, int nh,
                   int nkv, int dph, int pos_base, int n_queries, void* d_workspace,
-                  size_t workspace_bytes, sde_stream_t stream, const RopeArgs* rope) {
+                  size_t workspace_bytes, sde_stream_t stream, const RopeArgs* rope,
+                  const sde::gen::GenRope* grope = nullptr) {
   sde::DeviceGuard guard(cache->device);
   if (!guard.ok()) return SDE_ERR_HIP;
 
   const int G = nh / nkv;
   const int R = n_queries * G;
   const int L_max = pos_base + n_queries;
-  const StreamPlan plan = plan_for(L_max, nkv, R, cache->n_cus);
-  if ((int64_t)nkv * plan.row_groups > sde::kMaxAttnCounters) return SDE_ERR_UNSUPPORTED;
-  const size_t need = partial_bytes(nkv, R, plan.n_parts, dph);
+  const bool generic = sde::gen::needs_generic(dph, cache->cfg.block_size);
+  StreamPlan plan{};
+  sde::gen::GenPlan gplan{};
+  size_t need = 0;
+  if (generic) {
+    gplan = sde::gen::generic_plan(L_max, nkv, R, cache->n_cus, parts_bound(L_max));
+    need = sde::gen::generic_partial_bytes(gplan, nkv, R, dph);
+  } else {
+    plan = plan_for(L_max, nkv, R, cache->n_cus);
+    if ((int64_t)nkv * plan.row_groups > sde::kMaxAttnCounters) return SDE_ERR_UNSUPPORTED;
+    need = partial_bytes(nkv, R, plan.n_parts, dph);
+  }
   float* partials = nullptr;
   if (need > 0) {
     if (d_workspace) {
@@ -237,6 +247,12 @@ int run_attention(sde_kv_cache* cache, int layer, const float* d_q, float* d_out
       partials = static_cast<float*>(cache->workspace);
     }
   }
+
+  if (generic)
+    return sde::gen::generic_attention(cache->pool, sde::layer_table(cache, layer),
+                                       cache->cfg.kv_dim, cache->cfg.block_size, d_q, d_out,
+                                       partials, nh, nkv, dph, pos_base, n_queries, gplan, grope,
+                                       (hipStream_t)stream);
 
   AttnArgs a;
   a.src.pool = cache->pool;
@@ -305,6 +321,18 @@ int sde_rope_append_attention(sde_kv_cache* cache, int layer, const float* d_q,
                    factor > 1.0;
   rp.pos_div = div ? rope->scaling_factor : 1.0f;
   const double log_theta = std::log(theta);
+  if (sde::gen::needs_generic(dph, cache->cfg.block_size)) {
+    // the generic path: RoPE of k and the append, then attention with q
+    // rotated in-kernel (same frequency rule, up to dph / 2 = 256 pairs)
+    sde::gen::GenRope gr;
+    gr.k_new = d_k;
+    gr.v_new = d_v;
+    gr.pos_div = rp.pos_div;
+    for (int j = 0; j < sde::gen::kMaxDph / 2; j++)
+      gr.inv_freq[j] = j < dph / 2 ? (float)std::exp(-log_theta * (2.0 * j) / dph) : 0.f;
+    return run_attention(cache, layer, d_q, d_out, nh, nkv, dph, pos_base, n_queries,
+                         d_workspace, workspace_bytes, stream, nullptr, &gr);
+  }
   for (int j = 0; j < 64; j++)
     rp.inv_freq[j] = j < dph / 2 ? (float)std::exp(-log_theta * (2.0 * j) / dph) : 0.f;
   return run_attention(cache, layer, d_q, d_out, nh, nkv, dph, pos_base, n_queries,

@@ -248,11 +248,7 @@ def test_attention_argument_errors(gpu):
         cache.attention(0, torch.zeros(1, 4 * 64, device="cuda"), 4, 4, 64, 0,
                         attn_type=N.SDE_ATTN_SLIDING_WINDOW)
     assert e.value.status == N.SDE_ERR_UNSUPPORTED
-    c32 = KVCache(1, 256, 4, 16, pool_blocks=4)
+    c520 = KVCache(1, 520, 4, 16, pool_blocks=4)
     with pytest.raises(SDEError) as e:
-        c32.attention(0, torch.zeros(1, 8 * 32, device="cuda"), 8, 8, 32, 0)  # dph 32
-    assert e.value.status == N.SDE_ERR_UNSUPPORTED
-    c4 = KVCache(1, 128, 16, 4, pool_blocks=16)
-    with pytest.raises(SDEError) as e:
-        c4.attention(0, torch.zeros(1, 2 * 64, device="cuda"), 2, 2, 64, 0)  # block_size 4
+        c520.attention(0, torch.zeros(1, 520, device="cuda"), 1, 1, 520, 0)  # dph > 512
     assert e.value.status == N.SDE_ERR_UNSUPPORTED
