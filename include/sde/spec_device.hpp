@@ -124,10 +124,14 @@ __host__ __device__ inline void spec_draws(uint64_t seed, uint64_t offset, int b
 
 constexpr int kSpecMaxK = 64;
 constexpr int kSpecMaxSlices = 64;
-// Scratch words: [0] row arrivals; [1 + r] slice arrivals of row r (both
-// zero at rest); [1 + R + 2r] (flag, token) of row r; then per (row,
-// slice) the statistics (mp, sp, mq, sq) and the weight totals (residual, p).
-constexpr int kSpecScratchWords = 1 + 3 * (kSpecMaxK + 1) + 6 * (kSpecMaxK + 1) * kSpecMaxSlices;
+// Scratch words, at offsets that do not depend on the call's k (calls with
+// different k share one scratch, and its counters must stay zero at rest):
+// [0] row arrivals; [1 + r] slice arrivals of row r (both zero at rest);
+// [1 + kMaxRows + 2r] (flag, token) of row r; then, from
+// 1 + 3 kMaxRows, per (row, slice) the statistics (mp, sp, mq, sq) and the
+// weight totals (residual, p) of the call.
+constexpr int kSpecMaxRows = kSpecMaxK + 1;
+constexpr int kSpecScratchWords = 1 + 3 * kSpecMaxRows + 6 * kSpecMaxRows * kSpecMaxSlices;
 
 namespace spec {
 
@@ -345,16 +349,17 @@ struct RowWeights {
 
 struct Scratch {
   uint32_t* base;
-  int R;  // rows = k + 1
+  int R;  // rows of this call = k + 1
   int S;
   __device__ uint32_t* rows_arrived() const { return base; }
   __device__ uint32_t* slices_arrived(int r) const { return base + 1 + r; }
-  __device__ uint32_t* row_out(int r) const { return base + 1 + R + 2 * r; }
+  __device__ uint32_t* row_out(int r) const { return base + 1 + kSpecMaxRows + 2 * r; }
   __device__ float* stats(int r, int s) const {
-    return reinterpret_cast<float*>(base + 1 + 3 * R) + 4 * ((size_t)r * S + s);
+    return reinterpret_cast<float*>(base + 1 + 3 * kSpecMaxRows) + 4 * ((size_t)r * S + s);
   }
   __device__ float* totals(int r, int s) const {
-    return reinterpret_cast<float*>(base + 1 + 3 * R) + 4 * (size_t)R * S + 2 * ((size_t)r * S + s);
+    return reinterpret_cast<float*>(base + 1 + 3 * kSpecMaxRows) + 4 * (size_t)R * S +
+           2 * ((size_t)r * S + s);
   }
 };
 

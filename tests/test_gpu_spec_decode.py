@@ -189,6 +189,40 @@ def test_device_stochastic_matches_oracle(gpu, oracle, V, k, tt, td):
     dc.free()
 
 
+def test_device_stochastic_with_k_changing_between_calls(gpu, oracle):
+    """Calls with different k on one cache share its scratch (the
+    reference's loop shrinks k near max_new_tokens, kernels.cu:3216-3220):
+    every call must still match the oracle (the scratch's counters sit at
+    offsets independent of k)."""
+    case_banner("device stochastic, k changing")
+    rng = np.random.default_rng(31)
+    V = 1000
+    tc = KVCache(1, 64, 8, 16, 8)
+    dc = KVCache(1, 64, 8, 16, 8)
+    off = torch.zeros(1, dtype=torch.int64, device="cuda")
+    checked = 0
+    for call, k in enumerate([4, 0, 2, 6, 1, 4, 0, 3, 8, 2]):
+        tl = rng.standard_normal((k + 1, V)) * 2.0
+        dl = tl[:k] + rng.standard_normal((k, V)) * 0.7
+        drafts = [int(np.argmax(dl[i] + rng.gumbel(size=V))) for i in range(k)]
+        ts, ds = 20 + call, 10 + call
+        tc.set_seq_len(ts + k + 1)
+        dc.set_seq_len(ds + k)
+        res = _stoch(tc, dc, tl, dl, drafts, k, ts, ds, 4321, off).cpu().numpy()
+        r = oracle.spec_accept_stochastic(tl.astype(np.float32), dl.astype(np.float32) if k
+                                          else None, drafts, k, 1.0, 1.0, 4321, call, ts, ds, False)
+        n = r["n_accepted"]
+        assert int(off.item()) == call + 1
+        if min(r["accept_margin"][: min(n + 1, k)] + [1.0]) < 1e-4 or r["sample_margin"][n] < 1e-5:
+            continue
+        checked += 1
+        assert list(res[:4]) == [n, r["token"], r["target_seq"], r["draft_seq"]]
+        assert list(res[4:4 + n + 1]) == r["emitted"]
+    assert checked >= 7
+    tc.free()
+    dc.free()
+
+
 def test_device_speculative_sampling_preserves_the_target_distribution(gpu, oracle):
     """Leviathan et al.'s theorem on the device: with drafts sampled from q,
     the first emitted token is distributed as p."""
