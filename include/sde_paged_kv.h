@@ -470,8 +470,9 @@ typedef struct sde_loop_model {
   int32_t head_dim;     /* 64 or 128; n_kv_heads*head_dim == the cache's kv_dim */
 } sde_loop_model;
 
-/* Workspace bytes of sde_spec_loop_greedy for this cache, model and k; 0 for
- * invalid shapes.  No initialisation needed (the loop zeroes what it uses). */
+/* Workspace bytes of sde_spec_loop_greedy and sde_spec_loop_stochastic for
+ * this cache, model and k; 0 for invalid shapes.  No initialisation needed
+ * (the loop zeroes what it uses). */
 size_t sde_spec_loop_workspace_size(const sde_kv_cache* cache, const sde_loop_model* model,
                                     int k);
 
@@ -490,6 +491,42 @@ int sde_spec_loop_greedy(sde_kv_cache* cache, const sde_loop_model* model, int k
                          int max_new, int32_t* d_state, int32_t* d_emitted,
                          int32_t* d_accepted, void* d_workspace, size_t workspace_bytes,
                          sde_stream_t stream);
+
+/* Sampling parameters of the stochastic loop: the megakernel's
+ * draft_temp_initial, adaptive_enabled, min/max_draft_temp,
+ * adapt_tgt_accept, adapt_gain, adapt_ewma_mix and rng_seed
+ * (kernels.cu:3108-3133). */
+typedef struct sde_loop_sampling {
+  float draft_temp;     /* initial draft temperature (below 1e-6 acts as 1e-6) */
+  int32_t adaptive;     /* adapt the draft temperature after every round      */
+  float min_temp;       /* clamp of the adapted temperature                   */
+  float max_temp;
+  float target_accept;  /* acceptance rate the adaptation aims at             */
+  float gain;           /* temperature step per unit of rate error            */
+  float ewma_mix;       /* weight of a round in the rate average (1e-6..1-1e-6) */
+  uint64_t seed;        /* Philox key of every draw                           */
+} sde_loop_sampling;
+
+/* megakernel_speculative_stochastic_kernel (kernels.cu:3108-3481) in its
+ * self-speculative form, in one cooperative launch like
+ * sde_spec_loop_greedy: each draft token is sampled from the prefix layers'
+ * logits at the draft temperature T_d, the window is verified by the
+ * remaining layers, and speculative sampling (sde_spec_accept_stochastic's
+ * rules and draws: target temperature 1, q at T_d) accepts, emits the
+ * corrected or bonus sample and rewinds seq_len; T_d then adapts when
+ * `adaptive` (an exponential average of the round's acceptance rate, moved
+ * toward target_accept by gain, clamped).  Random draws: Philox4x32-10 keyed
+ * by seed at the call index *d_rng_offset (device uint64, 8-byte aligned),
+ * one call per draft token and one per acceptance, in that order.  d_state
+ * as for sde_spec_loop_greedy, plus out [6] the final T_d and [7] the rate
+ * average (float bits).  Same limits and errors as sde_spec_loop_greedy,
+ * plus SDE_ERR_INVALID_ARGUMENT for a NULL sampling / offset, non-finite
+ * parameters or min_temp > max_temp with adaptive set. */
+int sde_spec_loop_stochastic(sde_kv_cache* cache, const sde_loop_model* model, int k,
+                             int n_draft, int max_new, const sde_loop_sampling* sampling,
+                             uint64_t* d_rng_offset, int32_t* d_state, int32_t* d_emitted,
+                             int32_t* d_accepted, void* d_workspace, size_t workspace_bytes,
+                             sde_stream_t stream);
 
 #ifdef __cplusplus
 } /* extern "C" */

@@ -294,6 +294,82 @@ _PHILOX_M = (0xD2511F53, 0xCD9E8D57)   # Salmon et al., SC'11 (Philox4x32)
 _PHILOX_W = (0x9E3779B9, 0xBB67AE85)
 
 
+def spec_loop_stochastic(model: PagedKVModel, emb_q, emb_k, emb_v, head_bits, nh: int,
+                         nkv: int, dph: int, anchor: int, k: int, n_draft: int, max_new: int,
+                         seed: int, offset: int = 0, draft_temp: float = 1.0,
+                         adaptive: bool = False, min_temp: float = 0.1, max_temp: float = 2.0,
+                         target_accept: float = 0.7, gain: float = 0.1, ewma_mix: float = 0.2):
+    """The persistent self-speculative sampling loop
+    (megakernel_speculative_stochastic_kernel, kernels.cu:3108-3481) over
+    the byte model, with spec_loop_greedy's model and rounds: draft token
+    i+1 = spec_accept_stochastic with no drafts (its bonus sample) on the
+    prefix layers' logits of row i at the draft temperature T_d, one call
+    index each; then the window's target logits (temperature 1) and the
+    draft rows' logits (T_d) go to spec_accept_stochastic for the accept
+    tests and the corrected / bonus sample, one more call index; seq_len <-
+    P + n + 1.  With `adaptive`, after each round (kernels.cu:3441-3458,
+    in float32): r = n / k, ewma = r the first time else (1 - mix) ewma +
+    mix r with mix clamped to [1e-6, 1 - 1e-6], T_d += gain (ewma -
+    target_accept), clamped to [min_temp, max_temp].  Returns (tokens,
+    accepted per round, rounds, final T_d, final ewma, final offset, the
+    smallest distance of any accept test / sample from its boundary)."""
+    L = model.n_layers
+    d = nh * dph
+    head = f16_bits_to_f32(np.asarray(head_bits, dtype=np.uint16)).astype(np.float64)
+    M = k + 1
+    f32 = np.float32
+    temp, ewma = f32(draft_temp), f32(-1.0)
+    mix = min(max(f32(ewma_mix), f32(1e-6)), f32(1.0) - f32(1e-6))
+    tokens_out, accepted = [], []
+    margin = float("inf")
+    cur = int(anchor)
+    while len(tokens_out) < max_new:
+        P = model.seq_len
+        window = [cur] + [0] * k
+        h = np.zeros((M, d), dtype=np.float32)
+
+        def layers(lo, hi, r0, n):
+            for l in range(lo, hi):
+                toks = window[r0:r0 + n]
+                model.append(l, emb_k[l][toks], emb_v[l][toks], P + r0)
+                q = emb_q[l][toks].astype(np.float32)
+                if l > 0:
+                    q = q + h[r0:r0 + n]
+                out = model.attention(l, q, nh, nkv, dph, P + r0, mode="f64")
+                h[r0:r0 + n] = out.astype(np.float32)
+            return h[r0:r0 + n].astype(np.float64) @ head
+
+        lo = 0
+        dlog = []
+        if k > 0:
+            for i in range(M):
+                logits = layers(0, n_draft, i, 1)
+                if i < k:
+                    r = spec_accept_stochastic(logits, None, [], 0, float(temp), 1.0, seed,
+                                               offset, 0, 0, True)
+                    offset += 1
+                    margin = min(margin, r["sample_margin"][0])
+                    window[i + 1] = r["token"]
+                    dlog.append(logits[0])
+            lo = n_draft
+        logits = layers(lo, L, 0, M)
+        r = spec_accept_stochastic(logits, np.array(dlog) if k else None, window[1:], k, 1.0,
+                                   float(temp), seed, offset, P, P, True)
+        offset += 1
+        n = r["n_accepted"]
+        margin = min([margin] + r["accept_margin"][:min(n + 1, k)] + [r["sample_margin"][n]])
+        tokens_out += r["emitted"]
+        accepted.append(n)
+        model.seq_len = r["target_seq"]
+        cur = r["token"]
+        if adaptive and k > 0:
+            rr = f32(n) / f32(k)
+            ewma = rr if ewma < 0 else f32((f32(1.0) - mix) * ewma + mix * rr)
+            temp = f32(temp + f32(gain) * f32(ewma - f32(target_accept)))
+            temp = f32(max(f32(min_temp), min(f32(max_temp), temp)))
+    return tokens_out, accepted, len(accepted), float(temp), float(ewma), offset, margin
+
+
 def philox4x32_10(ctr, key) -> list:
     """Philox4x32-10 (Salmon, Moraes, Dror, Shaw, "Parallel random numbers:
     as easy as 1, 2, 3", SC'11), the counter-based generator of

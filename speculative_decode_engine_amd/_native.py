@@ -110,6 +110,20 @@ class LoopModel(ctypes.Structure):
     ]
 
 
+class LoopSampling(ctypes.Structure):
+    """sde_loop_sampling: the stochastic loop's temperature schedule and seed."""
+    _fields_ = [
+        ("draft_temp", ctypes.c_float),
+        ("adaptive", ctypes.c_int32),
+        ("min_temp", ctypes.c_float),
+        ("max_temp", ctypes.c_float),
+        ("target_accept", ctypes.c_float),
+        ("gain", ctypes.c_float),
+        ("ewma_mix", ctypes.c_float),
+        ("seed", ctypes.c_uint64),
+    ]
+
+
 class LayerWeights(ctypes.Structure):
     """sde_layer_weights: device pointers (model.h:32-47)."""
     _fields_ = [(n, ctypes.c_void_p) for n in LAYER_TENSORS]
@@ -174,6 +188,9 @@ PROTOTYPES = {
     "sde_spec_loop_workspace_size": (_sz, [_vp, ctypes.POINTER(LoopModel), _c_int]),
     "sde_spec_loop_greedy": (_c_int, [_vp, ctypes.POINTER(LoopModel), _c_int, _c_int, _c_int,
                                       _vp, _vp, _vp, _vp, _sz, _vp]),
+    "sde_spec_loop_stochastic": (_c_int, [_vp, ctypes.POINTER(LoopModel), _c_int, _c_int,
+                                          _c_int, ctypes.POINTER(LoopSampling), _vp, _vp, _vp,
+                                          _vp, _vp, _sz, _vp]),
 }
 
 _LIB = None

@@ -1,13 +1,18 @@
 // The persistent speculative decoding loop on gfx950: one cooperative
-// launch runs round after round of self-speculative greedy decoding over a
-// paged KV cache, with every token decision and every rewind made on the
-// device.
+// launch runs round after round of self-speculative decoding over a paged
+// KV cache -- greedy, or speculative sampling -- with every token decision
+// and every rewind made on the device.
 //
 // Reference (arkhamHack/speculative_decode_engine):
 //   cuda/src/kernels.cu:2864-3106  megakernel_speculative_kernel: draft k
 //                                  tokens, verify the window [last, drafts]
 //                                  in one batched pass, greedy accept,
 //                                  rewind target / draft seq_len
+//   cuda/src/kernels.cu:3108-3481  megakernel_speculative_stochastic_kernel:
+//                                  drafts sampled at a draft temperature
+//                                  (adapted per round toward a target
+//                                  acceptance), speculative-sampling accept
+//                                  with the corrected or bonus sample
 //   cuda/src/model.cu:838-890      self-speculative verify: layers
 //                                  [n_draft, n_layers) over the saved
 //                                  hiddens of the prefix layers
@@ -24,6 +29,7 @@
 // speculation must leave exactly the greedy decoder's bytes below seq_len.
 #include <hip/hip_runtime.h>
 
+#include <cmath>
 #include <cstdint>
 
 #include "sde/attention_device.hpp"
@@ -46,6 +52,8 @@ enum : int {
   kStatus = 3,    // first error (SDE_OK when none)
   kProposed = 4,  // drafts proposed
   kAccepted = 5,  // drafts accepted
+  kTemp = 6,      // sampling loop: the draft temperature (float bits), in and out
+  kEwma = 7,      // sampling loop: the acceptance-rate average (float bits, < 0: none yet)
   kStateWords = 8
 };
 
@@ -69,13 +77,20 @@ struct LoopArgs {
   void* mv_ws;
   size_t mv_ws_bytes;
   uint32_t* bar;  // [0] arrivals (zero at rest), [1] generation
+  // speculative sampling (sde_spec_loop_stochastic)
+  float* dlogits;      // [k][vocab]: the draft rows' logits
+  int32_t* sres;       // [k+5]: the acceptance's result
+  int32_t* dres;       // [8]: a draft sample's result, then a scratch seq_len word
+  uint32_t* sscratch;  // the stochastic device function's workspace (counters zero at rest)
+  uint64_t* offset;    // the random stream's call index (device, caller-owned)
+  sde_loop_sampling smp;
 };
 
 // Workspace layout: attention workspace (counters first), projection
 // workspace (counters first), then the loop's buffers, each 256-byte
 // aligned.
 struct Layout {
-  size_t attn, mv, q, h, logits, tokens, bar, total;
+  size_t attn, mv, q, h, logits, tokens, bar, dlogits, sres, dres, sscratch, total;
 };
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -91,7 +106,11 @@ inline Layout layout(int nh, int nkv, int dph, int vocab, int k, int cap) {
   l.logits = l.h + align256(M * d * sizeof(float));
   l.tokens = l.logits + align256((size_t)M * vocab * sizeof(float));
   l.bar = l.tokens + align256(2 * M * sizeof(int32_t));
-  l.total = l.bar + 256;
+  l.dlogits = l.bar + 256;
+  l.sres = l.dlogits + align256((size_t)(k > 0 ? k : 1) * vocab * sizeof(float));
+  l.dres = l.sres + align256((k + 5) * sizeof(int32_t));
+  l.sscratch = l.dres + 256;
+  l.total = l.sscratch + align256(spec_stochastic_workspace_size());
   return l;
 }
 
@@ -268,11 +287,18 @@ __global__ void spec_loop_init_kernel(LoopArgs a) {
   uint32_t* mc = static_cast<uint32_t*>(a.mv_ws);
   const int nmc = (int)(mv::mv_counter_bytes(a.m.vocab, a.k + 1) / sizeof(uint32_t));
   for (int i = threadIdx.x; i < nmc; i += blockDim.x) mc[i] = 0u;
+  if (a.offset) {  // the sampling loop: its device function's counters, its state words
+    for (int i = threadIdx.x; i < kSpecScratchWords; i += blockDim.x) a.sscratch[i] = 0u;
+  }
   if (threadIdx.x == 0) {
     a.bar[0] = 0u;
     a.bar[1] = 0u;
     a.tokens[0] = a.state[kAnchor];
     for (int i = kEmitted; i < kStateWords; i++) a.state[i] = 0;
+    if (a.offset) {
+      a.state[kTemp] = __float_as_int(a.smp.draft_temp);
+      a.state[kEwma] = __float_as_int(-1.f);
+    }
   }
 }
 
@@ -321,26 +347,125 @@ __global__ __launch_bounds__(kThreads) void spec_loop_kernel(LoopArgs a) {
   }
 }
 
+// The grid barrier as the stochastic device function's `sync`.
+struct GridSync {
+  const LoopArgs* a;
+  __device__ void operator()() const { barrier(*a); }
+};
+
+// The draft temperature's update after a round (kernels.cu:3441-3458): an
+// exponential average of the round's acceptance rate, moved toward the
+// target rate by `gain`, clamped to [min_temp, max_temp].
+__device__ void adapt_temperature(const LoopArgs& a, int n_accepted) {
+  if (!a.smp.adaptive || a.k < 1) return;
+  const float mix = fminf(fmaxf(a.smp.ewma_mix, 1e-6f), 1.f - 1e-6f);
+  const float rr = (float)n_accepted / (float)a.k;
+  float ewma = __int_as_float(a.state[kEwma]);
+  ewma = ewma < 0.f ? rr : (1.f - mix) * ewma + mix * rr;
+  float t = __int_as_float(a.state[kTemp]);
+  t += a.smp.gain * (ewma - a.smp.target_accept);
+  t = fmaxf(a.smp.min_temp, fminf(a.smp.max_temp, t));
+  a.state[kEwma] = __float_as_int(ewma);
+  a.state[kTemp] = __float_as_int(t);
+}
+
+// Speculative sampling over the same rounds (megakernel_speculative_
+// stochastic_kernel, kernels.cu:3108-3481, self-speculative): draft token
+// i+1 is sampled from softmax(draft logits of row i / T_d) by the
+// stochastic device function with no drafts (its bonus row); the window's
+// target logits and every draft row's logits then go to the same function
+// for the accept tests and the corrected or bonus sample (target temperature
+// 1, as the reference), which also rewinds seq_len; T_d adapts per round.
+// Unlike the reference, the draft rows' logits are kept from drafting
+// instead of recomputed after a rejection (the same values).
+__global__ __launch_bounds__(kThreads) void spec_loop_stochastic_kernel(LoopArgs a) {
+  const int M = a.k + 1;
+  const int V = a.m.vocab;
+  const int n_layers = a.kv.n_layers;
+  const GridSync sync{&a};
+  const size_t sbytes = spec_stochastic_workspace_size();
+  sde_kv_view dv = a.kv;  // draft samples rewind nothing: their seq_len word is scratch
+  dv.seq_len = a.dres + 7;
+
+  for (int round = 0;; round++) {
+    const int P = load_word(a.kv.seq_len);
+    if (load_word(a.state + kEmitted) >= a.max_new || load_word(a.state + kStatus) != SDE_OK)
+      break;
+    if (P < 0 || P + M > a.cap) {
+      if (blockIdx.x == 0 && threadIdx.x == 0) store_word(a.state + kStatus, SDE_ERR_CAPACITY);
+      break;
+    }
+    const float temp = __int_as_float(load_word(a.state + kTemp));
+    if (a.k > 0) {
+      for (int i = 0; i < M; i++) {
+        run_layers(a, 0, a.n_draft, i, 1, P);
+        if (i < a.k) {
+          float* dl = a.dlogits + (size_t)i * V;
+          int st = device_matvec_grid(a.h_buf + (size_t)i * a.d, a.m.head, dl, a.d, V, 1, 0,
+                                      a.mv_ws, a.mv_ws_bytes);
+          note_error(a, st);
+          barrier(a);
+          st = device_spec_accept_stochastic_grid(dl, nullptr, nullptr, 0, V, temp, 1.f,
+                                                  a.smp.seed, a.offset, 0, 0, dv, nullptr,
+                                                  a.dres, a.sscratch, sbytes, sync);
+          note_error(a, st);
+          barrier(a);
+          if (blockIdx.x == 0 && threadIdx.x == 0) {
+            // (a token outside the vocabulary would index the tables out of
+            // bounds: record an error and continue with token 0)
+            const int tok = a.dres[1];
+            const bool ok = tok >= 0 && tok < V;
+            a.tokens[i + 1] = ok ? tok : 0;
+            if (!ok) atomicCAS(reinterpret_cast<int*>(a.state + kStatus), SDE_OK, SDE_ERR_HIP);
+          }
+          barrier(a);
+        }
+      }
+    }
+    run_layers(a, a.n_draft, n_layers, 0, M, P);
+    int st = device_matvec_grid(a.h_buf, a.m.head, a.logits, a.d, V, M, 0, a.mv_ws,
+                                a.mv_ws_bytes);
+    note_error(a, st);
+    barrier(a);
+    st = device_spec_accept_stochastic_grid(a.logits, a.dlogits, a.tokens + 1, a.k, V, 1.f, temp,
+                                            a.smp.seed, a.offset, P, P, a.kv, nullptr, a.sres,
+                                            a.sscratch, sbytes, sync);
+    note_error(a, st);
+    barrier(a);
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+      const int n = a.sres[0];
+      const int E = a.state[kEmitted];
+      if (n < 0 || n > a.k || a.sres[1] < 0 || a.sres[1] >= V || a.sres[2] != P + n + 1) {
+        // not a result of the acceptance: stop with an error, cache untouched
+        atomicCAS(reinterpret_cast<int*>(a.state + kStatus), SDE_OK, SDE_ERR_HIP);
+        store_word(a.kv.seq_len, P);
+      } else {
+        for (int j = 0; j <= n; j++) a.emitted[E + j] = a.sres[4 + j];
+        store_word(a.kv.seq_len, a.sres[2]);
+        store_word(a.state + kEmitted, E + n + 1);
+        a.state[kAnchor] = a.sres[1];
+        a.state[kRounds] = round + 1;
+        a.state[kProposed] += a.k;
+        a.state[kAccepted] += n;
+        a.accepted[round] = n;
+        a.tokens[0] = a.sres[1];
+        adapt_temperature(a, n);
+      }
+    }
+    barrier(a);
+  }
+}
+
 }  // namespace loop
 }  // namespace sde
 
-extern "C" {
+namespace {
 
-size_t sde_spec_loop_workspace_size(const sde_kv_cache* cache, const sde_loop_model* model,
-                                    int k) {
-  if (!cache || !model || k < 0 || k + 1 > sde::loop::kMaxWindow) return 0;
-  if (model->n_heads < 1 || model->n_kv_heads < 1 || model->head_dim < 1 || model->vocab < 1)
-    return 0;
-  const int cap = cache->cfg.max_blocks_per_layer * cache->cfg.block_size;
-  return sde::loop::layout(model->n_heads, model->n_kv_heads, model->head_dim, model->vocab, k,
-                           cap)
-      .total;
-}
-
-int sde_spec_loop_greedy(sde_kv_cache* cache, const sde_loop_model* model, int k, int n_draft,
-                         int max_new, int32_t* d_state, int32_t* d_emitted,
-                         int32_t* d_accepted, void* d_workspace, size_t workspace_bytes,
-                         sde_stream_t stream) {
+// The checks and the launch shared by the greedy and the sampling loops.
+int launch_loop(sde_kv_cache* cache, const sde_loop_model* model, int k, int n_draft,
+                int max_new, int32_t* d_state, int32_t* d_emitted, int32_t* d_accepted,
+                void* d_workspace, size_t workspace_bytes, sde_stream_t stream,
+                const sde_loop_sampling* smp, uint64_t* d_offset) {
   using namespace sde::loop;
   if (!cache || !model || !d_state || !d_emitted || !d_accepted || !d_workspace)
     return SDE_ERR_INVALID_ARGUMENT;
@@ -356,6 +481,14 @@ int sde_spec_loop_greedy(sde_kv_cache* cache, const sde_loop_model* model, int k
   if (k < 0 || k + 1 > kMaxWindow) return SDE_ERR_RANGE;
   const int n_layers = cache->cfg.n_layers;
   if (k > 0 && (n_draft < 1 || n_draft >= n_layers)) return SDE_ERR_INVALID_ARGUMENT;
+  if (smp) {
+    if (!d_offset || !std::isfinite(smp->draft_temp) || !std::isfinite(smp->min_temp) ||
+        !std::isfinite(smp->max_temp) || !std::isfinite(smp->target_accept) ||
+        !std::isfinite(smp->gain) || !std::isfinite(smp->ewma_mix) ||
+        (smp->adaptive && smp->min_temp > smp->max_temp))
+      return SDE_ERR_INVALID_ARGUMENT;
+    if ((reinterpret_cast<uintptr_t>(d_offset) & 7u) != 0) return SDE_ERR_INVALID_ARGUMENT;
+  }
   // Every position the loop can reach must have a physical block.
   int cap = cache->cfg.max_blocks_per_layer * cache->cfg.block_size;
   for (int l = 0; l < n_layers; l++) {
@@ -369,11 +502,12 @@ int sde_spec_loop_greedy(sde_kv_cache* cache, const sde_loop_model* model, int k
 
   sde::DeviceGuard guard(cache->device);
   if (!guard.ok()) return SDE_ERR_HIP;
+  const void* kernel = smp ? reinterpret_cast<const void*>(spec_loop_stochastic_kernel)
+                           : reinterpret_cast<const void*>(spec_loop_kernel);
   int coop = 0, per_cu = 0;
   if (hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, cache->device) !=
           hipSuccess ||
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, spec_loop_kernel, kThreads, 0) !=
-          hipSuccess)
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kThreads, 0) != hipSuccess)
     return SDE_ERR_HIP;
   if (!coop || per_cu < 1) return SDE_ERR_UNSUPPORTED;
 
@@ -398,17 +532,55 @@ int sde_spec_loop_greedy(sde_kv_cache* cache, const sde_loop_model* model, int k
   a.logits = reinterpret_cast<float*>(ws + lay.logits);
   a.tokens = reinterpret_cast<int32_t*>(ws + lay.tokens);
   a.bar = reinterpret_cast<uint32_t*>(ws + lay.bar);
+  a.dlogits = reinterpret_cast<float*>(ws + lay.dlogits);
+  a.sres = reinterpret_cast<int32_t*>(ws + lay.sres);
+  a.dres = reinterpret_cast<int32_t*>(ws + lay.dres);
+  a.sscratch = reinterpret_cast<uint32_t*>(ws + lay.sscratch);
+  a.offset = smp ? d_offset : nullptr;
+  a.smp = smp ? *smp : sde_loop_sampling{};
   spec_loop_init_kernel<<<1, 256, 0, static_cast<hipStream_t>(stream)>>>(a);
   if (hipGetLastError() != hipSuccess) return SDE_ERR_HIP;
   // A cooperative launch: every block resident at once, which the grid
   // barrier needs.
   void* args[] = {&a};
-  const hipError_t e = hipLaunchCooperativeKernel(
-      reinterpret_cast<const void*>(spec_loop_kernel), dim3(cache->n_cus), dim3(kThreads), args,
-      0, static_cast<hipStream_t>(stream));
+  const hipError_t e = hipLaunchCooperativeKernel(kernel, dim3(cache->n_cus), dim3(kThreads),
+                                                  args, 0, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return SDE_ERR_HIP;
   cache->seq_len_on_device = true;
   return SDE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t sde_spec_loop_workspace_size(const sde_kv_cache* cache, const sde_loop_model* model,
+                                    int k) {
+  if (!cache || !model || k < 0 || k + 1 > sde::loop::kMaxWindow) return 0;
+  if (model->n_heads < 1 || model->n_kv_heads < 1 || model->head_dim < 1 || model->vocab < 1)
+    return 0;
+  const int cap = cache->cfg.max_blocks_per_layer * cache->cfg.block_size;
+  return sde::loop::layout(model->n_heads, model->n_kv_heads, model->head_dim, model->vocab, k,
+                           cap)
+      .total;
+}
+
+int sde_spec_loop_greedy(sde_kv_cache* cache, const sde_loop_model* model, int k, int n_draft,
+                         int max_new, int32_t* d_state, int32_t* d_emitted,
+                         int32_t* d_accepted, void* d_workspace, size_t workspace_bytes,
+                         sde_stream_t stream) {
+  return launch_loop(cache, model, k, n_draft, max_new, d_state, d_emitted, d_accepted,
+                     d_workspace, workspace_bytes, stream, nullptr, nullptr);
+}
+
+int sde_spec_loop_stochastic(sde_kv_cache* cache, const sde_loop_model* model, int k,
+                             int n_draft, int max_new, const sde_loop_sampling* sampling,
+                             uint64_t* d_rng_offset, int32_t* d_state, int32_t* d_emitted,
+                             int32_t* d_accepted, void* d_workspace, size_t workspace_bytes,
+                             sde_stream_t stream) {
+  if (!sampling) return SDE_ERR_INVALID_ARGUMENT;
+  return launch_loop(cache, model, k, n_draft, max_new, d_state, d_emitted, d_accepted,
+                     d_workspace, workspace_bytes, stream, sampling, d_rng_offset);
 }
 
 }  // extern "C"

@@ -1,4 +1,5 @@
-"""The persistent speculative decoding loop (sde_spec_loop_greedy) from Python.
+"""The persistent speculative decoding loops (sde_spec_loop_greedy,
+sde_spec_loop_stochastic) from Python.
 
 Reference (arkhamHack/speculative_decode_engine): megakernel_speculative,
 cuda/src/kernels.cu:2864-3106 (loop) and 3593-3755 (host launcher), in its
@@ -6,7 +7,10 @@ self-speculative form (model.cu:838-890).  One cooperative launch runs every
 round on the device: the first n_draft layers draft k tokens one at a time,
 the remaining layers verify the window [last token, drafts], the leading
 matches plus the target's next token are emitted, and seq_len rewinds to
-save + n_accepted + 1.  k = 0 is plain greedy decoding.
+save + n_accepted + 1.  k = 0 is plain greedy decoding.  The stochastic
+loop (megakernel_speculative_stochastic_kernel, kernels.cu:3108-3481)
+samples the drafts at a draft temperature and accepts by speculative
+sampling; k = 0 is plain sampling at temperature 1.
 
 The loop's model is the paged-KV path's: layer l of token t has q, k, v rows
 emb_q/emb_k/emb_v[l][t] (q adds the previous layer's attention output of
@@ -22,7 +26,7 @@ from typing import Optional
 import torch
 
 from . import _native
-from ._native import LoopModel, check
+from ._native import LoopModel, LoopSampling, check
 from .kv_cache import KVCache, _stream_handle
 
 STATE_WORDS = 8
@@ -35,6 +39,8 @@ class LoopResult:
     rounds: int
     seq_len: int          # the cache's device seq_len afterwards
     status: int
+    draft_temp: float = 0.0   # stochastic loop: the final draft temperature
+    accept_ewma: float = -1.0  # stochastic loop: the acceptance-rate average (< 0: none)
 
 
 class SpecLoopModel:
@@ -95,3 +101,41 @@ def spec_loop_greedy(cache: KVCache, model: SpecLoopModel, anchor: int, k: int, 
     return LoopResult(tokens=emitted[:n].cpu().tolist(),
                       accepted=accepted[:rounds].cpu().tolist(), rounds=rounds,
                       seq_len=cache.device_seq_len(), status=st[3])
+
+
+def spec_loop_stochastic(cache: KVCache, model: SpecLoopModel, anchor: int, k: int, n_draft: int,
+                         max_new: int, seed: int, draft_temp: float = 1.0, adaptive: bool = False,
+                         min_temp: float = 0.1, max_temp: float = 2.0,
+                         target_accept: float = 0.7, gain: float = 0.1, ewma_mix: float = 0.2,
+                         offset: Optional[torch.Tensor] = None,
+                         stream: Optional[torch.cuda.Stream] = None,
+                         workspace: Optional[torch.Tensor] = None) -> LoopResult:
+    """spec_loop_greedy's rounds with speculative sampling.  `offset` is the
+    device uint64 call index of the random stream (a fresh zero when None;
+    the call advances it by k + 1 per round)."""
+    dev = cache.device
+    state = torch.zeros(STATE_WORDS, dtype=torch.int32, device=dev)
+    state[0] = anchor
+    emitted = torch.full((max(max_new + k, 1),), -1, dtype=torch.int32, device=dev)
+    accepted = torch.full((max(max_new, 1),), -1, dtype=torch.int32, device=dev)
+    if offset is None:
+        offset = torch.zeros(1, dtype=torch.int64, device=dev)
+    if workspace is None:
+        workspace = torch.empty(max(workspace_size(cache, model, k), 256), dtype=torch.uint8,
+                                device=dev)
+    smp = LoopSampling(draft_temp, int(bool(adaptive)), min_temp, max_temp, target_accept, gain,
+                       ewma_mix, seed & 0xFFFFFFFFFFFFFFFF)
+    lib = _native.load()
+    check(lib.sde_spec_loop_stochastic(
+        cache.handle, ctypes.byref(model.c), k, n_draft, max_new, ctypes.byref(smp),
+        ctypes.c_void_p(offset.data_ptr()), ctypes.c_void_p(state.data_ptr()),
+        ctypes.c_void_p(emitted.data_ptr()), ctypes.c_void_p(accepted.data_ptr()),
+        ctypes.c_void_p(workspace.data_ptr()), workspace.numel() * workspace.element_size(),
+        _stream_handle(stream)), "spec_loop_stochastic")
+    torch.cuda.synchronize(dev)
+    st = state.cpu()
+    n, rounds = int(st[1]), int(st[2])
+    fl = st[6:8].view(torch.float32).tolist()
+    return LoopResult(tokens=emitted[:n].cpu().tolist(), accepted=accepted[:rounds].cpu().tolist(),
+                      rounds=rounds, seq_len=cache.device_seq_len(), status=int(st[3]),
+                      draft_temp=fl[0], accept_ewma=fl[1])

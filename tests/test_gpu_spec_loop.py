@@ -12,6 +12,14 @@ each round starts at the device seq_len the previous one wrote.  Checked:
     main.cu:311-337) and leaves the greedy run's K/V bytes below seq_len;
   * a window past the mapped blocks stops the loop with SDE_ERR_CAPACITY
     after the rounds that fit; bad arguments are rejected before any work.
+
+The sampling loop (sde_spec_loop_stochastic, kernels.cu:3108-3481) against
+oracle.spec_loop_stochastic: the same tokens, acceptances, seq_len, pool
+SHA-256, final call index and (adapted) draft temperature, for seeds whose
+every accept test and sample lies at least 1e-4 from its decision boundary
+(the oracle reports that distance; device and oracle logits differ by
+rounding, ~1e-5 of a probability here), with and without adaptation, and
+k = 0 (plain sampling).
 """
 import hashlib
 
@@ -22,7 +30,8 @@ import torch
 from conftest import case_banner
 from loop_model import make_loop_model, prefill, prompt_tokens
 from speculative_decode_engine_amd import KVCache, SDEError
-from speculative_decode_engine_amd.spec_loop import SpecLoopModel, spec_loop_greedy
+from speculative_decode_engine_amd.spec_loop import (SpecLoopModel, spec_loop_greedy,
+                                                     spec_loop_stochastic)
 
 pytestmark = pytest.mark.gpu
 
@@ -143,4 +152,85 @@ def test_spec_loop_rejects_bad_arguments(gpu):
     assert e.value.status == 4  # vocab not a multiple of 8
     torch.cuda.synchronize()
     assert torch.equal(cache.pool, before) and cache.device_seq_len() == 10
+    cache.free()
+
+
+STOCH_CASES = [
+    # seed, (L, nh, nkv, dph, V), P0, k, n_draft, draft temp, adaptive, rng seed
+    (3, (4, 4, 2, 64, 256), 40, 4, 2, 1.0, False, 14),
+    (3, (4, 4, 2, 64, 256), 40, 4, 2, 1.0, False, 16),
+    (6, (4, 4, 2, 64, 256), 40, 7, 1, 0.8, True, 9),
+    (6, (4, 4, 2, 64, 256), 40, 7, 1, 0.8, True, 36),
+    (5, (3, 8, 2, 128, 512), 300, 4, 1, 1.0, False, 25),
+    (3, (4, 4, 2, 64, 256), 40, 0, 0, 1.0, False, 1),   # k = 0: plain sampling
+]
+
+
+@pytest.mark.parametrize("seed,shape,P0,k,n_draft,temp,adaptive,rseed", STOCH_CASES)
+def test_stochastic_loop_matches_oracle(gpu, oracle, seed, shape, P0, k, n_draft, temp,
+                                        adaptive, rseed):
+    L, nh, nkv, dph, V = shape
+    case_banner("spec loop stochastic", seed, shape, P0, k, n_draft, temp, adaptive, rseed)
+    m = make_loop_model(seed, n_layers=L, nh=nh, nkv=nkv, dph=dph, vocab=V, noise=0.1,
+                        q_scale=2.0, head_scale=8.0)
+    max_new = 16
+    nblk = -(-(P0 + max_new + k + 1) // 16)
+    kvd = nkv * dph
+    cache = KVCache(L, kvd, nblk, 16, L * nblk)
+    model = oracle.PagedKVModel(L, kvd, nblk, 16, L * nblk)
+    prompt = prompt_tokens(seed, P0, V)
+    prefill(DeviceKV(cache), m, prompt)
+    prefill(model, m, prompt)
+    anchor = int(np.random.default_rng(seed).integers(0, V))
+    toks, acc, rounds, t_fin, ewma, off, margin = oracle.spec_loop_stochastic(
+        model, m.emb_q, m.emb_k, m.emb_v, m.head, nh, nkv, dph, anchor, k, n_draft, max_new,
+        rseed, 0, temp, adaptive)
+    assert margin > 1e-4  # the case's decisions are all clear of their boundaries
+    offset = torch.zeros(1, dtype=torch.int64, device="cuda")
+    res = spec_loop_stochastic(cache, device_model(m), anchor, k, n_draft, max_new, rseed,
+                               draft_temp=temp, adaptive=adaptive, offset=offset)
+    assert res.status == 0
+    assert res.tokens == toks and res.accepted == acc and res.rounds == rounds
+    assert res.seq_len == model.seq_len == P0 + len(toks)
+    assert int(offset.item()) == off == rounds * (k + 1)
+    assert pool_sha(cache) == model.pool_sha256()
+    assert abs(res.draft_temp - t_fin) <= 1e-5 * max(1.0, abs(t_fin))
+    if adaptive:
+        assert res.draft_temp != temp and abs(res.accept_ewma - ewma) <= 1e-5
+    else:
+        assert res.draft_temp == np.float32(temp) and res.accept_ewma == -1.0
+    cache.free()
+
+
+def test_stochastic_loop_rejects_bad_arguments(gpu):
+    case_banner("spec loop stochastic errors")
+    import ctypes
+    from speculative_decode_engine_amd import _native as N
+    m = make_loop_model(3, noise=0.1, q_scale=2.0)
+    cache = KVCache(m.n_layers, m.nkv * m.dph, 8, 16, m.n_layers * 8)
+    cache.set_seq_len(10)
+    dm = device_model(m)
+    lib = N.load()
+    state = torch.zeros(8, dtype=torch.int32, device="cuda")
+    em = torch.zeros(16, dtype=torch.int32, device="cuda")
+    ac = torch.zeros(8, dtype=torch.int32, device="cuda")
+    off = torch.zeros(1, dtype=torch.int64, device="cuda")
+    ws = torch.empty(lib.sde_spec_loop_workspace_size(cache.handle, ctypes.byref(dm.c), 2),
+                     dtype=torch.uint8, device="cuda")
+    vp = lambda t: ctypes.c_void_p(t.data_ptr())
+
+    def call(smp, offp):
+        return lib.sde_spec_loop_stochastic(cache.handle, ctypes.byref(dm.c), 2, 1, 4, smp, offp,
+                                            vp(state), vp(em), vp(ac), vp(ws), ws.numel(), None)
+    good = N.LoopSampling(1.0, 0, 0.1, 2.0, 0.7, 0.1, 0.2, 5)
+    assert call(None, vp(off)) == N.SDE_ERR_INVALID_ARGUMENT
+    assert call(ctypes.byref(good), None) == N.SDE_ERR_INVALID_ARGUMENT
+    bad = N.LoopSampling(float("nan"), 0, 0.1, 2.0, 0.7, 0.1, 0.2, 5)
+    assert call(ctypes.byref(bad), vp(off)) == N.SDE_ERR_INVALID_ARGUMENT
+    bad = N.LoopSampling(1.0, 1, 2.0, 0.1, 0.7, 0.1, 0.2, 5)  # min > max, adaptive
+    assert call(ctypes.byref(bad), vp(off)) == N.SDE_ERR_INVALID_ARGUMENT
+    assert call(ctypes.byref(good), ctypes.c_void_p(off.data_ptr() + 4)) == \
+        N.SDE_ERR_INVALID_ARGUMENT  # offset alignment
+    torch.cuda.synchronize()
+    assert cache.device_seq_len() == 10 and int(off.item()) == 0
     cache.free()

@@ -220,3 +220,54 @@ def test_loop_restatement_planted_rewind_mistake(oracle, shift):
     base, _, _ = loop_run(oracle, m, 0, 0, 40, 3)
     spec, _, _ = loop_run(oracle, m, 4, 2, 40, 3, shift=shift)
     assert spec[:40] != base
+
+
+# ---- the sampling loop's restatement (oracle.spec_loop_stochastic) ----------
+# With one-hot distributions (logits thousands apart, draft temperature
+# 1e-6) speculative sampling picks every argmax: the sampling loop must then
+# emit exactly the greedy loop's tokens, acceptances and K/V bytes -- the
+# window, the accept rule, the corrected sample and the rewind all line up.
+# Its call indices advance by k + 1 per round, and the adaptive temperature
+# follows its float32 rule.
+
+def stoch_run(oracle, m, k, n_draft, max_new, seed, P0=40, **kw):
+    from loop_model import prefill, prompt_tokens
+    nblk = -(-(P0 + 2 * max_new + k + 1) // 16)
+    model = oracle.PagedKVModel(m.n_layers, m.nkv * m.dph, nblk, 16, m.n_layers * nblk)
+    prefill(model, m, prompt_tokens(seed, P0, m.vocab))
+    anchor = int(np.random.default_rng(seed).integers(0, m.vocab))
+    out = oracle.spec_loop_stochastic(model, m.emb_q, m.emb_k, m.emb_v, m.head, m.nh, m.nkv,
+                                      m.dph, anchor, k, n_draft, max_new, 11, 0, **kw)
+    return out, model
+
+
+@pytest.mark.parametrize("seed,k,n_draft", [(3, 4, 2), (6, 7, 1), (3, 0, 0)])
+def test_sampling_loop_restatement_with_one_hot_distributions_is_greedy(oracle, seed, k,
+                                                                         n_draft):
+    from loop_model import make_loop_model
+    m = make_loop_model(seed, noise=0.1, q_scale=2.0, head_scale=4000.0)
+    greedy, g_acc, gm = loop_run(oracle, m, k, n_draft, 24, seed)
+    (toks, acc, rounds, temp, ewma, off, _), sm = stoch_run(oracle, m, k, n_draft, 24, seed,
+                                                             draft_temp=1e-6)
+    assert toks == greedy and acc == g_acc and sm.seq_len == gm.seq_len
+    assert off == rounds * (k + 1) and temp == np.float32(1e-6) and ewma == -1.0
+    if k:
+        assert any(a > 0 for a in acc) and any(a < k for a in acc)
+    assert sm.pool_sha256() == gm.pool_sha256()
+
+
+def test_sampling_loop_restatement_adapts_the_draft_temperature(oracle):
+    from loop_model import make_loop_model
+    m = make_loop_model(6, noise=0.1, q_scale=2.0, head_scale=8.0)
+    k = 7
+    (toks, acc, rounds, temp, ewma, off, _), _ = stoch_run(
+        oracle, m, k, 1, 16, 6, draft_temp=0.8, adaptive=True, min_temp=0.1, max_temp=2.0,
+        target_accept=0.7, gain=0.1, ewma_mix=0.2)
+    f = np.float32
+    t, e = f(0.8), f(-1.0)
+    for a in acc:  # the rule, restated once more
+        r = f(a) / f(k)
+        e = r if e < 0 else f(f(0.8) * e + f(0.2) * r)
+        t = f(min(f(2.0), max(f(0.1), f(t + f(0.1) * f(e - f(0.7))))))
+    assert abs(temp - float(t)) < 1e-6 and abs(ewma - float(e)) < 1e-6
+    assert off == rounds * (k + 1) and temp != np.float32(0.8)
