@@ -497,12 +497,15 @@ def bench_grid_device_fn(torch, W, steps, warmup):
 
 
 def bench_spec_loop(torch, max_new=64):
-    """The persistent speculative loop (sde_spec_loop_greedy, one cooperative
-    launch): us per round and per emitted token at a Llama-3-8B head shape
-    (32 q / 8 KV heads, dph 128), 4 layers, 4K context, vocabulary 4096,
-    greedy (k = 0) and self-speculative (k = 4, one draft layer)."""
+    """The persistent speculative loops (sde_spec_loop_greedy and
+    sde_spec_loop_stochastic, one cooperative launch each): us per round and
+    per emitted token at a Llama-3-8B head shape (32 q / 8 KV heads, dph
+    128), 4 layers, 4K context, vocabulary 4096, greedy (k = 0) and
+    self-speculative (k = 4, one draft layer); the sampling loop at draft
+    temperature 1 with adaptation."""
     from speculative_decode_engine_amd import KVCache
-    from speculative_decode_engine_amd.spec_loop import SpecLoopModel, spec_loop_greedy
+    from speculative_decode_engine_amd.spec_loop import (SpecLoopModel, spec_loop_greedy,
+                                                         spec_loop_stochastic)
     L, nh, nkv, dph, V, P0 = 4, 32, 8, 128, 4096, 4096
     g = torch.Generator(device="cuda")
     g.manual_seed(31)
@@ -515,7 +518,7 @@ def bench_spec_loop(torch, max_new=64):
                           (torch.randn(nh * dph, V, device="cuda", generator=g) /
                            math.sqrt(nh * dph)).half(), nh, nkv, dph)
     out = {}
-    for k in (0, 4):
+    for name, k in (("k0", 0), ("k4", 4), ("sampling_k0", 0), ("sampling_k4", 4)):
         nblk = -(-(P0 + max_new + k + 1) // 16)
         cache = KVCache(L, nkv * dph, nblk, 16, L * nblk)
         toks = torch.randint(0, V, (P0,), device="cuda", generator=g)
@@ -525,9 +528,13 @@ def bench_spec_loop(torch, max_new=64):
         cache.set_seq_len(P0)
         torch.cuda.synchronize()
         t = time.perf_counter()
-        res = spec_loop_greedy(cache, model, 7, k, 1 if k else 0, max_new)
+        if name.startswith("sampling"):
+            res = spec_loop_stochastic(cache, model, 7, k, 1 if k else 0, max_new, seed=5,
+                                       draft_temp=1.0, adaptive=True)
+        else:
+            res = spec_loop_greedy(cache, model, 7, k, 1 if k else 0, max_new)
         dt = time.perf_counter() - t
-        out[f"k{k}"] = dict(rounds=res.rounds, tokens=len(res.tokens),
+        out[name] = dict(rounds=res.rounds, tokens=len(res.tokens),
                             accepted=sum(res.accepted), status=res.status,
                             us_per_round=round(dt / max(res.rounds, 1) * 1e6, 1),
                             us_per_token=round(dt / max(len(res.tokens), 1) * 1e6, 1))
