@@ -193,8 +193,12 @@ size_t sde_grid_attention_workspace_size(int nh, int nkv, int dph, int n_queries
  * (SDE_ERR_UNSUPPORTED for dph > 512): dph 64 / 128 with block sizes that
  * are multiples of 8 run the matrix-core tile kernels (those also need
  * nkv * ceil(n_queries * nh/nkv / 4) <= 4096), every other shape a plain
- * fp32 kernel with the same semantics and workspace.  Calls on one cache
- * must be ordered on one stream (they share the cache's arrival counters). */
+ * fp32 kernel with the same semantics and workspace.  The tile kernels
+ * feed q * log2(e)/sqrt(dph) to the matrix cores as fp16 hi + lo parts, so
+ * its elements must stay below 65504 in magnitude (|q| < 5.1e5 at dph 128,
+ * 3.6e5 at dph 64; larger values overflow to Inf); the softmax weights are
+ * at most 1.  Calls on one cache must be ordered on one stream (they share
+ * the cache's arrival counters). */
 int sde_paged_attention(sde_kv_cache* cache, int layer, const float* d_q,
                         float* d_out, int nh, int nkv, int dph, int pos_base,
                         int n_queries, void* d_workspace,
@@ -334,10 +338,15 @@ size_t sde_matvec_workspace_size(int d_in, int d_out, int n_rows);
  * accumulate = 0) and the multi-kernel path's Wo GEMM + residual add
  * (kernels.cu:1069-1075, here with fp32 activations).  1 <= n_rows <= 16;
  * d_out_dim a multiple of 8, W 16-byte aligned, and one row range of W
- * (d_in split over the CUs) under 2 GiB (SDE_ERR_UNSUPPORTED otherwise).  d_workspace holds sde_matvec_workspace_size(...) bytes
+ * (d_in split over the CUs) under 2 GiB (SDE_ERR_UNSUPPORTED otherwise).
+ * d_workspace holds sde_matvec_workspace_size(...) bytes
  * (SDE_ERR_WORKSPACE when smaller); calls sharing a workspace must be
  * ordered on one stream.  Deterministic: the sum order does not depend on
- * scheduling. */
+ * scheduling.  One or two rows of x multiply in fp32 on the VALU (any
+ * finite x); three or more go to the matrix cores as fp16 hi + lo parts,
+ * which needs |x| < 65504 -- always so for Wo, whose input (an attention
+ * output, a convex combination of fp16 V rows) is bounded by max |V|;
+ * sde_matvec_packed takes any finite x at every row count. */
 int sde_matvec(const float* d_x, const uint16_t* d_W, float* d_out, int d_in,
                int d_out_dim, int n_rows, int accumulate, void* d_workspace,
                size_t workspace_bytes, sde_stream_t stream);
