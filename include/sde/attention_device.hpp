@@ -992,13 +992,15 @@ __host__ __device__ inline StreamPlan stream_plan(int L_max, int nkv, int R, int
   const int64_t by_len = (n_tiles + waves - 1) / waves;
   if (parts > by_len) parts = by_len;
   const int per_wave = (int)((n_tiles + parts * waves - 1) / (parts * waves));
-  // When the tiles exceed a whole number of tiles per wave by at most one
-  // per wave (a window's few positions past a round context length), the
-  // last partition takes the extra tiles instead of every wave taking one
-  // more (measured on MI355X: Qwen2.5-7B 9-query window at 8K 21.6 -> 20.7
-  // us, a 5-query window at 16K 34.6 -> 30.5; other shapes unchanged).
+  // When the tiles exceed a whole number (2 or more) of tiles per wave by
+  // at most one per wave (a window's few positions past a round context
+  // length), the last partition takes the extra tiles instead of every wave
+  // taking one more (measured on MI355X: Qwen2.5-7B 9-query window at 8K
+  // 21.6 -> 20.7 us, a 5-query window at 16K 34.6 -> 30.5; with one tile
+  // per wave the extra tile doubles the last partition's work: the grid
+  // device function's 4K window took 22.3 us that way against 20.7).
   const int64_t whole = n_tiles / (parts * waves);
-  if (per_wave >= 2 && whole >= 1 && whole <= max_chunk &&
+  if (per_wave >= 3 && whole >= 2 && whole <= max_chunk &&
       n_tiles - whole * parts * waves <= waves) {
     p.chunk = (int)whole;
     p.tiles_per_part = waves * p.chunk;
