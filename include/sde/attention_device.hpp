@@ -35,6 +35,7 @@
 #include <cstdint>
 
 #include "sde_paged_kv.h"
+#include "sde/wave_uniform.hpp"
 
 namespace sde {
 namespace attn {
@@ -268,7 +269,8 @@ __device__ __forceinline__ float4 load_dev16(const float* base, uint32_t bytes,
   constexpr int kSc1 = 16;                     // cache policy bit of sc1
   constexpr int kRsrcWord3 = 0x00020000;       // gfx9 raw buffer, 32-bit data format
   const __amdgpu_buffer_rsrc_t r =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, (int)bytes, kRsrcWord3);
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(wave_uniform(base)), 0,
+                                        (int)wave_uniform(bytes), kRsrcWord3);
   // Bit-cast the whole vector: extracting elements of the builtin's integer
   // vector result makes this compiler shrink the load to one dword.
   typedef float f4v __attribute__((ext_vector_type(4)));
@@ -1223,6 +1225,21 @@ __device__ __forceinline__ int device_attention_dispatch(int attn_type, const fl
 
 // ---- grid-cooperative split-context attention (persistent kernels) -------
 
+// The view with every field read into scalar registers (see wave_uniform).
+__device__ __forceinline__ sde_kv_view uniform_view(const sde_kv_view& v) {
+  sde_kv_view u;
+  u.pool = wave_uniform(v.pool);
+  u.block_tables = wave_uniform(v.block_tables);
+  u.seq_len = wave_uniform(v.seq_len);
+  u.n_layers = wave_uniform(v.n_layers);
+  u.kv_dim = wave_uniform(v.kv_dim);
+  u.block_size = wave_uniform(v.block_size);
+  u.max_blocks_per_layer = wave_uniform(v.max_blocks_per_layer);
+  u.pool_blocks = wave_uniform(v.pool_blocks);
+  u.reserved = wave_uniform(v.reserved);
+  return u;
+}
+
 // Arrival counters at the head of the grid function's workspace: a fixed
 // area, so calls of different shapes sharing one workspace never find
 // partial data where another shape keeps its counters.
@@ -1270,13 +1287,26 @@ __host__ __device__ inline size_t grid_attention_workspace_size(int nh, int nkv,
 template <int MaxWaves = 4>
 __device__ __forceinline__ int device_flash_attention_gqa_grid(const float* q_all,
                                                                float* attn_out,
-                                                               const sde_kv_view& kv, int layer,
+                                                               const sde_kv_view& kv_in, int layer,
                                                                int nh, int nkv, int dph,
                                                                int pos_base, int n_queries,
                                                                void* workspace,
                                                                size_t workspace_bytes) {
   using namespace attn;
   static_assert(MaxWaves == 4 || MaxWaves == 8, "grid workgroups of 4 or 8 waves");
+  // The arguments are the same in every thread: in scalar registers also
+  // where the caller is a function of its own.
+  q_all = wave_uniform(q_all);
+  attn_out = wave_uniform(attn_out);
+  workspace = wave_uniform(workspace);
+  workspace_bytes = wave_uniform(workspace_bytes);
+  layer = wave_uniform(layer);
+  nh = wave_uniform(nh);
+  nkv = wave_uniform(nkv);
+  dph = wave_uniform(dph);
+  pos_base = wave_uniform(pos_base);
+  n_queries = wave_uniform(n_queries);
+  const sde_kv_view kv = uniform_view(kv_in);
   if (blockDim.x < 256 || blockDim.x % 64 != 0) return SDE_ERR_UNSUPPORTED;
   if ((dph != 64 && dph != 128) || kv.block_size % 8 != 0) return SDE_ERR_UNSUPPORTED;
   if (nh < 1 || nkv < 1 || nh % nkv != 0 || nkv * dph != kv.kv_dim || layer < 0 ||

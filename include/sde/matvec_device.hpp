@@ -29,6 +29,7 @@
 #include <cstdint>
 
 #include "sde_paged_kv.h"
+#include "sde/wave_uniform.hpp"
 
 namespace sde {
 namespace mv {
@@ -128,7 +129,8 @@ __device__ __forceinline__ void mv_store_dev16(float* base, uint32_t bytes, uint
   typedef float f4v __attribute__((ext_vector_type(4)));
   typedef uint32_t u4v __attribute__((ext_vector_type(4)));
   const __amdgpu_buffer_rsrc_t r =
-      __builtin_amdgcn_make_buffer_rsrc(base, 0, (int)bytes, kRsrcWord3);
+      __builtin_amdgcn_make_buffer_rsrc(wave_uniform(base), 0, (int)wave_uniform(bytes),
+                                        kRsrcWord3);
   const f4v d = {v.x, v.y, v.z, v.w};
   __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4v, d), r, off, 0, kSc1);
 }
@@ -137,7 +139,8 @@ __device__ __forceinline__ float4 mv_load_dev16(const float* base, uint32_t byte
   constexpr int kRsrcWord3 = 0x00020000;
   typedef float f4v __attribute__((ext_vector_type(4)));
   const __amdgpu_buffer_rsrc_t r =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, (int)bytes, kRsrcWord3);
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(wave_uniform(base)), 0,
+                                        (int)wave_uniform(bytes), kRsrcWord3);
   const f4v v = __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kSc1));
   return make_float4(v.x, v.y, v.z, v.w);
 }
@@ -165,8 +168,8 @@ __device__ __forceinline__ MvRows mv_rows(const MvArgs& a, int r0, int r1, int c
   MvRows t;
   t.row_bytes = (uint32_t)a.d_out * 2u;
   t.rsrc = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(a.W + (size_t)r0 * a.d_out), 0,
-      (int)((uint32_t)(r1 - r0) * t.row_bytes), kRsrcWord3);
+      const_cast<uint16_t*>(wave_uniform(a.W + (size_t)r0 * a.d_out)), 0,
+      (int)wave_uniform((uint32_t)(r1 - r0) * t.row_bytes), kRsrcWord3);
   t.lane_off = (uint32_t)colc * 2u + (uint32_t)rp * t.row_bytes;
   t.r0 = r0;
   t.r1 = r1;
@@ -709,10 +712,21 @@ __device__ inline void device_matvec_batched(const float* g_x, const uint16_t* W
 // that must be zero before the first call (every call leaves them zero).
 // Returns SDE_OK in every thread, or an error code before any work; out is
 // complete once the grid has synchronized after the call.
-__device__ inline int device_matvec_grid(const float* x, const uint16_t* W, float* out,
-                                         int d_in, int d_out, int M, int accumulate,
-                                         void* workspace, size_t workspace_bytes) {
+__device__ __forceinline__ int device_matvec_grid(const float* x, const uint16_t* W, float* out,
+                                                  int d_in, int d_out, int M, int accumulate,
+                                                  void* workspace, size_t workspace_bytes) {
   using namespace mv;
+  // The arguments are the same in every thread: in scalar registers also
+  // where the caller is a function of its own.
+  x = wave_uniform(x);
+  W = wave_uniform(W);
+  out = wave_uniform(out);
+  d_in = wave_uniform(d_in);
+  d_out = wave_uniform(d_out);
+  M = wave_uniform(M);
+  accumulate = wave_uniform(accumulate);
+  workspace = wave_uniform(workspace);
+  workspace_bytes = wave_uniform(workspace_bytes);
   if (blockDim.x < 256 || blockDim.x % 64 != 0) return SDE_ERR_UNSUPPORTED;
   if (d_out % 8 != 0 || (reinterpret_cast<uintptr_t>(W) & 15u) != 0) return SDE_ERR_UNSUPPORTED;
   if (!x || !W || !out || !workspace || d_in < 1 || d_out < 8 || M < 1 || M > kMaxRows)
