@@ -303,24 +303,38 @@ struct RowWeights {
     return fmaxf(pi - qi, 0.f);
   }
   __device__ __forceinline__ float operator()(int i) const { return of(p[i], q ? q[i] : 0.f); }
+  // A virtual thread's batch of kUnroll tokens i0, i0 + 1024, ...: the
+  // logits, -inf / 0 past hi.
+  struct Batch {
+    float p[kUnroll], q[kUnroll];
+  };
+  __device__ __forceinline__ void load(int i0, int hi, Batch& x) const {
+#pragma unroll
+    for (int u = 0; u < kUnroll; u++) {
+      const int i = i0 + u * kVThreads;
+      x.p[u] = i < hi ? p[i] : -INFINITY;
+      x.q[u] = (q && i < hi) ? q[i] : 0.f;
+    }
+  }
   // Virtual thread vt's sums of the residual max(0, p - q) and of p over
   // tokens lo + vt, lo + vt + 1024, ... below hi (q non-null); each sum in
-  // thread_sum's order.
-  __device__ __forceinline__ float2 thread_sums(int vt, int lo, int hi) const {
+  // thread_sum's order.  With PRE the first batch is `first`, loaded
+  // earlier (load(lo + vt, hi, first)).
+  template <bool PRE = false>
+  __device__ __forceinline__ float2 thread_sums(int vt, int lo, int hi,
+                                                const Batch* first = nullptr) const {
     float cr = 0.f, cp = 0.f;
     for (int i0 = lo + vt; i0 < hi; i0 += kVThreads * kUnroll) {
-      float xp[kUnroll], xq[kUnroll];
-#pragma unroll
-      for (int u = 0; u < kUnroll; u++) {
-        const int i = i0 + u * kVThreads;
-        xp[u] = i < hi ? p[i] : -INFINITY;
-        xq[u] = i < hi ? q[i] : 0.f;
-      }
+      Batch x;
+      if (PRE && i0 == lo + vt)
+        x = *first;
+      else
+        load(i0, hi, x);
 #pragma unroll
       for (int u = 0; u < kUnroll; u++)
         if (i0 + u * kVThreads < hi) {
-          const float pi = __expf(xp[u] * inv_tt - mp) * inv_sp;
-          const float qi = __expf(xq[u] * inv_td - mq) * inv_sq;
+          const float pi = __expf(x.p[u] * inv_tt - mp) * inv_sp;
+          const float qi = __expf(x.q[u] * inv_td - mq) * inv_sq;
           cr += fmaxf(pi - qi, 0.f);
           cp += pi;
         }
@@ -328,20 +342,20 @@ struct RowWeights {
     return make_float2(cr, cp);
   }
   // Sum of virtual thread vt's weights over tokens lo + vt, lo + vt + 1024,
-  // ... below hi, loads batched.
-  __device__ __forceinline__ float thread_sum(int vt, int lo, int hi) const {
+  // ... below hi, loads batched (PRE: as in thread_sums).
+  template <bool PRE = false>
+  __device__ __forceinline__ float thread_sum(int vt, int lo, int hi,
+                                              const Batch* first = nullptr) const {
     float cs = 0.f;
     for (int i0 = lo + vt; i0 < hi; i0 += kVThreads * kUnroll) {
-      float xp[kUnroll], xq[kUnroll];
-#pragma unroll
-      for (int u = 0; u < kUnroll; u++) {
-        const int i = i0 + u * kVThreads;
-        xp[u] = i < hi ? p[i] : -INFINITY;
-        xq[u] = (q && i < hi) ? q[i] : 0.f;
-      }
+      Batch x;
+      if (PRE && i0 == lo + vt)
+        x = *first;
+      else
+        load(i0, hi, x);
 #pragma unroll
       for (int u = 0; u < kUnroll; u++)
-        if (i0 + u * kVThreads < hi) cs += of(xp[u], xq[u]);
+        if (i0 + u * kVThreads < hi) cs += of(x.p[u], x.q[u]);
     }
     return cs;
   }
@@ -418,7 +432,7 @@ __device__ void slice_stats(const StochArgs& a, int s, int b, float2* red2) {
 struct SampleLds {
   float red[kVWaves];
   float2 red2[kVWaves];
-  int pick, last_pos, token, last_slice;
+  int pick, last_pos, token, last_slice, last_row;
   float before;
 };
 
@@ -432,13 +446,20 @@ __device__ void slice_sample(const StochArgs& a, int s, int b, SampleLds& sl) {
   const int tid = threadIdx.x;
   const int V = a.V;
   const Scratch sc{a.scratch, a.k + 1, a.S};
-  // read before any block can arrive last (the last row's arrival needs
-  // this item's totals, published below)
-  const uint64_t offset = *a.offset;
-  float u_accept, u_sample;
-  spec_draws(a.seed, offset, b, u_accept, u_sample);
   const float* p = a.target_logits + (size_t)b * V;
   const float* q = b < a.k ? a.draft_logits + (size_t)b * V : nullptr;
+  const int lo = s * a.L, hi = min(V, lo + a.L);
+  // The accept test's draft token (slice 0, one thread), the call index,
+  // this slice's first batch of logits and the row statistics below are
+  // all requested before any of them is used: one round trip for the lot.
+  const bool gate = q && s == 0 && tid == 0;
+  const int d = gate ? a.draft_tokens[b] : 0;
+  // (the call index is read before any block can arrive last: the last
+  // row's arrival needs this item's totals, published below)
+  const uint64_t offset = *a.offset;
+  const RowWeights ahead{p, q, 0.f, 0.f, 0.f, 0.f, a.inv_tt, a.inv_td};
+  RowWeights::Batch first;
+  ahead.load(lo + vthread<VT>(0), hi, first);
 
   // Row statistics: lane i of each wave loads slice i's (one round trip)
   // and a fixed xor butterfly merges them (S <= 64).
@@ -458,10 +479,12 @@ __device__ void slice_sample(const StochArgs& a, int s, int b, SampleLds& sl) {
     }
   }
 
+  float u_accept, u_sample;
+  spec_draws(a.seed, offset, b, u_accept, u_sample);
+
   if (s == 0 && tid == 0) {  // accept test of draft token b (batch_stochastic_accept_kernel)
     int flag = 1;
     if (q) {
-      const int d = a.draft_tokens[b];
       if (d < 0 || d >= V) {
         flag = 0;
       } else {
@@ -474,14 +497,14 @@ __device__ void slice_sample(const StochArgs& a, int s, int b, SampleLds& sl) {
   }
 
   // This slice's totals of the residual max(0, p - q) and of p.
-  const int lo = s * a.L, hi = min(V, lo + a.L);
   RowWeights w{p, q, mp, 1.f / sp, mq, q ? 1.f / sq : 0.f, a.inv_tt, a.inv_td};
   float tr, tp;
   if (q) {
     float xr[VT], xp[VT];
 #pragma unroll
     for (int j = 0; j < VT; j++) {
-      const float2 ts = w.thread_sums(vthread<VT>(j), lo, hi);
+      const float2 ts = j == 0 ? w.thread_sums<true>(vthread<VT>(j), lo, hi, &first)
+                               : w.thread_sums(vthread<VT>(j), lo, hi);
       xr[j] = ts.x;
       xp[j] = ts.y;
     }
@@ -491,7 +514,9 @@ __device__ void slice_sample(const StochArgs& a, int s, int b, SampleLds& sl) {
   } else {
     float x[VT];
 #pragma unroll
-    for (int j = 0; j < VT; j++) x[j] = w.thread_sum(vthread<VT>(j), lo, hi);
+    for (int j = 0; j < VT; j++)
+      x[j] = j == 0 ? w.thread_sum<true>(vthread<VT>(j), lo, hi, &first)
+                    : w.thread_sum(vthread<VT>(j), lo, hi);
     tr = tp = block_sum<VT>(x, sl.red);
   }
   if (tid == 0) {
@@ -597,26 +622,42 @@ __device__ void slice_sample(const StochArgs& a, int s, int b, SampleLds& sl) {
     __builtin_amdgcn_s_waitcnt(0);
     const uint32_t prev = __hip_atomic_fetch_add(sc.rows_arrived(), 1u, __ATOMIC_RELAXED,
                                                  __HIP_MEMORY_SCOPE_AGENT);
-    if (prev == (uint32_t)a.k) {  // k+1 rows arrived
-      __hip_atomic_store(sc.rows_arrived(), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      int n = 0;
-      while (n < a.k &&
-             __hip_atomic_load(sc.row_out(n), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u)
-        n++;
-      const int tok = (int)__hip_atomic_load(sc.row_out(n) + 1, __ATOMIC_RELAXED,
-                                             __HIP_MEMORY_SCOPE_AGENT);
-      for (int i = 0; i < n; i++) a.result[4 + i] = a.draft_tokens[i];
-      a.result[4 + n] = tok;
-      const int t_seq = a.target_save + n + 1;
-      const int d_seq = a.has_draft ? a.draft_save + n : t_seq;
-      a.result[0] = n;
-      a.result[1] = tok;
-      a.result[2] = t_seq;
-      a.result[3] = d_seq;
-      *a.target.seq_len = t_seq;
-      if (a.has_draft) *a.draft.seq_len = d_seq;
-      *a.offset = offset + 1;
-    }
+    const int last = prev == (uint32_t)a.k;  // k+1 rows arrived
+    if (last) __hip_atomic_store(sc.rows_arrived(), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    sl.last_row = last;
+  }
+  __syncthreads();
+  if (!sl.last_row || tid >= 64) return;
+  // Wave 0 of the last row: lane i loads draft row i's accept flag, row i's
+  // token and draft token i together (one round trip); the first rejected
+  // row n (k when every draft is accepted) gives the corrected token, or
+  // the bonus row's token.
+  const bool draft_lane = lane < a.k;
+  const uint32_t flag = draft_lane ? __hip_atomic_load(sc.row_out(lane), __ATOMIC_RELAXED,
+                                                       __HIP_MEMORY_SCOPE_AGENT)
+                                   : 1u;
+  const int row_tok = lane <= a.k ? (int)__hip_atomic_load(sc.row_out(lane) + 1,
+                                                           __ATOMIC_RELAXED,
+                                                           __HIP_MEMORY_SCOPE_AGENT)
+                                  : 0;
+  const int drafted = draft_lane ? a.draft_tokens[lane] : 0;
+  const uint64_t rejected = __ballot(draft_lane && flag == 0u);
+  const int n = rejected ? (int)__builtin_ctzll(rejected) : a.k;
+  int tok = __shfl(row_tok, n & 63);
+  if (n >= 64)  // k = 64 and every draft accepted: the bonus row is past the lanes
+    tok = (int)__hip_atomic_load(sc.row_out(n) + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (lane < n) a.result[4 + lane] = drafted;
+  if (lane == 0) {
+    a.result[4 + n] = tok;
+    const int t_seq = a.target_save + n + 1;
+    const int d_seq = a.has_draft ? a.draft_save + n : t_seq;
+    a.result[0] = n;
+    a.result[1] = tok;
+    a.result[2] = t_seq;
+    a.result[3] = d_seq;
+    *a.target.seq_len = t_seq;
+    if (a.has_draft) *a.draft.seq_len = d_seq;
+    *a.offset = offset + 1;
   }
 }
 
