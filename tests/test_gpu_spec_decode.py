@@ -223,6 +223,45 @@ def test_device_stochastic_with_k_changing_between_calls(gpu, oracle):
     dc.free()
 
 
+@pytest.mark.parametrize("k,mode", [(33, "perturbed"), (63, "perturbed"), (63, "identical"),
+                                    (64, "perturbed"), (64, "identical")])
+def test_device_stochastic_long_windows(gpu, oracle, k, mode):
+    """Windows up to the 64 drafts the acceptance takes: the last row's wave
+    reads one row per lane (every draft accepted at k = 64 takes the bonus
+    row past the lanes).  A draft identical to the target accepts every
+    token (p / q = 1)."""
+    case_banner("device stochastic long window", k, mode)
+    rng = np.random.default_rng(k + len(mode))
+    V = 5000
+    tc = KVCache(1, 64, 8, 16, 8)
+    dc = KVCache(1, 64, 8, 16, 8)
+    off = torch.zeros(1, dtype=torch.int64, device="cuda")
+    checked = 0
+    for call in range(4):
+        tl = rng.standard_normal((k + 1, V)) * 2.0
+        dl = tl[:k].copy() if mode == "identical" else tl[:k] + rng.standard_normal((k, V)) * 0.3
+        drafts = [int(np.argmax(dl[i] + rng.gumbel(size=V))) for i in range(k)]
+        ts, ds = 20 + call, 10 + call
+        tc.set_seq_len(ts + k + 1)
+        dc.set_seq_len(ds + k)
+        res = _stoch(tc, dc, tl, dl, drafts, k, ts, ds, 777, off).cpu().numpy()
+        r = oracle.spec_accept_stochastic(tl.astype(np.float32), dl.astype(np.float32), drafts, k,
+                                          1.0, 1.0, 777, call, ts, ds, False)
+        n = r["n_accepted"]
+        assert int(off.item()) == call + 1
+        if mode == "identical":
+            assert n == k  # the oracle's decision, whatever the margins
+        if min(r["accept_margin"][: min(n + 1, k)] + [1.0]) < 1e-4 or r["sample_margin"][n] < 1e-5:
+            continue
+        checked += 1
+        assert list(res[:4]) == [n, r["token"], r["target_seq"], r["draft_seq"]]
+        assert list(res[4:4 + n + 1]) == r["emitted"]
+        assert tc.device_seq_len() == r["target_seq"] and dc.device_seq_len() == r["draft_seq"]
+    assert checked >= 2
+    tc.free()
+    dc.free()
+
+
 def test_device_speculative_sampling_preserves_the_target_distribution(gpu, oracle):
     """Leviathan et al.'s theorem on the device: with drafts sampled from q,
     the first emitted token is distributed as p."""
