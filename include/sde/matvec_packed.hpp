@@ -98,7 +98,8 @@ __device__ __forceinline__ uint4 packed_unit(const uint16_t* __restrict__ W, int
   return *reinterpret_cast<const uint4*>(W + (size_t)r * d_out + c0);
 }
 
-__global__ void __launch_bounds__(256) matvec_pack_kernel(const uint16_t* __restrict__ W,
+// (static: every source file that includes this header gets its own copy)
+static __global__ void __launch_bounds__(256) matvec_pack_kernel(const uint16_t* __restrict__ W,
                                                            uint4* __restrict__ P, int d_in,
                                                            int d_out) {
   const PackedShape s = packed_shape(d_in, d_out);
@@ -124,8 +125,8 @@ struct PackedStep {
 };
 
 // Eight zero floats (device globals are zero-initialized; nothing writes
-// them): the x operand of rows past d_in.
-__device__ __attribute__((aligned(16))) float packed_zero_x[kSteps];
+// them): the x operand of rows past d_in (one copy per source file).
+static __device__ __attribute__((aligned(16))) float packed_zero_x[kSteps];
 
 template <int MB, int LPR, int JR>
 __device__ __forceinline__ void packed_load(const PackedArgs& a, const uint4* __restrict__ P,

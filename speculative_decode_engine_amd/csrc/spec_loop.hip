@@ -33,7 +33,7 @@
 #include <cstdint>
 
 #include "sde/attention_device.hpp"
-#include "sde/matvec_device.hpp"
+#include "sde/matvec_packed.hpp"
 #include "sde/spec_device.hpp"
 #include "sde_internal.hpp"
 
@@ -86,8 +86,7 @@ struct LoopArgs {
   int32_t* tokens;    // [2(k+1)]: window tokens, then the target's tokens
   void* attn_ws;
   size_t attn_ws_bytes;
-  void* mv_ws;
-  size_t mv_ws_bytes;
+  const uint4* head_packed;  // the head's panel-packed copy (made by the launch)
   uint32_t* bar;  // grid barrier words (kBar*), zero at rest
   // speculative sampling (sde_spec_loop_stochastic)
   float* dlogits;      // [k][vocab]: the draft rows' logits
@@ -98,11 +97,10 @@ struct LoopArgs {
   sde_loop_sampling smp;
 };
 
-// Workspace layout: attention workspace (counters first), projection
-// workspace (counters first), then the loop's buffers, each 256-byte
-// aligned.
+// Workspace layout: attention workspace (counters first), the loop's
+// buffers, then the head's packed copy, each 256-byte aligned.
 struct Layout {
-  size_t attn, mv, q, h, logits, tokens, bar, dlogits, sres, dres, sscratch, total;
+  size_t attn, q, h, logits, tokens, bar, dlogits, sres, dres, sscratch, head, total;
 };
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -112,8 +110,7 @@ inline Layout layout(int nh, int nkv, int dph, int vocab, int k, int cap) {
   const int M = k + 1;
   const size_t d = (size_t)nh * dph;
   l.attn = 0;
-  l.mv = align256(grid_attention_workspace_size(nh, nkv, dph, M, cap));
-  l.q = l.mv + align256(mv::mv_workspace_size((int)d, vocab, M));
+  l.q = align256(grid_attention_workspace_size(nh, nkv, dph, M, cap));
   l.h = l.q + align256(M * d * sizeof(float));
   l.logits = l.h + align256(M * d * sizeof(float));
   l.tokens = l.logits + align256((size_t)M * vocab * sizeof(float));
@@ -122,7 +119,8 @@ inline Layout layout(int nh, int nkv, int dph, int vocab, int k, int cap) {
   l.sres = l.dlogits + align256((size_t)(k > 0 ? k : 1) * vocab * sizeof(float));
   l.dres = l.sres + align256((k + 5) * sizeof(int32_t));
   l.sscratch = l.dres + 256;
-  l.total = l.sscratch + align256(spec_stochastic_workspace_size());
+  l.head = l.sscratch + align256(spec_stochastic_workspace_size());
+  l.total = l.head + align256(mvp::packed_shape((int)d, vocab).units * 16);
   return l;
 }
 
@@ -339,20 +337,62 @@ __device__ __forceinline__ void run_layers(const LoopArgs& a, int lo, int hi, in
   }
 }
 
-// The output head (device_matvec_grid) as a function of its own: the
-// kernels keep their register budget for the attention, and the projection
-// (its descriptors taken from lane 0) pays only a call.
-__device__ __attribute__((noinline)) int head_logits(const LoopArgs& a, int r0, int n,
-                                                     float* logits) {
-  return device_matvec_grid(a.h_buf + (size_t)r0 * a.d, a.m.head, logits, a.d, a.m.vocab, n, 0,
-                            a.mv_ws, a.mv_ws_bytes);
+// The output head over its panel-packed copy (sde_matvec_packed's
+// workgroup body): every block takes (panel, pass) items in turn and writes
+// whole output columns -- no partials, no arrival counters, no combining
+// block.  A function of its own: the kernels keep their register budget
+// for their loops.  Rows n <= 16 (two passes above 9).
+template <int MB, int LPR>
+__device__ __forceinline__ void head_items(const mvp::PackedArgs& pa, int panels, int passes) {
+  const int blk = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+  const int nblk = gridDim.x * gridDim.y * gridDim.z;
+  for (int it = blk; it < panels * passes; it += nblk) {
+    mvp::packed_item<MB, LPR, (MB == 1 ? 8 : 4)>(pa, it % panels, it / panels);
+    __syncthreads();  // the item's LDS sums are read before the next item writes them
+  }
+}
+
+template <int LPR>
+__device__ __forceinline__ void head_rows(const mvp::PackedArgs& pa, int panels, int passes) {
+  switch (pa.pass_rows) {
+    case 1: head_items<1, LPR>(pa, panels, passes); break;
+    case 2: head_items<2, LPR>(pa, panels, passes); break;
+    case 3: head_items<3, LPR>(pa, panels, passes); break;
+    case 4: head_items<4, LPR>(pa, panels, passes); break;
+    case 5: head_items<5, LPR>(pa, panels, passes); break;
+    case 6: head_items<6, LPR>(pa, panels, passes); break;
+    case 7: head_items<7, LPR>(pa, panels, passes); break;
+    case 8: head_items<8, LPR>(pa, panels, passes); break;
+    default: head_items<9, LPR>(pa, panels, passes); break;
+  }
+}
+
+__device__ __attribute__((noinline)) void head_logits(const LoopArgs& a, int r0, int n,
+                                                      float* logits) {
+  const int d = wave_uniform(a.d), V = wave_uniform(a.m.vocab);
+  n = wave_uniform(n);
+  const mvp::PackedShape sh = mvp::packed_shape(d, V);
+  mvp::PackedArgs pa;
+  pa.W = wave_uniform(a.head_packed);
+  pa.x = wave_uniform(a.h_buf + (size_t)wave_uniform(r0) * d);
+  pa.out = wave_uniform(logits);
+  pa.d_in = d;
+  pa.d_out = V;
+  pa.M = n;
+  pa.pass_rows = mvp::packed_pass_rows(n);
+  pa.n_batches = sh.n_batches;
+  pa.accumulate = 0;
+  const int passes = mvp::packed_passes(n);
+  if (sh.lpr == 2)
+    head_rows<2>(pa, sh.panels, passes);
+  else
+    head_rows<1>(pa, sh.panels, passes);
 }
 
 // Logits of window rows [r0, r0+n) from their h_buf rows, then their
 // argmaxes into tokens[dst + row].
 __device__ __forceinline__ void decide(const LoopArgs& a, int r0, int n, int dst) {
-  const int st = head_logits(a, r0, n, a.logits);
-  note_error(a, st);
+  head_logits(a, r0, n, a.logits);
   barrier(a);
   argmax_rows(a, n, dst);
   barrier(a);
@@ -377,9 +417,6 @@ __device__ __forceinline__ Step round_step(const LoopArgs& a, int s, int n_steps
 __global__ void spec_loop_init_kernel(LoopArgs a) {
   uint32_t* c = static_cast<uint32_t*>(a.attn_ws);
   for (int i = threadIdx.x; i < kGridCounters; i += blockDim.x) c[i] = 0u;
-  uint32_t* mc = static_cast<uint32_t*>(a.mv_ws);
-  const int nmc = (int)(mv::mv_counter_bytes(a.m.vocab, a.k + 1) / sizeof(uint32_t));
-  for (int i = threadIdx.x; i < nmc; i += blockDim.x) mc[i] = 0u;
   for (int i = threadIdx.x; i < kBarWords; i += blockDim.x) a.bar[i] = 0u;
   if (a.offset) {  // the sampling loop: its device function's counters, its state words
     for (int i = threadIdx.x; i < kSpecScratchWords; i += blockDim.x) a.sscratch[i] = 0u;
@@ -496,11 +533,10 @@ __global__ __launch_bounds__(kThreads) void spec_loop_stochastic_kernel(LoopArgs
       run_layers(a, t.lo, t.hi, t.r0, t.n, P);
       if (!t.verify && s >= a.k) continue;
       float* lg = t.verify ? a.logits : a.dlogits + (size_t)s * V;
-      int st = head_logits(a, t.r0, t.n, lg);
-      note_error(a, st);
+      head_logits(a, t.r0, t.n, lg);
       barrier(a);
       if (t.verify) break;
-      st = device_spec_accept_stochastic_grid(lg, nullptr, nullptr, 0, V, temp, 1.f, a.smp.seed,
+      int st = device_spec_accept_stochastic_grid(lg, nullptr, nullptr, 0, V, temp, 1.f, a.smp.seed,
                                               a.offset, 0, 0, dv, nullptr, a.dres, a.sscratch,
                                               sbytes, sync);
       note_error(a, st);
@@ -612,9 +648,8 @@ int launch_loop(sde_kv_cache* cache, const sde_loop_model* model, int k, int n_d
   a.accepted = d_accepted;
   char* ws = static_cast<char*>(d_workspace);
   a.attn_ws = ws + lay.attn;
-  a.attn_ws_bytes = lay.mv - lay.attn;
-  a.mv_ws = ws + lay.mv;
-  a.mv_ws_bytes = lay.q - lay.mv;
+  a.attn_ws_bytes = lay.q - lay.attn;
+  a.head_packed = reinterpret_cast<const uint4*>(ws + lay.head);
   a.q_buf = reinterpret_cast<float*>(ws + lay.q);
   a.h_buf = reinterpret_cast<float*>(ws + lay.h);
   a.logits = reinterpret_cast<float*>(ws + lay.logits);
@@ -626,6 +661,16 @@ int launch_loop(sde_kv_cache* cache, const sde_loop_model* model, int k, int n_d
   a.sscratch = reinterpret_cast<uint32_t*>(ws + lay.sscratch);
   a.offset = smp ? d_offset : nullptr;
   a.smp = smp ? *smp : sde_loop_sampling{};
+  // The head's panel-packed copy for this launch (a one-time re-layout per
+  // call, amortized over its rounds).
+  const sde::mvp::PackedShape hs = sde::mvp::packed_shape(a.d, m.vocab);
+  if (hs.panels == 0) return SDE_ERR_UNSUPPORTED;
+  const size_t pack_blocks = (hs.units + 255) / 256;
+  const int pb = (int)(pack_blocks < (size_t)cache->n_cus * 16 ? pack_blocks
+                                                              : (size_t)cache->n_cus * 16);
+  sde::mvp::matvec_pack_kernel<<<pb, 256, 0, static_cast<hipStream_t>(stream)>>>(
+      m.head, reinterpret_cast<uint4*>(ws + lay.head), a.d, m.vocab);
+  if (hipGetLastError() != hipSuccess) return SDE_ERR_HIP;
   spec_loop_init_kernel<<<1, 256, 0, static_cast<hipStream_t>(stream)>>>(a);
   if (hipGetLastError() != hipSuccess) return SDE_ERR_HIP;
   // A cooperative launch: every block resident at once, which the grid
