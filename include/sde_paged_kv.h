@@ -462,8 +462,9 @@ int sde_model_free(sde_model* model);
  * attention output of the same row, and `head` (fp16, row-major [in][out] as
  * the reference stores weights, model.h:19) maps the last layer's attention
  * output to logits.  Every block of the grid runs the attention
- * (sde::device_flash_attention_gqa_grid) and the head
- * (sde::device_matvec_grid); each round drafts k tokens by greedy argmax,
+ * (sde::device_flash_attention_gqa_grid) and the head (over a panel-packed
+ * copy of it that the launch makes first in the workspace, sde_matvec_pack's
+ * layout); each round drafts k tokens by greedy argmax,
  * verifies them, accepts the leading matches plus the target's next token
  * (sde::spec_accept_greedy) and rewinds seq_len to save + n_accepted + 1; the
  * next round starts at the device seq_len.  k = 0 is plain greedy decoding
@@ -480,8 +481,9 @@ typedef struct sde_loop_model {
 } sde_loop_model;
 
 /* Workspace bytes of sde_spec_loop_greedy and sde_spec_loop_stochastic for
- * this cache, model and k; 0 for invalid shapes.  No initialisation needed
- * (the loop zeroes what it uses). */
+ * this cache, model and k (the packed head copy included:
+ * sde_matvec_packed_size(n_heads * head_dim, vocab) of them); 0 for invalid
+ * shapes.  No initialisation needed (the loop writes what it uses). */
 size_t sde_spec_loop_workspace_size(const sde_kv_cache* cache, const sde_loop_model* model,
                                     int k);
 
