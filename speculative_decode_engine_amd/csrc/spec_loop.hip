@@ -87,6 +87,8 @@ struct LoopArgs {
   void* attn_ws;
   size_t attn_ws_bytes;
   const uint4* head_packed;  // the head's panel-packed copy (made by the launch)
+  uint2* cand;               // [kMaxWindow][panels]: each panel's (max logit, column) per row
+  uint32_t* cand_arrivals;   // the head's items done (zero at rest)
   uint32_t* bar;  // grid barrier words (kBar*), zero at rest
   // speculative sampling (sde_spec_loop_stochastic)
   float* dlogits;      // [k][vocab]: the draft rows' logits
@@ -100,7 +102,7 @@ struct LoopArgs {
 // Workspace layout: attention workspace (counters first), the loop's
 // buffers, then the head's packed copy, each 256-byte aligned.
 struct Layout {
-  size_t attn, q, h, logits, tokens, bar, dlogits, sres, dres, sscratch, head, total;
+  size_t attn, q, h, logits, tokens, bar, dlogits, sres, dres, sscratch, head, cand, total;
 };
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -120,7 +122,8 @@ inline Layout layout(int nh, int nkv, int dph, int vocab, int k, int cap) {
   l.dres = l.sres + align256((k + 5) * sizeof(int32_t));
   l.sscratch = l.dres + 256;
   l.head = l.sscratch + align256(spec_stochastic_workspace_size());
-  l.total = l.head + align256(mvp::packed_shape((int)d, vocab).units * 16);
+  l.cand = l.head + align256(mvp::packed_shape((int)d, vocab).units * 16);
+  l.total = l.cand + 256 + align256((size_t)kMaxWindow * (vocab / 8) * sizeof(uint2));
   return l;
 }
 
@@ -270,50 +273,6 @@ __device__ void append_rows(const LoopArgs& a, int l, int r0, int n, int pos0) {
   }
 }
 
-// argmax of logits row r (the lowest index among equal maxima; NaN never
-// wins) into tokens[dst + r], one block per row.
-__device__ void argmax_rows(const LoopArgs& a, int n, int dst) {
-  __shared__ float s_val[kThreads / 64];
-  __shared__ int s_idx[kThreads / 64];
-  const int V = a.m.vocab;
-  for (int r = blockIdx.x; r < n; r += gridDim.x) {
-    const float* x = a.logits + (size_t)r * V;
-    const int tid = attn::item_tid();
-    float best = -INFINITY;
-    int bi = V;
-    for (int i = tid; i < V; i += blockDim.x) {
-      const float v = x[i];
-      if (v > best) {  // ascending i per thread: the first maximum stays
-        best = v;
-        bi = i;
-      }
-    }
-    for (int off = 32; off > 0; off >>= 1) {
-      const float ov = __shfl_xor(best, off);
-      const int oi = __shfl_xor(bi, off);
-      if (ov > best || (ov == best && oi < bi)) {
-        best = ov;
-        bi = oi;
-      }
-    }
-    const int w = tid >> 6;
-    if ((tid & 63) == 0) {
-      s_val[w] = best;
-      s_idx[w] = bi;
-    }
-    __syncthreads();
-    if (tid == 0) {
-      for (int i = 1; i < (int)(blockDim.x >> 6); i++)
-        if (s_val[i] > best || (s_val[i] == best && s_idx[i] < bi)) {
-          best = s_val[i];
-          bi = s_idx[i];
-        }
-      a.tokens[dst + r] = bi < V ? bi : 0;  // all NaN: token 0
-    }
-    __syncthreads();
-  }
-}
-
 // The grid attention of layer l over window rows [r0, r0+n) at positions
 // pos0 + row, as a function of its own: its tile loop gets the whole register
 // budget instead of sharing it with the values the loops around it keep.
@@ -342,33 +301,139 @@ __device__ __forceinline__ void run_layers(const LoopArgs& a, int lo, int hi, in
 // whole output columns -- no partials, no arrival counters, no combining
 // block.  A function of its own: the kernels keep their register budget
 // for their loops.  Rows n <= 16 (two passes above 9).
+// The greedy loop's argmax rides on the head (the lowest column among equal
+// maxima, NaN never winning, all-NaN rows giving token 0): after an item,
+// one thread per
+// row of its pass scans the panel's logits it just wrote (visible to the
+// block after the barrier) and publishes the panel's (max, column) with a
+// device-scope store; the last item to arrive reduces every panel's
+// candidates, in panel (column) order, into tokens[dst + row].
+struct HeadArgmax {
+  int dst;  // tokens[dst + row]; < 0: no argmax
+};
+
+__device__ __forceinline__ bool arg_better(float v, int i, float bv, int bi) {
+  return v > bv || (v == bv && i < bi);
+}
+
+template <int PW>
+__device__ __forceinline__ void panel_candidates(const LoopArgs& a, const mvp::PackedArgs& pa,
+                                                 int panel, int pass, int panels) {
+  const int m0 = pass * pa.pass_rows;
+  const int mc = min(pa.pass_rows, pa.M - m0);
+  const int t = (int)threadIdx.x;
+  if (t < mc) {
+    const float* row = pa.out + (size_t)(m0 + t) * pa.d_out + (size_t)panel * PW;
+    float best = -INFINITY;
+    int bi = pa.d_out;
+#pragma unroll
+    for (int c = 0; c < PW; c++) {
+      const float v = row[c];
+      if (v > best) {
+        best = v;
+        bi = panel * PW + c;
+      }
+    }
+    const uint64_t bits = (uint64_t)__builtin_bit_cast(uint32_t, best) |
+                          ((uint64_t)(uint32_t)bi << 32);
+    __hip_atomic_store(reinterpret_cast<uint64_t*>(a.cand + (size_t)(m0 + t) * panels + panel),
+                       bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// The last item's block: row r's winner over its panels' candidates.
+__device__ __forceinline__ void reduce_candidates(const LoopArgs& a, int n, int panels, int V,
+                                                  int dst) {
+  __shared__ float s_val[kThreads / 64];
+  __shared__ int s_idx[kThreads / 64];
+  const int tid = (int)threadIdx.x;
+  for (int r = 0; r < n; r++) {
+    float best = -INFINITY;
+    int bi = V;
+    for (int p = tid; p < panels; p += blockDim.x) {  // ascending panels per thread
+      const uint64_t bits = __hip_atomic_load(
+          reinterpret_cast<uint64_t*>(a.cand + (size_t)r * panels + p), __ATOMIC_RELAXED,
+          __HIP_MEMORY_SCOPE_AGENT);
+      const float v = __builtin_bit_cast(float, (uint32_t)bits);
+      const int i = (int)(uint32_t)(bits >> 32);
+      if (arg_better(v, i, best, bi)) {
+        best = v;
+        bi = i;
+      }
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+      const float ov = __shfl_xor(best, off);
+      const int oi = __shfl_xor(bi, off);
+      if (arg_better(ov, oi, best, bi)) {
+        best = ov;
+        bi = oi;
+      }
+    }
+    if ((tid & 63) == 0) {
+      s_val[tid >> 6] = best;
+      s_idx[tid >> 6] = bi;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      for (int w = 1; w < (int)(blockDim.x >> 6); w++)
+        if (arg_better(s_val[w], s_idx[w], best, bi)) {
+          best = s_val[w];
+          bi = s_idx[w];
+        }
+      a.tokens[dst + r] = bi < V ? bi : 0;  // all NaN: token 0
+    }
+    __syncthreads();
+  }
+}
+
 template <int MB, int LPR>
-__device__ __forceinline__ void head_items(const mvp::PackedArgs& pa, int panels, int passes) {
+__device__ __forceinline__ void head_items(const LoopArgs& a, const mvp::PackedArgs& pa,
+                                           int panels, int passes, HeadArgmax am) {
+  constexpr int PW = 8 * LPR;
+  __shared__ int s_last;
   const int blk = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
   const int nblk = gridDim.x * gridDim.y * gridDim.z;
-  for (int it = blk; it < panels * passes; it += nblk) {
-    mvp::packed_item<MB, LPR, (MB == 1 ? 8 : 4)>(pa, it % panels, it / panels);
-    __syncthreads();  // the item's LDS sums are read before the next item writes them
+  const int items = panels * passes;
+  for (int it = blk; it < items; it += nblk) {
+    const int panel = it % panels, pass = it / panels;
+    mvp::packed_item<MB, LPR, (MB == 1 ? 8 : 4)>(pa, panel, pass);
+    __syncthreads();  // the item's logits are written; its LDS sums are read
+    if (am.dst >= 0) {
+      panel_candidates<PW>(a, pa, panel, pass, panels);
+      __builtin_amdgcn_s_waitcnt(0);  // the candidates reached the coherence point
+      __syncthreads();
+      if (threadIdx.x == 0) {
+        const uint32_t prev = __hip_atomic_fetch_add(a.cand_arrivals, 1u, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+        const int last = prev == (uint32_t)(items - 1);
+        if (last)
+          __hip_atomic_store(a.cand_arrivals, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = last;
+      }
+      __syncthreads();
+      if (s_last) reduce_candidates(a, pa.M, panels, pa.d_out, am.dst);
+    }
   }
 }
 
 template <int LPR>
-__device__ __forceinline__ void head_rows(const mvp::PackedArgs& pa, int panels, int passes) {
+__device__ __forceinline__ void head_rows(const LoopArgs& a, const mvp::PackedArgs& pa,
+                                          int panels, int passes, HeadArgmax am) {
   switch (pa.pass_rows) {
-    case 1: head_items<1, LPR>(pa, panels, passes); break;
-    case 2: head_items<2, LPR>(pa, panels, passes); break;
-    case 3: head_items<3, LPR>(pa, panels, passes); break;
-    case 4: head_items<4, LPR>(pa, panels, passes); break;
-    case 5: head_items<5, LPR>(pa, panels, passes); break;
-    case 6: head_items<6, LPR>(pa, panels, passes); break;
-    case 7: head_items<7, LPR>(pa, panels, passes); break;
-    case 8: head_items<8, LPR>(pa, panels, passes); break;
-    default: head_items<9, LPR>(pa, panels, passes); break;
+    case 1: head_items<1, LPR>(a, pa, panels, passes, am); break;
+    case 2: head_items<2, LPR>(a, pa, panels, passes, am); break;
+    case 3: head_items<3, LPR>(a, pa, panels, passes, am); break;
+    case 4: head_items<4, LPR>(a, pa, panels, passes, am); break;
+    case 5: head_items<5, LPR>(a, pa, panels, passes, am); break;
+    case 6: head_items<6, LPR>(a, pa, panels, passes, am); break;
+    case 7: head_items<7, LPR>(a, pa, panels, passes, am); break;
+    case 8: head_items<8, LPR>(a, pa, panels, passes, am); break;
+    default: head_items<9, LPR>(a, pa, panels, passes, am); break;
   }
 }
 
 __device__ __attribute__((noinline)) void head_logits(const LoopArgs& a, int r0, int n,
-                                                      float* logits) {
+                                                      float* logits, int argmax_dst) {
   const int d = wave_uniform(a.d), V = wave_uniform(a.m.vocab);
   n = wave_uniform(n);
   const mvp::PackedShape sh = mvp::packed_shape(d, V);
@@ -383,18 +448,17 @@ __device__ __attribute__((noinline)) void head_logits(const LoopArgs& a, int r0,
   pa.n_batches = sh.n_batches;
   pa.accumulate = 0;
   const int passes = mvp::packed_passes(n);
+  const HeadArgmax am{wave_uniform(argmax_dst)};
   if (sh.lpr == 2)
-    head_rows<2>(pa, sh.panels, passes);
+    head_rows<2>(a, pa, sh.panels, passes, am);
   else
-    head_rows<1>(pa, sh.panels, passes);
+    head_rows<1>(a, pa, sh.panels, passes, am);
 }
 
 // Logits of window rows [r0, r0+n) from their h_buf rows, then their
 // argmaxes into tokens[dst + row].
 __device__ __forceinline__ void decide(const LoopArgs& a, int r0, int n, int dst) {
-  head_logits(a, r0, n, a.logits);
-  barrier(a);
-  argmax_rows(a, n, dst);
+  head_logits(a, r0, n, a.logits, dst);
   barrier(a);
 }
 
@@ -418,6 +482,7 @@ __global__ void spec_loop_init_kernel(LoopArgs a) {
   uint32_t* c = static_cast<uint32_t*>(a.attn_ws);
   for (int i = threadIdx.x; i < kGridCounters; i += blockDim.x) c[i] = 0u;
   for (int i = threadIdx.x; i < kBarWords; i += blockDim.x) a.bar[i] = 0u;
+  if (threadIdx.x == 0) *a.cand_arrivals = 0u;
   if (a.offset) {  // the sampling loop: its device function's counters, its state words
     for (int i = threadIdx.x; i < kSpecScratchWords; i += blockDim.x) a.sscratch[i] = 0u;
   }
@@ -533,7 +598,7 @@ __global__ __launch_bounds__(kThreads) void spec_loop_stochastic_kernel(LoopArgs
       run_layers(a, t.lo, t.hi, t.r0, t.n, P);
       if (!t.verify && s >= a.k) continue;
       float* lg = t.verify ? a.logits : a.dlogits + (size_t)s * V;
-      head_logits(a, t.r0, t.n, lg);
+      head_logits(a, t.r0, t.n, lg, -1);
       barrier(a);
       if (t.verify) break;
       int st = device_spec_accept_stochastic_grid(lg, nullptr, nullptr, 0, V, temp, 1.f, a.smp.seed,
@@ -650,6 +715,8 @@ int launch_loop(sde_kv_cache* cache, const sde_loop_model* model, int k, int n_d
   a.attn_ws = ws + lay.attn;
   a.attn_ws_bytes = lay.q - lay.attn;
   a.head_packed = reinterpret_cast<const uint4*>(ws + lay.head);
+  a.cand_arrivals = reinterpret_cast<uint32_t*>(ws + lay.cand);
+  a.cand = reinterpret_cast<uint2*>(ws + lay.cand + 256);
   a.q_buf = reinterpret_cast<float*>(ws + lay.q);
   a.h_buf = reinterpret_cast<float*>(ws + lay.h);
   a.logits = reinterpret_cast<float*>(ws + lay.logits);
