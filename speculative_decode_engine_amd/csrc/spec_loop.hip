@@ -20,8 +20,9 @@
 //
 // What differs from the reference by design: attention runs on every block
 // (device_flash_attention_gqa_grid) instead of block 0, the output head on
-// every block (device_matvec_grid), and the window's appends and argmaxes on
-// one block per window row.  The model is the paged-KV path's own: layer l
+// every block (over a panel-packed copy of its weights, whole output
+// columns per block, with the greedy argmax reduced from per-panel
+// candidates), and the window's appends on one block per window row.  The model is the paged-KV path's own: layer l
 // of token t reads q, k, v rows from per-layer embedding tables, q adds the
 // previous layer's attention output (a residual stream through the
 // attention), and fp16 head weights map the last layer's attention output to
@@ -42,7 +43,7 @@ namespace loop {
 
 constexpr int kThreads = 512;
 constexpr uint32_t kSpinLimit = 1u << 18;  // polls of a grid barrier before it gives up
-constexpr int kMaxWindow = 16;  // k + 1 rows (device_matvec_grid's limit)
+constexpr int kMaxWindow = 16;  // k + 1 rows (two passes of the packed head)
 
 // Words of d_state.
 enum : int {
