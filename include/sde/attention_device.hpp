@@ -983,17 +983,18 @@ struct StreamPlan {
 
 __host__ __device__ inline StreamPlan stream_plan(int L_max, int nkv, int R, int blocks,
                                                   int waves, int max_chunk, int rows) {
+  // (32-bit divisions: every quotient here is small, and a grid device
+  // function's blocks each compute this plan before their first load)
   StreamPlan p;
   p.rpw = rows;
   p.row_groups = (R + p.rpw - 1) / p.rpw;
   const int n_tiles = (L_max + kTile - 1) / kTile;
   const int64_t units = (int64_t)nkv * p.row_groups;
-  int64_t parts = blocks / units;
-  if (parts < 1) parts = 1;
+  int parts = units >= blocks ? 1 : blocks / (int)units;
   if (parts > kStreamMaxParts) parts = kStreamMaxParts;
-  const int64_t by_len = (n_tiles + waves - 1) / waves;
+  const int by_len = (n_tiles + waves - 1) / waves;
   if (parts > by_len) parts = by_len;
-  const int per_wave = (int)((n_tiles + parts * waves - 1) / (parts * waves));
+  const int per_wave = (n_tiles + parts * waves - 1) / (parts * waves);
   // When the tiles exceed a whole number (2 or more) of tiles per wave by
   // at most one per wave (a window's few positions past a round context
   // length), the last partition takes the extra tiles instead of every wave
@@ -1001,12 +1002,12 @@ __host__ __device__ inline StreamPlan stream_plan(int L_max, int nkv, int R, int
   // 21.6 -> 20.7 us, a 5-query window at 16K 34.6 -> 30.5; with one tile
   // per wave the extra tile doubles the last partition's work: the grid
   // device function's 4K window took 22.3 us that way against 20.7).
-  const int64_t whole = n_tiles / (parts * waves);
+  const int whole = n_tiles / (parts * waves);
   if (per_wave >= 3 && whole >= 2 && whole <= max_chunk &&
       n_tiles - whole * parts * waves <= waves) {
-    p.chunk = (int)whole;
+    p.chunk = whole;
     p.tiles_per_part = waves * p.chunk;
-    p.n_parts = (int)parts;
+    p.n_parts = parts;
     return p;
   }
   p.chunk = per_wave < max_chunk ? (per_wave < 1 ? 1 : per_wave) : max_chunk;
@@ -1016,9 +1017,22 @@ __host__ __device__ inline StreamPlan stream_plan(int L_max, int nkv, int R, int
   return p;
 }
 
-// Rows per group of the device functions: 4 (decode of up to 4 q heads per
-// KV head) or 16 (everything larger) -- the MFMA computes 16 rows either
-// way; fewer rows per group give a KV head more workgroups.
+// Rows per group of the 8-wave kernels (libsde_paged's and the 8-wave grid
+// device function; an MFMA tile holds 16; measured on MI355X): up to 8 rows
+// (decode) in groups of 4 (2 for up to 2), so a KV head's rows keep twice
+// the workgroups pulling K/V; verify windows of up to 48 rows over contexts
+// up to 16K in groups of 8, whose repeated K/V reads are cache hits; larger
+// windows and longer contexts in groups of 16, the fewest repeated reads.
+__host__ __device__ inline int stream_rows(int R, int L_max) {
+  if (R <= 2) return 2;
+  if (R <= 8) return 4;
+  if (R <= 48 && L_max <= 16384) return 8;
+  return 16;
+}
+
+// Rows per group of the 4-wave device functions: 4 (decode of up to 4 q
+// heads per KV head) or 16 (everything larger) -- the MFMA computes 16 rows
+// either way; fewer rows per group give a KV head more workgroups.
 __host__ __device__ inline int device_rows(int R) { return R <= 4 ? 4 : 16; }
 
 // Static LDS shared by the device functions of one kernel (a function-scope
@@ -1042,33 +1056,65 @@ __device__ __forceinline__ void block_units(const AttnArgs& a, int nwaves) {
   }
 }
 
-template <int DPH, int RPW, int WAVES, int MaxWaves>
+// The items (partition, KV head, row group) of a call, taken by the grid's
+// blocks in turns, CHUNK tiles per wave in flight; in libsde_paged's
+// workgroup order (with four tiles per wave or more the KV head fastest:
+// blocks that run together read the adjacent KV-head slices of the same
+// token rows).
+template <int DPH, int RPW, int CHUNK, int WAVES, int MaxWaves>
 __device__ __forceinline__ void grid_items(const AttnArgs& a) {
   auto& lds = *reinterpret_cast<MfmaLds<DPH, MaxWaves>*>(device_lds<MaxWaves>());
   const int n_blocks = gridDim.x * gridDim.y * gridDim.z;
   const int block = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
   const int items = a.nkv * a.row_groups * a.n_parts;
   for (int it = block; it < items; it += n_blocks) {
-    const int part = it % a.n_parts;
-    const int unit = it / a.n_parts;
-    __syncthreads();  // the previous item's readers of lds are done
-    stream_item<DPH, RPW, 2, WAVES>(a, part, unit % a.nkv, unit / a.nkv, lds);
+    int part, kvh, rg;
+    if constexpr (CHUNK >= 4) {
+      kvh = it % a.nkv;
+      part = (it / a.nkv) % a.n_parts;
+      rg = it / (a.nkv * a.n_parts);
+    } else {
+      part = it % a.n_parts;
+      const int unit = it / a.n_parts;
+      kvh = unit % a.nkv;
+      rg = unit / a.nkv;
+    }
+    stream_item<DPH, RPW, CHUNK, WAVES>(a, part, kvh, rg, lds);
+    if (it + n_blocks < items) __syncthreads();  // this item's readers of lds are done
   }
 }
 
-template <int WAVES, int MaxWaves>
-__device__ __forceinline__ void grid_dispatch(const AttnArgs& a, int dph, int rpw) {
-  static_assert(WAVES <= MaxWaves, "staging for every wave");
-  if (dph == 128) {
-    if (rpw == 4)
-      grid_items<128, 4, WAVES, MaxWaves>(a);
-    else
-      grid_items<128, 16, WAVES, MaxWaves>(a);
-  } else {
-    if (rpw == 4)
-      grid_items<64, 4, WAVES, MaxWaves>(a);
-    else
-      grid_items<64, 16, WAVES, MaxWaves>(a);
+// 4-wave blocks: rows per group 4 or 16, two tiles per wave in flight (on
+// the MaxWaves-sized staging).
+template <int DPH, int MaxWaves>
+__device__ __forceinline__ void grid_dispatch4(const AttnArgs& a, int rpw) {
+  if (rpw == 4)
+    grid_items<DPH, 4, 2, 4, MaxWaves>(a);
+  else
+    grid_items<DPH, 16, 2, 4, MaxWaves>(a);
+}
+
+// 8-wave blocks: the plans of libsde_paged's kernel (2-16 rows per group,
+// 1-4 tiles per wave in flight; a wave with one tile and a chunk of two
+// loads and multiplies a second, masked tile: measured on MI355X at the 4K
+// decode, 15.3 against 11.8 us with a chunk of one).
+template <int DPH, int RPW>
+__device__ __forceinline__ void grid_chunks8(const AttnArgs& a, int chunk) {
+  switch (chunk) {
+    case 1: grid_items<DPH, RPW, 1, 8, 8>(a); break;
+    case 2: grid_items<DPH, RPW, 2, 8, 8>(a); break;
+    case 3: grid_items<DPH, RPW, 3, 8, 8>(a); break;
+    default: grid_items<DPH, RPW, 4, 8, 8>(a); break;
+  }
+}
+
+template <int DPH>
+__device__ __forceinline__ void grid_dispatch8(const AttnArgs& a, int rpw, int chunk) {
+  switch (rpw) {
+    case 2: grid_chunks8<DPH, 2>(a, chunk); break;
+    case 4: grid_chunks8<DPH, 4>(a, chunk); break;
+    case 8: grid_chunks8<DPH, 8>(a, chunk); break;
+    default: grid_chunks8<DPH, 16>(a, chunk); break;
   }
 }
 
@@ -1320,8 +1366,10 @@ __device__ __forceinline__ int device_flash_attention_gqa_grid(const float* q_al
   const int waves = (MaxWaves == 8 && blockDim.x >= 512) ? 8 : 4;
   const int G = nh / nkv;
   const int R = n_queries * G;
-  const StreamPlan p = stream_plan(L_max, nkv, R, gridDim.x * gridDim.y * gridDim.z, waves, 2,
-                                   device_rows(R));
+  const int n_blocks = gridDim.x * gridDim.y * gridDim.z;
+  const StreamPlan p = waves == 8
+                           ? stream_plan(L_max, nkv, R, n_blocks, 8, 4, stream_rows(R, L_max))
+                           : stream_plan(L_max, nkv, R, n_blocks, 4, 2, device_rows(R));
   if ((int64_t)nkv * p.row_groups > kGridCounters) return SDE_ERR_UNSUPPORTED;
   AttnArgs a;
   a.src = TileSource{kv.pool, kv.block_tables + (size_t)layer * kv.max_blocks_per_layer,
@@ -1342,12 +1390,18 @@ __device__ __forceinline__ int device_flash_attention_gqa_grid(const float* q_al
 
   if constexpr (MaxWaves == 8) {
     if (waves == 8) {
-      attn::grid_dispatch<8, MaxWaves>(a, dph, p.rpw);
+      if (dph == 128)
+        attn::grid_dispatch8<128>(a, p.rpw, p.chunk);
+      else
+        attn::grid_dispatch8<64>(a, p.rpw, p.chunk);
       __syncthreads();
       return SDE_OK;
     }
   }
-  attn::grid_dispatch<4, MaxWaves>(a, dph, p.rpw);
+  if (dph == 128)
+    attn::grid_dispatch4<128, MaxWaves>(a, p.rpw);
+  else
+    attn::grid_dispatch4<64, MaxWaves>(a, p.rpw);
   __syncthreads();
   return SDE_OK;
 }

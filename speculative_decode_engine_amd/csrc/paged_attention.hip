@@ -91,22 +91,9 @@ int parts_bound(int max_total_len) {
   return by_len < kStreamMaxParts ? by_len : kStreamMaxParts;
 }
 
-// Rows per group on the MFMA path (an MFMA tile holds 16; measured on
-// MI355X): up to 8 rows (decode) in groups of 4, so a KV head's rows keep
-// twice the workgroups pulling K/V; verify windows of up to 48 rows over
-// contexts up to 16K in groups of 8, whose repeated K/V reads are cache
-// hits; larger windows and longer contexts in groups of 16, the fewest
-// repeated reads.
-int mfma_rows(int R, int L_max) {
-  if (R <= 2) return 2;
-  if (R <= 8) return 4;
-  if (R <= 48 && L_max <= 16384) return 8;
-  return 16;
-}
-
 // The plan of a call: 8-wave workgroups, one per CU.
 StreamPlan plan_for(int L_max, int nkv, int R, int n_cus) {
-  return stream_plan(L_max, nkv, R, n_cus, kStreamWaves, 4, mfma_rows(R, L_max));
+  return stream_plan(L_max, nkv, R, n_cus, kStreamWaves, 4, stream_rows(R, L_max));
 }
 
 size_t partial_bytes(int nkv, int R, int n_parts, int dph) {
