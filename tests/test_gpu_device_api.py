@@ -330,6 +330,9 @@ def grid_attention(dev, cache, q, nh, nkv, dph, pos_base, blocks, threads, ws, l
     (32, 4, 64, 16, 2048, 1, 37, 320, 4),      # TinyLlama, odd grid, a wave past the four
     (4, 2, 64, 16, 128, 1, 1, 256, 4),         # config 1 shape on a single block
     (8, 8, 128, 8, 77, 2, 512, 512, 8),        # ragged last tile, more blocks than work
+    (32, 8, 128, 16, 4096, 5, 256, 512, 8),    # 4K verify window, 8-wave: 8-row groups, 2 tiles
+    (4, 2, 64, 16, 40, 1, 256, 512, 8),        # G = 2 decode, 8-wave: 2-row groups, 1 tile
+    (32, 8, 128, 16, 17000, 5, 256, 512, 8),   # window past 16K, 8-wave: 16-row groups
 ])
 def test_grid_attention_matches_oracle_and_host_entry(dev, oracle, nh, nkv, dph, bs, ctx, M,
                                                       blocks, threads, max_waves):
