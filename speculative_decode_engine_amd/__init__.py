@@ -10,8 +10,10 @@ from .kv_cache import (ATTN_KDA, ATTN_LINEAR, ATTN_SLIDING_WINDOW, ATTN_SOFTMAX,
 from ._native import SDEError
 from .matvec import PackedWeight, matvec, matvec_packed, matvec_workspace
 from .sdec import SDECModel, load_sdec, read_header, write_sdec
+from .spec_loop import SpecLoopModel, spec_loop_greedy, spec_loop_stochastic
 
 __all__ = ["KVCache", "kv_cache_alloc", "kv_cache_free", "kv_cache_reset", "SDEError",
            "spec_accept_greedy", "spec_accept_stochastic", "matvec", "matvec_workspace", "PackedWeight", "matvec_packed",
            "SDECModel", "load_sdec", "read_header", "write_sdec",
+           "SpecLoopModel", "spec_loop_greedy", "spec_loop_stochastic",
            "ATTN_SOFTMAX", "ATTN_SLIDING_WINDOW", "ATTN_KDA", "ATTN_LINEAR"]
