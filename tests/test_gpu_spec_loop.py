@@ -80,6 +80,8 @@ CASES = [
     (6, (4, 4, 2, 64, 256), 40, 7, 1),
     (5, (3, 8, 2, 128, 512), 700, 4, 1),
     (9, (2, 32, 8, 128, 1024), 2000, 5, 1),   # Llama-3-8B heads, multi-partition windows
+    (7, (3, 8, 2, 64, 512), 300, 15, 1),      # the largest window: the head in two passes of 8
+    (8, (2, 8, 2, 128, 256), 100, 9, 1),      # 10 rows: two passes of 5
 ]
 
 
