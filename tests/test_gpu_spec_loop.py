@@ -165,6 +165,8 @@ STOCH_CASES = [
     (6, (4, 4, 2, 64, 256), 40, 7, 1, 0.8, True, 36),
     (5, (3, 8, 2, 128, 512), 300, 4, 1, 1.0, False, 25),
     (3, (4, 4, 2, 64, 256), 40, 0, 0, 1.0, False, 1),   # k = 0: plain sampling
+    (7, (3, 8, 2, 64, 512), 60, 15, 1, 0.8, True, 19),  # the largest window: two head passes
+    (8, (2, 8, 2, 128, 256), 40, 9, 1, 1.0, False, 2),  # 10 rows
 ]
 
 
