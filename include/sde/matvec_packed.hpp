@@ -75,6 +75,26 @@ __host__ __device__ inline int packed_pass_rows(int M) {
   return (M + n - 1) / n;
 }
 
+// Passes of one host launch of M rows (the grid's second dimension).  The
+// passes of one panel are workgroups p, p + panels, ...; with the panel
+// count a multiple of 8 they run on one XCD, so when the whole packed
+// matrix fits the 8 XCDs' L2 (at most 28 MiB of their 8 x 4 MiB) the later
+// passes re-read the panel from that L2, and passes of up to 3 rows (97
+// VGPRs: several workgroups per CU) beat one pass of up to 9 rows (up to 212
+// VGPRs: one workgroup per CU) when that one-pass grid takes more than one
+// round of the CUs or holds more than 5 rows.  Measured on MI355X, us, one
+// pass vs 3-row passes: 3584 x 3584 with 9 rows 18.0 vs 14.5, 5 rows 12.4
+// vs 11.4; 2048 x 2048 with 9 rows 8.1 vs 7.5, 5 rows 5.9 vs 6.1 (kept at
+// one pass); 4096 x 4096 (32 MiB) with 9 rows 13.7 vs 14.3; 14336 x 4096
+// with 9 rows 31.5 vs 50.7.
+inline int packed_launch_passes(int M, const PackedShape& s, int n_cus) {
+  const int one = packed_passes(M);
+  if (M <= 3 || one > 1 || s.panels % 8 != 0) return one;
+  if (s.units * 16 > ((size_t)28 << 20)) return one;
+  if (s.panels <= n_cus && M <= 5) return one;
+  return (M + 2) / 3;
+}
+
 struct PackedArgs {
   const uint4* W;   // packed units
   const float* x;   // [M][d_in], 16-byte aligned

@@ -170,10 +170,14 @@ int sde_matvec_packed(const float* d_x, const void* d_packed, float* d_out, int 
   a.d_in = d_in;
   a.d_out = d_out_dim;
   a.M = M;
-  a.pass_rows = sde::mvp::packed_pass_rows(M);
+  int st = SDE_OK;
+  const int n_cus = current_cus(&st);
+  if (st != SDE_OK) return st;
+  const int passes = sde::mvp::packed_launch_passes(M, sh, n_cus);
+  a.pass_rows = (M + passes - 1) / passes;
   a.n_batches = sh.n_batches;
   a.accumulate = accumulate ? 1 : 0;
-  const dim3 grid(sh.panels, sde::mvp::packed_passes(M));
+  const dim3 grid(sh.panels, passes);
   const dim3 block(64 * sde::mvp::kWaves);
   const hipStream_t s = (hipStream_t)stream;
 #define SDE_MVP(MB)                                                                  \

@@ -79,7 +79,9 @@ SHAPES = [
     (5, 4096, 4096),     # Llama-3-8B verify window
     (1, 14336, 4096),    # Llama-3-8B W_down
     (5, 14336, 4096),
-    (9, 3584, 3584),     # Qwen2.5-7B verify window: one pass of 9 rows, 8-column panels
+    (9, 3584, 3584),     # Qwen2.5-7B verify window: three passes of 3 rows, 8-column panels
+    (5, 3584, 3584),     # passes of 3 + 2 rows (448 panels, more than one round of the CUs)
+    (7, 2048, 2048),     # passes of 3 + 3 + 1 rows (more than 5 rows, 2048 x 2048 fits L2)
     (1, 2048, 2048),     # TinyLlama
     (1, 256, 256),       # tiny model
     (16, 640, 520),      # the largest row count: two passes of 8
@@ -87,8 +89,8 @@ SHAPES = [
     (7, 264, 4112),      # 16-column panels with d_in shorter than one batch
     (3, 8, 8),           # one unit row
     (2, 4096, 1024),
-    (4, 2048, 2048),
-    (8, 8192, 512),
+    (4, 2048, 2048),     # one pass of 4 rows
+    (8, 8192, 512),      # passes of 3 + 3 + 2 rows
 ]
 
 
