@@ -369,14 +369,37 @@ def bench_sdec_load(torch, layers=2):
         shutil.rmtree(tmp, ignore_errors=True)
 
 
+def measure_lib():
+    """libsde_measure.so: the streaming-read and load-skeleton kernels."""
+    import ctypes
+    from speculative_decode_engine_amd import _native
+    _native.load()
+    path = ROOT / "speculative_decode_engine_amd" / "libsde_measure.so"
+    if not path.exists():
+        raise RuntimeError(f"{path} is not built; run __graft_entry__.build()")
+    lib = ctypes.CDLL(str(path))
+    vp, sz = ctypes.c_void_p, ctypes.c_size_t
+    lib.sde_measure_stream_read.argtypes = [vp, sz, ctypes.c_int, vp, vp]
+    lib.sde_measure_stream_read.restype = ctypes.c_int
+    ci = ctypes.c_int
+    lib.sde_measure_attention_loads.argtypes = [vp, ci, ci, ci, ci, ci, ci, ci, vp, vp]
+    lib.sde_measure_attention_loads.restype = ctypes.c_int
+    return lib
+
+
 def measured_hbm(torch, nbytes=2 << 30, reps=5):
-    """Same-process reference points for the HBM roofline: the best of
-    `reps` device-to-device copies of an nbytes buffer (read + write bytes
-    over the time) and the best of `reps` fp32 sums over it (read bytes over
-    the time), each between HIP events on the current stream."""
+    """Same-process reference points for the HBM roofline: a hand-written
+    HIP streaming read of an nbytes buffer (sde_measure_stream_read:
+    16-byte loads, eight in flight per thread; the best of `reps` runs at
+    each of several grid sizes, read bytes over the time) and the best of
+    `reps` device-to-device copies (torch copy_, read + write bytes), each
+    between HIP events on the current stream."""
+    import ctypes
+    lib = measure_lib()
     src = torch.ones(nbytes // 4, device="cuda")
-    dst = torch.empty_like(src)
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda")
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    n_cus = torch.cuda.get_device_properties(0).multi_processor_count
 
     def best(fn):
         fn()
@@ -389,54 +412,141 @@ def measured_hbm(torch, nbytes=2 << 30, reps=5):
             torch.cuda.synchronize()
             t.append(e0.elapsed_time(e1) * 1e-3)
         return min(t)
+
+    def read(blocks):
+        rc = lib.sde_measure_stream_read(ctypes.c_void_p(src.data_ptr()), nbytes, blocks,
+                                         ctypes.c_void_p(sink.data_ptr()),
+                                         ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        if rc != 0:
+            raise RuntimeError(f"sde_measure_stream_read: {rc}")
+    t_read = {b: best(lambda b=b: read(b)) for b in (n_cus * 2, n_cus * 4, n_cus * 8, n_cus * 16)}
+    blocks = min(t_read, key=t_read.get)
+    dst = torch.empty_like(src)
     t_copy = best(lambda: dst.copy_(src))
-    t_read = best(lambda: src.sum())
     del src, dst
     torch.cuda.empty_cache()
-    return dict(copy_gbps=round(2 * nbytes / t_copy / 1e9, 1),
-                read_gbps=round(nbytes / t_read / 1e9, 1), bytes=nbytes,
-                how="best of 5: torch copy_ of a 2 GiB fp32 buffer (read+write bytes), "
-                    "torch sum over it (read bytes)")
+    return dict(read_gbps=round(nbytes / t_read[blocks] / 1e9, 1),
+                copy_gbps=round(2 * nbytes / t_copy / 1e9, 1), bytes=nbytes,
+                read_blocks=blocks,
+                how="HIP streaming read (sde_measure_stream_read, 512-thread workgroups, best "
+                    "grid of 2-16 per CU, best of 5) of a 2 GiB buffer, read bytes; torch "
+                    "copy_ of it, read + write bytes")
+
+
+def bench_pattern_floor(torch, W, w, steps, warmup):
+    """The load skeleton of the headline's attention call
+    (sde_measure_attention_loads: the kernel's plan, grid, workgroup
+    mapping, per-wave tiles, table lookups and K/V loads in the same order,
+    no arithmetic, staging, merge or combine), graph-replayed over the same
+    2 GiB rotation as the kernel: the floor of the kernel's access pattern,
+    measured in the same process."""
+    import ctypes
+    lib = measure_lib()
+    pos_base = w.l_max - 1
+    l_max = pos_base + 1
+    per_layer = 4 * w.kv_dim * l_max
+    n_layers = max(1, min(4096, math.ceil(ROTATE_BYTES / per_layer)))
+    nblk = -(-l_max // w.block_size)
+    cache = make_rotation_cache(torch, W, w, n_layers, l_max,
+                                max(w.pool_blocks, n_layers * nblk), w.seed)
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+    n_cus = torch.cuda.get_device_properties(0).multi_processor_count
+
+    def step(i):
+        rc = lib.sde_measure_attention_loads(
+            cache.handle, i % n_layers, w.nh, w.nkv, w.dph, pos_base, 1,
+            n_cus, ctypes.c_void_p(sink.data_ptr()),
+            ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        if rc != 0:
+            raise RuntimeError(f"sde_measure_attention_loads: {rc}")
+    ms = graph_step_ms(torch, step, steps, warmup)
+    cache.free()
+    nbytes = w.algorithmic_bytes(l_max=l_max, n_app=0, n_queries=1)
+    return dict(us=round(ms * 1e3, 3), gbps=round(nbytes / (ms * 1e-3) / 1e9, 1),
+                rotated_layers=n_layers,
+                how="load skeleton of the same call (sde_measure_attention_loads), "
+                    "graph-replayed like the kernel")
 
 
 def cpu_threads():
-    return int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
+    """Host threads for the CPU baseline: the box's CPU share (its
+    OMP_NUM_THREADS, else the process's CPU affinity), not every core the
+    host reports."""
+    env = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    try:
+        share = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        share = os.cpu_count() or 1
+    return min(env, share) if env else share
 
 
-def cpu_config(W, w, mode, seconds):
-    """The CPU oracle on one layer-step of `mode` (bench_config's modes) at
-    workload w's shape: the append of the window (fp32 -> fp16) and the
-    literal fp32 tile restatement of attention.h (OpenMP over (query, head)
-    pairs), repeated for about `seconds`.  Fused modes time the same two
-    steps (the oracle has no fused form; RoPE is excluded)."""
+def cpu_model() -> str:
+    """The host CPU as /proc/cpuinfo names it (model name, family / model /
+    stepping, logical CPUs the host reports)."""
+    info = {}
+    try:
+        for line in open("/proc/cpuinfo"):
+            if ":" in line:
+                k, v = line.split(":", 1)
+                info.setdefault(k.strip(), v.strip())
+    except OSError:
+        return "unknown"
+    return (f"{info.get('model name', 'unknown')} (vendor {info.get('vendor_id', '?')}, family "
+            f"{info.get('cpu family', '?')} model {info.get('model', '?')} stepping "
+            f"{info.get('stepping', '?')}; {os.cpu_count()} logical CPUs on the host)")
+
+
+def cpu_step(W, w, mode, seconds, reps_min=5):
+    """One layer-step of `mode` (bench_config's modes) at workload w's shape
+    on the CPU, BASELINE.md's torch-CPU restatement of the reference
+    semantics (oracle.attention_torch_cpu: block-table index_select gather,
+    fp32 q.K^T * dph^-1/2, causal mask, softmax, .V; the window's append as
+    an fp32 -> fp16 scatter into the pool), torch on cpu_threads() threads.
+    2 warm-ups, then at least reps_min repetitions and about `seconds`;
+    the median per step.  Fused modes time the same steps (RoPE excluded)."""
+    import torch
     from oracle import paged_kv as O
     threads = cpu_threads()
+    torch.set_num_threads(threads)
     n_q = 1 if mode.startswith(("attn", "decode")) else w.n_queries
     n_app = 0 if mode == "attn" else n_q
     pos_base = w.ctx if mode != "attn" else w.l_max - 1
     l_max = pos_base + n_q
     rng = np.random.default_rng(w.seed)
     nblk = -(-l_max // w.block_size)
-    pool = 2 * nblk
-    m = O.PagedKVModel(1, w.kv_dim, nblk, w.block_size, pool)
-    m.set_block_table(0, rng.permutation(pool)[:nblk])
-    m.pool[...] = (rng.standard_normal(m.pool.shape, dtype=np.float32)
-                   .astype(np.float16).view(np.uint16))
-    q = W.queries(rng, n_q, w.nh, w.dph)
-    k, v = W.new_kv(rng, max(n_app, 1), w.kv_dim)
-    reps = 0
-    t0 = time.perf_counter()
-    while True:
-        if n_app:
-            m.append(0, k[:n_app], v[:n_app], pos_base)
-        m.attention(0, q, w.nh, w.nkv, w.dph, pos_base, mode="tiled", threads=threads)
-        reps += 1
-        if time.perf_counter() - t0 >= seconds:
-            break
-    dt = (time.perf_counter() - t0) / reps
+    pool_blocks = 2 * nblk
+    pool = torch.from_numpy(rng.standard_normal((pool_blocks, 2, w.block_size, w.kv_dim),
+                                                dtype=np.float32).astype(np.float16))
+    table = torch.from_numpy(rng.permutation(pool_blocks)[:nblk].astype(np.int64))
+    q = torch.from_numpy(W.queries(rng, n_q, w.nh, w.dph))
+    k, v = (torch.from_numpy(x) for x in W.new_kv(rng, max(n_app, 1), w.kv_dim))
+    pos = torch.arange(pos_base, pos_base + n_app)
+    blk, slot = table[pos // w.block_size], pos % w.block_size
+
+    def step():
+        if n_app:  # kv_cache_append: fp32 -> fp16 (RNE) at (table[pos/BS], pos%BS)
+            pool[blk, 0, slot] = k[:n_app].half()
+            pool[blk, 1, slot] = v[:n_app].half()
+        return O.attention_torch_cpu(pool, table, q, w.nh, w.nkv, w.dph, w.block_size, pos_base)
+
+    for _ in range(2):
+        step()
+    times = []
+    t_end = time.perf_counter() + seconds
+    while len(times) < reps_min or time.perf_counter() < t_end:
+        t = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t)
+    dt = float(np.median(times))
     nbytes = w.algorithmic_bytes(l_max=l_max, n_app=n_app, n_queries=n_q)
     return dict(us_per_layer_step=round(dt * 1e6, 1), gbps=round(nbytes / dt / 1e9, 3),
-                reps=reps, cores=threads)
+                reps=len(times), cores=threads, kind="port",
+                how="torch-CPU gather + fp32 softmax attention (oracle.attention_torch_cpu)")
+
+
+def cpu_config(W, w, mode, seconds):
+    """cpu_step for a configs entry (a bounded sample)."""
+    return cpu_step(W, w, mode, seconds)
 
 
 def bench_grid_device_fn(torch, W, steps, warmup):
@@ -554,42 +664,18 @@ def bench_spec_loop(torch, max_new=64):
 
 
 def cpu_baseline(W, w, seconds):
-    """The CPU oracle's tile restatement of attention.h (OpenMP over
-    (query, head) pairs) on one 32K-key layer-step of the same shape, run
-    repeatedly for about `seconds`."""
-    from oracle import paged_kv as O
-    threads = cpu_threads()
-    rng = np.random.default_rng(w.seed)
-    l_max = w.l_max
-    nblk = l_max // w.block_size
-    pool = 2 * nblk
-    m = O.PagedKVModel(1, w.kv_dim, nblk, w.block_size, pool)
-    m.set_block_table(0, rng.permutation(pool)[:nblk])
-    m.pool[...] = (rng.standard_normal(m.pool.shape, dtype=np.float32)
-                   .astype(np.float16).view(np.uint16))
-    q = W.queries(rng, 1, w.nh, w.dph)
-    reps = 0
-    t0 = time.perf_counter()
-    while True:
-        m.attention(0, q, w.nh, w.nkv, w.dph, l_max - 1, mode="tiled", threads=threads)
-        reps += 1
-        if time.perf_counter() - t0 >= seconds:
-            break
-    dt = (time.perf_counter() - t0) / reps
-    nbytes = w.algorithmic_bytes(l_max=l_max, n_app=0, n_queries=1)
-    cpu_model = ""
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                cpu_model = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
-    return dict(value=round(nbytes / dt / 1e9, 3), unit="GB/s", cores=threads, kind="port",
-                us_per_layer_step=round(dt * 1e6, 1),
-                sample=f"{reps} x one {l_max}-key layer-step ({w.nh}q/{w.nkv}kv heads, dph "
-                       f"{w.dph}, bs {w.block_size}), fp32 tile restatement of attention.h "
-                       f"in C, {threads} OpenMP threads, {cpu_model}")
+    """The headline layer-step (one query over 32768 keys, Llama-3-8B
+    heads) on the host cores: cpu_step's torch-CPU restatement, median over
+    about `seconds` of repetitions."""
+    c = cpu_step(W, w, "attn", seconds)
+    nbytes = w.algorithmic_bytes(l_max=w.l_max, n_app=0, n_queries=1)
+    return dict(value=round(nbytes / (c["us_per_layer_step"] * 1e-6) / 1e9, 3), unit="GB/s",
+                cores=c["cores"], kind="port", us_per_layer_step=c["us_per_layer_step"],
+                sample=f"median of {c['reps']} x one {w.l_max}-key layer-step ({w.nh}q/{w.nkv}kv "
+                       f"heads, dph {w.dph}, bs {w.block_size}, fragmented table): torch-CPU "
+                       f"index_select gather of the fp16 blocks, fp32 q.K^T, softmax, .V "
+                       f"(oracle.attention_torch_cpu), {c['cores']} torch threads, "
+                       f"{cpu_model()}")
 
 
 def measured_traffic(workload: str):
@@ -702,14 +788,19 @@ def main():
     achieved = nbytes / (kernel_us * 1e-6) / 1e9
     hbm = measured_hbm(torch)
     log("[bench] hbm", json.dumps(hbm))
+    floor = bench_pattern_floor(torch, W, w, steps, warmup)
+    log("[bench] pattern floor", json.dumps(floor))
     roofline = dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBPS, unit="GB/s",
                     frac=round(achieved / HBM_PEAK_GBPS, 4),
                     traffic=measured_traffic(HEADLINE), kernel=KERNEL,
                     bytes_per_launch=nbytes, kernel_us=kernel_us,
                     kernel_us_eager_events=head.get("kernel_us_events"),
-                    measured_copy_gbps=hbm["copy_gbps"], measured_read_gbps=hbm["read_gbps"],
+                    measured_read_gbps=hbm["read_gbps"], measured_copy_gbps=hbm["copy_gbps"],
+                    frac_of_measured_read=round(achieved / hbm["read_gbps"], 4),
                     frac_of_measured_copy=round(achieved / hbm["copy_gbps"], 4),
-                    frac_of_measured_read=round(achieved / hbm["read_gbps"], 4))
+                    pattern_floor_us=floor["us"], pattern_floor_gbps=floor["gbps"],
+                    kernel_over_pattern_floor=round(kernel_us / floor["us"], 4),
+                    reference_points=dict(read=hbm["how"], pattern_floor=floor["how"]))
 
     cpu = None
     if not args.no_cpu:

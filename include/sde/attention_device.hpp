@@ -85,6 +85,23 @@ __device__ __forceinline__ float half_pair_total(float a, float b) {
   return __builtin_bit_cast(float, (int)p[0]) + __builtin_bit_cast(float, (int)p[1]);
 }
 
+// Max / sum over the four 16-lane rows of a wave, returned to every lane
+// (fixed order: rows (0 + 2) and (1 + 3), then the two pairs).
+__device__ __forceinline__ float groups_max(float x) {
+  const int v = __builtin_bit_cast(int, x);
+  const auto h = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  x = fmaxf(__builtin_bit_cast(float, (int)h[0]), __builtin_bit_cast(float, (int)h[1]));
+  const int w = __builtin_bit_cast(int, x);
+  const auto r = __builtin_amdgcn_permlane16_swap(w, w, false, false);
+  return fmaxf(__builtin_bit_cast(float, (int)r[0]), __builtin_bit_cast(float, (int)r[1]));
+}
+
+__device__ __forceinline__ float groups_sum(float x) {
+  x = half_pair_total(x, x);
+  const float2 p = row_pair(x);
+  return p.x + p.y;
+}
+
 typedef const __attribute__((address_space(4))) int32_t* const_table_t;
 
 // The block table is read-only during the kernel: reading it through the
@@ -278,89 +295,126 @@ __device__ __forceinline__ float4 load_dev16(const float* base, uint32_t bytes,
   return make_float4(v.x, v.y, v.z, v.w);
 }
 
-// One pass of the partition combine over NIT row slices: thread
-// (row, float4 column c4, quarter sub) of slice it loads (max, sum, acc[c4])
-// of partitions sub, sub+4, ... for all of its slices first -- every
-// partial of the pass in one round trip, no LDS -- then weights them by
-// exp2(m_p - max), and the four quarters of a (row, column) (adjacent
-// lanes) reduce through DPP in a fixed order, so the result does not
-// depend on arrival order.  (max, sum) of partition p is loaded once per
-// wave, by lane p (a wave's lanes serve one row), and read across lanes.
-// Within a live slice every load is issued unconditionally (indices past
-// P re-read partition P-1, then weigh 0), so they all travel in one round
-// trip: a load under `if (p < P)` would get a wait of its own at the join.
+// 8 bytes at base + byte_off, device scope like load_dev2, through a raw
+// buffer of `bytes` bytes: an offset past the range reads zeros and sends
+// no request to memory.
+__device__ __forceinline__ float2 load_dev8(const float* base, uint32_t bytes, uint32_t byte_off) {
+  constexpr int kSc1 = 16;
+  constexpr int kRsrcWord3 = 0x00020000;
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(wave_uniform(base)), 0,
+                                        (int)wave_uniform(bytes), kRsrcWord3);
+  typedef float f2v __attribute__((ext_vector_type(2)));
+  const f2v v = __builtin_bit_cast(f2v, __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, kSc1));
+  return make_float2(v.x, v.y);
+}
+
+// An offset no buffer of this library's partials reaches: the load returns
+// zeros without a memory request.
+constexpr uint32_t kOutOfRange = 0xFFFFFFF0u;
+
+// Lane i ^ 4 / i ^ 8 (ds_swizzle, bit-mask mode within 32 lanes).
+__device__ __forceinline__ float swz_xor4(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, x), 0x101F));
+}
+__device__ __forceinline__ float swz_xor8(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, x), 0x201F));
+}
+
+// Max / sum over the 64 lanes by xor butterflies (within 16-lane rows, then
+// across rows): every lane gets the same bits, in a fixed order.
+__device__ __forceinline__ float wave_max(float x) {
+  x = fmaxf(x, dpp_f(x, 0));
+  x = fmaxf(x, dpp_f(x, 1));
+  x = fmaxf(x, swz_xor4(x));
+  x = fmaxf(x, swz_xor8(x));
+  return groups_max(x);
+}
+__device__ __forceinline__ float wave_sum(float x) {
+  x += dpp_f(x, 0);
+  x += dpp_f(x, 1);
+  x += swz_xor4(x);
+  x += swz_xor8(x);
+  return groups_sum(x);
+}
+
+// One pass of the partition combine.  An item is one row's 64-feature
+// column slice, served by a whole wave: lane (sub = lane/16, c = lane%16)
+// takes float4 column c of the slice for partitions sub, sub+4, ..., so the
+// 16 lanes of a sub-group read 256 contiguous bytes of one partition's
+// record.  The combine is bound by the rate at which one CU issues these
+// device-scope loads, so slots past the last partition load from beyond
+// the buffer (zeros, no request), and every load of the pass is issued
+// before any arithmetic (one round trip; a load under `if (p < P)` would
+// get a wait of its own at the join).  Per item, lane p holds partition
+// p's (max, sum): the row's max, each partition's weight exp2(m_p - max)
+// and the weighted sum of the sums are wave reductions done once, and each
+// lane reads its partitions' weights across lanes; the four sub-groups of
+// a column then reduce by lane swaps in a fixed order, so the result does
+// not depend on arrival order.
 template <int DPH, int PMAX, int NIT, int WAVES>
 __device__ __forceinline__ void combine_pass(const AttnArgs& a, int tid, int kvh, int r0,
                                              int nrows, int it0) {
-  constexpr int C4 = DPH / 4;
   constexpr int SUB = 4;
-  constexpr int NT = 64 * WAVES;
+  constexpr int SLICES = DPH / 64;  // column slices per row
   const int P = a.n_parts;
   const int lane = tid & 63;
-  const int sub = tid & (SUB - 1);
-  const int col4 = (tid / SUB) % C4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int sub = lane >> 4;
+  const int c = lane & 15;
   const size_t acc_floats = (size_t)a.nkv * a.R * P * DPH;
   const uint32_t acc_bytes = (uint32_t)(acc_floats * 4);
+  const uint32_t all_bytes = (uint32_t)((acc_floats + (size_t)a.nkv * a.R * P * 2) * 4);
   float4 v[NIT][PMAX];
-  float2 mine[NIT];
+  float2 ml[NIT];
 #pragma unroll
   for (int it = 0; it < NIT; it++) {
-    const int r = (tid + (it0 + it) * NT) / (SUB * C4);  // uniform per wave
+    const int item = wave + (it0 + it) * WAVES;  // uniform per wave
+    const int r = item / SLICES;
     if (r < nrows) {
+      const int col4 = (item - r * SLICES) * 16 + c;
       const size_t row = (size_t)kvh * a.R + r0 + r;
       const uint32_t acc_off = (uint32_t)((row * P * DPH + 4 * col4) * 4);
 #pragma unroll
       for (int i = 0; i < PMAX; i++) {
-        const int p = min(sub + i * SUB, P - 1);
-        v[it][i] = load_dev16(a.partials, acc_bytes, acc_off + (uint32_t)p * (DPH * 4));
+        const int p = sub + i * SUB;
+        v[it][i] = load_dev16(a.partials, acc_bytes,
+                              p < P ? acc_off + (uint32_t)p * (DPH * 4) : kOutOfRange);
       }
-      mine[it] = load_dev2(a.partials + acc_floats + row * P * 2 + (size_t)min(lane, P - 1) * 2);
+      ml[it] = load_dev8(a.partials, all_bytes,
+                         lane < P ? (uint32_t)((acc_floats + row * P * 2 + (size_t)lane * 2) * 4)
+                                  : kOutOfRange);
     }
   }
 #pragma unroll
   for (int it = 0; it < NIT; it++) {
-    const int r = (tid + (it0 + it) * NT) / (SUB * C4);
+    const int item = wave + (it0 + it) * WAVES;
+    const int r = item / SLICES;
     if (r >= nrows) break;
-    float2 e[PMAX];
-#pragma unroll
-    for (int i = 0; i < PMAX; i++) {
-      e[i].x = __shfl(mine[it].x, sub + i * SUB);
-      e[i].y = __shfl(mine[it].y, sub + i * SUB);
-      if (sub + i * SUB >= P) {
-        e[i] = make_float2(-INFINITY, 0.f);
-        v[it][i] = make_float4(0.f, 0.f, 0.f, 0.f);
-      }
-    }
-    float mx = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < PMAX; i++) mx = fmaxf(mx, e[i].x);
-    mx = fmaxf(mx, dpp_f(mx, 0));
-    mx = fmaxf(mx, dpp_f(mx, 1));
-    float l = 0.f;
+    const int col4 = (item - r * SLICES) * 16 + c;
+    const float m = lane < P ? ml[it].x : -INFINITY;
+    const float mx = wave_max(m);
+    const float wgt = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - mx);
+    const float l = wave_sum(lane < P ? ml[it].y * wgt : 0.f);
     float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (int i = 0; i < PMAX; i++) {
-      const float w = e[i].x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(e[i].x - mx);
-      l += e[i].y * w;
+      const float w = __shfl(wgt, sub + i * SUB);  // 0 past the last partition
       o.x += w * v[it][i].x;
       o.y += w * v[it][i].y;
       o.z += w * v[it][i].z;
       o.w += w * v[it][i].w;
     }
-#pragma unroll
-    for (int k = 0; k < 2; k++) {
-      l += dpp_f(l, k);
-      o.x += dpp_f(o.x, k);
-      o.y += dpp_f(o.y, k);
-      o.z += dpp_f(o.z, k);
-      o.w += dpp_f(o.w, k);
-    }
+    o.x = groups_sum(o.x);
+    o.y = groups_sum(o.y);
+    o.z = groups_sum(o.z);
+    o.w = groups_sum(o.w);
     if (sub == 0) {
       const float inv = finish_scale(l);
       const int gr = r0 + r;
-      const int m = gr / a.G;
-      const int h = kvh * a.G + (gr - m * a.G);
-      float2* dst = reinterpret_cast<float2*>(a.out + (size_t)m * a.nh * DPH + (size_t)h * DPH +
+      const int mq = gr / a.G;
+      const int h = kvh * a.G + (gr - mq * a.G);
+      float2* dst = reinterpret_cast<float2*>(a.out + (size_t)mq * a.nh * DPH + (size_t)h * DPH +
                                               4 * col4);
       dst[0] = make_float2(o.x * inv, o.y * inv);
       dst[1] = make_float2(o.z * inv, o.w * inv);
@@ -372,11 +426,12 @@ __device__ __forceinline__ void combine_pass(const AttnArgs& a, int tid, int kvh
 template <int DPH, int RPW, int PMAX, int WAVES>
 __device__ __forceinline__ void combine_rows(const AttnArgs& a, int tid, int kvh, int r0,
                                              int nrows) {
-  constexpr int SLICES = (RPW * DPH + 64 * WAVES - 1) / (64 * WAVES);  // RPW*C4*SUB / threads
+  constexpr int ITEMS = RPW * (DPH / 64);
+  constexpr int PER_WAVE = (ITEMS + WAVES - 1) / WAVES;
   constexpr int CAP = 32 / PMAX;
-  constexpr int NIT = SLICES < CAP ? SLICES : CAP;
+  constexpr int NIT = PER_WAVE < CAP ? PER_WAVE : CAP;
 #pragma unroll
-  for (int it0 = 0; it0 < SLICES; it0 += NIT)
+  for (int it0 = 0; it0 < PER_WAVE; it0 += NIT)
     combine_pass<DPH, PMAX, NIT, WAVES>(a, tid, kvh, r0, nrows, it0);
 }
 
@@ -386,7 +441,7 @@ template <int DPH, int RPW, int WAVES>
 __device__ __forceinline__ void stream_combine(const AttnArgs& a, int tid, int kvh, int r0,
                                                int nrows) {
   static_assert(kStreamMaxParts == 64, "combine buckets");
-  static_assert((4 * (DPH / 4)) % 64 == 0, "each wave's lanes serve one row");
+  static_assert(DPH % 64 == 0, "a wave serves one 64-feature column slice of a row");
   if (tid >= 64 * WAVES) return;  // waves past WAVES idle
   const int P = a.n_parts;
   if (P <= 16)
@@ -472,21 +527,6 @@ struct MfmaShape {
   static constexpr int TILEB = kTile * ROWB;  // bytes of one staged K or V tile
   static constexpr int WAVEB = 2 * TILEB;     // LDS bytes per wave (K and V)
 };
-
-__device__ __forceinline__ float groups_max(float x) {
-  const int v = __builtin_bit_cast(int, x);
-  const auto h = __builtin_amdgcn_permlane32_swap(v, v, false, false);
-  x = fmaxf(__builtin_bit_cast(float, (int)h[0]), __builtin_bit_cast(float, (int)h[1]));
-  const int w = __builtin_bit_cast(int, x);
-  const auto r = __builtin_amdgcn_permlane16_swap(w, w, false, false);
-  return fmaxf(__builtin_bit_cast(float, (int)r[0]), __builtin_bit_cast(float, (int)r[1]));
-}
-
-__device__ __forceinline__ float groups_sum(float x) {
-  x = half_pair_total(x, x);
-  const float2 p = row_pair(x);
-  return p.x + p.y;
-}
 
 // x = hi + lo to ~22 bits: hi = fp16(x), lo = fp16(x - hi) (the difference
 // is exact in fp32).  x is pinned as a rounded fp32 register first: when x
@@ -913,20 +953,32 @@ __device__ __forceinline__ void stream_item(const AttnArgs& a, int part, int kvh
   __syncthreads();
 
   // ---- workgroup merge: thread (row, feature pair) over the waves --------
+  // Every wave's record is read up front (waves past nwaves re-read the
+  // last one and weigh nothing), so the LDS reads overlap instead of
+  // forming a chain of round trips; the sums run in wave order.
   constexpr int DP = DPH / 2;
   for (int idx = tid; idx < nrows * DP; idx += blockDim.x) {
     const int r = idx / DP;
     const int dcol = 2 * (idx - r * DP);
+    float2 ml[WAVES], x[WAVES];
+#pragma unroll
+    for (int w = 0; w < WAVES; w++) {
+      const int ws = min(w, nwaves - 1);
+      ml[w] = lds.ml_at(ws, r);
+      x[w] = *reinterpret_cast<const float2*>(lds.acc_at(ws, r) + dcol);
+    }
     float mx = -INFINITY;
-    for (int w = 0; w < nwaves; w++) mx = fmaxf(mx, lds.ml_at(w, r).x);
+#pragma unroll
+    for (int w = 0; w < WAVES; w++)
+      if (w < nwaves) mx = fmaxf(mx, ml[w].x);
     float l = 0.f, o0 = 0.f, o1 = 0.f;
-    for (int w = 0; w < nwaves; w++) {
-      const float2 ml = lds.ml_at(w, r);
-      const float wt = ml.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ml.x - mx);
-      l += ml.y * wt;
-      const float2 x = *reinterpret_cast<const float2*>(lds.acc_at(w, r) + dcol);
-      o0 += x.x * wt;
-      o1 += x.y * wt;
+#pragma unroll
+    for (int w = 0; w < WAVES; w++) {
+      const float wt =
+          (w >= nwaves || ml[w].x == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(ml[w].x - mx);
+      l += ml[w].y * wt;
+      o0 += x[w].x * wt;
+      o1 += x[w].y * wt;
     }
     const int gr = r0 + r;
     if (a.n_parts == 1) {
@@ -1015,6 +1067,23 @@ __host__ __device__ inline StreamPlan stream_plan(int L_max, int nkv, int R, int
   p.tiles_per_part = waves * p.chunk * (reps < 1 ? 1 : reps);
   p.n_parts = (n_tiles + p.tiles_per_part - 1) / p.tiles_per_part;
   return p;
+}
+
+// Workgroup -> (partition, KV head, row group) of libsde_paged's kernels,
+// whose grid is (n_parts, nkv, row_groups).  Long contexts (waves of four
+// tiles or more) take the KV head fastest in the linear workgroup index:
+// consecutive workgroups then read the adjacent KV-head slices of the same
+// token rows at the same time, which the memory system serves faster than
+// the same slices read by workgroups far apart in dispatch order.
+template <int CHUNK>
+__device__ __forceinline__ int3 stream_coords() {
+  if constexpr (CHUNK < 4) {
+    return make_int3(blockIdx.x, blockIdx.y, blockIdx.z);
+  } else {
+    const int lin = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+    return make_int3((lin / gridDim.y) % gridDim.x, lin % gridDim.y,
+                     lin / (gridDim.x * gridDim.y));
+  }
 }
 
 // Rows per group of the 8-wave kernels (libsde_paged's and the 8-wave grid

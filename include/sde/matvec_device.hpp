@@ -321,18 +321,56 @@ template <int WAVES>
 struct MvMfmaLds {
   MvLds<WAVES> base;
   uint4 wst[WAVES][kStageBytes / 16];
+  float xmax[WAVES][kMaxRows];  // per wave: max |x| of each row over the item's range
+  float xscale[kMaxRows];       // per row of x: the power-of-two scale (1 in fp16 range)
 };
+
+// Per row of x, a power of two s with max |x| * s < 2^14 over the item's
+// rows [r0, r1) (s = 1 when x already fits, and for non-finite x, which
+// then propagates as in fp32), so the fp16 hi + lo split below never
+// overflows; the sums are multiplied by 1/s, exactly, before they leave
+// the item.  Scaling by a power of two commutes with every fp16 and fp32
+// rounding here, so the result equals the unscaled computation's wherever
+// that one is finite.  Every thread calls it; ends with a barrier.
+template <int WAVES>
+__device__ __forceinline__ void mv_row_scales(const MvArgs& a, const float* xl, int xrows,
+                                              int r0, int r1, MvMfmaLds<WAVES>& L) {
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int lane = threadIdx.x & 63;
+  for (int m = 0; m < a.M; m++) {
+    float mx = 0.f;
+    if (wave < WAVES)
+      for (int i = wave * 64 + lane; i < xrows; i += WAVES * 64)
+        mx = fmaxf(mx, fabsf(xl ? xl[m * xrows + i] : a.x[(size_t)m * a.d_in + r0 + i]));
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    if (wave < WAVES && lane == 0) L.xmax[wave][m] = mx;
+  }
+  __syncthreads();
+  if ((int)threadIdx.x < a.M) {
+    float mx = 0.f;
+    for (int w = 0; w < WAVES; w++) mx = fmaxf(mx, L.xmax[w][threadIdx.x]);
+    float sc = 1.f;
+    if (mx >= 16384.f && mx <= 3.0e38f) {  // (finite and past the fp16-safe range)
+      int e;
+      (void)frexpf(mx, &e);          // mx < 2^e
+      sc = ldexpf(1.f, 14 - e);      // mx * sc < 2^14
+    }
+    L.xscale[threadIdx.x] = sc;
+  }
+  __syncthreads();
+}
 __device__ __forceinline__ int mv_staged(int r, int u) { return r * (kCols * 2) + 16 * (u ^ (r & 15)); }
 template <int WAVES>
 __device__ __forceinline__ void mv_x_operand(const MvArgs& a, const float* xl, int xrows, int r0,
-                                             int r1, int rbase, int lane, mv_h4& xh, mv_h4& xo) {
+                                             int r1, int rbase, int lane, float sc, mv_h4& xh,
+                                             mv_h4& xo) {
   const int m = lane & 15, g = lane >> 4;
 #pragma unroll
   for (int q = 0; q < 4; q++) {
     const int lr = 4 * g + q;
     const int row = rbase + (lr >> 1) * WAVES * kRowPhases + (lr & 1);
     float v = 0.f;
-    if (m < a.M && row < r1) v = xl ? xl[m * xrows + row - r0] : a.x[(size_t)m * a.d_in + row];
+    if (m < a.M && row < r1) v = (xl ? xl[m * xrows + row - r0] : a.x[(size_t)m * a.d_in + row]) * sc;
     asm("" : "+v"(v));  // rounded once: hi = fp16(v), lo = fp16(v - hi)
     const _Float16 h = (_Float16)v;
     xh[q] = h;
@@ -401,6 +439,7 @@ __device__ __forceinline__ void mv_item(const MvArgs& a, int ct, int ks, Lds& L)
     __syncthreads();
     xl = lds.xs;
   }
+  if constexpr (MFMA) mv_row_scales<WAVES>(a, xl, xrows, r0, r1, L);
 
   if (wave < WAVES) {
     // Row blocks of kRowPhases rows: the wave takes blocks wave, wave +
@@ -413,16 +452,17 @@ __device__ __forceinline__ void mv_item(const MvArgs& a, int ct, int ks, Lds& L)
     const int first = r0 + wave * kRowPhases;
     if constexpr (MFMA) {
       char* st = reinterpret_cast<char*>(L.wst[wave]);
+      const float sc = L.xscale[min(lane & 15, a.M - 1)];  // this lane's row of x
       for (int r = first; r < r1; r += 2 * step) {
         uint4 wa[U], wb[U];
         mv_load_batch<WAVES, U>(rows, r, wa);
         mv_load_batch<WAVES, U>(rows, r + step, wb);
         mv_h4 xh, xo;
-        mv_x_operand<WAVES>(a, xl, xrows, r0, r1, r, lane, xh, xo);
+        mv_x_operand<WAVES>(a, xl, xrows, r0, r1, r, lane, sc, xh, xo);
         mv_stage<U>(st, rp, lc, wa);
         mv_mfma_batch(st, lane, xh, xo, cm);
         if (r + step < r1) {
-          mv_x_operand<WAVES>(a, xl, xrows, r0, r1, r + step, lane, xh, xo);
+          mv_x_operand<WAVES>(a, xl, xrows, r0, r1, r + step, lane, sc, xh, xo);
           mv_stage<U>(st, rp, lc, wb);  // (a wave's LDS operations complete in order)
           mv_mfma_batch(st, lane, xh, xo, cm);
         }
@@ -466,10 +506,11 @@ __device__ __forceinline__ void mv_item(const MvArgs& a, int ct, int ks, Lds& L)
     float* red = reinterpret_cast<float*>(L.wst);
     __syncthreads();
     if (wave < WAVES && (lane & 15) < a.M) {
+      const float inv = 1.f / L.xscale[lane & 15];  // a power of two: exact
 #pragma unroll
       for (int cb = 0; cb < kColBlocks; cb++)
         *reinterpret_cast<mv_f4*>(red + ((lane & 15) * WAVES + wave) * kCols +
-                                  4 * ((4 * cb + (lane >> 4)) ^ (lane & 15))) = cm[cb];
+                                  4 * ((4 * cb + (lane >> 4)) ^ (lane & 15))) = cm[cb] * inv;
     }
     __syncthreads();
     const int t = threadIdx.x;

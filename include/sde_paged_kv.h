@@ -205,9 +205,11 @@ int sde_paged_attention(sde_kv_cache* cache, int layer, const float* d_q,
                         size_t workspace_bytes, sde_stream_t stream);
 
 /* Bytes of the static device array sde_paged_attention_noalloc keeps its
- * partials in (one per device).  A call's partials are at most
- * (CUs x 16 rows) x (dph + 2) x 4 bytes: 2.1 MB on MI355X's 256 CUs, so
- * every plan there fits. */
+ * partials in (one per device).  The tile kernels' partials (head sizes
+ * 64 / 128) are at most (CUs x 16 rows) x (dph + 2) x 4 bytes, 2.1 MB on
+ * MI355X's 256 CUs; the plain fp32 kernel of the other head sizes caps its
+ * partition count so that its partials fit this size.  So on MI355X every
+ * plan fits, and both entry points run the same plan. */
 #define SDE_NOALLOC_SCRATCH_BYTES ((size_t)4 << 20)
 
 /* sde_paged_attention without a workspace, allocating nothing: the
@@ -342,11 +344,11 @@ size_t sde_matvec_workspace_size(int d_in, int d_out, int n_rows);
  * d_workspace holds sde_matvec_workspace_size(...) bytes
  * (SDE_ERR_WORKSPACE when smaller); calls sharing a workspace must be
  * ordered on one stream.  Deterministic: the sum order does not depend on
- * scheduling.  One or two rows of x multiply in fp32 on the VALU (any
- * finite x); three or more go to the matrix cores as fp16 hi + lo parts,
- * which needs |x| < 65504 -- always so for Wo, whose input (an attention
- * output, a convex combination of fp16 V rows) is bounded by max |V|;
- * sde_matvec_packed takes any finite x at every row count. */
+ * scheduling.  One or two rows of x multiply in fp32 on the VALU; three or
+ * more go to the matrix cores as fp16 hi + lo parts of x scaled, per row
+ * and workgroup, by a power of two that keeps it within the fp16 range
+ * (1 for |x| < 16384, so every Wo input; the sums are scaled back exactly):
+ * any finite x at every row count, as in sde_matvec_packed. */
 int sde_matvec(const float* d_x, const uint16_t* d_W, float* d_out, int d_in,
                int d_out_dim, int n_rows, int accumulate, void* d_workspace,
                size_t workspace_bytes, sde_stream_t stream);

@@ -20,6 +20,7 @@ cuda/src/kv_cache.cu, cuda/include/attention.h, cuda/src/kernels.cu.
 from __future__ import annotations
 
 import ctypes
+import math
 import hashlib
 import subprocess
 from pathlib import Path
@@ -527,6 +528,38 @@ def attention_f64_np(q: np.ndarray, K: np.ndarray, V: np.ndarray, nh: int, nkv: 
             w /= w.sum(axis=1, keepdims=True)
             out[m, heads] = w @ Vg[:L]
     return out.reshape(M, nh * dph)
+
+
+def attention_torch_cpu(pool, table, q, nh: int, nkv: int, dph: int, block_size: int,
+                        pos_base: int):
+    """The reference's paged attention semantics as a torch-CPU step
+    (attention.h:21-127 driven by cublas_attention_kernel, kernels.cu:904-940):
+    block-table gather (index_select) of the fp16 K/V blocks, fp32
+    q.K^T * dph^-1/2, causal mask per query (query m sees pos_base+m+1 keys),
+    softmax, .V.  The timed CPU baseline of bench.py (torch's own threads);
+    the tile loop and the fp64 brute force stay the parity checkers.
+
+    pool: torch.int16/float16 [pool_blocks][2][block_size][nkv*dph] (fp16
+    bits); table: torch int64 [>= ceil(L/block_size)]; q: torch float32
+    [M][nh*dph].  Returns float32 [M][nh*dph]."""
+    import torch
+    M = q.shape[0]
+    L = pos_base + M
+    G = nh // nkv
+    nblk = -(-L // block_size)
+    blocks = pool.view(torch.float16).index_select(0, table[:nblk])  # [nblk][2][BS][kv_dim]
+    K = blocks[:, 0].reshape(nblk * block_size, nkv, dph)[:L].float().permute(1, 0, 2)
+    V = blocks[:, 1].reshape(nblk * block_size, nkv, dph)[:L].float().permute(1, 0, 2)
+    # rows of KV head g: (query m, head-in-group j) -> q head g*G + j
+    qg = q.reshape(M, nkv, G, dph).permute(1, 0, 2, 3).reshape(nkv, M * G, dph)
+    s = torch.bmm(qg, K.transpose(1, 2).contiguous()) * (1.0 / math.sqrt(dph))
+    if M > 1:
+        lim = pos_base + torch.arange(M).repeat_interleave(G)  # last visible key per row
+        hidden = torch.arange(L)[None, :] > lim[:, None]
+        s = s.masked_fill(hidden[None], float("-inf"))
+    p = torch.softmax(s, dim=-1)
+    out = torch.bmm(p, V.contiguous())  # [nkv][M*G][dph]
+    return out.reshape(nkv, M, G, dph).permute(1, 0, 2, 3).reshape(M, nh * dph)
 
 
 # ---- the output projection (Wo) -------------------------------------------

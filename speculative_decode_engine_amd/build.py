@@ -25,6 +25,11 @@ OFFLOAD_ARCH = "gfx950"
 SOURCES = ["kv_cache.hip", "paged_attention.hip", "attention_generic.hip", "spec_accept.hip", "matvec.hip",
            "model_loader.hip", "spec_loop.hip"]
 
+# Measurement kernels for bench.py (a streaming read and the attention's
+# load skeleton): a library of their own, not part of the product.
+MEASURE_SRC = CSRC / "measure.hip"
+MEASURE_LIB = PKG_DIR / "libsde_measure.so"
+
 # Test infrastructure: kernels that call the device-side API of
 # include/sde/attention_device.hpp from inside a caller's kernel.
 DEVICE_TEST_SRC = REPO_ROOT / "tests" / "device" / "device_api_test.hip"
@@ -81,8 +86,20 @@ def build(verbose: bool = False) -> Path:
     os.replace(tmp, LIB_PATH)
     if verbose:
         print(f"built {LIB_PATH}")
+    build_measure(verbose)
     build_device_tests(verbose)
     return LIB_PATH
+
+
+def build_measure(verbose: bool = False) -> Path:
+    """Compiles bench.py's measurement kernels into libsde_measure.so."""
+    tmp = MEASURE_LIB.with_suffix(".so.tmp")
+    _run([hipcc(), *HIP_FLAGS, "-shared", str(MEASURE_SRC), "-o", str(tmp),
+          f"-L{PKG_DIR}", "-lsde_paged", "-Wl,-rpath,$ORIGIN"])
+    os.replace(tmp, MEASURE_LIB)
+    if verbose:
+        print(f"built {MEASURE_LIB}")
+    return MEASURE_LIB
 
 
 def build_device_tests(verbose: bool = False) -> Path:

@@ -260,7 +260,7 @@ __global__ __launch_bounds__(kThreads) void gen_combine_kernel(GenArgs a) {
 
 }  // namespace
 
-GenPlan generic_plan(int L_max, int nkv, int R, int n_cus, int max_parts) {
+GenPlan generic_plan(int L_max, int nkv, int R, int dph, int n_cus, int max_parts) {
   GenPlan p;
   p.row_groups = (R + kRows - 1) / kRows;
   const int64_t units = (int64_t)nkv * p.row_groups;
@@ -268,6 +268,11 @@ GenPlan generic_plan(int L_max, int nkv, int R, int n_cus, int max_parts) {
   if (parts > max_parts) parts = max_parts;
   const int64_t by_len = ((int64_t)L_max + 63) / 64;
   if (parts > by_len) parts = by_len;
+  // Every plan's partials fit the static array of the allocation-free entry
+  // point, so both entry points run the same plan (same results, same errors).
+  const int64_t by_bytes =
+      (int64_t)(SDE_NOALLOC_SCRATCH_BYTES / ((size_t)nkv * R * (size_t)(dph + 2) * sizeof(float)));
+  if (parts > by_bytes) parts = by_bytes;
   if (parts < 1) parts = 1;
   const int64_t len = ((L_max + parts - 1) / parts + 63) / 64 * 64;
   p.part_len = (int)len;

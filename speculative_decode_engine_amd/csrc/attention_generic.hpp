@@ -35,9 +35,10 @@ struct GenPlan {
 };
 
 // The partition plan of a call: partitions of at least 64 tokens, at most
-// as many as parts_bound (the bound the attention workspace is sized for)
-// and about two workgroups per CU over all (KV head, row group) units.
-GenPlan generic_plan(int L_max, int nkv, int R, int n_cus, int max_parts);
+// as many as parts_bound (the bound the attention workspace is sized for),
+// about two workgroups per CU over all (KV head, row group) units, and no
+// more partials than SDE_NOALLOC_SCRATCH_BYTES holds.
+GenPlan generic_plan(int L_max, int nkv, int R, int dph, int n_cus, int max_parts);
 
 // Bytes of partials the plan needs (0 for one partition).
 size_t generic_partial_bytes(const GenPlan& p, int nkv, int R, int dph);

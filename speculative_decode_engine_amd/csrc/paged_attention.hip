@@ -39,22 +39,6 @@
 namespace sde {
 namespace attn {
 
-// Workgroup -> (partition, KV head, row group).  Long contexts (waves of
-// four tiles or more) take the KV head fastest in the linear workgroup
-// index: consecutive workgroups then read the adjacent KV-head slices of the
-// same token rows at the same time, which the memory system serves faster
-// than the same slices read by workgroups far apart in dispatch order.
-template <int CHUNK>
-__device__ __forceinline__ int3 stream_coords() {
-  if constexpr (CHUNK < 4) {
-    return make_int3(blockIdx.x, blockIdx.y, blockIdx.z);
-  } else {
-    const int lin = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
-    return make_int3((lin / gridDim.y) % gridDim.x, lin % gridDim.y,
-                     lin / (gridDim.x * gridDim.y));
-  }
-}
-
 // Decode and verify steps on the MFMA tile path.
 template <int DPH, int RPW, int CHUNK>
 __global__ __launch_bounds__(64 * kStreamWaves) void attn_mfma_kernel(AttnArgs a) {
@@ -204,7 +188,7 @@ int run_attention(sde_kv_cache* cache, int layer, const float* d_q, float* d_out
   sde::gen::GenPlan gplan{};
   size_t need = 0;
   if (generic) {
-    gplan = sde::gen::generic_plan(L_max, nkv, R, cache->n_cus, parts_bound(L_max));
+    gplan = sde::gen::generic_plan(L_max, nkv, R, dph, cache->n_cus, parts_bound(L_max));
     need = sde::gen::generic_partial_bytes(gplan, nkv, R, dph);
   } else {
     plan = plan_for(L_max, nkv, R, cache->n_cus);
@@ -221,15 +205,18 @@ int run_attention(sde_kv_cache* cache, int layer, const float* d_q, float* d_out
         // Grow the cache-owned workspace.  Not while the stream is being
         // captured: the allocation cannot be recorded, and a graph would
         // keep its address.  The old buffer stays allocated (queued work
-        // or an earlier graph may still use it) until the cache is freed.
+        // or an earlier graph may still use it) until the cache is freed,
+        // so the size at least doubles: a context that grows call by call
+        // retires O(log) buffers, at most about twice the peak need in all.
         hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
         if (hipStreamIsCapturing((hipStream_t)stream, &cap) != hipSuccess) return SDE_ERR_HIP;
         if (cap != hipStreamCaptureStatusNone) return SDE_ERR_WORKSPACE;
+        const size_t grow = need > 2 * cache->workspace_bytes ? need : 2 * cache->workspace_bytes;
         void* grown = nullptr;
-        if (hipMalloc(&grown, need) != hipSuccess) return SDE_ERR_HIP;
+        if (hipMalloc(&grown, grow) != hipSuccess) return SDE_ERR_HIP;
         if (cache->workspace) cache->retired_workspaces.push_back(cache->workspace);
         cache->workspace = grown;
-        cache->workspace_bytes = need;
+        cache->workspace_bytes = grow;
       }
       partials = static_cast<float*>(cache->workspace);
     }

@@ -134,9 +134,21 @@ __device__ __forceinline__ uint32_t xcd_id() {
   return x & 7u;
 }
 
+// Whether an error has been recorded (the launch is ending).
+__device__ __forceinline__ bool failed(const LoopArgs& a) {
+  return __hip_atomic_load(a.state + kStatus, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) !=
+         SDE_OK;
+}
+
+// Waits for the barrier generation to move past `gen`.  Returns at once
+// once an error is recorded, so after one broken barrier (which records
+// SDE_ERR_HIP when its spin budget runs out) every later wait of the launch
+// returns immediately instead of spending a budget of its own: the blocks
+// reach the next round check, see the status and leave together.
 __device__ __forceinline__ void wait_generation(const LoopArgs& a, uint32_t gen) {
   uint32_t polls = 0;
   while (__hip_atomic_load(a.bar + kBarGen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gen) {
+    if (failed(a)) break;
     if (++polls == kSpinLimit) {
       atomicCAS(reinterpret_cast<int*>(a.state + kStatus), SDE_OK, SDE_ERR_HIP);
       break;
@@ -158,12 +170,13 @@ __device__ __forceinline__ void wait_generation(const LoopArgs& a, uint32_t gen)
 // barrier and phase against 12.7 for a release fence in every block (9.4 vs
 // 24.9 with 16 KiB written per block), and no stale read in either.  A wait
 // gives up after kSpinLimit polls and records SDE_ERR_HIP, so a broken
-// barrier ends the launch instead of hanging it (every later round check
-// sees the status and exits).
+// barrier ends the launch instead of hanging it; once a status is recorded
+// the barrier does not wait at all (every later round check sees the status
+// and exits; the barrier words are cleared by the next launch's init).
 __device__ __forceinline__ void barrier(const LoopArgs& a) {
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (threadIdx.x == 0) {
+  if (threadIdx.x == 0 && !failed(a)) {
     const uint32_t gen =
         __hip_atomic_load(a.bar + kBarGen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const uint32_t x = xcd_id();
@@ -277,6 +290,8 @@ __device__ void append_rows(const LoopArgs& a, int l, int r0, int n, int pos0) {
 // The grid attention of layer l over window rows [r0, r0+n) at positions
 // pos0 + row, as a function of its own: its tile loop gets the whole register
 // budget instead of sharing it with the values the loops around it keep.
+// 4-wave staging (64 KiB of LDS): the 8-wave form is off in the loop (see
+// the design notes on the loop's attention).
 __device__ __attribute__((noinline)) int layer_attention(const LoopArgs& a, int l, int r0, int n,
                                                          int pos0) {
   return device_flash_attention_gqa_grid<4>(
@@ -488,8 +503,13 @@ __global__ void spec_loop_init_kernel(LoopArgs a) {
     for (int i = threadIdx.x; i < kSpecScratchWords; i += blockDim.x) a.sscratch[i] = 0u;
   }
   if (threadIdx.x == 0) {
-    a.tokens[0] = a.state[kAnchor];
+    // The anchor indexes the embedding tables: one outside the vocabulary
+    // stops the launch at its first round check, before any table read.
+    const int anchor = a.state[kAnchor];
+    const bool ok = anchor >= 0 && anchor < a.m.vocab;
+    a.tokens[0] = ok ? anchor : 0;
     for (int i = kEmitted; i < kStateWords; i++) a.state[i] = 0;
+    if (!ok) a.state[kStatus] = SDE_ERR_INVALID_ARGUMENT;
     if (a.offset) {
       a.state[kTemp] = __float_as_int(a.smp.draft_temp);
       a.state[kEwma] = __float_as_int(-1.f);

@@ -67,6 +67,13 @@ class SpecLoopModel:
                            head.data_ptr(), V, n_heads, n_kv_heads, head_dim)
 
 
+def _check_anchor(model: SpecLoopModel, anchor: int) -> None:
+    # The anchor indexes the embedding tables (the device also rejects it,
+    # with SDE_ERR_INVALID_ARGUMENT in the status word).
+    if not 0 <= int(anchor) < model.vocab:
+        raise ValueError(f"anchor token {anchor} is outside the vocabulary [0, {model.vocab})")
+
+
 def workspace_size(cache: KVCache, model: SpecLoopModel, k: int) -> int:
     return int(_native.load().sde_spec_loop_workspace_size(cache.handle, ctypes.byref(model.c),
                                                            k))
@@ -78,6 +85,7 @@ def spec_loop_greedy(cache: KVCache, model: SpecLoopModel, anchor: int, k: int, 
     """Runs the loop from the cache's device seq_len (positions below it hold
     the context) with `anchor` the last emitted token; synchronizes and
     returns the emitted tokens and per-round acceptances."""
+    _check_anchor(model, anchor)
     dev = cache.device
     state = torch.zeros(STATE_WORDS, dtype=torch.int32, device=dev)
     state[0] = anchor
@@ -113,6 +121,7 @@ def spec_loop_stochastic(cache: KVCache, model: SpecLoopModel, anchor: int, k: i
     """spec_loop_greedy's rounds with speculative sampling.  `offset` is the
     device uint64 call index of the random stream (a fresh zero when None;
     the call advances it by k + 1 per round)."""
+    _check_anchor(model, anchor)
     dev = cache.device
     state = torch.zeros(STATE_WORDS, dtype=torch.int32, device=dev)
     state[0] = anchor

@@ -42,6 +42,11 @@ CASES = [
     (8, 2, 128, 20, 20000, 1),    # 20000 keys: a multi-partition combine
     (4, 2, 512, 16, 2000, 2),     # the largest head size
     (8, 2, 96, 16, 0, 6),         # no context: the window alone
+    # partials capped to the no-allocation array (plans that asked for
+    # 4.23 MB at 16129 keys before the cap)
+    (16, 8, 256, 16, 16125, 4),   # head size 256, 4-query window
+    (64, 8, 256, 16, 16128, 1),   # head size 256, 64 q heads
+    (32, 4, 512, 16, 16128, 1),   # head size 512
 ]
 
 

@@ -113,6 +113,36 @@ def test_matvec_closed_forms_are_exact(gpu):
         assert np.array_equal(got[m], Wb[k].view(np.float16).astype(np.float32))
 
 
+@pytest.mark.parametrize("M,d_in,d_out", [(5, 4096, 4096), (3, 14336, 1024), (9, 3584, 3584)])
+def test_matvec_large_inputs_beyond_fp16_range(gpu, oracle, M, d_in, d_out):
+    """Rows of x past the fp16 range (|x| up to 1e9) on the matrix-core form
+    (three or more rows): every row is scaled by a power of two for the
+    fp16 hi + lo split and scaled back, so the result stays within the fp32
+    summation bound of the float64 product, with no Inf; scaling x by 2^k
+    scales the result by exactly 2^k."""
+    case_banner("matvec large x", M, d_in, d_out)
+    rng = np.random.default_rng(M * 7 + d_in)
+    x, Wb = _case(rng, M, d_in, d_out)
+    x[0] *= np.float32(1e9)               # row 0: every element past 65504
+    x[1, ::97] = np.float32(3.0e5)        # row 1: a few elements past it
+    got = _run(gpu, x, Wb)
+    assert np.all(np.isfinite(got))
+    y, mag = oracle.matvec_f64(x, Wb)
+    err = np.abs(got - y)
+    assert np.all(err <= MV_TOL * mag + 1e-30), float((err / mag).max())
+    # Rows past the range are normalized by their power-of-two scale, so two
+    # power-of-two multiples of a row give exactly proportional results (an
+    # in-range row keeps scale 1 and its own fp16 rounding of the lo part).
+    x2, x3 = x.copy(), x.copy()
+    x2[2] *= np.float32(2.0 ** 20)
+    x3[2] *= np.float32(2.0 ** 24)
+    got2, got3 = _run(gpu, x2, Wb), _run(gpu, x3, Wb)
+    assert np.array_equal(got3[2], got2[2] * np.float32(16.0))
+    y2, mag2 = oracle.matvec_f64(x2, Wb)
+    assert np.all(np.abs(got2 - y2) <= MV_TOL * mag2 + 1e-30)
+    assert np.array_equal(got2[3:], got[3:]) and np.array_equal(got2[:2], got[:2])
+
+
 def test_matvec_is_deterministic(gpu):
     case_banner("matvec determinism")
     rng = np.random.default_rng(5)

@@ -82,6 +82,7 @@ CASES = [
     (9, (2, 32, 8, 128, 1024), 2000, 5, 1),   # Llama-3-8B heads, multi-partition windows
     (7, (3, 8, 2, 64, 512), 300, 15, 1),      # the largest window: the head in two passes of 8
     (8, (2, 8, 2, 128, 256), 100, 9, 1),      # 10 rows: two passes of 5
+    (11, (2, 8, 2, 64, 4096), 120, 4, 1),     # vocab 4096: 16-column head panels into the argmax
 ]
 
 
@@ -119,6 +120,48 @@ def test_spec_loop_matches_oracle_and_greedy(gpu, oracle, seed, shape, P0, k, n_
         assert torch.equal(gk, sk) and torch.equal(gv, sv)
     gcache.free()
     scache.free()
+
+
+@pytest.mark.parametrize("stochastic", [False, True])
+def test_spec_loop_rejects_out_of_vocabulary_anchor(gpu, stochastic):
+    """An anchor outside [0, vocab) reaches the device through the C-ABI
+    (the Python wrappers refuse it): the launch records
+    SDE_ERR_INVALID_ARGUMENT and stops at its first round check, before any
+    table read -- no token, no append, seq_len unchanged."""
+    case_banner("spec loop bad anchor", stochastic)
+    import ctypes
+    from speculative_decode_engine_amd import _native as N
+    m = make_loop_model(3, noise=0.1, q_scale=2.0)
+    cache = KVCache(m.n_layers, m.nkv * m.dph, 8, 16, m.n_layers * 8)
+    cache.set_seq_len(10)
+    dm = device_model(m)
+    with pytest.raises(ValueError):
+        spec_loop_greedy(cache, dm, m.vocab, 2, 1, 4)
+    lib = N.load()
+    state = torch.zeros(8, dtype=torch.int32, device="cuda")
+    state[0] = m.vocab + 5
+    em = torch.full((16,), -1, dtype=torch.int32, device="cuda")
+    ac = torch.full((8,), -1, dtype=torch.int32, device="cuda")
+    ws = torch.empty(lib.sde_spec_loop_workspace_size(cache.handle, ctypes.byref(dm.c), 2),
+                     dtype=torch.uint8, device="cuda")
+    vp = lambda t: ctypes.c_void_p(t.data_ptr())
+    before = cache.pool.clone()
+    if stochastic:
+        off = torch.zeros(1, dtype=torch.int64, device="cuda")
+        smp = N.LoopSampling(1.0, 0, 0.1, 2.0, 0.7, 0.1, 0.2, 5)
+        rc = lib.sde_spec_loop_stochastic(cache.handle, ctypes.byref(dm.c), 2, 1, 4,
+                                          ctypes.byref(smp), vp(off), vp(state), vp(em), vp(ac),
+                                          vp(ws), ws.numel(), None)
+    else:
+        rc = lib.sde_spec_loop_greedy(cache.handle, ctypes.byref(dm.c), 2, 1, 4, vp(state),
+                                      vp(em), vp(ac), vp(ws), ws.numel(), None)
+    assert rc == 0  # the launch itself is valid; the device rejects the anchor
+    torch.cuda.synchronize()
+    st = state.cpu().tolist()
+    assert st[3] == N.SDE_ERR_INVALID_ARGUMENT and st[1] == 0 and st[2] == 0
+    assert torch.equal(cache.pool, before) and cache.device_seq_len() == 10
+    assert (em == -1).all() and (ac == -1).all()
+    cache.free()
 
 
 def test_spec_loop_stops_at_capacity(gpu, oracle):
@@ -170,13 +213,17 @@ STOCH_CASES = [
 ]
 
 
-@pytest.mark.parametrize("seed,shape,P0,k,n_draft,temp,adaptive,rseed", STOCH_CASES)
+@pytest.mark.parametrize("seed,shape,P0,k,n_draft,temp,adaptive,rseed,head_scale",
+                         [c + (8.0,) for c in STOCH_CASES] +
+                         # vocab 8192: two vocabulary slices per row (a sharper head keeps
+                         # every decision clear of its boundary at this vocabulary size)
+                         [(12, (2, 8, 2, 64, 8192), 60, 4, 1, 1.0, False, 8, 32.0)])
 def test_stochastic_loop_matches_oracle(gpu, oracle, seed, shape, P0, k, n_draft, temp,
-                                        adaptive, rseed):
+                                        adaptive, rseed, head_scale):
     L, nh, nkv, dph, V = shape
     case_banner("spec loop stochastic", seed, shape, P0, k, n_draft, temp, adaptive, rseed)
     m = make_loop_model(seed, n_layers=L, nh=nh, nkv=nkv, dph=dph, vocab=V, noise=0.1,
-                        q_scale=2.0, head_scale=8.0)
+                        q_scale=2.0, head_scale=head_scale)
     max_new = 16
     nblk = -(-(P0 + max_new + k + 1) // 16)
     kvd = nkv * dph

@@ -198,6 +198,31 @@ def test_tiled_vs_bruteforce_vs_numpy_vs_torch(oracle, nh, nkv, dph, bs):
         np.testing.assert_allclose(f64[mq], ref, rtol=1e-10, atol=1e-12)
 
 
+@pytest.mark.parametrize("nh,nkv,dph,bs,M", [(4, 2, 64, 16, 1), (32, 8, 128, 16, 5),
+                                             (28, 4, 128, 32, 9), (6, 1, 64, 1, 3)])
+def test_torch_cpu_baseline_matches_bruteforce(oracle, nh, nkv, dph, bs, M):
+    """The benchmark's torch-CPU restatement (the timed CPU baseline) against
+    the fp64 brute force, on the same fragmented pool; a planted K/V head
+    mix-up (KV head h % nkv instead of h * nkv // nh) must fail."""
+    m, q, K, V = _attn_case(oracle, nh, nkv, dph, bs, L=70, M=M)
+    pos_base = 70
+    f64 = m.attention(0, q, nh, nkv, dph, pos_base, mode="f64")
+    pool = torch.from_numpy(m.pool.view(np.int16))
+    table = torch.from_numpy(m.tables[0].astype(np.int64))
+    got = oracle.attention_torch_cpu(pool, table, torch.from_numpy(q), nh, nkv, dph, bs,
+                                     pos_base).numpy()
+    np.testing.assert_allclose(got, f64, rtol=1e-5, atol=2e-6)
+    if nkv > 1 and nh // nkv > 1:
+        Kp = K.reshape(-1, nkv, dph)
+        Vp = V.reshape(-1, nkv, dph)
+        G = nh // nkv
+        perm = [h % nkv for h in range(nh)]  # wrong head mapping
+        Kw = np.stack([Kp[:, perm[g * G], :] for g in range(nkv)], axis=1).reshape(K.shape)
+        Vw = np.stack([Vp[:, perm[g * G], :] for g in range(nkv)], axis=1).reshape(V.shape)
+        bad = oracle.attention_f64_np(q, Kw, Vw, nh, nkv, dph, pos_base)
+        assert not _close(got, bad)
+
+
 def test_total_len_zero_gives_zeros(oracle):
     m, q, K, V = _attn_case(oracle)
     out = m.attention_one(0, q[0], 4, 2, 64, 0)
