@@ -17,7 +17,10 @@ code; the reference aborts instead (utils.h:387-395).
 """
 from __future__ import annotations
 
+import atexit
 import ctypes
+import sys
+import weakref
 from typing import Optional
 
 import numpy as np
@@ -32,6 +35,26 @@ ATTN_KDA = _native.SDE_ATTN_KDA
 ATTN_LINEAR = _native.SDE_ATTN_LINEAR
 
 KV_BLOCK_SIZE = 16  # reference default (config.h:10)
+
+# Caches still alive when the interpreter exits are destroyed by an exit
+# handler, while the HIP runtime is still up; after it (and during the
+# interpreter's own teardown, when module globals and the runtime may already
+# be gone) a cache's destructor does nothing.
+_LIVE: "weakref.WeakSet[KVCache]" = weakref.WeakSet()
+_EXITING = False
+
+
+def _free_live_caches() -> None:
+    global _EXITING
+    for cache in list(_LIVE):
+        try:
+            cache.free()
+        except Exception:
+            pass
+    _EXITING = True
+
+
+atexit.register(_free_live_caches)
 
 
 def _stream_handle(stream: Optional[torch.cuda.Stream]) -> ctypes.c_void_p:
@@ -92,6 +115,7 @@ class KVCache:
                       "kv_cache_alloc")
             else:
                 raise ValueError("pool must be 'torch' or 'library'")
+        _LIVE.add(self)
 
     # ---- lifetime (kv_cache_free) -------------------------------------------
     def free(self) -> None:
@@ -101,6 +125,8 @@ class KVCache:
         self.pool = None
 
     def __del__(self):
+        if _EXITING or sys.is_finalizing():
+            return
         try:
             self.free()
         except Exception:
