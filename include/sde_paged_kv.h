@@ -541,6 +541,49 @@ int sde_spec_loop_stochastic(sde_kv_cache* cache, const sde_loop_model* model, i
                              int32_t* d_accepted, void* d_workspace, size_t workspace_bytes,
                              sde_stream_t stream);
 
+/* The loop's whole configuration: GenerationParams' spec_k, max_new_tokens,
+ * eos_token and self_speculative (config.h:139-160) as megakernel_speculative
+ * (kernels.cu:3593-3755) reads them.  With draft_cache and draft_model set
+ * (self_speculative false, kernels.cu:2864-2875 shared_kv false) a separate
+ * draft model over a cache of its own drafts: per round, k one-token steps
+ * through all its layers (window token s at draft position D+s, D its device
+ * seq_len at the round's start), then the target verifies the window through
+ * all its layers.  After the accept (sde::spec_accept_greedy, or the sampling
+ * accept) the target rewinds to P + n + 1 and the draft to D + n
+ * (draft_save + n_accepted), then the draft's catch-up forward
+ * (kernels.cu:3079-3093) appends, at D + n, the last draft when all k were
+ * accepted, else the bonus (the reference's order: the bonus then also sits
+ * at D + n + 1 after the next round's first step), leaving the draft's
+ * seq_len at D + n + 1.  eos_token >= 0 ends the loop after a round whose
+ * bonus (its last emitted token) is that token (kernels.cu:3095, 3471);
+ * d_state[1] then counts the tokens out, possibly below max_new. */
+typedef struct sde_spec_loop_config {
+  int32_t k;                        /* drafts per round, 0..15 (>= 1 with a draft model) */
+  int32_t n_draft;                  /* self-speculative prefix layers (no draft model)   */
+  int32_t max_new;                  /* tokens to emit (>= 1)                             */
+  int32_t eos_token;                /* < 0: none                                        */
+  sde_kv_cache* draft_cache;        /* NULL: self-speculative over `cache`              */
+  const sde_loop_model* draft_model; /* the draft model over draft_cache (same vocab)   */
+} sde_spec_loop_config;
+
+/* Workspace bytes of sde_spec_loop for this configuration (both heads'
+ * packed copies and the larger model's buffers included); 0 when invalid. */
+size_t sde_spec_loop_config_workspace_size(const sde_kv_cache* cache,
+                                           const sde_loop_model* model,
+                                           const sde_spec_loop_config* cfg);
+
+/* sde_spec_loop_greedy (sampling NULL) or sde_spec_loop_stochastic under a
+ * configuration: the same state words, buffers, limits and errors, plus
+ * SDE_ERR_INVALID_ARGUMENT for a draft model without its cache (or the
+ * reverse), the target's own cache as the draft's, k = 0 with a draft model,
+ * a different vocabulary or device.  Both caches' seq_len are then on the
+ * device. */
+int sde_spec_loop(sde_kv_cache* cache, const sde_loop_model* model,
+                  const sde_spec_loop_config* cfg, const sde_loop_sampling* sampling,
+                  uint64_t* d_rng_offset, int32_t* d_state, int32_t* d_emitted,
+                  int32_t* d_accepted, void* d_workspace, size_t workspace_bytes,
+                  sde_stream_t stream);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif

@@ -234,7 +234,7 @@ def spec_accept_greedy(draft_tokens, target_tokens, k: int, target_save: int,
 
 def spec_loop_greedy(model: PagedKVModel, emb_q, emb_k, emb_v, head_bits, nh: int, nkv: int,
                      dph: int, anchor: int, k: int, n_draft: int, max_new: int,
-                     shift_rewind: int = 0):
+                     shift_rewind: int = 0, eos_token: int = -1):
     """The persistent self-speculative greedy loop (megakernel_speculative,
     kernels.cu:2864-3106; self-speculative verify model.cu:838-890) over the
     byte model, with the loop model of sde_spec_loop_greedy: layer l of token
@@ -251,7 +251,8 @@ def spec_loop_greedy(model: PagedKVModel, emb_q, emb_k, emb_v, head_bits, nh: in
     the argmaxes of every row; spec_accept_greedy emits the accepted drafts
     and the bonus and seq_len <- P + n + 1 (kernels.cu:3050-3072).
     `shift_rewind` plants a rewind mistake (for the tests that must catch
-    one).  Returns (tokens, accepted per round, rounds)."""
+    one).  The loop stops after a round whose bonus is eos_token >= 0
+    (kernels.cu:3095).  Returns (tokens, accepted per round, rounds)."""
     L = model.n_layers
     d = nh * dph
     head = f16_bits_to_f32(np.asarray(head_bits, dtype=np.uint16)).astype(np.float64)
@@ -288,7 +289,157 @@ def spec_loop_greedy(model: PagedKVModel, emb_q, emb_k, emb_v, head_bits, nh: in
         accepted.append(n)
         model.seq_len = t_seq + shift_rewind
         cur = bonus
+        if eos_token >= 0 and bonus == eos_token:
+            break
     return tokens_out, accepted, len(accepted)
+
+
+def _forward_rows(model: PagedKVModel, lm, window, h, lo: int, hi: int, r0: int, n: int,
+                  pos0: int):
+    """Layers [lo, hi) of loop model lm = (emb_q, emb_k, emb_v, head_bits, nh, nkv, dph)
+    over window rows [r0, r0+n) at positions pos0 + row: append each row's
+    K/V, q = emb_q (+ the previous layer's output in h), fp64 attention
+    rounded to fp32 into h.  Returns the rows' logits (fp64, h @ head)."""
+    emb_q, emb_k, emb_v, head_bits, nh, nkv, dph = lm
+    for l in range(lo, hi):
+        toks = window[r0:r0 + n]
+        model.append(l, emb_k[l][toks], emb_v[l][toks], pos0 + r0)
+        q = emb_q[l][toks].astype(np.float32)
+        if l > 0:
+            q = q + h[r0:r0 + n]
+        out = model.attention(l, q, nh, nkv, dph, pos0 + r0, mode="f64")
+        h[r0:r0 + n] = out.astype(np.float32)
+    head = f16_bits_to_f32(np.asarray(head_bits, dtype=np.uint16)).astype(np.float64)
+    return h[r0:r0 + n].astype(np.float64) @ head
+
+
+def _catch_up(draft: PagedKVModel, dm, tok: int, pos: int) -> None:
+    """The draft model's forward of one token at `pos` as the cache sees it
+    (kernels.cu:3079-3093): its K/V rows in every layer (the K/V of the loop
+    model depend on (token, position) only; the forward's logits are unused)."""
+    _, emb_k, emb_v = dm[0], dm[1], dm[2]
+    for l in range(draft.n_layers):
+        draft.append(l, emb_k[l][[tok]], emb_v[l][[tok]], pos)
+
+
+def spec_loop_greedy_two(target: PagedKVModel, draft: PagedKVModel, tm, dm, anchor: int, k: int,
+                         max_new: int, eos_token: int = -1, shift_draft_rewind: int = 0):
+    """The persistent greedy loop with a separate draft model and cache
+    (megakernel_speculative_kernel with shared_kv false, kernels.cu:2864-3106).
+    tm, dm: (emb_q, emb_k, emb_v, head_bits, nh, nkv, dph) of the target and
+    draft models.  Each round from P = target.seq_len, D = draft.seq_len:
+      * draft steps i = 0..k-1 (kernels.cu:2948-2958): the draft model appends
+        window token i (the anchor, then each draft) at D+i in all its layers,
+        attends with one query, and its head's argmax is window token i+1;
+      * verify (model_batch_forward_logits, model.cu:657-714): the target
+        appends the window [anchor, drafts] at P.. and attends causally; the
+        argmax of every row is the target's token;
+      * accept (kernels.cu:3050-3076): n leading matches, emit drafts[:n] and
+        the bonus target[n]; target seq_len <- P+n+1, draft seq_len <- D+n;
+      * catch-up (kernels.cu:3079-3093): the draft model's forward of the
+        last draft when all k were accepted (its K/V were never written) or
+        of the bonus otherwise, at D+n; draft seq_len <- D+n+1.  (In the
+        second case the bonus lands where the last accepted draft was, as in
+        the reference: the draft cache then trails the true sequence by that
+        token, which costs acceptance, never output.)
+      * stop once max_new tokens are out, or after a round whose bonus is
+        eos_token >= 0 (kernels.cu:3095: the bonus is checked, not the
+        accepted drafts).
+    `shift_draft_rewind` plants a draft-rewind mistake for the tests.
+    Returns (tokens, accepted per round, rounds)."""
+    assert k >= 1
+    M = k + 1
+    dt = dm[4] * dm[6]
+    tt = tm[4] * tm[6]
+    tokens_out, accepted = [], []
+    cur = int(anchor)
+    while len(tokens_out) < max_new:
+        P, D = target.seq_len, draft.seq_len
+        window = [cur] + [0] * k
+        hd = np.zeros((M, dt), dtype=np.float32)
+        for i in range(k):
+            logits = _forward_rows(draft, dm, window, hd, 0, draft.n_layers, i, 1, D)
+            window[i + 1] = int(np.argmax(logits[0]))
+        ht = np.zeros((M, tt), dtype=np.float32)
+        logits = _forward_rows(target, tm, window, ht, 0, target.n_layers, 0, M, P)
+        tgt = [int(np.argmax(logits[m])) for m in range(M)]
+        n, bonus, t_seq, d_seq, emitted = spec_accept_greedy(window[1:], tgt, k, P, D, False)
+        tokens_out += emitted
+        accepted.append(n)
+        target.seq_len = t_seq
+        d_seq += shift_draft_rewind
+        _catch_up(draft, dm, window[k] if n == k else bonus, d_seq)
+        draft.seq_len = d_seq + 1
+        cur = bonus
+        if eos_token >= 0 and bonus == eos_token:
+            break
+    return tokens_out, accepted, len(accepted)
+
+
+def spec_loop_stochastic_two(target: PagedKVModel, draft: PagedKVModel, tm, dm, anchor: int,
+                             k: int, max_new: int, seed: int, offset: int = 0,
+                             draft_temp: float = 1.0, adaptive: bool = False,
+                             min_temp: float = 0.1, max_temp: float = 2.0,
+                             target_accept: float = 0.7, gain: float = 0.1,
+                             ewma_mix: float = 0.2, eos_token: int = -1):
+    """The sampling loop with a separate draft model and cache
+    (megakernel_speculative_stochastic_kernel with shared_kv false,
+    kernels.cu:3108-3481), on spec_loop_greedy_two's rounds: draft token i+1
+    is sampled (spec_accept_stochastic with no drafts, its bonus row) from
+    the draft model's logits of row i at T_d, one call index each; the
+    window's target logits (temperature 1) and the draft rows' logits (T_d)
+    go to spec_accept_stochastic for the accept tests and the corrected or
+    bonus sample, one more call index; target seq_len <- P+n+1, draft
+    seq_len <- D+n, then the draft catch-up of spec_loop_greedy_two; T_d
+    adapts as in spec_loop_stochastic; the EOS stop as in the greedy loop.
+    (The target rewinds like the batched verify path, without the
+    reference's extra target forward of a rejection's corrected token.)
+    Returns spec_loop_stochastic's tuple."""
+    assert k >= 1
+    M = k + 1
+    f32 = np.float32
+    temp, ewma = f32(draft_temp), f32(-1.0)
+    mix = min(max(f32(ewma_mix), f32(1e-6)), f32(1.0) - f32(1e-6))
+    dt = dm[4] * dm[6]
+    tt = tm[4] * tm[6]
+    tokens_out, accepted = [], []
+    margin = float("inf")
+    cur = int(anchor)
+    while len(tokens_out) < max_new:
+        P, D = target.seq_len, draft.seq_len
+        window = [cur] + [0] * k
+        hd = np.zeros((M, dt), dtype=np.float32)
+        dlog = []
+        for i in range(k):
+            logits = _forward_rows(draft, dm, window, hd, 0, draft.n_layers, i, 1, D)
+            r = spec_accept_stochastic(logits, None, [], 0, float(temp), 1.0, seed, offset, 0, 0,
+                                       True)
+            offset += 1
+            margin = min(margin, r["sample_margin"][0])
+            window[i + 1] = r["token"]
+            dlog.append(logits[0])
+        ht = np.zeros((M, tt), dtype=np.float32)
+        logits = _forward_rows(target, tm, window, ht, 0, target.n_layers, 0, M, P)
+        r = spec_accept_stochastic(logits, np.array(dlog), window[1:], k, 1.0, float(temp), seed,
+                                   offset, P, D, False)
+        offset += 1
+        n = r["n_accepted"]
+        margin = min([margin] + r["accept_margin"][:min(n + 1, k)] + [r["sample_margin"][n]])
+        tokens_out += r["emitted"]
+        accepted.append(n)
+        target.seq_len = r["target_seq"]
+        bonus = r["token"]
+        _catch_up(draft, dm, window[k] if n == k else bonus, r["draft_seq"])
+        draft.seq_len = r["draft_seq"] + 1
+        cur = bonus
+        if adaptive:
+            rr = f32(n) / f32(k)
+            ewma = rr if ewma < 0 else f32((f32(1.0) - mix) * ewma + mix * rr)
+            temp = f32(temp + f32(gain) * f32(ewma - f32(target_accept)))
+            temp = f32(max(f32(min_temp), min(f32(max_temp), temp)))
+        if eos_token >= 0 and bonus == eos_token:
+            break
+    return tokens_out, accepted, len(accepted), float(temp), float(ewma), offset, margin
 
 
 _PHILOX_M = (0xD2511F53, 0xCD9E8D57)   # Salmon et al., SC'11 (Philox4x32)
@@ -299,7 +450,8 @@ def spec_loop_stochastic(model: PagedKVModel, emb_q, emb_k, emb_v, head_bits, nh
                          nkv: int, dph: int, anchor: int, k: int, n_draft: int, max_new: int,
                          seed: int, offset: int = 0, draft_temp: float = 1.0,
                          adaptive: bool = False, min_temp: float = 0.1, max_temp: float = 2.0,
-                         target_accept: float = 0.7, gain: float = 0.1, ewma_mix: float = 0.2):
+                         target_accept: float = 0.7, gain: float = 0.1, ewma_mix: float = 0.2,
+                         eos_token: int = -1):
     """The persistent self-speculative sampling loop
     (megakernel_speculative_stochastic_kernel, kernels.cu:3108-3481) over
     the byte model, with spec_loop_greedy's model and rounds: draft token
@@ -368,6 +520,8 @@ def spec_loop_stochastic(model: PagedKVModel, emb_q, emb_k, emb_v, head_bits, nh
             ewma = rr if ewma < 0 else f32((f32(1.0) - mix) * ewma + mix * rr)
             temp = f32(temp + f32(gain) * f32(ewma - f32(target_accept)))
             temp = f32(max(f32(min_temp), min(f32(max_temp), temp)))
+        if eos_token >= 0 and cur == eos_token:
+            break
     return tokens_out, accepted, len(accepted), float(temp), float(ewma), offset, margin
 
 

@@ -134,6 +134,20 @@ class ModelGlobals(ctypes.Structure):
     _fields_ = [(n, ctypes.c_void_p) for n in GLOBAL_TENSORS]
 
 
+class LoopConfig(ctypes.Structure):
+    """sde_spec_loop_config: GenerationParams' spec_k, max_new_tokens, eos_token
+    and self_speculative (config.h:139-160); the draft cache handle and draft
+    model (NULL: self-speculative)."""
+    _fields_ = [
+        ("k", ctypes.c_int32),
+        ("n_draft", ctypes.c_int32),
+        ("max_new", ctypes.c_int32),
+        ("eos_token", ctypes.c_int32),
+        ("draft_cache", ctypes.c_void_p),
+        ("draft_model", ctypes.POINTER(LoopModel)),
+    ]
+
+
 _c_int = ctypes.c_int
 _vp = ctypes.c_void_p
 _sz = ctypes.c_size_t
@@ -191,6 +205,10 @@ PROTOTYPES = {
     "sde_spec_loop_stochastic": (_c_int, [_vp, ctypes.POINTER(LoopModel), _c_int, _c_int,
                                           _c_int, ctypes.POINTER(LoopSampling), _vp, _vp, _vp,
                                           _vp, _vp, _sz, _vp]),
+    "sde_spec_loop_config_workspace_size": (_sz, [_vp, ctypes.POINTER(LoopModel),
+                                                  ctypes.POINTER(LoopConfig)]),
+    "sde_spec_loop": (_c_int, [_vp, ctypes.POINTER(LoopModel), ctypes.POINTER(LoopConfig),
+                               ctypes.POINTER(LoopSampling), _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
 }
 
 _LIB = None

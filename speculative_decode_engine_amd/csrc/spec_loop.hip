@@ -70,24 +70,33 @@ enum : int {
 };
 constexpr size_t kBarBytes = kBarWords * sizeof(uint32_t);
 
-struct LoopArgs {
+// One model of the loop over its cache: the target (whose prefix layers
+// also draft in the self-speculative form), or a separate draft model.
+struct Side {
   sde_kv_view kv;
   sde_loop_model m;
-  int d;  // n_heads * head_dim
+  int d;    // n_heads * head_dim
+  int cap;  // positions every layer's table maps
+  const uint4* head_packed;  // the head's panel-packed copy (made by the launch)
+};
+
+struct LoopArgs {
+  Side t;      // the target model and cache
+  Side dr;     // the draft model and its cache (when `two`)
+  int two;     // a separate draft model and cache (kernels.cu:2864-2875, shared_kv false)
+  int eos;     // stop after a round whose bonus is this token; < 0: never
   int k;
   int n_draft;
   int max_new;
-  int cap;  // positions the layer tables map
   int32_t* state;
   int32_t* emitted;   // [max_new + k]
   int32_t* accepted;  // [max_new], per round
   float* q_buf;       // [k+1][d]
   float* h_buf;       // [k+1][d]
   float* logits;      // [k+1][vocab]
-  int32_t* tokens;    // [2(k+1)]: window tokens, then the target's tokens
+  int32_t* tokens;    // [2(k+1) + 2]: window tokens, the target's tokens, kCatchUp, kDone
   void* attn_ws;
   size_t attn_ws_bytes;
-  const uint4* head_packed;  // the head's panel-packed copy (made by the launch)
   uint2* cand;               // [kMaxWindow][panels]: each panel's (max logit, column) per row
   uint32_t* cand_arrivals;   // the head's items done (zero at rest)
   uint32_t* bar;  // grid barrier words (kBar*), zero at rest
@@ -101,29 +110,48 @@ struct LoopArgs {
 };
 
 // Workspace layout: attention workspace (counters first), the loop's
-// buffers, then the head's packed copy, each 256-byte aligned.
+// buffers, then the heads' packed copies, each 256-byte aligned.
 struct Layout {
-  size_t attn, q, h, logits, tokens, bar, dlogits, sres, dres, sscratch, head, cand, total;
+  size_t attn, q, h, logits, tokens, bar, dlogits, sres, dres, sscratch, head, dhead, cand, total;
 };
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-inline Layout layout(int nh, int nkv, int dph, int vocab, int k, int cap) {
+// A model's attention shape and its cache's positions.
+struct Shape {
+  int nh, nkv, dph, cap;
+};
+
+// tokens[] words after the window's and the target's tokens.
+__host__ __device__ inline int catch_up_slot(int k) { return 2 * (k + 1); }  // the draft catch-up's token
+__host__ __device__ inline int done_slot(int k) { return 2 * (k + 1) + 1; }  // 1 once an EOS bonus is out
+
+inline Layout layout(const Shape& t, const Shape* d, int vocab, int k) {
   Layout l;
   const int M = k + 1;
-  const size_t d = (size_t)nh * dph;
+  const size_t dt = (size_t)t.nh * t.dph;
+  const size_t dd = d ? (size_t)d->nh * d->dph : 0;
+  const size_t dmax = dt > dd ? dt : dd;
+  // The target's window calls and the draft's one-query calls share the
+  // attention workspace (a grid barrier separates them).
+  size_t ws = grid_attention_workspace_size(t.nh, t.nkv, t.dph, M, t.cap);
+  if (d) {
+    const size_t wd = grid_attention_workspace_size(d->nh, d->nkv, d->dph, 1, d->cap);
+    if (wd > ws) ws = wd;
+  }
   l.attn = 0;
-  l.q = align256(grid_attention_workspace_size(nh, nkv, dph, M, cap));
-  l.h = l.q + align256(M * d * sizeof(float));
-  l.logits = l.h + align256(M * d * sizeof(float));
+  l.q = align256(ws);
+  l.h = l.q + align256(M * dmax * sizeof(float));
+  l.logits = l.h + align256(M * dmax * sizeof(float));
   l.tokens = l.logits + align256((size_t)M * vocab * sizeof(float));
-  l.bar = l.tokens + align256(2 * M * sizeof(int32_t));
+  l.bar = l.tokens + align256((2 * M + 2) * sizeof(int32_t));
   l.dlogits = l.bar + align256(kBarBytes);
   l.sres = l.dlogits + align256((size_t)(k > 0 ? k : 1) * vocab * sizeof(float));
   l.dres = l.sres + align256((k + 5) * sizeof(int32_t));
   l.sscratch = l.dres + 256;
   l.head = l.sscratch + align256(spec_stochastic_workspace_size());
-  l.cand = l.head + align256(mvp::packed_shape((int)d, vocab).units * 16);
+  l.dhead = l.head + align256(mvp::packed_shape((int)dt, vocab).units * 16);
+  l.cand = l.dhead + (d ? align256(mvp::packed_shape((int)dd, vocab).units * 16) : 0);
   l.total = l.cand + 256 + align256((size_t)kMaxWindow * (vocab / 8) * sizeof(uint2));
   return l;
 }
@@ -247,16 +275,16 @@ __device__ __forceinline__ void note_error(const LoopArgs& a, int st) {
     atomicCAS(reinterpret_cast<int*>(a.state + kStatus), SDE_OK, st);
 }
 
-// q rows [r0, r0+n) of layer l: the token's embedding, plus the previous
-// layer's attention output of the row (residual), by the whole grid.
-__device__ void build_q(const LoopArgs& a, int l, int r0, int n, bool residual) {
-  const int d = a.d, V = a.m.vocab;
+// q rows [r0, r0+n) of layer l of model s: the token's embedding, plus the
+// previous layer's attention output of the row (residual), by the whole grid.
+__device__ void build_q(const LoopArgs& a, const Side& s, int l, int r0, int n, bool residual) {
+  const int d = s.d, V = s.m.vocab;
   const int total = n * d;
   for (int i = blockIdx.x * blockDim.x + attn::item_tid(); i < total;
        i += gridDim.x * blockDim.x) {
     const int m = r0 + i / d, e = i - (i / d) * d;
     const int tok = a.tokens[m];
-    float x = a.m.emb_q[((size_t)l * V + tok) * d + e];
+    float x = s.m.emb_q[((size_t)l * V + tok) * d + e];
     if (residual) x += a.h_buf[(size_t)m * d + e];
     a.q_buf[(size_t)m * d + e] = x;
   }
@@ -268,23 +296,37 @@ __device__ void build_q(const LoopArgs& a, int l, int r0, int n, bool residual) 
 // (Thread indices here and below come through attn::item_tid(), so the
 // compiler cannot keep them live across the attention's register-heavy
 // tile loop.)
-__device__ void append_rows(const LoopArgs& a, int l, int r0, int n, int pos0) {
-  const int kvd = a.kv.kv_dim, V = a.m.vocab;
-  for (int r = r0 + blockIdx.x; r < r0 + n; r += gridDim.x) {
-    const int tok = a.tokens[r];
-    const float* k = a.m.emb_k + ((size_t)l * V + tok) * kvd;
-    const float* v = a.m.emb_v + ((size_t)l * V + tok) * kvd;
-    const int pos = pos0 + r;
-    const int lb = pos / a.kv.block_size;
-    const int pb = a.kv.block_tables[(size_t)l * a.kv.max_blocks_per_layer + lb];
-    uint16_t* kd = a.kv.pool + ((size_t)pb * 2u * a.kv.block_size + (pos - lb * a.kv.block_size)) *
-                                   (size_t)kvd;
-    uint16_t* vd = kd + (size_t)a.kv.block_size * kvd;
-    for (int i = attn::item_tid(); i < kvd; i += blockDim.x) {
-      kd[i] = __builtin_bit_cast(uint16_t, (_Float16)k[i]);
-      vd[i] = __builtin_bit_cast(uint16_t, (_Float16)v[i]);
-    }
+// Token tok's K/V rows of layer l of model s at position pos, by the
+// calling block.
+__device__ __forceinline__ void append_token(const Side& s, int l, int tok, int pos) {
+  const int kvd = s.kv.kv_dim, V = s.m.vocab;
+  const float* k = s.m.emb_k + ((size_t)l * V + tok) * kvd;
+  const float* v = s.m.emb_v + ((size_t)l * V + tok) * kvd;
+  const int lb = pos / s.kv.block_size;
+  const int pb = s.kv.block_tables[(size_t)l * s.kv.max_blocks_per_layer + lb];
+  uint16_t* kd = s.kv.pool + ((size_t)pb * 2u * s.kv.block_size + (pos - lb * s.kv.block_size)) *
+                                 (size_t)kvd;
+  uint16_t* vd = kd + (size_t)s.kv.block_size * kvd;
+  for (int i = attn::item_tid(); i < kvd; i += blockDim.x) {
+    kd[i] = __builtin_bit_cast(uint16_t, (_Float16)k[i]);
+    vd[i] = __builtin_bit_cast(uint16_t, (_Float16)v[i]);
   }
+}
+
+__device__ void append_rows(const LoopArgs& a, const Side& s, int l, int r0, int n, int pos0) {
+  for (int r = r0 + blockIdx.x; r < r0 + n; r += gridDim.x)
+    append_token(s, l, a.tokens[r], pos0 + r);
+}
+
+// The draft model's catch-up forward of megakernel_speculative_kernel
+// (kernels.cu:3079-3093) as the draft cache sees it: token
+// tokens[catch_up_slot] (the last draft when all were accepted, else the
+// bonus) at position pos in every draft layer, one block per layer.  (The
+// loop model's K/V depend on the token and the position alone; the
+// forward's logits are unused.)
+__device__ void catch_up(const LoopArgs& a, int pos) {
+  const int tok = a.tokens[catch_up_slot(a.k)];
+  for (int l = blockIdx.x; l < a.dr.kv.n_layers; l += gridDim.x) append_token(a.dr, l, tok, pos);
 }
 
 // The grid attention of layer l over window rows [r0, r0+n) at positions
@@ -292,22 +334,22 @@ __device__ void append_rows(const LoopArgs& a, int l, int r0, int n, int pos0) {
 // budget instead of sharing it with the values the loops around it keep.
 // 4-wave staging (64 KiB of LDS): the 8-wave form is off in the loop (see
 // the design notes on the loop's attention).
-__device__ __attribute__((noinline)) int layer_attention(const LoopArgs& a, int l, int r0, int n,
-                                                         int pos0) {
+__device__ __attribute__((noinline)) int layer_attention(const LoopArgs& a, const Side& s, int l,
+                                                         int r0, int n, int pos0) {
   return device_flash_attention_gqa_grid<4>(
-      a.q_buf + (size_t)r0 * a.d, a.h_buf + (size_t)r0 * a.d, a.kv, l, a.m.n_heads,
-      a.m.n_kv_heads, a.m.head_dim, pos0 + r0, n, a.attn_ws, a.attn_ws_bytes);
+      a.q_buf + (size_t)r0 * s.d, a.h_buf + (size_t)r0 * s.d, s.kv, l, s.m.n_heads,
+      s.m.n_kv_heads, s.m.head_dim, pos0 + r0, n, a.attn_ws, a.attn_ws_bytes);
 }
 
-// Layers [lo, hi) on window rows [r0, r0+n) at positions pos0 + row:
-// append, q, grid attention; h_buf rows hold the last layer's output.
-__device__ __forceinline__ void run_layers(const LoopArgs& a, int lo, int hi, int r0, int n,
-                                           int pos0) {
+// Layers [lo, hi) of model s on window rows [r0, r0+n) at positions pos0 +
+// row: append, q, grid attention; h_buf rows hold the last layer's output.
+__device__ __forceinline__ void run_layers(const LoopArgs& a, const Side& s, int lo, int hi,
+                                           int r0, int n, int pos0) {
   for (int l = lo; l < hi; l++) {
-    append_rows(a, l, r0, n, pos0);
-    build_q(a, l, r0, n, l > 0);
+    append_rows(a, s, l, r0, n, pos0);
+    build_q(a, s, l, r0, n, l > 0);
     barrier(a);
-    note_error(a, layer_attention(a, l, r0, n, pos0));
+    note_error(a, layer_attention(a, s, l, r0, n, pos0));
     barrier(a);
   }
 }
@@ -448,13 +490,13 @@ __device__ __forceinline__ void head_rows(const LoopArgs& a, const mvp::PackedAr
   }
 }
 
-__device__ __attribute__((noinline)) void head_logits(const LoopArgs& a, int r0, int n,
-                                                      float* logits, int argmax_dst) {
-  const int d = wave_uniform(a.d), V = wave_uniform(a.m.vocab);
+__device__ __attribute__((noinline)) void head_logits(const LoopArgs& a, const Side& s, int r0,
+                                                      int n, float* logits, int argmax_dst) {
+  const int d = wave_uniform(s.d), V = wave_uniform(s.m.vocab);
   n = wave_uniform(n);
   const mvp::PackedShape sh = mvp::packed_shape(d, V);
   mvp::PackedArgs pa;
-  pa.W = wave_uniform(a.head_packed);
+  pa.W = wave_uniform(s.head_packed);
   pa.x = wave_uniform(a.h_buf + (size_t)wave_uniform(r0) * d);
   pa.out = wave_uniform(logits);
   pa.d_in = d;
@@ -471,10 +513,10 @@ __device__ __attribute__((noinline)) void head_logits(const LoopArgs& a, int r0,
     head_rows<1>(a, pa, sh.panels, passes, am);
 }
 
-// Logits of window rows [r0, r0+n) from their h_buf rows, then their
-// argmaxes into tokens[dst + row].
-__device__ __forceinline__ void decide(const LoopArgs& a, int r0, int n, int dst) {
-  head_logits(a, r0, n, a.logits, dst);
+// Logits of window rows [r0, r0+n) from their h_buf rows (model s's head),
+// then their argmaxes into tokens[dst + row].
+__device__ __forceinline__ void decide(const LoopArgs& a, const Side& s, int r0, int n, int dst) {
+  head_logits(a, s, r0, n, a.logits, dst);
   barrier(a);
 }
 
@@ -506,8 +548,9 @@ __global__ void spec_loop_init_kernel(LoopArgs a) {
     // The anchor indexes the embedding tables: one outside the vocabulary
     // stops the launch at its first round check, before any table read.
     const int anchor = a.state[kAnchor];
-    const bool ok = anchor >= 0 && anchor < a.m.vocab;
+    const bool ok = anchor >= 0 && anchor < a.t.m.vocab;
     a.tokens[0] = ok ? anchor : 0;
+    a.tokens[done_slot(a.k)] = 0;
     for (int i = kEmitted; i < kStateWords; i++) a.state[i] = 0;
     if (!ok) a.state[kStatus] = SDE_ERR_INVALID_ARGUMENT;
     if (a.offset) {
@@ -517,38 +560,73 @@ __global__ void spec_loop_init_kernel(LoopArgs a) {
   }
 }
 
+// The round's opening checks, the same in every block: stop when max_new
+// tokens are out, on a recorded status or after an EOS bonus; a window past
+// the mapped positions records SDE_ERR_CAPACITY and stops.
+__device__ __forceinline__ bool round_open(const LoopArgs& a, int P, int D) {
+  if (load_word(a.state + kEmitted) >= a.max_new || load_word(a.state + kStatus) != SDE_OK ||
+      load_word(a.tokens + done_slot(a.k)) != 0)
+    return false;
+  const int M = a.k + 1;
+  if (P < 0 || P + M > a.t.cap || (a.two && (D < 0 || D + M > a.dr.cap))) {
+    if (blockIdx.x == 0 && threadIdx.x == 0) store_word(a.state + kStatus, SDE_ERR_CAPACITY);
+    return false;
+  }
+  return true;
+}
+
+// After the accept (block 0, thread 0): the two-cache loop's catch-up token
+// and draft seq_len (draft_save + n + 1, the catch-up's position + 1), and
+// the EOS flag.
+__device__ __forceinline__ void round_close(const LoopArgs& a, int n, int bonus, int draft_seq) {
+  if (a.two) {
+    a.tokens[catch_up_slot(a.k)] = n == a.k ? a.tokens[a.k] : bonus;
+    store_word(a.dr.kv.seq_len, draft_seq + 1);
+  }
+  if (a.eos >= 0 && bonus == a.eos) store_word(a.tokens + done_slot(a.k), 1);
+}
+
 __global__ __launch_bounds__(kThreads) void spec_loop_kernel(LoopArgs a) {
   const int M = a.k + 1;
-  const int n_layers = a.kv.n_layers;
+  const int n_layers = a.t.kv.n_layers;
   register_blocks(a);
 
   for (int round = 0;; round++) {
     // Every block reads the same words after the barrier: the loop's exits
     // are uniform over the grid, so every block meets every barrier.
-    const int P = load_word(a.kv.seq_len);
-    if (load_word(a.state + kEmitted) >= a.max_new || load_word(a.state + kStatus) != SDE_OK)
-      break;
-    if (P < 0 || P + M > a.cap) {
-      if (blockIdx.x == 0 && threadIdx.x == 0) store_word(a.state + kStatus, SDE_ERR_CAPACITY);
-      break;
+    const int P = load_word(a.t.kv.seq_len);
+    const int D = a.two ? load_word(a.dr.kv.seq_len) : P;
+    if (!round_open(a, P, D)) break;
+    if (a.two) {
+      // Draft (kernels.cu:2948-2958): the draft model, all its layers, window
+      // token s at D+s; its argmax proposes token s+1.  Verify
+      // (model_batch_forward_logits, model.cu:657-714): the target, all
+      // layers, the whole window at P; the target's token for every row.
+      for (int s = 0; s < a.k; s++) {
+        run_layers(a, a.dr, 0, a.dr.kv.n_layers, s, 1, D);
+        decide(a, a.dr, s, 1, s + 1);
+      }
+      run_layers(a, a.t, 0, n_layers, 0, M, P);
+      decide(a, a.t, 0, M, M);
+    } else {
+      // Draft (kernels.cu:2960-3006), steps 0..k when k > 0: the prefix
+      // layers for window token s at P+s, one token at a time; the first k
+      // outputs propose window token s+1.  Verify (model.cu:838-890), the
+      // last step: the remaining layers over the whole window, then the
+      // target's token for every row.
+      const int n_steps = a.k > 0 ? M + 1 : 1;
+      for (int s = 0; s < n_steps; s++) {
+        const Step t = round_step(a, s, n_steps, n_layers);
+        run_layers(a, a.t, t.lo, t.hi, t.r0, t.n, P);
+        if (t.verify || s < a.k) decide(a, a.t, t.r0, t.n, t.verify ? M : s + 1);
+      }
     }
-    // Draft (kernels.cu:2960-3006), steps 0..k when k > 0: the prefix
-    // layers for window token s at P+s, one token at a time; the first k
-    // outputs propose window token s+1.  Verify (model.cu:838-890), the last
-    // step: the remaining layers over the whole window, then the target's
-    // token for every row.
-    const int n_steps = a.k > 0 ? M + 1 : 1;
-    for (int s = 0; s < n_steps; s++) {
-      const Step t = round_step(a, s, n_steps, n_layers);
-      run_layers(a, t.lo, t.hi, t.r0, t.n, P);
-      if (t.verify || s < a.k) decide(a, t.r0, t.n, t.verify ? M : s + 1);
-    }
-    // Greedy accept and O(1) rewind (kernels.cu:3050-3072).
+    // Greedy accept and O(1) rewinds (kernels.cu:3050-3076).
     if (blockIdx.x == 0 && threadIdx.x == 0) {
       const int E = a.state[kEmitted];
-      const SpecAccept r = spec_accept_greedy(a.tokens + 1, a.tokens + M, a.k, P, P, a.kv,
-                                              nullptr, a.emitted + E);
-      store_word(a.kv.seq_len, r.target_seq);  // (spec_accept_greedy wrote it plainly)
+      const SpecAccept r = spec_accept_greedy(a.tokens + 1, a.tokens + M, a.k, P, D, a.t.kv,
+                                              a.two ? &a.dr.kv : nullptr, a.emitted + E);
+      store_word(a.t.kv.seq_len, r.target_seq);  // (spec_accept_greedy wrote it plainly)
       store_word(a.state + kEmitted, E + r.n_accepted + 1);
       a.state[kAnchor] = r.bonus;
       a.state[kRounds] = round + 1;
@@ -556,8 +634,13 @@ __global__ __launch_bounds__(kThreads) void spec_loop_kernel(LoopArgs a) {
       a.state[kAccepted] += r.n_accepted;
       a.accepted[round] = r.n_accepted;
       a.tokens[0] = r.bonus;
+      round_close(a, r.n_accepted, r.bonus, r.draft_seq);
     }
     barrier(a);
+    if (a.two) {  // the draft's catch-up (kernels.cu:3079-3093)
+      catch_up(a, load_word(a.dr.kv.seq_len) - 1);
+      barrier(a);
+    }
   }
 }
 
@@ -594,32 +677,33 @@ __device__ void adapt_temperature(const LoopArgs& a, int n_accepted) {
 // instead of recomputed after a rejection (the same values).
 __global__ __launch_bounds__(kThreads) void spec_loop_stochastic_kernel(LoopArgs a) {
   const int M = a.k + 1;
-  const int V = a.m.vocab;
-  const int n_layers = a.kv.n_layers;
+  const int V = a.t.m.vocab;
+  const int n_layers = a.t.kv.n_layers;
   const GridSync sync{&a};
   const size_t sbytes = spec_stochastic_workspace_size();
-  sde_kv_view dv = a.kv;  // draft samples rewind nothing: their seq_len word is scratch
+  sde_kv_view dv = a.t.kv;  // draft samples rewind nothing: their seq_len word is scratch
   dv.seq_len = a.dres + 7;
   register_blocks(a);
 
   for (int round = 0;; round++) {
-    const int P = load_word(a.kv.seq_len);
-    if (load_word(a.state + kEmitted) >= a.max_new || load_word(a.state + kStatus) != SDE_OK)
-      break;
-    if (P < 0 || P + M > a.cap) {
-      if (blockIdx.x == 0 && threadIdx.x == 0) store_word(a.state + kStatus, SDE_ERR_CAPACITY);
-      break;
-    }
+    const int P = load_word(a.t.kv.seq_len);
+    const int D = a.two ? load_word(a.dr.kv.seq_len) : P;
+    if (!round_open(a, P, D)) break;
     const float temp = __int_as_float(load_word(a.state + kTemp));
     // The greedy loop's steps: drafts 0..k-1 sample the next window token
-    // from their logits (draft step k only appends), the last step verifies.
-    const int n_steps = a.k > 0 ? M + 1 : 1;
+    // from their logits (the self-speculative draft step k only appends),
+    // the last step verifies; with a draft model, its k steps draft and the
+    // target verifies.
+    const int n_steps = a.two ? M : (a.k > 0 ? M + 1 : 1);
     for (int s = 0; s < n_steps; s++) {
-      const Step t = round_step(a, s, n_steps, n_layers);
-      run_layers(a, t.lo, t.hi, t.r0, t.n, P);
+      const Step t = a.two ? (s < a.k ? Step{0, a.dr.kv.n_layers, s, 1, false}
+                                      : Step{0, n_layers, 0, M, true})
+                           : round_step(a, s, n_steps, n_layers);
+      const Side& sd = a.two && !t.verify ? a.dr : a.t;
+      run_layers(a, sd, t.lo, t.hi, t.r0, t.n, t.verify ? P : (a.two ? D : P));
       if (!t.verify && s >= a.k) continue;
       float* lg = t.verify ? a.logits : a.dlogits + (size_t)s * V;
-      head_logits(a, t.r0, t.n, lg, -1);
+      head_logits(a, sd, t.r0, t.n, lg, -1);
       barrier(a);
       if (t.verify) break;
       int st = device_spec_accept_stochastic_grid(lg, nullptr, nullptr, 0, V, temp, 1.f, a.smp.seed,
@@ -638,20 +722,23 @@ __global__ __launch_bounds__(kThreads) void spec_loop_stochastic_kernel(LoopArgs
       barrier(a);
     }
     int st = device_spec_accept_stochastic_grid(a.logits, a.dlogits, a.tokens + 1, a.k, V, 1.f, temp,
-                                            a.smp.seed, a.offset, P, P, a.kv, nullptr, a.sres,
-                                            a.sscratch, sbytes, sync);
+                                            a.smp.seed, a.offset, P, D, a.t.kv,
+                                            a.two ? &a.dr.kv : nullptr, a.sres, a.sscratch, sbytes,
+                                            sync);
     note_error(a, st);
     barrier(a);
     if (blockIdx.x == 0 && threadIdx.x == 0) {
       const int n = a.sres[0];
       const int E = a.state[kEmitted];
-      if (n < 0 || n > a.k || a.sres[1] < 0 || a.sres[1] >= V || a.sres[2] != P + n + 1) {
-        // not a result of the acceptance: stop with an error, cache untouched
+      if (n < 0 || n > a.k || a.sres[1] < 0 || a.sres[1] >= V || a.sres[2] != P + n + 1 ||
+          (a.two && a.sres[3] != D + n)) {
+        // not a result of the acceptance: stop with an error, caches untouched
         atomicCAS(reinterpret_cast<int*>(a.state + kStatus), SDE_OK, SDE_ERR_HIP);
-        store_word(a.kv.seq_len, P);
+        store_word(a.t.kv.seq_len, P);
+        if (a.two) store_word(a.dr.kv.seq_len, D);
       } else {
         for (int j = 0; j <= n; j++) a.emitted[E + j] = a.sres[4 + j];
-        store_word(a.kv.seq_len, a.sres[2]);
+        store_word(a.t.kv.seq_len, a.sres[2]);
         store_word(a.state + kEmitted, E + n + 1);
         a.state[kAnchor] = a.sres[1];
         a.state[kRounds] = round + 1;
@@ -660,9 +747,14 @@ __global__ __launch_bounds__(kThreads) void spec_loop_stochastic_kernel(LoopArgs
         a.accepted[round] = n;
         a.tokens[0] = a.sres[1];
         adapt_temperature(a, n);
+        round_close(a, n, a.sres[1], D + n);
       }
     }
     barrier(a);
+    if (a.two && load_word(a.state + kStatus) == SDE_OK) {  // the draft's catch-up
+      catch_up(a, load_word(a.dr.kv.seq_len) - 1);
+      barrier(a);
+    }
   }
 }
 
@@ -671,26 +763,103 @@ __global__ __launch_bounds__(kThreads) void spec_loop_stochastic_kernel(LoopArgs
 
 namespace {
 
-// The checks and the launch shared by the greedy and the sampling loops.
-int launch_loop(sde_kv_cache* cache, const sde_loop_model* model, int k, int n_draft,
-                int max_new, int32_t* d_state, int32_t* d_emitted, int32_t* d_accepted,
-                void* d_workspace, size_t workspace_bytes, sde_stream_t stream,
-                const sde_loop_sampling* smp, uint64_t* d_offset) {
-  using namespace sde::loop;
-  if (!cache || !model || !d_state || !d_emitted || !d_accepted || !d_workspace)
-    return SDE_ERR_INVALID_ARGUMENT;
+// A loop model's checks against its cache (the same for the target and a
+// draft model).
+int check_model(const sde_kv_cache* cache, const sde_loop_model* model) {
+  if (!cache || !model) return SDE_ERR_INVALID_ARGUMENT;
   const sde_loop_model& m = *model;
   if (!m.emb_q || !m.emb_k || !m.emb_v || !m.head) return SDE_ERR_INVALID_ARGUMENT;
   if (m.n_heads < 1 || m.n_kv_heads < 1 || m.n_heads % m.n_kv_heads != 0 ||
-      m.n_kv_heads * m.head_dim != cache->cfg.kv_dim || m.vocab < 8 || max_new < 1)
+      m.n_kv_heads * m.head_dim != cache->cfg.kv_dim || m.vocab < 8)
     return SDE_ERR_INVALID_ARGUMENT;
   if (m.head_dim != 64 && m.head_dim != 128) return SDE_ERR_UNSUPPORTED;
   if (cache->cfg.block_size % 8 != 0 || m.vocab % 8 != 0 ||
       (reinterpret_cast<uintptr_t>(m.head) & 15u) != 0)
     return SDE_ERR_UNSUPPORTED;
-  if (k < 0 || k + 1 > kMaxWindow) return SDE_ERR_RANGE;
+  return SDE_OK;
+}
+
+// A model's attention shape over its cache (the attention workspace is
+// sized for the cache's whole table).
+sde::loop::Shape shape_of(const sde_kv_cache* cache, const sde_loop_model* m) {
+  return {m->n_heads, m->n_kv_heads, m->head_dim,
+          cache->cfg.max_blocks_per_layer * cache->cfg.block_size};
+}
+
+// Positions every layer of the cache maps to a physical block.
+int mapped_positions(const sde_kv_cache* cache) {
+  int cap = cache->cfg.max_blocks_per_layer * cache->cfg.block_size;
+  for (int l = 0; l < cache->cfg.n_layers; l++) {
+    const int mapped = (int)sde::mapped_tokens(cache, l);
+    if (mapped < cap) cap = mapped;
+  }
+  return cap;
+}
+
+// The workspace layout for a configuration (its shapes checked by the caller).
+sde::loop::Layout config_layout(const sde_kv_cache* cache, const sde_loop_model* model,
+                                const sde_spec_loop_config& c) {
+  const sde::loop::Shape t = shape_of(cache, model);
+  if (c.draft_cache) {
+    const sde::loop::Shape d = shape_of(c.draft_cache, c.draft_model);
+    return sde::loop::layout(t, &d, model->vocab, c.k);
+  }
+  return sde::loop::layout(t, nullptr, model->vocab, c.k);
+}
+
+sde::loop::Side make_side(const sde_kv_view& kv, const sde_loop_model& m, int cap,
+                          const char* packed) {
+  sde::loop::Side s;
+  s.kv = kv;
+  s.m = m;
+  s.d = m.n_heads * m.head_dim;
+  s.cap = cap;
+  s.head_packed = reinterpret_cast<const uint4*>(packed);
+  return s;
+}
+
+// The head's panel-packed copy for this launch (a one-time re-layout per
+// call, amortized over its rounds).
+int pack_head(const sde_loop_model& m, char* dst, int n_cus, hipStream_t stream) {
+  const int d = m.n_heads * m.head_dim;
+  const sde::mvp::PackedShape hs = sde::mvp::packed_shape(d, m.vocab);
+  if (hs.panels == 0) return SDE_ERR_UNSUPPORTED;
+  const size_t pack_blocks = (hs.units + 255) / 256;
+  const int pb = (int)(pack_blocks < (size_t)n_cus * 16 ? pack_blocks : (size_t)n_cus * 16);
+  sde::mvp::matvec_pack_kernel<<<pb, 256, 0, stream>>>(m.head, reinterpret_cast<uint4*>(dst), d,
+                                                       m.vocab);
+  return hipGetLastError() == hipSuccess ? SDE_OK : SDE_ERR_HIP;
+}
+
+// The checks and the launch shared by the greedy and the sampling loops,
+// self-speculative or with a draft model over a cache of its own.
+int launch_loop(sde_kv_cache* cache, const sde_loop_model* model, const sde_spec_loop_config* cfg,
+                int32_t* d_state, int32_t* d_emitted, int32_t* d_accepted, void* d_workspace,
+                size_t workspace_bytes, sde_stream_t stream, const sde_loop_sampling* smp,
+                uint64_t* d_offset) {
+  using namespace sde::loop;
+  if (!cfg || !d_state || !d_emitted || !d_accepted || !d_workspace)
+    return SDE_ERR_INVALID_ARGUMENT;
+  const sde_spec_loop_config c = *cfg;
+  int st = check_model(cache, model);
+  if (st != SDE_OK) return st;
+  const sde_loop_model& m = *model;
+  if (c.max_new < 1) return SDE_ERR_INVALID_ARGUMENT;
+  if (c.k < 0 || c.k + 1 > kMaxWindow) return SDE_ERR_RANGE;
   const int n_layers = cache->cfg.n_layers;
-  if (k > 0 && (n_draft < 1 || n_draft >= n_layers)) return SDE_ERR_INVALID_ARGUMENT;
+  const bool two = c.draft_cache != nullptr || c.draft_model != nullptr;
+  if (two) {
+    // A draft model over its own cache (kernels.cu:3593-3627, not
+    // self_speculative): the same vocabulary, another cache on the device.
+    if (!c.draft_cache || !c.draft_model || c.draft_cache == cache || c.k < 1)
+      return SDE_ERR_INVALID_ARGUMENT;
+    st = check_model(c.draft_cache, c.draft_model);
+    if (st != SDE_OK) return st;
+    if (c.draft_model->vocab != m.vocab || c.draft_cache->device != cache->device)
+      return SDE_ERR_INVALID_ARGUMENT;
+  } else if (c.k > 0 && (c.n_draft < 1 || c.n_draft >= n_layers)) {
+    return SDE_ERR_INVALID_ARGUMENT;
+  }
   if (smp) {
     if (!d_offset || !std::isfinite(smp->draft_temp) || !std::isfinite(smp->min_temp) ||
         !std::isfinite(smp->max_temp) || !std::isfinite(smp->target_accept) ||
@@ -699,14 +868,7 @@ int launch_loop(sde_kv_cache* cache, const sde_loop_model* model, int k, int n_d
       return SDE_ERR_INVALID_ARGUMENT;
     if ((reinterpret_cast<uintptr_t>(d_offset) & 7u) != 0) return SDE_ERR_INVALID_ARGUMENT;
   }
-  // Every position the loop can reach must have a physical block.
-  int cap = cache->cfg.max_blocks_per_layer * cache->cfg.block_size;
-  for (int l = 0; l < n_layers; l++) {
-    const int mapped = (int)sde::mapped_tokens(cache, l);
-    if (mapped < cap) cap = mapped;
-  }
-  const Layout lay = layout(m.n_heads, m.n_kv_heads, m.head_dim, m.vocab, k,
-                            cache->cfg.max_blocks_per_layer * cache->cfg.block_size);
+  const Layout lay = config_layout(cache, model, c);
   if (workspace_bytes < lay.total) return SDE_ERR_WORKSPACE;
   if ((reinterpret_cast<uintptr_t>(d_workspace) & 255u) != 0) return SDE_ERR_INVALID_ARGUMENT;
 
@@ -721,21 +883,25 @@ int launch_loop(sde_kv_cache* cache, const sde_loop_model* model, int k, int n_d
     return SDE_ERR_HIP;
   if (!coop || per_cu < 1) return SDE_ERR_UNSUPPORTED;
 
+  char* ws = static_cast<char*>(d_workspace);
+  sde_kv_view tv, dv{};
+  if (sde_kv_get_view(cache, &tv) != SDE_OK) return SDE_ERR_INVALID_ARGUMENT;
+  if (two && sde_kv_get_view(c.draft_cache, &dv) != SDE_OK) return SDE_ERR_INVALID_ARGUMENT;
   LoopArgs a;
-  if (sde_kv_get_view(cache, &a.kv) != SDE_OK) return SDE_ERR_INVALID_ARGUMENT;
-  a.m = m;
-  a.d = m.n_heads * m.head_dim;
-  a.k = k;
-  a.n_draft = k > 0 ? n_draft : 0;
-  a.max_new = max_new;
-  a.cap = cap;
+  // Every position the loop can reach must have a physical block.
+  a.t = make_side(tv, m, mapped_positions(cache), ws + lay.head);
+  a.dr = two ? make_side(dv, *c.draft_model, mapped_positions(c.draft_cache), ws + lay.dhead)
+             : a.t;
+  a.two = two ? 1 : 0;
+  a.eos = c.eos_token < 0 ? -1 : c.eos_token;
+  a.k = c.k;
+  a.n_draft = two || c.k == 0 ? 0 : c.n_draft;
+  a.max_new = c.max_new;
   a.state = d_state;
   a.emitted = d_emitted;
   a.accepted = d_accepted;
-  char* ws = static_cast<char*>(d_workspace);
   a.attn_ws = ws + lay.attn;
   a.attn_ws_bytes = lay.q - lay.attn;
-  a.head_packed = reinterpret_cast<const uint4*>(ws + lay.head);
   a.cand_arrivals = reinterpret_cast<uint32_t*>(ws + lay.cand);
   a.cand = reinterpret_cast<uint2*>(ws + lay.cand + 256);
   a.q_buf = reinterpret_cast<float*>(ws + lay.q);
@@ -749,49 +915,72 @@ int launch_loop(sde_kv_cache* cache, const sde_loop_model* model, int k, int n_d
   a.sscratch = reinterpret_cast<uint32_t*>(ws + lay.sscratch);
   a.offset = smp ? d_offset : nullptr;
   a.smp = smp ? *smp : sde_loop_sampling{};
-  // The head's panel-packed copy for this launch (a one-time re-layout per
-  // call, amortized over its rounds).
-  const sde::mvp::PackedShape hs = sde::mvp::packed_shape(a.d, m.vocab);
-  if (hs.panels == 0) return SDE_ERR_UNSUPPORTED;
-  const size_t pack_blocks = (hs.units + 255) / 256;
-  const int pb = (int)(pack_blocks < (size_t)cache->n_cus * 16 ? pack_blocks
-                                                              : (size_t)cache->n_cus * 16);
-  sde::mvp::matvec_pack_kernel<<<pb, 256, 0, static_cast<hipStream_t>(stream)>>>(
-      m.head, reinterpret_cast<uint4*>(ws + lay.head), a.d, m.vocab);
-  if (hipGetLastError() != hipSuccess) return SDE_ERR_HIP;
-  spec_loop_init_kernel<<<1, 256, 0, static_cast<hipStream_t>(stream)>>>(a);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  st = pack_head(m, ws + lay.head, cache->n_cus, s);
+  if (st == SDE_OK && two) st = pack_head(*c.draft_model, ws + lay.dhead, cache->n_cus, s);
+  if (st != SDE_OK) return st;
+  spec_loop_init_kernel<<<1, 256, 0, s>>>(a);
   if (hipGetLastError() != hipSuccess) return SDE_ERR_HIP;
   // A cooperative launch: every block resident at once, which the grid
   // barrier needs.
   void* args[] = {&a};
-  const hipError_t e = hipLaunchCooperativeKernel(kernel, dim3(cache->n_cus), dim3(kThreads),
-                                                  args, 0, static_cast<hipStream_t>(stream));
+  const hipError_t e =
+      hipLaunchCooperativeKernel(kernel, dim3(cache->n_cus), dim3(kThreads), args, 0, s);
   if (e != hipSuccess) return SDE_ERR_HIP;
   cache->seq_len_on_device = true;
+  if (two) c.draft_cache->seq_len_on_device = true;
   return SDE_OK;
+}
+
+sde_spec_loop_config self_config(int k, int n_draft, int max_new) {
+  sde_spec_loop_config c{};
+  c.k = k;
+  c.n_draft = n_draft;
+  c.max_new = max_new;
+  c.eos_token = -1;
+  return c;
 }
 
 }  // namespace
 
 extern "C" {
 
+size_t sde_spec_loop_config_workspace_size(const sde_kv_cache* cache, const sde_loop_model* model,
+                                           const sde_spec_loop_config* cfg) {
+  if (!cfg || cfg->k < 0 || cfg->k + 1 > sde::loop::kMaxWindow) return 0;
+  if (check_model(cache, model) != SDE_OK) return 0;
+  if (cfg->draft_cache || cfg->draft_model) {
+    if (!cfg->draft_cache || !cfg->draft_model ||
+        check_model(cfg->draft_cache, cfg->draft_model) != SDE_OK ||
+        cfg->draft_model->vocab != model->vocab)
+      return 0;
+  }
+  return config_layout(cache, model, *cfg).total;
+}
+
 size_t sde_spec_loop_workspace_size(const sde_kv_cache* cache, const sde_loop_model* model,
                                     int k) {
   if (!cache || !model || k < 0 || k + 1 > sde::loop::kMaxWindow) return 0;
   if (model->n_heads < 1 || model->n_kv_heads < 1 || model->head_dim < 1 || model->vocab < 1)
     return 0;
-  const int cap = cache->cfg.max_blocks_per_layer * cache->cfg.block_size;
-  return sde::loop::layout(model->n_heads, model->n_kv_heads, model->head_dim, model->vocab, k,
-                           cap)
-      .total;
+  return sde::loop::layout(shape_of(cache, model), nullptr, model->vocab, k).total;
+}
+
+int sde_spec_loop(sde_kv_cache* cache, const sde_loop_model* model, const sde_spec_loop_config* cfg,
+                  const sde_loop_sampling* sampling, uint64_t* d_rng_offset, int32_t* d_state,
+                  int32_t* d_emitted, int32_t* d_accepted, void* d_workspace,
+                  size_t workspace_bytes, sde_stream_t stream) {
+  return launch_loop(cache, model, cfg, d_state, d_emitted, d_accepted, d_workspace,
+                     workspace_bytes, stream, sampling, d_rng_offset);
 }
 
 int sde_spec_loop_greedy(sde_kv_cache* cache, const sde_loop_model* model, int k, int n_draft,
                          int max_new, int32_t* d_state, int32_t* d_emitted,
                          int32_t* d_accepted, void* d_workspace, size_t workspace_bytes,
                          sde_stream_t stream) {
-  return launch_loop(cache, model, k, n_draft, max_new, d_state, d_emitted, d_accepted,
-                     d_workspace, workspace_bytes, stream, nullptr, nullptr);
+  const sde_spec_loop_config c = self_config(k, n_draft, max_new);
+  return launch_loop(cache, model, &c, d_state, d_emitted, d_accepted, d_workspace,
+                     workspace_bytes, stream, nullptr, nullptr);
 }
 
 int sde_spec_loop_stochastic(sde_kv_cache* cache, const sde_loop_model* model, int k,
@@ -800,8 +989,9 @@ int sde_spec_loop_stochastic(sde_kv_cache* cache, const sde_loop_model* model, i
                              int32_t* d_accepted, void* d_workspace, size_t workspace_bytes,
                              sde_stream_t stream) {
   if (!sampling) return SDE_ERR_INVALID_ARGUMENT;
-  return launch_loop(cache, model, k, n_draft, max_new, d_state, d_emitted, d_accepted,
-                     d_workspace, workspace_bytes, stream, sampling, d_rng_offset);
+  const sde_spec_loop_config c = self_config(k, n_draft, max_new);
+  return launch_loop(cache, model, &c, d_state, d_emitted, d_accepted, d_workspace,
+                     workspace_bytes, stream, sampling, d_rng_offset);
 }
 
 }  // extern "C"
