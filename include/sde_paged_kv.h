@@ -86,7 +86,10 @@ const char* sde_status_string(int status);
 
 /* Host-only check of a configuration (no device work).  Rules:
  * n_layers, kv_dim, max_blocks_per_layer >= 1; block_size in [1, 1024];
- * pool_blocks >= 0 (0 = reference sizing) and >= max_blocks_per_layer. */
+ * pool_blocks >= 0 (0 = reference sizing) and >= max_blocks_per_layer; the
+ * resolved pool_blocks and max_blocks_per_layer * block_size fit int32; the
+ * pool's byte size (pool_blocks * 2 * block_size * kv_dim * 2) fits
+ * ptrdiff_t. */
 int sde_kv_config_validate(const sde_kv_config* cfg);
 
 /* Bytes of the pool a configuration needs (0 on an invalid config). */

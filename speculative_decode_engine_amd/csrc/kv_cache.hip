@@ -142,6 +142,11 @@ bool valid_config(const sde_kv_config* cfg) {
   if (pool < cfg->max_blocks_per_layer) return false;
   // Token positions are int32 everywhere (as in the reference).
   if ((int64_t)cfg->max_blocks_per_layer * cfg->block_size > INT32_MAX) return false;
+  // The pool's byte size must be representable: K and V fp16 rows of every
+  // block (without this, a large kv_dim wraps the size_t product and the
+  // pool would be allocated smaller than its tables address).
+  const int64_t block_bytes = (int64_t)4 * cfg->block_size * cfg->kv_dim;
+  if (pool > PTRDIFF_MAX / block_bytes) return false;
   return true;
 }
 

@@ -49,6 +49,8 @@ def test_status_strings(lib):
     ((4, 128, 9, 16, 8), False),      # pool smaller than one layer's table
     ((4, 128, 9, 16, -1), False),
     ((1 << 20, 128, 1 << 12, 16, 0), False),  # pool block count overflows int32
+    ((52, 1765861560, 1 << 20, 128, 0), False),  # pool bytes wrap size_t (found by fuzzing)
+    ((1, (1 << 31) - 1, 1, 1024, 0), True),       # 8 TiB: representable, rejected only on alloc
 ])
 def test_config_validation(lib, cfg, ok):
     c = N.KVConfig(*cfg)
