@@ -35,6 +35,7 @@
 #include <cstdint>
 
 #include "sde_paged_kv.h"
+#include "sde/attention_generic_device.hpp"
 #include "sde/wave_uniform.hpp"
 
 namespace sde {
@@ -1248,17 +1249,54 @@ __device__ inline void kv_cache_rollback(const sde_kv_view& kv, int target_len) 
 // Inlined into the caller; its tile loop needs up to ~240 VGPRs per lane,
 // so the calling kernel should be declared __launch_bounds__(512) or
 // smaller (two waves per SIMD), else the compiler spills.
-// head_dim 64 or 128, block_size a multiple of 8, nkv | nh; returns
-// SDE_ERR_UNSUPPORTED (writing nothing) otherwise.
+// Other head sizes (up to 512) and block sizes run the generic fp32 path
+// (sde/attention_generic_device.hpp: up to 256 of the block's threads, its
+// LDS inside the same static area).  nkv | nh and blockDim.x a multiple of 64; returns
+// SDE_ERR_UNSUPPORTED (writing nothing) otherwise, or for head_dim > 512.
 template <int MaxWaves = 4>
 __device__ __forceinline__ int device_flash_attention_gqa(const float* q_all, float* attn_out,
                                                           const sde_kv_view& kv, int layer, int nh,
                                                           int nkv, int dph, int total_len) {
   using namespace attn;
   static_assert(MaxWaves == 1 || MaxWaves == 2 || MaxWaves == 4 || MaxWaves == 8, "waves");
-  if (nkv < 1 || nh % nkv != 0 || kv.block_size % 8 != 0 || total_len < 0 ||
-      (dph != 64 && dph != 128) || blockDim.x % 64 != 0)
+  if (nkv < 1 || nh % nkv != 0 || total_len < 0 || dph < 1 || dph > gen::kMaxDph ||
+      blockDim.x % 64 != 0)
     return SDE_ERR_UNSUPPORTED;
+  if (gen::needs_generic(dph, kv.block_size)) {
+    if (total_len == 0) {
+      for (int i = threadIdx.x; i < nh * dph; i += blockDim.x) attn_out[i] = 0.f;
+      __syncthreads();
+      return SDE_OK;
+    }
+    gen::GenArgs g;
+    g.pool = kv.pool;
+    g.table = kv.block_tables + (size_t)layer * kv.max_blocks_per_layer;
+    g.q = q_all;
+    g.out = attn_out;
+    g.partials = nullptr;
+    g.kv_dim = kv.kv_dim;
+    g.bs = kv.block_size;
+    g.nh = nh;
+    g.nkv = nkv;
+    g.dph = dph;
+    g.G = nh / nkv;
+    g.R = g.G;
+    g.pos_base = total_len - 1;  // one query seeing [0, total_len)
+    g.L_max = total_len;
+    g.n_parts = 1;
+    g.part_len = total_len;
+    g.qscale = (float)(kLog2e / __builtin_sqrt((double)dph));
+    static_assert(sizeof(gen::GenLds) <= sizeof(MfmaLds<128, MaxWaves>), "generic LDS fits");
+    auto& lds = *reinterpret_cast<gen::GenLds*>(device_lds<MaxWaves>());
+    const int nt = gen::gen_threads(blockDim.x);
+    if (nt == 256)
+      gen::gen_block_units<256>(g, lds);
+    else if (nt == 128)
+      gen::gen_block_units<128>(g, lds);
+    else
+      gen::gen_block_units<64>(g, lds);
+    return SDE_OK;
+  }
   const int G = nh / nkv;
   const int rows = device_rows(G);
   AttnArgs a;
@@ -1394,11 +1432,15 @@ __host__ __device__ inline size_t grid_attention_workspace_size(int nh, int nkv,
 // Blocks run 8 waves when MaxWaves is 8 and blockDim.x >= 512, else 4;
 // static LDS sizeof(attn::MfmaLds<128, MaxWaves>) (64 KiB by default),
 // shared with device_flash_attention_gqa.  Like it, the caller's kernel
-// should be declared __launch_bounds__(512) or smaller.  Returns the same
-// status in every thread: SDE_OK, SDE_ERR_UNSUPPORTED (dph not 64/128, block_size not a
-// multiple of 8, blockDim.x < 256, more than kGridCounters (KV head, row
-// group) pairs), SDE_ERR_INVALID_ARGUMENT, SDE_ERR_CAPACITY (window past
-// the layer's table) or SDE_ERR_WORKSPACE; nothing is written on error.
+// should be declared __launch_bounds__(512) or smaller.  Head sizes other
+// than 64 / 128 (up to 512) and block sizes that are not multiples of 8 run
+// the generic fp32 path on 256 threads of each block, with the same
+// workspace layout (items taken in turns, the last block of a (KV head,
+// group of 8 rows) merging its partitions).  Returns the same status in
+// every thread: SDE_OK, SDE_ERR_UNSUPPORTED (dph above 512, blockDim.x <
+// 256, more than kGridCounters (KV head, row group) pairs),
+// SDE_ERR_INVALID_ARGUMENT, SDE_ERR_CAPACITY (window past the layer's
+// table) or SDE_ERR_WORKSPACE; nothing is written on error.
 template <int MaxWaves = 4>
 __device__ __forceinline__ int device_flash_attention_gqa_grid(const float* q_all,
                                                                float* attn_out,
@@ -1423,7 +1465,7 @@ __device__ __forceinline__ int device_flash_attention_gqa_grid(const float* q_al
   n_queries = wave_uniform(n_queries);
   const sde_kv_view kv = uniform_view(kv_in);
   if (blockDim.x < 256 || blockDim.x % 64 != 0) return SDE_ERR_UNSUPPORTED;
-  if ((dph != 64 && dph != 128) || kv.block_size % 8 != 0) return SDE_ERR_UNSUPPORTED;
+  if (dph < 1 || dph > gen::kMaxDph) return SDE_ERR_UNSUPPORTED;
   if (nh < 1 || nkv < 1 || nh % nkv != 0 || nkv * dph != kv.kv_dim || layer < 0 ||
       layer >= kv.n_layers || pos_base < 0 || n_queries < 1 || !q_all || !attn_out || !workspace)
     return SDE_ERR_INVALID_ARGUMENT;
@@ -1431,6 +1473,41 @@ __device__ __forceinline__ int device_flash_attention_gqa_grid(const float* q_al
   if ((int64_t)L_max > (int64_t)kv.max_blocks_per_layer * kv.block_size) return SDE_ERR_CAPACITY;
   if (workspace_bytes < grid_attention_workspace_size(nh, nkv, dph, n_queries, L_max))
     return SDE_ERR_WORKSPACE;
+  if (gen::needs_generic(dph, kv.block_size)) {
+    gen::GenArgs g;
+    g.pool = kv.pool;
+    g.table = kv.block_tables + (size_t)layer * kv.max_blocks_per_layer;
+    g.q = q_all;
+    g.out = attn_out;
+    g.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + kGridCounterBytes);
+    g.kv_dim = kv.kv_dim;
+    g.bs = kv.block_size;
+    g.nh = nh;
+    g.nkv = nkv;
+    g.dph = dph;
+    g.G = nh / nkv;
+    g.R = n_queries * g.G;
+    g.pos_base = pos_base;
+    g.L_max = L_max;
+    // Partitions of 256 tokens or more, about one item per block, no more
+    // than the workspace holds (its bound: a partition per 4 tiles, at most
+    // kStreamMaxParts).
+    const int rgs = (g.R + gen::kGenRows - 1) / gen::kGenRows;
+    if ((int64_t)nkv * rgs > kGridCounters) return SDE_ERR_UNSUPPORTED;
+    const int n_blocks = gridDim.x * gridDim.y * gridDim.z;
+    int parts = n_blocks / (nkv * rgs);
+    const int by_len = (L_max + gen::kGenChunk - 1) / gen::kGenChunk;
+    if (parts > by_len) parts = by_len;
+    if (parts > attn::kStreamMaxParts) parts = attn::kStreamMaxParts;
+    if (parts < 1) parts = 1;
+    g.part_len = (L_max + parts - 1) / parts;
+    g.n_parts = (L_max + g.part_len - 1) / g.part_len;
+    g.qscale = (float)(attn::kLog2e / __builtin_sqrt((double)dph));
+    static_assert(sizeof(gen::GenLds) <= sizeof(MfmaLds<128, MaxWaves>), "generic LDS fits");
+    gen::gen_grid_items<256>(g, static_cast<uint32_t*>(workspace),
+                             *reinterpret_cast<gen::GenLds*>(device_lds<MaxWaves>()));
+    return SDE_OK;
+  }
 
   const int waves = (MaxWaves == 8 && blockDim.x >= 512) ? 8 : 4;
   const int G = nh / nkv;

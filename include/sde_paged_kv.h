@@ -473,7 +473,11 @@ int sde_model_free(sde_model* model);
  * verifies them, accepts the leading matches plus the target's next token
  * (sde::spec_accept_greedy) and rewinds seq_len to save + n_accepted + 1; the
  * next round starts at the device seq_len.  k = 0 is plain greedy decoding
- * through all layers (one token per round). */
+ * through all layers (one token per round).  Head sizes 64 / 128 with block
+ * sizes that are multiples of 8 run the grid attention's MFMA tile path;
+ * other head sizes (up to 512) and block sizes run its generic fp32 path
+ * (SDE_ERR_UNSUPPORTED above 512, or when n_heads * head_dim is not a
+ * multiple of 8). */
 typedef struct sde_loop_model {
   const float* emb_q;   /* [n_layers][vocab][n_heads*head_dim]                  */
   const float* emb_k;   /* [n_layers][vocab][kv_dim]                            */
@@ -482,7 +486,7 @@ typedef struct sde_loop_model {
   int32_t vocab;        /* a multiple of 8                                      */
   int32_t n_heads;
   int32_t n_kv_heads;
-  int32_t head_dim;     /* 64 or 128; n_kv_heads*head_dim == the cache's kv_dim */
+  int32_t head_dim;     /* up to 512; n_kv_heads*head_dim == the cache's kv_dim */
 } sde_loop_model;
 
 /* Workspace bytes of sde_spec_loop_greedy and sde_spec_loop_stochastic for

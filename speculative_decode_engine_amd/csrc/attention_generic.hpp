@@ -8,25 +8,12 @@
 #include <cstddef>
 #include <cstdint>
 
+#include "sde/attention_generic_device.hpp"
+
 namespace sde {
 namespace gen {
 
-constexpr int kMaxDph = 512;   // head_dim limit of the generic kernel (LDS for q)
-
-// The generic path serves every (dph, block size) the tile kernels do not.
-inline bool needs_generic(int dph, int block_size) {
-  return !(dph == 64 || dph == 128) || block_size % 8 != 0;
-}
-
-// Rotate-half RoPE of the fused entry point: inv_freq[j] for j < dph / 2
-// (theta already NTK-scaled, computed on the host in double precision and
-// rounded to fp32) and the linear / YaRN position divisor.
-struct GenRope {
-  const float* k_new;  // [M][kv_dim] fp32, before RoPE
-  const float* v_new;  // [M][kv_dim] fp32
-  float pos_div;
-  float inv_freq[kMaxDph / 2];
-};
+// (kMaxDph, needs_generic and GenRope come from sde/attention_generic_device.hpp.)
 
 struct GenPlan {
   int row_groups;

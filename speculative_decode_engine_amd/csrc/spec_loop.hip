@@ -772,8 +772,11 @@ int check_model(const sde_kv_cache* cache, const sde_loop_model* model) {
   if (m.n_heads < 1 || m.n_kv_heads < 1 || m.n_heads % m.n_kv_heads != 0 ||
       m.n_kv_heads * m.head_dim != cache->cfg.kv_dim || m.vocab < 8)
     return SDE_ERR_INVALID_ARGUMENT;
-  if (m.head_dim != 64 && m.head_dim != 128) return SDE_ERR_UNSUPPORTED;
-  if (cache->cfg.block_size % 8 != 0 || m.vocab % 8 != 0 ||
+  // Head sizes 64 / 128 with block sizes that are multiples of 8 run the
+  // tile path of the grid attention, the others (head_dim up to 512) its
+  // generic path; the packed head needs n_heads * head_dim and the
+  // vocabulary to be multiples of 8.
+  if (m.head_dim > sde::gen::kMaxDph || (m.n_heads * m.head_dim) % 8 != 0 || m.vocab % 8 != 0 ||
       (reinterpret_cast<uintptr_t>(m.head) & 15u) != 0)
     return SDE_ERR_UNSUPPORTED;
   return SDE_OK;

@@ -63,6 +63,13 @@ def device_attention(dev, cache, q, nh, nkv, dph, pos_base, threads=256, attn_ty
     (32, 8, 128, 16, 4096, 5),    # Llama-3-8B verify window
     (28, 4, 128, 32, 1000, 9),    # Qwen2.5-7B (G = 7), block size 32
     (8, 8, 128, 8, 77, 2),        # MHA, block size 8, ragged last tile
+    # the generic fp32 path: other head sizes and block sizes
+    (8, 2, 96, 16, 300, 1),       # head size 96
+    (16, 4, 256, 12, 500, 3),     # head size 256 (Gemma), block size 12
+    (4, 1, 80, 10, 1000, 2),      # head size 80, block size 10
+    (8, 2, 512, 16, 200, 1),      # the largest head size
+    (4, 4, 32, 5, 77, 1),         # head size 32, block size 5
+    (32, 8, 64, 12, 600, 5),      # head size 64 with block size 12
 ])
 def test_device_attention_matches_oracle(dev, oracle, nh, nkv, dph, bs, ctx, M):
     case_banner("device attention", nh, nkv, dph, bs, ctx, M)
@@ -81,9 +88,12 @@ def test_device_attention_matches_oracle(dev, oracle, nh, nkv, dph, bs, ctx, M):
 
 
 @pytest.mark.parametrize("threads", [64, 192, 256, 512])
-def test_device_attention_any_block_size(dev, oracle, threads):
-    case_banner("device attention threads", threads)
-    nh, nkv, dph, ctx = 32, 8, 128, 700
+@pytest.mark.parametrize("dph", [128, 96])
+def test_device_attention_any_block_size(dev, oracle, threads, dph):
+    """Any multiple of 64 threads: the tile path spreads over the block's
+    waves; the generic path (head size 96) uses 64, 128 or 256 threads."""
+    case_banner("device attention threads", threads, dph)
+    nh, nkv, ctx = 32, 8, 700
     cache, K, V, rng = build_layer(nh, nkv, dph, 16, ctx, 1, 80, threads)
     q = W.queries(rng, 1, nh, dph)
     out, status = device_attention(dev, cache, torch.from_numpy(q).cuda(), nh, nkv, dph, ctx,
@@ -333,6 +343,13 @@ def grid_attention(dev, cache, q, nh, nkv, dph, pos_base, blocks, threads, ws, l
     (32, 8, 128, 16, 4096, 5, 256, 512, 8),    # 4K verify window, 8-wave: 8-row groups, 2 tiles
     (4, 2, 64, 16, 40, 1, 256, 512, 8),        # G = 2 decode, 8-wave: 2-row groups, 1 tile
     (32, 8, 128, 16, 17000, 5, 256, 512, 8),   # window past 16K, 8-wave: 16-row groups
+    # the generic fp32 path (other head sizes, block sizes not a multiple of 8)
+    (8, 2, 96, 16, 3000, 3, 256, 512, 4),      # head size 96, 8-row groups, partitions
+    (16, 4, 256, 12, 2000, 5, 64, 512, 8),     # head size 256, block size 12, few blocks
+    (4, 1, 80, 10, 700, 1, 300, 256, 4),       # head size 80, more blocks than items
+    (32, 8, 256, 16, 4096, 5, 256, 512, 8),    # Gemma-like verify window
+    (28, 4, 64, 12, 1500, 9, 256, 512, 4),     # head size 64 with block size 12
+    (8, 2, 512, 16, 900, 2, 40, 256, 4),       # the largest head size
 ])
 def test_grid_attention_matches_oracle_and_host_entry(dev, oracle, nh, nkv, dph, bs, ctx, M,
                                                       blocks, threads, max_waves):
@@ -402,6 +419,9 @@ def test_grid_attention_errors_write_nothing(dev):
     assert (status == N.SDE_ERR_UNSUPPORTED).all() and torch.isnan(out).all()
     out, status = grid_attention(dev, cache, q, nh, nkv, dph, ctx + 5000, 16, 512, ws)
     assert (status == N.SDE_ERR_CAPACITY).all() and torch.isnan(out).all()
+    big = torch.zeros(1, 600, device="cuda")   # head size above 512
+    out, status = grid_attention(dev, cache, big, 1, 1, 600, ctx, 16, 512, ws)
+    assert (status == N.SDE_ERR_UNSUPPORTED).all() and torch.isnan(out).all()
     cache.free()
 
 

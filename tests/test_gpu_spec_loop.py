@@ -83,6 +83,7 @@ CASES = [
     (7, (3, 8, 2, 64, 512), 300, 15, 1),      # the largest window: the head in two passes of 8
     (8, (2, 8, 2, 128, 256), 100, 9, 1),      # 10 rows: two passes of 5
     (11, (2, 8, 2, 64, 4096), 120, 4, 1),     # vocab 4096: 16-column head panels into the argmax
+    (13, (3, 4, 2, 96, 256), 300, 3, 1),      # head size 96: the grid attention's generic path
 ]
 
 
