@@ -627,23 +627,26 @@ def bench_spec_loop(torch, max_new=64):
     model = SpecLoopModel(mk(base_q), mk(base_k), mk(base_v),
                           (torch.randn(nh * dph, V, device="cuda", generator=g) /
                            math.sqrt(nh * dph)).half(), nh, nkv, dph)
+    # the same model cut to its first two layers (the per-layer cost below)
+    model2 = SpecLoopModel(model.emb_q[:2].contiguous(), model.emb_k[:2].contiguous(),
+                           model.emb_v[:2].contiguous(), model.head, nh, nkv, dph)
     out = {}
 
-    def run(name, k, n_new):
+    def run(name, k, n_new, m=model):
+        nl = m.n_layers
         nblk = -(-(P0 + n_new + k + 1) // 16)
-        cache = KVCache(L, nkv * dph, nblk, 16, L * nblk)
+        cache = KVCache(nl, nkv * dph, nblk, 16, nl * nblk)
         toks = torch.randint(0, V, (P0,), device="cuda", generator=g)
-        for l in range(L):
-            cache.append(l, model.emb_k[l][toks].contiguous(), model.emb_v[l][toks].contiguous(),
-                         0)
+        for l in range(nl):
+            cache.append(l, m.emb_k[l][toks].contiguous(), m.emb_v[l][toks].contiguous(), 0)
         cache.set_seq_len(P0)
         torch.cuda.synchronize()
         t = time.perf_counter()
         if name.startswith("sampling"):
-            res = spec_loop_stochastic(cache, model, 7, k, 1 if k else 0, n_new, seed=5,
+            res = spec_loop_stochastic(cache, m, 7, k, 1 if k else 0, n_new, seed=5,
                                        draft_temp=1.0, adaptive=True)
         else:
-            res = spec_loop_greedy(cache, model, 7, k, 1 if k else 0, n_new)
+            res = spec_loop_greedy(cache, m, 7, k, 1 if k else 0, n_new)
         dt = time.perf_counter() - t
         cache.free()
         return res, dt
@@ -658,6 +661,12 @@ def bench_spec_loop(torch, max_new=64):
                             accepted=sum(res.accepted), status=res.status,
                             us_per_round=round(dt / max(res.rounds, 1) * 1e6, 1),
                             us_per_token=round(dt / max(len(res.tokens), 1) * 1e6, 1))
+    # Per layer of a greedy k = 0 round: the 4-layer round minus the 2-layer
+    # round of the same model, halved (one layer's append + q phase, its grid
+    # attention phase and their two grid barriers), best of 3 each.
+    t4 = min(run("k0", 0, max_new)[1] for _ in range(3))
+    t2 = min(run("k0", 0, max_new, model2)[1] for _ in range(3))
+    out["k0_per_layer_us"] = round((t4 - t2) / max_new / 2 * 1e6, 1)
     out["shape"] = dict(layers=L, nh=nh, nkv=nkv, dph=dph, vocab=V, context=P0,
                         n_draft=1, note="wall time of one launch incl. launch and sync")
     return out
@@ -777,6 +786,10 @@ def main():
         extra["grid_device_fn"] = bench_grid_device_fn(torch, W, steps, warmup)
         log("[bench] grid device fn", json.dumps(extra["grid_device_fn"]))
         extra["spec_loop"] = bench_spec_loop(torch)
+        # a loop layer (same heads, 4K context, one query) against the
+        # library's decode step (append + attention launches, graph-replayed)
+        extra["spec_loop"]["k0_per_layer_over_decode_step"] = round(
+            extra["spec_loop"]["k0_per_layer_us"] / configs["llama3_8b_4k_decode"]["us_per_layer_step"], 3)
         log("[bench] spec loop", json.dumps(extra["spec_loop"]))
         for k_, v_ in configs.items():
             log(f"[bench] {k_}: {v_['us_per_layer_step']} us/layer-step, {v_['gbps']} GB/s")

@@ -226,10 +226,23 @@ __device__ __forceinline__ float packed_wave_sum(float v) {
 // wave (ping-pong registers, no loop-carried copies); each lane accumulates
 // its 8 columns over its rows, the wave sums its lanes, and the 8 waves'
 // sums are added in wave order through LDS.  Deterministic.
-template <int MB, int LPR, int JR>
-__device__ __forceinline__ void packed_item(const PackedArgs& a, int panel, int pass) {
+// ext_red: when not null, the waves' sums go through this caller-provided
+// LDS (at least MB * kWaves * 8 * LPR floats) instead of the function's own
+// array (one per instantiation): a kernel running several row counts can
+// give them one array.
+template <int MB, int LPR, int JR, bool EXT_RED = false>
+__device__ __forceinline__ void packed_item(const PackedArgs& a, int panel, int pass,
+                                            float* ext_red = nullptr) {
   constexpr int PW = 8 * LPR;
-  __shared__ float red[MB][kWaves][PW];
+  using Red = float[MB][kWaves][PW];
+  Red* red_p;
+  if constexpr (EXT_RED) {
+    red_p = reinterpret_cast<Red*>(ext_red);
+  } else {
+    __shared__ float own[MB][kWaves][PW];
+    red_p = &own;
+  }
+  Red& red = *red_p;
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int lane = threadIdx.x & 63;
   const int m0 = pass * a.pass_rows;

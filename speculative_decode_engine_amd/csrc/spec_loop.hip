@@ -444,6 +444,13 @@ __device__ __forceinline__ void reduce_candidates(const LoopArgs& a, int n, int 
   }
 }
 
+// The head's cross-wave sums: one LDS array for every row count (9 rows,
+// 8 waves, 16-column panels) instead of one per instantiation.
+__device__ __forceinline__ float* head_red() {
+  __shared__ float buf[9 * mvp::kWaves * 16];
+  return buf;
+}
+
 template <int MB, int LPR>
 __device__ __forceinline__ void head_items(const LoopArgs& a, const mvp::PackedArgs& pa,
                                            int panels, int passes, HeadArgmax am) {
@@ -454,7 +461,8 @@ __device__ __forceinline__ void head_items(const LoopArgs& a, const mvp::PackedA
   const int items = panels * passes;
   for (int it = blk; it < items; it += nblk) {
     const int panel = it % panels, pass = it / panels;
-    mvp::packed_item<MB, LPR, (MB == 1 ? 8 : 4)>(pa, panel, pass);
+    static_assert(MB <= 9 && LPR <= 2, "head_red holds 9 rows of 16-column panels");
+    mvp::packed_item<MB, LPR, (MB == 1 ? 8 : 4), true>(pa, panel, pass, head_red());
     __syncthreads();  // the item's logits are written; its LDS sums are read
     if (am.dst >= 0) {
       panel_candidates<PW>(a, pa, panel, pass, panels);
