@@ -199,6 +199,20 @@ struct RopeArgs {
   float inv_freq[64];  // dph/2 entries
 };
 
+// A persistent loop's window taken straight from its model's tables (the
+// gathered form of the grid attention): q row m is q_table row tok[m], plus
+// q_add row m when q_add is set (the previous layer's output); the window's
+// K / V rows (positions pos_base + m) are k_table / v_table rows tok[m],
+// rounded to fp16 and appended by the partitions that read them.
+struct GatherArgs {
+  const int32_t* tok;     // [M] the window's tokens
+  const float* q_table;   // [vocab][nh*dph] (the layer's)
+  const float* q_add;     // [M][nh*dph], or null
+  const float* k_table;   // [vocab][kv_dim] (the layer's)
+  const float* v_table;   // [vocab][kv_dim]
+  uint16_t* pool;         // the pool (written)
+};
+
 __device__ __forceinline__ float rope_angle(const RopeArgs& rp, int pos, int j) {
   return ((float)pos / rp.pos_div) * rp.inv_freq[j];
 }
@@ -877,17 +891,45 @@ struct MfmaLds {
   }
 };
 
+// The window's K / V rows of KV head kvh from the gathered tables, rounded
+// to fp16 (RNE, as kv_cache_append) into the pool by the whole workgroup;
+// returns once the stores are visible to the workgroup's loads.
+template <int DPH>
+__device__ __forceinline__ void gather_append_slice(const AttnArgs& a, const GatherArgs& g,
+                                                    int kvh) {
+  const int M = a.R / a.G;
+  const int kvd = a.src.kv_dim;
+  const int bs = a.src.bs;
+  for (int t = item_tid(); t < M * DPH; t += blockDim.x) {
+    const int m = t / DPH;
+    const int d = t - m * DPH;
+    const int pos = a.pos_base + m;
+    const int lb = pos / bs;
+    const int slot = pos - lb * bs;
+    const size_t src = (size_t)g.tok[m] * kvd + (size_t)kvh * DPH + d;
+    uint16_t* kd = g.pool + ((size_t)(uint32_t)a.src.table[lb] * 2u * bs + slot) * kvd +
+                   (size_t)kvh * DPH + d;
+    kd[0] = __builtin_bit_cast(uint16_t, (_Float16)g.k_table[src]);
+    kd[(size_t)bs * kvd] = __builtin_bit_cast(uint16_t, (_Float16)g.v_table[src]);
+  }
+  __syncthreads();
+}
+
 // Partition `part` of (KV head kvh, row group rg) on the calling workgroup:
 // waves 0..nwaves-1 (nwaves <= WAVES) take tiles tb+w, tb+w+nwaves, ...
 // (further waves idle), merge their states through LDS, and either write
 // the normalised output (one partition) or publish a partial and count the
 // arrival; the last arrival combines all partitions (with WAVES waves).
 // Every thread of the workgroup calls it.
-template <int DPH, int RPW, int CHUNK, int WAVES, bool ROPE = false, class Lds>
+// GATHER: the window comes from `ga` (GatherArgs) instead of a.q and
+// earlier appends.
+template <int DPH, int RPW, int CHUNK, int WAVES, bool ROPE = false, class Lds,
+          bool GATHER = false>
 __device__ __forceinline__ void stream_item(const AttnArgs& a, int part, int kvh, int rg,
                                             Lds& lds, int nwaves = WAVES,
                                             const RopeArgs* rp = nullptr,
-                                            float2* rope_cs = nullptr) {
+                                            float2* rope_cs = nullptr,
+                                            const GatherArgs* ga = nullptr) {
   static_assert(DPH == 64 || DPH == 128, "head_dim");
   static_assert(RPW == 2 || RPW == 4 || RPW == 8 || RPW == 16, "rows per group");
   using Mh = MfmaShape<DPH>;
@@ -911,6 +953,10 @@ __device__ __forceinline__ void stream_item(const AttnArgs& a, int part, int kvh
     // bytes.
     if (te * kTile > a.pos_base) rope_append_slice<DPH>(a, *rp, rope_cs, kvh);
   }
+  if constexpr (GATHER) {
+    // (as above: a partition reading window positions writes them first)
+    if (te * kTile > a.pos_base) gather_append_slice<DPH>(a, *ga, kvh);
+  }
 
   if (wave < nwaves) {
     // Lane l serves row r0 + l%16 (rows past nrows are padding: zero q,
@@ -920,13 +966,31 @@ __device__ __forceinline__ void stream_item(const AttnArgs& a, int part, int kvh
     const int gr = min(r0 + l16, a.R - 1);
     const int m = gr / a.G;
     const int h = kvh * a.G + (gr - m * a.G);
-    const float2* qp = reinterpret_cast<const float2*>(a.q + (size_t)m * a.nh * DPH +
-                                                       (size_t)h * DPH + 8 * grp);
+    const float* qrow;
+    if constexpr (GATHER)
+      qrow = ga->q_table + (size_t)ga->tok[m] * a.nh * DPH;
+    else
+      qrow = a.q + (size_t)m * a.nh * DPH;
+    const float2* qp = reinterpret_cast<const float2*>(qrow + (size_t)h * DPH + 8 * grp);
     float2 qr[Mh::KS][4];
 #pragma unroll
     for (int ks = 0; ks < Mh::KS; ks++)
 #pragma unroll
       for (int w = 0; w < 4; w++) qr[ks][w] = qp[16 * ks + w];
+    if constexpr (GATHER) {
+      if (ga->q_add) {  // the residual, added in fp32 as the window's q rows are built
+        const float2* ap = reinterpret_cast<const float2*>(ga->q_add + (size_t)m * a.nh * DPH +
+                                                           (size_t)h * DPH + 8 * grp);
+#pragma unroll
+        for (int ks = 0; ks < Mh::KS; ks++)
+#pragma unroll
+          for (int w = 0; w < 4; w++) {
+            const float2 r = ap[16 * ks + w];
+            qr[ks][w].x += r.x;
+            qr[ks][w].y += r.y;
+          }
+      }
+    }
     const float2* cs = nullptr;
     if constexpr (ROPE) cs = rope_cs + m * (DPH / 2);
     const int lim = real ? a.pos_base + (r0 + l16) / a.G : -1;
@@ -1131,8 +1195,8 @@ __device__ __forceinline__ void block_units(const AttnArgs& a, int nwaves) {
 // workgroup order (with four tiles per wave or more the KV head fastest:
 // blocks that run together read the adjacent KV-head slices of the same
 // token rows).
-template <int DPH, int RPW, int CHUNK, int WAVES, int MaxWaves>
-__device__ __forceinline__ void grid_items(const AttnArgs& a) {
+template <int DPH, int RPW, int CHUNK, int WAVES, int MaxWaves, bool GATHER = false>
+__device__ __forceinline__ void grid_items(const AttnArgs& a, const GatherArgs* ga = nullptr) {
   auto& lds = *reinterpret_cast<MfmaLds<DPH, MaxWaves>*>(device_lds<MaxWaves>());
   const int n_blocks = gridDim.x * gridDim.y * gridDim.z;
   const int block = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
@@ -1149,19 +1213,21 @@ __device__ __forceinline__ void grid_items(const AttnArgs& a) {
       kvh = unit % a.nkv;
       rg = unit / a.nkv;
     }
-    stream_item<DPH, RPW, CHUNK, WAVES>(a, part, kvh, rg, lds);
+    stream_item<DPH, RPW, CHUNK, WAVES, false, MfmaLds<DPH, MaxWaves>, GATHER>(
+        a, part, kvh, rg, lds, WAVES, nullptr, nullptr, ga);
     if (it + n_blocks < items) __syncthreads();  // this item's readers of lds are done
   }
 }
 
 // 4-wave blocks: rows per group 4 or 16, two tiles per wave in flight (on
 // the MaxWaves-sized staging).
-template <int DPH, int MaxWaves>
-__device__ __forceinline__ void grid_dispatch4(const AttnArgs& a, int rpw) {
+template <int DPH, int MaxWaves, bool GATHER = false>
+__device__ __forceinline__ void grid_dispatch4(const AttnArgs& a, int rpw,
+                                               const GatherArgs* ga = nullptr) {
   if (rpw == 4)
-    grid_items<DPH, 4, 2, 4, MaxWaves>(a);
+    grid_items<DPH, 4, 2, 4, MaxWaves, GATHER>(a, ga);
   else
-    grid_items<DPH, 16, 2, 4, MaxWaves>(a);
+    grid_items<DPH, 16, 2, 4, MaxWaves, GATHER>(a, ga);
 }
 
 // 8-wave blocks: the plans of libsde_paged's kernel (2-16 rows per group,
@@ -1548,6 +1614,80 @@ __device__ __forceinline__ int device_flash_attention_gqa_grid(const float* q_al
     attn::grid_dispatch4<128, MaxWaves>(a, p.rpw);
   else
     attn::grid_dispatch4<64, MaxWaves>(a, p.rpw);
+  __syncthreads();
+  return SDE_OK;
+}
+
+// device_flash_attention_gqa_grid's 4-wave tile path over a gathered window
+// (attn::GatherArgs: a persistent loop whose model builds q rows and K / V
+// rows from per-token tables): no q buffer and no append phase, so the loop
+// needs no grid barrier between building the window and attending to it.
+// The same plans, workspace and results (bit for bit: the same q sums and
+// fp16 roundings) as building q, appending and calling
+// device_flash_attention_gqa_grid<4>.  Head sizes 64 / 128 with block sizes
+// that are multiples of 8 only (SDE_ERR_UNSUPPORTED otherwise: the caller
+// keeps the separate phases for the generic path); other errors as the grid
+// function's.
+__device__ __forceinline__ int device_attention_grid_gathered(const attn::GatherArgs& g_in,
+                                                              float* attn_out,
+                                                              const sde_kv_view& kv_in, int layer,
+                                                              int nh, int nkv, int dph,
+                                                              int pos_base, int n_queries,
+                                                              void* workspace,
+                                                              size_t workspace_bytes) {
+  using namespace attn;
+  GatherArgs g;
+  g.tok = wave_uniform(g_in.tok);
+  g.q_table = wave_uniform(g_in.q_table);
+  g.q_add = wave_uniform(g_in.q_add);
+  g.k_table = wave_uniform(g_in.k_table);
+  g.v_table = wave_uniform(g_in.v_table);
+  g.pool = wave_uniform(g_in.pool);
+  attn_out = wave_uniform(attn_out);
+  workspace = wave_uniform(workspace);
+  workspace_bytes = wave_uniform(workspace_bytes);
+  layer = wave_uniform(layer);
+  nh = wave_uniform(nh);
+  nkv = wave_uniform(nkv);
+  dph = wave_uniform(dph);
+  pos_base = wave_uniform(pos_base);
+  n_queries = wave_uniform(n_queries);
+  const sde_kv_view kv = uniform_view(kv_in);
+  if (blockDim.x < 256 || blockDim.x % 64 != 0 || gen::needs_generic(dph, kv.block_size))
+    return SDE_ERR_UNSUPPORTED;
+  if (nh < 1 || nkv < 1 || nh % nkv != 0 || nkv * dph != kv.kv_dim || layer < 0 ||
+      layer >= kv.n_layers || pos_base < 0 || n_queries < 1 || !g.tok || !g.q_table ||
+      !g.k_table || !g.v_table || !g.pool || !attn_out || !workspace)
+    return SDE_ERR_INVALID_ARGUMENT;
+  const int L_max = pos_base + n_queries;
+  if ((int64_t)L_max > (int64_t)kv.max_blocks_per_layer * kv.block_size) return SDE_ERR_CAPACITY;
+  if (workspace_bytes < grid_attention_workspace_size(nh, nkv, dph, n_queries, L_max))
+    return SDE_ERR_WORKSPACE;
+  const int G = nh / nkv;
+  const int R = n_queries * G;
+  const int n_blocks = gridDim.x * gridDim.y * gridDim.z;
+  const StreamPlan p = stream_plan(L_max, nkv, R, n_blocks, 4, 2, device_rows(R));
+  if ((int64_t)nkv * p.row_groups > kGridCounters) return SDE_ERR_UNSUPPORTED;
+  AttnArgs a;
+  a.src = TileSource{kv.pool, kv.block_tables + (size_t)layer * kv.max_blocks_per_layer,
+                     kv.kv_dim, kv.block_size, L_max};
+  a.q = nullptr;
+  a.out = attn_out;
+  a.counters = static_cast<uint32_t*>(workspace);
+  a.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + kGridCounterBytes);
+  a.nh = nh;
+  a.nkv = nkv;
+  a.G = G;
+  a.R = R;
+  a.row_groups = p.row_groups;
+  a.pos_base = pos_base;
+  a.n_parts = p.n_parts;
+  a.tiles_per_part = p.tiles_per_part;
+  a.qscale = (float)(kLog2e / __builtin_sqrt((double)dph));
+  if (dph == 128)
+    attn::grid_dispatch4<128, 4, true>(a, p.rpw, &g);
+  else
+    attn::grid_dispatch4<64, 4, true>(a, p.rpw, &g);
   __syncthreads();
   return SDE_OK;
 }

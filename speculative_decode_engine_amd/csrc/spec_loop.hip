@@ -91,8 +91,10 @@ struct LoopArgs {
   int32_t* state;
   int32_t* emitted;   // [max_new + k]
   int32_t* accepted;  // [max_new], per round
-  float* q_buf;       // [k+1][d]
-  float* h_buf;       // [k+1][d]
+  float* q_buf;       // [k+1][d] (the separate q phase of the generic shapes)
+  float* h_buf;       // two [k+1][d] halves: layer l's attention output in half l % 2
+  size_t h_half;      // floats per half
+  int fused;          // the attention builds the window itself (tile-path shapes)
   float* logits;      // [k+1][vocab]
   int32_t* tokens;    // [2(k+1) + 2]: window tokens, the target's tokens, kCatchUp, kDone
   void* attn_ws;
@@ -142,7 +144,7 @@ inline Layout layout(const Shape& t, const Shape* d, int vocab, int k) {
   l.attn = 0;
   l.q = align256(ws);
   l.h = l.q + align256(M * dmax * sizeof(float));
-  l.logits = l.h + align256(M * dmax * sizeof(float));
+  l.logits = l.h + align256(2 * M * dmax * sizeof(float));
   l.tokens = l.logits + align256((size_t)M * vocab * sizeof(float));
   l.bar = l.tokens + align256((2 * M + 2) * sizeof(int32_t));
   l.dlogits = l.bar + align256(kBarBytes);
@@ -275,6 +277,12 @@ __device__ __forceinline__ void note_error(const LoopArgs& a, int st) {
     atomicCAS(reinterpret_cast<int*>(a.state + kStatus), SDE_OK, st);
 }
 
+// Layer l's attention output rows (layer l - 1's are layer l's residual:
+// two halves, so a layer's attention never writes what its q rows read).
+__device__ __forceinline__ float* hbuf(const LoopArgs& a, int l) {
+  return a.h_buf + (size_t)(l & 1) * a.h_half;
+}
+
 // q rows [r0, r0+n) of layer l of model s: the token's embedding, plus the
 // previous layer's attention output of the row (residual), by the whole grid.
 __device__ void build_q(const LoopArgs& a, const Side& s, int l, int r0, int n, bool residual) {
@@ -285,7 +293,7 @@ __device__ void build_q(const LoopArgs& a, const Side& s, int l, int r0, int n, 
     const int m = r0 + i / d, e = i - (i / d) * d;
     const int tok = a.tokens[m];
     float x = s.m.emb_q[((size_t)l * V + tok) * d + e];
-    if (residual) x += a.h_buf[(size_t)m * d + e];
+    if (residual) x += hbuf(a, l - 1)[(size_t)m * d + e];
     a.q_buf[(size_t)m * d + e] = x;
   }
 }
@@ -333,22 +341,42 @@ __device__ void catch_up(const LoopArgs& a, int pos) {
 // pos0 + row, as a function of its own: its tile loop gets the whole register
 // budget instead of sharing it with the values the loops around it keep.
 // 4-wave staging (64 KiB of LDS): the 8-wave form is off in the loop (see
-// the design notes on the loop's attention).
+// the design notes on the loop's attention).  Tile-path shapes take the
+// window straight from the model's tables (device_attention_grid_gathered:
+// q rows, residual and the window's K / V appends inside the attention);
+// the generic shapes attend to the q rows and appends of the phase before.
 __device__ __attribute__((noinline)) int layer_attention(const LoopArgs& a, const Side& s, int l,
                                                          int r0, int n, int pos0) {
+  float* out = hbuf(a, l) + (size_t)r0 * s.d;
+  if (a.fused) {
+    const size_t V = (size_t)s.m.vocab;
+    attn::GatherArgs g;
+    g.tok = a.tokens + r0;
+    g.q_table = s.m.emb_q + (size_t)l * V * s.d;
+    g.q_add = l > 0 ? hbuf(a, l - 1) + (size_t)r0 * s.d : nullptr;
+    g.k_table = s.m.emb_k + (size_t)l * V * s.kv.kv_dim;
+    g.v_table = s.m.emb_v + (size_t)l * V * s.kv.kv_dim;
+    g.pool = s.kv.pool;
+    return device_attention_grid_gathered(g, out, s.kv, l, s.m.n_heads, s.m.n_kv_heads,
+                                          s.m.head_dim, pos0 + r0, n, a.attn_ws,
+                                          a.attn_ws_bytes);
+  }
   return device_flash_attention_gqa_grid<4>(
-      a.q_buf + (size_t)r0 * s.d, a.h_buf + (size_t)r0 * s.d, s.kv, l, s.m.n_heads,
-      s.m.n_kv_heads, s.m.head_dim, pos0 + r0, n, a.attn_ws, a.attn_ws_bytes);
+      a.q_buf + (size_t)r0 * s.d, out, s.kv, l, s.m.n_heads, s.m.n_kv_heads, s.m.head_dim,
+      pos0 + r0, n, a.attn_ws, a.attn_ws_bytes);
 }
 
 // Layers [lo, hi) of model s on window rows [r0, r0+n) at positions pos0 +
-// row: append, q, grid attention; h_buf rows hold the last layer's output.
+// row: (append, q, grid barrier,) grid attention, grid barrier; layer hi-1's
+// output rows are then in hbuf(a, hi - 1).
 __device__ __forceinline__ void run_layers(const LoopArgs& a, const Side& s, int lo, int hi,
                                            int r0, int n, int pos0) {
   for (int l = lo; l < hi; l++) {
-    append_rows(a, s, l, r0, n, pos0);
-    build_q(a, s, l, r0, n, l > 0);
-    barrier(a);
+    if (!a.fused) {
+      append_rows(a, s, l, r0, n, pos0);
+      build_q(a, s, l, r0, n, l > 0);
+      barrier(a);
+    }
     note_error(a, layer_attention(a, s, l, r0, n, pos0));
     barrier(a);
   }
@@ -498,14 +526,15 @@ __device__ __forceinline__ void head_rows(const LoopArgs& a, const mvp::PackedAr
   }
 }
 
-__device__ __attribute__((noinline)) void head_logits(const LoopArgs& a, const Side& s, int r0,
-                                                      int n, float* logits, int argmax_dst) {
+__device__ __attribute__((noinline)) void head_logits(const LoopArgs& a, const Side& s, int layer,
+                                                      int r0, int n, float* logits,
+                                                      int argmax_dst) {
   const int d = wave_uniform(s.d), V = wave_uniform(s.m.vocab);
   n = wave_uniform(n);
   const mvp::PackedShape sh = mvp::packed_shape(d, V);
   mvp::PackedArgs pa;
   pa.W = wave_uniform(s.head_packed);
-  pa.x = wave_uniform(a.h_buf + (size_t)wave_uniform(r0) * d);
+  pa.x = wave_uniform(hbuf(a, wave_uniform(layer)) + (size_t)wave_uniform(r0) * d);
   pa.out = wave_uniform(logits);
   pa.d_in = d;
   pa.d_out = V;
@@ -523,8 +552,9 @@ __device__ __attribute__((noinline)) void head_logits(const LoopArgs& a, const S
 
 // Logits of window rows [r0, r0+n) from their h_buf rows (model s's head),
 // then their argmaxes into tokens[dst + row].
-__device__ __forceinline__ void decide(const LoopArgs& a, const Side& s, int r0, int n, int dst) {
-  head_logits(a, s, r0, n, a.logits, dst);
+__device__ __forceinline__ void decide(const LoopArgs& a, const Side& s, int layer, int r0, int n,
+                                       int dst) {
+  head_logits(a, s, layer, r0, n, a.logits, dst);
   barrier(a);
 }
 
@@ -612,10 +642,10 @@ __global__ __launch_bounds__(kThreads) void spec_loop_kernel(LoopArgs a) {
       // layers, the whole window at P; the target's token for every row.
       for (int s = 0; s < a.k; s++) {
         run_layers(a, a.dr, 0, a.dr.kv.n_layers, s, 1, D);
-        decide(a, a.dr, s, 1, s + 1);
+        decide(a, a.dr, a.dr.kv.n_layers - 1, s, 1, s + 1);
       }
       run_layers(a, a.t, 0, n_layers, 0, M, P);
-      decide(a, a.t, 0, M, M);
+      decide(a, a.t, n_layers - 1, 0, M, M);
     } else {
       // Draft (kernels.cu:2960-3006), steps 0..k when k > 0: the prefix
       // layers for window token s at P+s, one token at a time; the first k
@@ -626,7 +656,7 @@ __global__ __launch_bounds__(kThreads) void spec_loop_kernel(LoopArgs a) {
       for (int s = 0; s < n_steps; s++) {
         const Step t = round_step(a, s, n_steps, n_layers);
         run_layers(a, a.t, t.lo, t.hi, t.r0, t.n, P);
-        if (t.verify || s < a.k) decide(a, a.t, t.r0, t.n, t.verify ? M : s + 1);
+        if (t.verify || s < a.k) decide(a, a.t, t.hi - 1, t.r0, t.n, t.verify ? M : s + 1);
       }
     }
     // Greedy accept and O(1) rewinds (kernels.cu:3050-3076).
@@ -711,7 +741,7 @@ __global__ __launch_bounds__(kThreads) void spec_loop_stochastic_kernel(LoopArgs
       run_layers(a, sd, t.lo, t.hi, t.r0, t.n, t.verify ? P : (a.two ? D : P));
       if (!t.verify && s >= a.k) continue;
       float* lg = t.verify ? a.logits : a.dlogits + (size_t)s * V;
-      head_logits(a, sd, t.r0, t.n, lg, -1);
+      head_logits(a, sd, t.hi - 1, t.r0, t.n, lg, -1);
       barrier(a);
       if (t.verify) break;
       int st = device_spec_accept_stochastic_grid(lg, nullptr, nullptr, 0, V, temp, 1.f, a.smp.seed,
@@ -917,6 +947,12 @@ int launch_loop(sde_kv_cache* cache, const sde_loop_model* model, const sde_spec
   a.cand = reinterpret_cast<uint2*>(ws + lay.cand + 256);
   a.q_buf = reinterpret_cast<float*>(ws + lay.q);
   a.h_buf = reinterpret_cast<float*>(ws + lay.h);
+  a.h_half = (size_t)(c.k + 1) * (size_t)(two ? (a.t.d > a.dr.d ? a.t.d : a.dr.d) : a.t.d);
+  // The gathered attention serves the tile-path shapes; every side must
+  // have one (the loop's phases are uniform over the grid).
+  a.fused = !sde::gen::needs_generic(m.head_dim, cache->cfg.block_size) &&
+            (!two || !sde::gen::needs_generic(c.draft_model->head_dim,
+                                              c.draft_cache->cfg.block_size));
   a.logits = reinterpret_cast<float*>(ws + lay.logits);
   a.tokens = reinterpret_cast<int32_t*>(ws + lay.tokens);
   a.bar = reinterpret_cast<uint32_t*>(ws + lay.bar);
