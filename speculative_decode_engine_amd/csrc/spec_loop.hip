@@ -395,8 +395,12 @@ __device__ __forceinline__ void run_layers(const LoopArgs& a, const Side& s, int
 // device-scope store; the last item to arrive reduces every panel's
 // candidates, in panel (column) order, into tokens[dst + row].
 struct HeadArgmax {
-  int dst;  // tokens[dst + row]; < 0: no argmax
+  int dst;     // tokens[dst + row]; < 0: no argmax
+  int accept;  // the greedy loop's verify: the argmax's block then accepts (accept_in_block)
+  int P, D, round;
 };
+
+__device__ void accept_in_block(const LoopArgs& a, const HeadArgmax& am);
 
 __device__ __forceinline__ bool arg_better(float v, int i, float bv, int bi) {
   return v > bv || (v == bv && i < bi);
@@ -479,7 +483,7 @@ __device__ __forceinline__ float* head_red() {
   return buf;
 }
 
-template <int MB, int LPR>
+template <int MB, int LPR, bool ACCEPT>
 __device__ __forceinline__ void head_items(const LoopArgs& a, const mvp::PackedArgs& pa,
                                            int panels, int passes, HeadArgmax am) {
   constexpr int PW = 8 * LPR;
@@ -505,30 +509,37 @@ __device__ __forceinline__ void head_items(const LoopArgs& a, const mvp::PackedA
         s_last = last;
       }
       __syncthreads();
-      if (s_last) reduce_candidates(a, pa.M, panels, pa.d_out, am.dst);
+      if (s_last) {
+        reduce_candidates(a, pa.M, panels, pa.d_out, am.dst);
+        if constexpr (ACCEPT) {
+          if (am.accept) accept_in_block(a, am);
+        }
+      }
     }
   }
 }
 
-template <int LPR>
+template <int LPR, bool ACCEPT>
 __device__ __forceinline__ void head_rows(const LoopArgs& a, const mvp::PackedArgs& pa,
                                           int panels, int passes, HeadArgmax am) {
   switch (pa.pass_rows) {
-    case 1: head_items<1, LPR>(a, pa, panels, passes, am); break;
-    case 2: head_items<2, LPR>(a, pa, panels, passes, am); break;
-    case 3: head_items<3, LPR>(a, pa, panels, passes, am); break;
-    case 4: head_items<4, LPR>(a, pa, panels, passes, am); break;
-    case 5: head_items<5, LPR>(a, pa, panels, passes, am); break;
-    case 6: head_items<6, LPR>(a, pa, panels, passes, am); break;
-    case 7: head_items<7, LPR>(a, pa, panels, passes, am); break;
-    case 8: head_items<8, LPR>(a, pa, panels, passes, am); break;
-    default: head_items<9, LPR>(a, pa, panels, passes, am); break;
+    case 1: head_items<1, LPR, ACCEPT>(a, pa, panels, passes, am); break;
+    case 2: head_items<2, LPR, ACCEPT>(a, pa, panels, passes, am); break;
+    case 3: head_items<3, LPR, ACCEPT>(a, pa, panels, passes, am); break;
+    case 4: head_items<4, LPR, ACCEPT>(a, pa, panels, passes, am); break;
+    case 5: head_items<5, LPR, ACCEPT>(a, pa, panels, passes, am); break;
+    case 6: head_items<6, LPR, ACCEPT>(a, pa, panels, passes, am); break;
+    case 7: head_items<7, LPR, ACCEPT>(a, pa, panels, passes, am); break;
+    case 8: head_items<8, LPR, ACCEPT>(a, pa, panels, passes, am); break;
+    default: head_items<9, LPR, ACCEPT>(a, pa, panels, passes, am); break;
   }
 }
 
+// ACCEPT: the greedy loop's form (its verify's argmax block accepts).
+template <bool ACCEPT>
 __device__ __attribute__((noinline)) void head_logits(const LoopArgs& a, const Side& s, int layer,
                                                       int r0, int n, float* logits,
-                                                      int argmax_dst) {
+                                                      HeadArgmax am) {
   const int d = wave_uniform(s.d), V = wave_uniform(s.m.vocab);
   n = wave_uniform(n);
   const mvp::PackedShape sh = mvp::packed_shape(d, V);
@@ -543,18 +554,20 @@ __device__ __attribute__((noinline)) void head_logits(const LoopArgs& a, const S
   pa.n_batches = sh.n_batches;
   pa.accumulate = 0;
   const int passes = mvp::packed_passes(n);
-  const HeadArgmax am{wave_uniform(argmax_dst)};
+  am.dst = wave_uniform(am.dst);
+  am.accept = wave_uniform(am.accept);
   if (sh.lpr == 2)
-    head_rows<2>(a, pa, sh.panels, passes, am);
+    head_rows<2, ACCEPT>(a, pa, sh.panels, passes, am);
   else
-    head_rows<1>(a, pa, sh.panels, passes, am);
+    head_rows<1, ACCEPT>(a, pa, sh.panels, passes, am);
 }
 
 // Logits of window rows [r0, r0+n) from their h_buf rows (model s's head),
 // then their argmaxes into tokens[dst + row].
 __device__ __forceinline__ void decide(const LoopArgs& a, const Side& s, int layer, int r0, int n,
-                                       int dst) {
-  head_logits(a, s, layer, r0, n, a.logits, dst);
+                                       int dst, HeadArgmax am = HeadArgmax{0, 0, 0, 0, 0}) {
+  am.dst = dst;
+  head_logits<true>(a, s, layer, r0, n, a.logits, am);
   barrier(a);
 }
 
@@ -645,7 +658,7 @@ __global__ __launch_bounds__(kThreads) void spec_loop_kernel(LoopArgs a) {
         decide(a, a.dr, a.dr.kv.n_layers - 1, s, 1, s + 1);
       }
       run_layers(a, a.t, 0, n_layers, 0, M, P);
-      decide(a, a.t, n_layers - 1, 0, M, M);
+      decide(a, a.t, n_layers - 1, 0, M, M, HeadArgmax{0, 1, P, D, round});
     } else {
       // Draft (kernels.cu:2960-3006), steps 0..k when k > 0: the prefix
       // layers for window token s at P+s, one token at a time; the first k
@@ -656,29 +669,44 @@ __global__ __launch_bounds__(kThreads) void spec_loop_kernel(LoopArgs a) {
       for (int s = 0; s < n_steps; s++) {
         const Step t = round_step(a, s, n_steps, n_layers);
         run_layers(a, a.t, t.lo, t.hi, t.r0, t.n, P);
-        if (t.verify || s < a.k) decide(a, a.t, t.hi - 1, t.r0, t.n, t.verify ? M : s + 1);
+        if (t.verify)
+          decide(a, a.t, t.hi - 1, t.r0, t.n, M, HeadArgmax{0, 1, P, D, round});
+        else if (s < a.k)
+          decide(a, a.t, t.hi - 1, t.r0, t.n, s + 1);
       }
     }
-    // Greedy accept and O(1) rewinds (kernels.cu:3050-3076).
-    if (blockIdx.x == 0 && threadIdx.x == 0) {
-      const int E = a.state[kEmitted];
-      const SpecAccept r = spec_accept_greedy(a.tokens + 1, a.tokens + M, a.k, P, D, a.t.kv,
-                                              a.two ? &a.dr.kv : nullptr, a.emitted + E);
-      store_word(a.t.kv.seq_len, r.target_seq);  // (spec_accept_greedy wrote it plainly)
-      store_word(a.state + kEmitted, E + r.n_accepted + 1);
-      a.state[kAnchor] = r.bonus;
-      a.state[kRounds] = round + 1;
-      a.state[kProposed] += a.k;
-      a.state[kAccepted] += r.n_accepted;
-      a.accepted[round] = r.n_accepted;
-      a.tokens[0] = r.bonus;
-      round_close(a, r.n_accepted, r.bonus, r.draft_seq);
-    }
-    barrier(a);
-    if (a.two) {  // the draft's catch-up (kernels.cu:3079-3093)
-      catch_up(a, load_word(a.dr.kv.seq_len) - 1);
-      barrier(a);
-    }
+    // (the verify's decide accepted, rewound and caught up: accept_in_block)
+  }
+}
+
+// Greedy accept and O(1) rewinds (kernels.cu:3050-3076), by the block that
+// reduced the verify's argmax, right after it (the target's tokens are its
+// own stores): thread 0 accepts; with a draft model the block then appends
+// the catch-up token's K / V at draft_save + n in every draft layer
+// (kernels.cu:3079-3093).  The decide's grid barrier follows, so the round
+// needs no barrier of its own for the accept or the catch-up.
+__device__ void accept_in_block(const LoopArgs& a, const HeadArgmax& am) {
+  __shared__ int s_pos;
+  const int M = a.k + 1;
+  if (threadIdx.x == 0) {
+    const int E = a.state[kEmitted];
+    const SpecAccept r = spec_accept_greedy(a.tokens + 1, a.tokens + M, a.k, am.P, am.D, a.t.kv,
+                                            a.two ? &a.dr.kv : nullptr, a.emitted + E);
+    store_word(a.t.kv.seq_len, r.target_seq);  // (spec_accept_greedy wrote it plainly)
+    store_word(a.state + kEmitted, E + r.n_accepted + 1);
+    a.state[kAnchor] = r.bonus;
+    a.state[kRounds] = am.round + 1;
+    a.state[kProposed] += a.k;
+    a.state[kAccepted] += r.n_accepted;
+    a.accepted[am.round] = r.n_accepted;
+    a.tokens[0] = r.bonus;
+    round_close(a, r.n_accepted, r.bonus, r.draft_seq);
+    s_pos = r.draft_seq;
+  }
+  __syncthreads();
+  if (a.two) {
+    const int tok = a.tokens[catch_up_slot(a.k)];
+    for (int l = 0; l < a.dr.kv.n_layers; l++) append_token(a.dr, l, tok, s_pos);
   }
 }
 
@@ -741,7 +769,7 @@ __global__ __launch_bounds__(kThreads) void spec_loop_stochastic_kernel(LoopArgs
       run_layers(a, sd, t.lo, t.hi, t.r0, t.n, t.verify ? P : (a.two ? D : P));
       if (!t.verify && s >= a.k) continue;
       float* lg = t.verify ? a.logits : a.dlogits + (size_t)s * V;
-      head_logits(a, sd, t.hi - 1, t.r0, t.n, lg, -1);
+      head_logits<false>(a, sd, t.hi - 1, t.r0, t.n, lg, HeadArgmax{-1, 0, 0, 0, 0});
       barrier(a);
       if (t.verify) break;
       int st = device_spec_accept_stochastic_grid(lg, nullptr, nullptr, 0, V, temp, 1.f, a.smp.seed,
