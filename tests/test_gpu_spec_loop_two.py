@@ -70,6 +70,9 @@ def draft_of(m, kind, V, head_scale=8.0):
     if kind == "other":      # another model, another shape (kv_dim 64)
         return make_loop_model(50, n_layers=2, nh=4, nkv=1, dph=64, vocab=V, noise=0.1,
                                q_scale=2.0, head_scale=head_scale)
+    if kind == "dph96":      # head size 96: the draft side on the generic attention path
+        return make_loop_model(52, n_layers=2, nh=4, nkv=2, dph=96, vocab=V, noise=0.1,
+                               q_scale=2.0, head_scale=head_scale)
     return make_loop_model(51, n_layers=1, nh=4, nkv=2, dph=64, vocab=V, noise=0.1,
                            q_scale=2.0, head_scale=head_scale)  # "small": dph 64 under dph 128
 
@@ -115,6 +118,7 @@ GREEDY_CASES = [
     (6, (4, 4, 2, 64, 256), "other", 40, 3),    # draft kv_dim 64 under target kv_dim 128
     (5, (3, 8, 2, 128, 512), "small", 700, 5),  # dph 64 draft, dph 128 multi-partition target
     (11, (2, 8, 2, 64, 4096), "prefix", 120, 4),  # vocab 4096: 16-column head panels
+    (6, (3, 4, 2, 64, 256), "dph96", 200, 3),   # a generic-path draft: separate q / append phases
 ]
 
 
@@ -226,6 +230,29 @@ def test_greedy_loop_stops_on_the_eos_bonus(gpu, oracle, two):
         assert pool_sha(p.cache) == p.tmod.pool_sha256()
     assert r2 == first + 1 and t2 == toks[:ends[first]] and len(t2) < max_new
     assert res.tokens[-1] == eos
+    p.free()
+
+
+def test_self_speculative_stochastic_loop_stops_on_the_eos_bonus(gpu, oracle):
+    """The self-speculative sampling loop's EOS stop (kernels.cu:3471)."""
+    case_banner("loop eos stochastic self")
+    m = make_loop_model(3, noise=0.1, q_scale=2.0, head_scale=8.0)
+    max_new, k, nd = 16, 4, 2
+    p = Pair(oracle, m, m, 40, max_new, k, 3)
+    toks, acc, *_ = oracle.spec_loop_stochastic(p.tmod, *lm(m), p.anchor, k, nd, max_new, 14)
+    p.free()
+    ends = _round_ends(acc)
+    eos = toks[ends[1] - 1]
+    p = Pair(oracle, m, m, 40, max_new, k, 3)
+    t2, a2, r2, _, _, off, margin = oracle.spec_loop_stochastic(p.tmod, *lm(m), p.anchor, k, nd,
+                                                                max_new, 14, eos_token=eos)
+    assert margin > 1e-4 and t2[-1] == eos and len(t2) < max_new
+    offset = torch.zeros(1, dtype=torch.int64, device="cuda")
+    res = spec_loop_stochastic(p.cache, p.tdev, p.anchor, k, nd, max_new, 14, offset=offset,
+                               eos_token=eos)
+    assert res.status == 0 and res.tokens == t2 and res.accepted == a2 and res.rounds == r2
+    assert res.seq_len == p.tmod.seq_len and pool_sha(p.cache) == p.tmod.pool_sha256()
+    assert int(offset.item()) == off
     p.free()
 
 
