@@ -441,8 +441,14 @@ struct SampleLds {
 // (slice 0), this slice's weight totals; the last slice of a row to arrive
 // finds the crossing slice and token; the last row to arrive decides and
 // rewinds.  Every thread of the block calls it.
-template <int VT>
-__device__ void slice_sample(const StochArgs& a, int s, int b, SampleLds& sl) {
+// (The default of slice_sample's `hook`: nothing.)
+struct NoHook {
+  __device__ void operator()(int, int, int, int) const {}
+};
+
+template <int VT, class Hook = NoHook>
+__device__ void slice_sample(const StochArgs& a, int s, int b, SampleLds& sl,
+                             const Hook& hook = Hook{}) {
   const int tid = threadIdx.x;
   const int V = a.V;
   const Scratch sc{a.scratch, a.k + 1, a.S};
@@ -658,11 +664,12 @@ __device__ void slice_sample(const StochArgs& a, int s, int b, SampleLds& sl) {
     *a.target.seq_len = t_seq;
     if (a.has_draft) *a.draft.seq_len = d_seq;
     *a.offset = offset + 1;
+    hook(n, tok, t_seq, d_seq);
   }
 }
 
-template <int VT, class Sync>
-__device__ void stochastic_grid(const StochArgs& a, Sync& sync) {
+template <int VT, class Sync, class Hook = NoHook>
+__device__ void stochastic_grid(const StochArgs& a, Sync& sync, const Hook& hook = Hook{}) {
   __shared__ float2 red2[kVWaves];
   __shared__ SampleLds sl;
   const int items = a.S * (a.k + 1);
@@ -674,7 +681,7 @@ __device__ void stochastic_grid(const StochArgs& a, Sync& sync) {
   }
   sync();
   for (int it = blk; it < items; it += nblk) {
-    slice_sample<VT>(a, it % a.S, it / a.S, sl);
+    slice_sample<VT>(a, it % a.S, it / a.S, sl, hook);
     __syncthreads();  // sl reused by the block's next item
   }
 }
@@ -702,13 +709,17 @@ __host__ __device__ inline size_t spec_stochastic_workspace_size() {
 // and offset give the same bits as sde_spec_accept_stochastic, whatever the
 // grid and block sizes.  Returns the same status in every thread, before any
 // work: SDE_ERR_UNSUPPORTED (block size), SDE_ERR_RANGE (k outside [0, 64]),
-// SDE_ERR_INVALID_ARGUMENT, SDE_ERR_WORKSPACE.
-template <class Sync>
+// SDE_ERR_INVALID_ARGUMENT, SDE_ERR_WORKSPACE.  `hook(n_accepted, token,
+// target_seq, draft_seq)`, when given, runs once per call on the one thread
+// that decides, right after it has written the result, the seq_len words and
+// *offset (a persistent loop's follow-up without a grid barrier of its own;
+// its stores are visible to the grid after the caller's next grid barrier).
+template <class Sync, class Hook = spec::NoHook>
 __device__ int device_spec_accept_stochastic_grid(
     const float* target_logits, const float* draft_logits, const int32_t* draft_tokens, int k,
     int vocab, float temp_target, float temp_draft, uint64_t seed, uint64_t* offset,
     int target_save, int draft_save, const sde_kv_view& target, const sde_kv_view* draft,
-    int32_t* result, void* workspace, size_t workspace_bytes, Sync sync) {
+    int32_t* result, void* workspace, size_t workspace_bytes, Sync sync, Hook hook = Hook{}) {
   using namespace spec;
   if (blockDim.x != 256 && blockDim.x != 512 && blockDim.x != 1024) return SDE_ERR_UNSUPPORTED;
   if (k < 0 || k > kSpecMaxK) return SDE_ERR_RANGE;
@@ -736,11 +747,11 @@ __device__ int device_spec_accept_stochastic_grid(
   a.result = result;
   a.scratch = static_cast<uint32_t*>(workspace);
   if (blockDim.x == 1024)
-    stochastic_grid<1>(a, sync);
+    stochastic_grid<1>(a, sync, hook);
   else if (blockDim.x == 512)
-    stochastic_grid<2>(a, sync);
+    stochastic_grid<2>(a, sync, hook);
   else
-    stochastic_grid<4>(a, sync);
+    stochastic_grid<4>(a, sync, hook);
   return SDE_OK;
 }
 

@@ -732,6 +732,51 @@ __device__ void adapt_temperature(const LoopArgs& a, int n_accepted) {
   a.state[kTemp] = __float_as_int(t);
 }
 
+// A draft sample's token into window slot `slot`, on the thread that drew
+// it (a token outside the vocabulary would index the tables out of bounds:
+// record an error and continue with token 0).
+struct DraftTokenHook {
+  const LoopArgs* a;
+  int slot;
+  __device__ void operator()(int, int tok, int, int) const {
+    const bool ok = tok >= 0 && tok < a->t.m.vocab;
+    a->tokens[slot] = ok ? tok : 0;
+    if (!ok) atomicCAS(reinterpret_cast<int*>(a->state + kStatus), SDE_OK, SDE_ERR_HIP);
+  }
+};
+
+// The round's bookkeeping after the sampling accept, on the thread that
+// decided it (emitted tokens: the accepted drafts, then the corrected or
+// bonus token), then the temperature update and the round's close.
+struct AcceptHook {
+  const LoopArgs* a;
+  int P, D, round;
+  __device__ void operator()(int n, int tok, int t_seq, int d_seq) const {
+    const LoopArgs& la = *a;
+    const int E = load_word(la.state + kEmitted);
+    if (n < 0 || n > la.k || tok < 0 || tok >= la.t.m.vocab || t_seq != P + n + 1 ||
+        (la.two && d_seq != D + n)) {
+      // not a result of the acceptance: stop with an error, caches untouched
+      atomicCAS(reinterpret_cast<int*>(la.state + kStatus), SDE_OK, SDE_ERR_HIP);
+      store_word(la.t.kv.seq_len, P);
+      if (la.two) store_word(la.dr.kv.seq_len, D);
+      return;
+    }
+    for (int j = 0; j < n; j++) la.emitted[E + j] = la.tokens[1 + j];
+    la.emitted[E + n] = tok;
+    store_word(la.t.kv.seq_len, t_seq);
+    store_word(la.state + kEmitted, E + n + 1);
+    la.state[kAnchor] = tok;
+    la.state[kRounds] = round + 1;
+    la.state[kProposed] += la.k;
+    la.state[kAccepted] += n;
+    la.accepted[round] = n;
+    la.tokens[0] = tok;
+    adapt_temperature(la, n);
+    round_close(la, n, tok, D + n);
+  }
+};
+
 // Speculative sampling over the same rounds (megakernel_speculative_
 // stochastic_kernel, kernels.cu:3108-3481, self-speculative): draft token
 // i+1 is sampled from softmax(draft logits of row i / T_d) by the
@@ -774,48 +819,15 @@ __global__ __launch_bounds__(kThreads) void spec_loop_stochastic_kernel(LoopArgs
       if (t.verify) break;
       int st = device_spec_accept_stochastic_grid(lg, nullptr, nullptr, 0, V, temp, 1.f, a.smp.seed,
                                               a.offset, 0, 0, dv, nullptr, a.dres, a.sscratch,
-                                              sbytes, sync);
+                                              sbytes, sync, DraftTokenHook{&a, s + 1});
       note_error(a, st);
-      barrier(a);
-      if (blockIdx.x == 0 && threadIdx.x == 0) {
-        // (a token outside the vocabulary would index the tables out of
-        // bounds: record an error and continue with token 0)
-        const int tok = a.dres[1];
-        const bool ok = tok >= 0 && tok < V;
-        a.tokens[s + 1] = ok ? tok : 0;
-        if (!ok) atomicCAS(reinterpret_cast<int*>(a.state + kStatus), SDE_OK, SDE_ERR_HIP);
-      }
       barrier(a);
     }
     int st = device_spec_accept_stochastic_grid(a.logits, a.dlogits, a.tokens + 1, a.k, V, 1.f, temp,
                                             a.smp.seed, a.offset, P, D, a.t.kv,
                                             a.two ? &a.dr.kv : nullptr, a.sres, a.sscratch, sbytes,
-                                            sync);
+                                            sync, AcceptHook{&a, P, D, round});
     note_error(a, st);
-    barrier(a);
-    if (blockIdx.x == 0 && threadIdx.x == 0) {
-      const int n = a.sres[0];
-      const int E = a.state[kEmitted];
-      if (n < 0 || n > a.k || a.sres[1] < 0 || a.sres[1] >= V || a.sres[2] != P + n + 1 ||
-          (a.two && a.sres[3] != D + n)) {
-        // not a result of the acceptance: stop with an error, caches untouched
-        atomicCAS(reinterpret_cast<int*>(a.state + kStatus), SDE_OK, SDE_ERR_HIP);
-        store_word(a.t.kv.seq_len, P);
-        if (a.two) store_word(a.dr.kv.seq_len, D);
-      } else {
-        for (int j = 0; j <= n; j++) a.emitted[E + j] = a.sres[4 + j];
-        store_word(a.t.kv.seq_len, a.sres[2]);
-        store_word(a.state + kEmitted, E + n + 1);
-        a.state[kAnchor] = a.sres[1];
-        a.state[kRounds] = round + 1;
-        a.state[kProposed] += a.k;
-        a.state[kAccepted] += n;
-        a.accepted[round] = n;
-        a.tokens[0] = a.sres[1];
-        adapt_temperature(a, n);
-        round_close(a, n, a.sres[1], D + n);
-      }
-    }
     barrier(a);
     if (a.two && load_word(a.state + kStatus) == SDE_OK) {  // the draft's catch-up
       catch_up(a, load_word(a.dr.kv.seq_len) - 1);
