@@ -76,6 +76,9 @@ def parse_args():
     p.add_argument("--only", default=None, metavar="CONFIG",
                    help="time one configs entry (e.g. llama3_8b_verify, "
                         "qwen25_7b_selfspec_verify_fused) and print its JSON (profiling)")
+    p.add_argument("--only-shares", action="store_true",
+                   help="time only the headline's per-GPU shares (KV-head and context "
+                        "sharding) and print their JSON")
     p.add_argument("--only-matvec", action="store_true",
                    help="time only the output projection (sde_matvec) and print its JSON")
     p.add_argument("--matvec-shape", default=None,
@@ -209,6 +212,33 @@ def bench_config(torch, W, w, steps, warmup, mode):
         res["kernel_us_events"] = round(launch_ms * 1e3, 3)
     cache.free()
     return res
+
+
+def bench_shares(torch, W, steps, warmup):
+    """The headline layer-step as one GPU of N would run it (N = 2, 4, 8;
+    the sharding is design only, every box here has one GPU): by KV head
+    (nkv/N KV heads with their q heads over the whole 32K context, a pool
+    of kv_dim/N, no exchange) and by context (all heads over 32768/N keys,
+    whose partials one all-gather would combine).  Each share is timed like
+    the headline (attention only, graph-replayed over a 2 GiB rotation);
+    `frac_of_hbm_peak` is the share's own algorithmic bytes over its time."""
+    import dataclasses
+    w = W.CONFIGS[HEADLINE]
+    out = {}
+    for n in (2, 4, 8):
+        heads = dataclasses.replace(w, name=f"{w.name}_heads_of_{n}", nh=w.nh // n,
+                                    nkv=w.nkv // n)
+        ctx = dataclasses.replace(w, name=f"{w.name}_context_of_{n}",
+                                  ctx=w.l_max // n - 1,
+                                  pool_blocks=max(w.pool_blocks // n, 1))
+        r = {}
+        for kind, sw in (("heads", heads), ("context", ctx)):
+            res = bench_config(torch, W, sw, steps, warmup, "attn")
+            r[kind] = dict(nh=sw.nh, nkv=sw.nkv, keys=res["keys"],
+                           us=res["us_per_layer_step"], gbps=res["gbps"],
+                           frac_of_hbm_peak=res["frac_of_hbm_peak"])
+        out[f"n{n}"] = r
+    return out
 
 
 def bench_rollback(torch, W, steps=2000):
@@ -728,6 +758,9 @@ def main():
             torch.cuda.synchronize()
         return
 
+    if args.only_shares:
+        print(json.dumps({"shares": bench_shares(torch, W, steps, warmup)}), flush=True)
+        return
     if args.only:
         modes = {"llama3_8b_verify": "verify", "llama3_8b_4k_decode": "decode",
                  "llama3_8b_4k_attn": "attn", "llama3_8b_verify_fused": "verify_fused",
@@ -785,6 +818,8 @@ def main():
         log("[bench] sdec load", json.dumps(extra["sdec_load"]))
         extra["grid_device_fn"] = bench_grid_device_fn(torch, W, steps, warmup)
         log("[bench] grid device fn", json.dumps(extra["grid_device_fn"]))
+        extra["shares"] = bench_shares(torch, W, steps, warmup)
+        log("[bench] shares", json.dumps(extra["shares"]))
         extra["spec_loop"] = bench_spec_loop(torch)
         # a loop layer (same heads, 4K context, one query) against the
         # library's decode step (append + attention launches, graph-replayed)
