@@ -1164,6 +1164,20 @@ __host__ __device__ inline int stream_rows(int R, int L_max) {
   return 16;
 }
 
+// The plan of the 8-wave kernels: stream_rows' group size, or twice it (up
+// to 16) when that leaves each wave fewer tiles -- a KV head's rows then
+// share every tile they read, where the smaller groups' extra workgroups
+// would have needed a second tile per wave (measured on MI355X: the
+// Qwen2.5-7B draft step, 7 rows per KV head over 8K keys, two 4-row groups
+// with two tiles per wave 15.9 us, one 8-row group with one 15.6 us).
+__host__ __device__ inline StreamPlan stream_plan8(int L_max, int nkv, int R, int blocks) {
+  const int rows = stream_rows(R, L_max);
+  const StreamPlan p = stream_plan(L_max, nkv, R, blocks, 8, 4, rows);
+  if (rows >= 16 || R <= rows) return p;
+  const StreamPlan w = stream_plan(L_max, nkv, R, blocks, 8, 4, 2 * rows);
+  return w.tiles_per_part < p.tiles_per_part ? w : p;
+}
+
 // Rows per group of the 4-wave device functions: 4 (decode of up to 4 q
 // heads per KV head) or 16 (everything larger) -- the MFMA computes 16 rows
 // either way; fewer rows per group give a KV head more workgroups.
@@ -1580,7 +1594,7 @@ __device__ __forceinline__ int device_flash_attention_gqa_grid(const float* q_al
   const int R = n_queries * G;
   const int n_blocks = gridDim.x * gridDim.y * gridDim.z;
   const StreamPlan p = waves == 8
-                           ? stream_plan(L_max, nkv, R, n_blocks, 8, 4, stream_rows(R, L_max))
+                           ? stream_plan8(L_max, nkv, R, n_blocks)
                            : stream_plan(L_max, nkv, R, n_blocks, 4, 2, device_rows(R));
   if ((int64_t)nkv * p.row_groups > kGridCounters) return SDE_ERR_UNSUPPORTED;
   AttnArgs a;

@@ -77,7 +77,7 @@ int parts_bound(int max_total_len) {
 
 // The plan of a call: 8-wave workgroups, one per CU.
 StreamPlan plan_for(int L_max, int nkv, int R, int n_cus) {
-  return stream_plan(L_max, nkv, R, n_cus, kStreamWaves, 4, stream_rows(R, L_max));
+  return stream_plan8(L_max, nkv, R, n_cus);
 }
 
 size_t partial_bytes(int nkv, int R, int n_parts, int dph) {
