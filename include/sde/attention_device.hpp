@@ -260,10 +260,14 @@ struct AttnArgs {
   int n_parts;
   int tiles_per_part;
   float qscale;    // log2(e) / sqrt(dph)
+  int ctr_stride = 1;  // words between the arrival counters (32: one 128-byte line each)
+  uint32_t slice_spin = 1u << 14;  // polls of a split combine's wait (kSliceSpinLimit)
 };
 
 constexpr int kStreamWaves = 8;      // waves per workgroup of libsde_paged's kernel
 constexpr int kStreamMaxParts = 64;  // partitions per (KV head, row group)
+constexpr int kSliceRows = 4;        // rows per slice of a split combine (stream_item)
+constexpr uint32_t kSliceSpinLimit = 1u << 14;  // polls of a slice's wait (~10 ms)
 
 // Device-scope (agent) relaxed atomic accesses for the partition partials.
 // Memory-ordering argument (gfx950): an agent-scope relaxed store is a
@@ -465,6 +469,55 @@ __device__ __forceinline__ void stream_combine(const AttnArgs& a, int tid, int k
     combine_rows<DPH, RPW, 8, WAVES>(a, tid, kvh, r0, nrows);
   else
     combine_rows<DPH, RPW, 16, WAVES>(a, tid, kvh, r0, nrows);
+}
+
+// A split combine's protocol on one 32-bit word per (KV head, row group),
+// zero at rest: bits 0-7 count the arrivals (n_parts <= 64), bits 8-15 the
+// waiting workgroups' final operations, bits 16-23 the slices given up.
+// The workgroup arriving s places before the last (1 <= s < n_slices)
+// waits for the arrivals to complete (bounded: `limit` polls), then adds
+// its final operation and combines slice s; if its wait runs out first it
+// adds its final operation with its give-up bit -- and still combines the
+// slice when that add shows every arrival in (the last arrival, having
+// come in between, did not see the bit).  The last arrival combines slice
+// 0 and every slice its arrival add shows given up.  Whichever operation
+// is the word's last (n_parts arrivals + n_slices - 1 finals) resets it.
+// So no wait holds up the grid, every slice is combined exactly once, and
+// nobody reads the word after its final operation.  Returns this
+// workgroup's slice (-1: none); `extra` receives, for the last arrival,
+// the slices given up (bit s: slice s).
+constexpr uint32_t kSliceFinal = 1u << 8;
+
+__device__ __forceinline__ int slice_arrive(uint32_t* ctr, uint32_t prev, int n_parts,
+                                            int n_slices, uint32_t limit, int& extra) {
+  const uint32_t want = (uint32_t)n_parts;
+  const uint32_t last_op = want | ((uint32_t)(n_slices - 1) << 8);  // the word after every op
+  const uint32_t arrived = prev & 0xFFu;
+  if (arrived >= want) return -1;  // impossible: the word is zero at rest
+  const int rank = n_parts - 1 - (int)arrived;
+  if (rank == 0) {  // the last arrival
+    const uint32_t now = prev + 1u;
+    if ((now & 0xFFFFu) == last_op)  // every wait gave up already
+      __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    extra = (int)((prev >> 16) & 0xFFu);
+    return 0;
+  }
+  if (rank >= n_slices) return -1;
+  bool all_in = false;
+  for (uint32_t spin = 0; spin < limit; spin++) {
+    if ((__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & 0xFFu) >= want) {
+      all_in = true;
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  const uint32_t add = kSliceFinal | (all_in ? 0u : (1u << (16 + rank)));
+  const uint32_t old = __hip_atomic_fetch_add(ctr, add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint32_t now = old + add;
+  if ((now & 0xFFFFu) == last_op)
+    __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // given up but every arrival already in: the last arrival did not see the bit
+  return (all_in || (old & 0xFFu) >= want) ? rank : -1;
 }
 
 // The window's rows (positions pos_base .. pos_base+M-1) of KV head kvh:
@@ -882,6 +935,7 @@ struct MfmaLds {
   char st[WAVES * MfmaShape<DPH>::WAVEB] __attribute__((aligned(16)));
   h8_t qop[2 * MfmaShape<DPH>::KS * 64];
   int last;
+  int extra;
   __device__ char* staging(int w) { return st + w * MfmaShape<DPH>::WAVEB; }
   __device__ float* acc_at(int w, int r) {
     return reinterpret_cast<float*>(staging(w)) + r * DPH;
@@ -920,11 +974,17 @@ __device__ __forceinline__ void gather_append_slice(const AttnArgs& a, const Gat
 // (further waves idle), merge their states through LDS, and either write
 // the normalised output (one partition) or publish a partial and count the
 // arrival; the last arrival combines all partitions (with WAVES waves).
+// SPLIT (libsde_paged's kernels, one item per workgroup, arrival counters
+// a line apart): a group of more than kSliceRows rows is combined in
+// slices of up to kSliceRows rows, slice s by the workgroup that arrived s
+// places before the last -- the last arrival takes slice 0 at once, the
+// ones before it wait (bounded) for it -- so several CUs read the partials
+// at once (one CU reads them at ~35 GB/s); see slice_arrive.
 // Every thread of the workgroup calls it.
 // GATHER: the window comes from `ga` (GatherArgs) instead of a.q and
 // earlier appends.
 template <int DPH, int RPW, int CHUNK, int WAVES, bool ROPE = false, class Lds,
-          bool GATHER = false>
+          bool GATHER = false, bool SPLIT = false>
 __device__ __forceinline__ void stream_item(const AttnArgs& a, int part, int kvh, int rg,
                                             Lds& lds, int nwaves = WAVES,
                                             const RopeArgs* rp = nullptr,
@@ -1061,22 +1121,51 @@ __device__ __forceinline__ void stream_item(const AttnArgs& a, int part, int kvh
   }
   if (a.n_parts == 1) return;
 
-  // ---- the last workgroup of (KV head, row group) combines --------------
+  // ---- the last workgroup(s) of (KV head, row group) combine ------------
   // Partials are device-scope stores; waiting for them (vmcnt) before the
   // arrival increment orders them before it (see store_dev2).
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
+  // Slices of a split combine (SPLIT, counters a line apart).
+  int n_slices = 1;
+  if constexpr (SPLIT)
+    if (a.ctr_stride > 1) n_slices = min((nrows + kSliceRows - 1) / kSliceRows, a.n_parts);
   if (tid == 0) {
-    uint32_t* ctr = a.counters + (size_t)kvh * a.row_groups + rg;
+    uint32_t* ctr = a.counters + ((size_t)kvh * a.row_groups + rg) * a.ctr_stride;
     const uint32_t prev =
         __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const int last = prev == (uint32_t)(a.n_parts - 1);
-    if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    lds.last = last;
+    int slice = -1;  // the slice this workgroup combines (-1: none)
+    int extra = 0;   // the last arrival's slices given up by their waits (bit s: slice s)
+    if (n_slices == 1) {
+      if (prev == (uint32_t)(a.n_parts - 1)) {
+        __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        slice = 0;
+      }
+    } else {
+      slice = slice_arrive(ctr, prev, a.n_parts, n_slices, a.slice_spin, extra);
+    }
+    lds.last = slice;
+    lds.extra = extra;
   }
   __syncthreads();
-  if (!lds.last) return;
-  stream_combine<DPH, RPW, WAVES>(a, tid, kvh, r0, nrows);
+  const int slice = lds.last;
+  if (slice < 0) return;
+  if (n_slices == 1) {
+    stream_combine<DPH, RPW, WAVES>(a, tid, kvh, r0, nrows);
+    return;
+  }
+  const int rs = (nrows + n_slices - 1) / n_slices;
+  const int s0 = slice * rs;
+  const int sn = min(rs, nrows - s0);
+  if (rs <= kSliceRows)
+    stream_combine<DPH, kSliceRows, WAVES>(a, tid, kvh, r0 + s0, sn);
+  else
+    stream_combine<DPH, RPW, WAVES>(a, tid, kvh, r0 + s0, sn);
+  // (the last arrival only, after waits that gave up)
+  for (int bits = lds.extra; bits != 0; bits &= bits - 1) {
+    const int e0 = __builtin_ctz((unsigned)bits) * rs;
+    stream_combine<DPH, RPW, WAVES>(a, tid, kvh, r0 + e0, min(rs, nrows - e0));
+  }
 }
 
 // Partition sizing shared by libsde_paged and the grid API: at most

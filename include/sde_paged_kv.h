@@ -232,6 +232,14 @@ int sde_paged_attention_noalloc(sde_kv_cache* cache, int layer, const float* d_q
                                 float* d_out, int nh, int nkv, int dph, int pos_base,
                                 int n_queries, sde_stream_t stream);
 
+/* Test hook for failure handling, no counterpart in the reference: sets the
+ * number of polls (process-wide, for later calls) that a workgroup waiting
+ * to combine a slice of a (KV head, row group)'s rows spends before it
+ * gives up and leaves its slice to the group's last arriving workgroup
+ * (0: give up at once).  Results are the same either way; only the combine's
+ * parallelism changes.  Returns the previous value (the default is 16384). */
+uint32_t sde_debug_set_slice_spin(uint32_t polls);
+
 /* Greedy acceptance + O(1) rewind of speculative decoding on the device,
  * with no host round trip (the reference's host loop kernels.cu:2428-2466
  * copies the tokens back and rewinds from the host; its megakernel does it

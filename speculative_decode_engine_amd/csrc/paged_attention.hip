@@ -44,7 +44,8 @@ template <int DPH, int RPW, int CHUNK>
 __global__ __launch_bounds__(64 * kStreamWaves) void attn_mfma_kernel(AttnArgs a) {
   __shared__ MfmaLds<DPH, kStreamWaves> lds;
   const int3 w = stream_coords<CHUNK>();
-  stream_item<DPH, RPW, CHUNK, kStreamWaves>(a, w.x, w.y, w.z, lds);
+  stream_item<DPH, RPW, CHUNK, kStreamWaves, false, MfmaLds<DPH, kStreamWaves>, false, true>(
+      a, w.x, w.y, w.z, lds);
 }
 
 // attn_mfma_kernel with RoPE of q and of the window's k, and the window's
@@ -54,8 +55,8 @@ __global__ __launch_bounds__(64 * kStreamWaves) void attn_rope_kernel(AttnArgs a
   __shared__ MfmaLds<DPH, kStreamWaves> lds;
   __shared__ float2 rope_cs[kRopeMaxQueries * (DPH / 2)];
   const int3 w = stream_coords<CHUNK>();
-  stream_item<DPH, RPW, CHUNK, kStreamWaves, true>(a, w.x, w.y, w.z, lds, kStreamWaves, &rp,
-                                                  rope_cs);
+  stream_item<DPH, RPW, CHUNK, kStreamWaves, true, MfmaLds<DPH, kStreamWaves>, false, true>(
+      a, w.x, w.y, w.z, lds, kStreamWaves, &rp, rope_cs);
 }
 
 }  // namespace attn
@@ -79,6 +80,9 @@ int parts_bound(int max_total_len) {
 StreamPlan plan_for(int L_max, int nkv, int R, int n_cus) {
   return stream_plan8(L_max, nkv, R, n_cus);
 }
+
+// Polls of a split combine's wait (sde_debug_set_slice_spin).
+std::atomic<uint32_t> g_slice_spin{kSliceSpinLimit};
 
 size_t partial_bytes(int nkv, int R, int n_parts, int dph) {
   return n_parts > 1 ? (size_t)nkv * R * n_parts * (size_t)(dph + 2) * sizeof(float) : 0;
@@ -247,6 +251,11 @@ int run_attention(sde_kv_cache* cache, int layer, const float* d_q, float* d_out
   a.n_parts = plan.n_parts;
   a.tiles_per_part = plan.tiles_per_part;
   a.qscale = (float)(kLog2e / std::sqrt((double)dph));
+  // Each arrival counter on a 128-byte line of its own where they fit: a
+  // split combine's waiting workgroups poll theirs while other groups'
+  // arrivals update theirs.
+  a.ctr_stride = (int64_t)nkv * plan.row_groups * 32 <= sde::kMaxAttnCounters ? 32 : 1;
+  a.slice_spin = g_slice_spin.load(std::memory_order_relaxed);
 
   const hipStream_t s = (hipStream_t)stream;
   return dph == 128 ? launch<128>(plan, a, nkv, s, rope) : launch<64>(plan, a, nkv, s, rope);
@@ -316,6 +325,10 @@ int sde_rope_append_attention(sde_kv_cache* cache, int layer, const float* d_q,
 int sde_paged_attention_noalloc(sde_kv_cache* cache, int layer, const float* d_q,
                                 float* d_out, int nh, int nkv, int dph, int pos_base,
                                 int n_queries, sde_stream_t stream);
+
+uint32_t sde_debug_set_slice_spin(uint32_t polls) {
+  return g_slice_spin.exchange(polls == 0 ? 0u : polls, std::memory_order_relaxed);
+}
 
 int sde_attention_dispatch(int attn_type, sde_kv_cache* cache, int layer,
                            const float* d_q, float* d_out, int nh, int nkv,

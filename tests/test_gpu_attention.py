@@ -252,3 +252,39 @@ def test_attention_argument_errors(gpu):
     with pytest.raises(SDEError) as e:
         c520.attention(0, torch.zeros(1, 520, device="cuda"), 1, 1, 520, 0)  # dph > 512
     assert e.value.status == N.SDE_ERR_UNSUPPORTED
+
+
+@pytest.mark.parametrize("nh,nkv,dph,bs,ctx,M", [(32, 8, 128, 16, 1500, 5),   # 8-row groups, 2 slices
+                                                 (28, 4, 128, 32, 3000, 9),   # 16-row groups, 4 slices
+                                                 (28, 4, 128, 32, 8192, 1),   # one 7-row group, 2 slices
+                                                 (32, 8, 128, 16, 1500, 3),   # one 12-row group, 3 slices
+                                                 (16, 2, 64, 16, 2000, 6)])   # dph 64, 16-row groups
+def test_split_combine_slices_and_their_fallback(gpu, oracle, nh, nkv, dph, bs, ctx, M):
+    """Row groups of more than 4 rows are combined in slices by the last
+    arriving workgroups; a slice whose wait gives up is combined by the
+    group's last arrival instead.  Both ways give the oracle's result, the
+    same bits (a slice's sums do not depend on which workgroup runs them),
+    and leave the arrival counters at rest (later calls, of other plans too,
+    stay correct)."""
+    case_banner("split combine", nh, nkv, dph, bs, ctx, M)
+    cache, K, V, rng = build_layer(nh, nkv, dph, bs, ctx, M, -(-(ctx + M) // bs) + 5, ctx + M)
+    q = torch.from_numpy(W.queries(rng, M, nh, dph)).cuda()
+    ref = oracle.attention_f64_np(q.cpu().numpy(), K, V, nh, nkv, dph, ctx)
+    lib = N.load()
+    outs = []
+    prev = lib.sde_debug_set_slice_spin(16384)
+    try:
+        for spin in (16384, 0, 16384, 1, 16384):
+            lib.sde_debug_set_slice_spin(spin)
+            for _ in range(2):
+                outs.append(cache.attention(0, q, nh, nkv, dph, ctx).clone())
+                one = cache.attention(0, q[:1].contiguous(), nh, nkv, dph, ctx)  # another plan
+            torch.cuda.synchronize()
+            assert_close(one.cpu().numpy(), oracle.attention_f64_np(
+                q[:1].cpu().numpy(), K[:ctx + 1], V[:ctx + 1], nh, nkv, dph, ctx), "decode after")
+    finally:
+        lib.sde_debug_set_slice_spin(prev)
+    for o in outs:
+        assert_close(o.cpu().numpy(), ref, f"split {nh}/{nkv} M{M}")
+        assert torch.equal(o, outs[0])
+    cache.free()
