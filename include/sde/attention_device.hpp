@@ -217,23 +217,19 @@ __device__ __forceinline__ float rope_angle(const RopeArgs& rp, int pos, int j) 
   return ((float)pos / rp.pos_div) * rp.inv_freq[j];
 }
 
-// Window rows the fused path supports: its (cos, sin) table lives in LDS.
+// Window rows the fused path supports.
 constexpr int kRopeMaxQueries = 32;
 
-// (cos, sin) of every (window query m, rotation pair j), m-major, into LDS
-// by the whole workgroup (one sincos per entry), then a barrier.
-template <int DPH>
-__device__ __forceinline__ void rope_table(const RopeArgs& rp, int pos_base, int M,
-                                           float2* cs) {
-  constexpr int HALF = DPH / 2;
-  for (int t = threadIdx.x; t < M * HALF; t += blockDim.x) {
-    const int m = t / HALF;
-    float sn, c;
-    sincosf(rope_angle(rp, pos_base + m, t - m * HALF), &sn, &c);
-    cs[t] = make_float2(c, sn);
-  }
-  __syncthreads();
-}
+// RoPE of a wave's q rows (mfma_pack_q): the window queries its rows
+// belong to are p0 .. p0+nm-1 (positions); lane l holds inv_freq[l % (dph/2)]
+// in fr (loaded before the lane's q, so the table waits for no q load) and
+// reads the table row of its own query, mi (0 for a padding row).  The
+// angle is rope_angle's, so q and the appended k rotate alike.
+struct QRope {
+  float fr;
+  float pos_div;
+  int p0, nm, mi;
+};
 
 // attention.h:120-126: normalise unless the sum is tiny or not finite.
 __device__ __forceinline__ float finish_scale(float l) {
@@ -522,11 +518,13 @@ __device__ __forceinline__ int slice_arrive(uint32_t* ctr, uint32_t prev, int n_
 
 // The window's rows (positions pos_base .. pos_base+M-1) of KV head kvh:
 // k rotated by RoPE, k and v rounded to fp16 (RNE) into the pool
-// (kv_cache_append, kv_cache.cu:70-93), by the whole workgroup; returns
-// once the stores are visible to the workgroup's loads.
+// (kv_cache_append, kv_cache.cu:70-93), by the whole workgroup, one thread
+// per (row, rotation pair) -- its k pair, v pair and sincos, all loads
+// issued together; returns once the stores are visible to the workgroup's
+// loads.
 template <int DPH>
 __device__ __forceinline__ void rope_append_slice(const AttnArgs& a, const RopeArgs& rp,
-                                                  const float2* rope_cs, int kvh) {
+                                                  int kvh) {
   constexpr int HALF = DPH / 2;
   const int M = a.R / a.G;
   const int kvd = a.src.kv_dim;
@@ -535,25 +533,20 @@ __device__ __forceinline__ void rope_append_slice(const AttnArgs& a, const RopeA
     const int m = t / HALF;
     const int j = t - m * HALF;
     const int pos = a.pos_base + m;
-    const float* kin = rp.k_new + (size_t)m * kvd + (size_t)kvh * DPH;
-    const float x0 = kin[j], x1 = kin[j + HALF];
-    const float cs = rope_cs[t].x, sn = rope_cs[t].y;
+    const size_t in = (size_t)m * kvd + (size_t)kvh * DPH + j;
+    const float x0 = rp.k_new[in], x1 = rp.k_new[in + HALF];
+    const float v0 = rp.v_new[in], v1 = rp.v_new[in + HALF];
     const int lb = pos / bs;
     const int slot = pos - lb * bs;
     uint16_t* kd = rp.pool + ((size_t)(uint32_t)a.src.table[lb] * 2u * bs + slot) * kvd +
-                   (size_t)kvh * DPH;
-    kd[j] = __builtin_bit_cast(uint16_t, (_Float16)(x0 * cs - x1 * sn));
-    kd[j + HALF] = __builtin_bit_cast(uint16_t, (_Float16)(x0 * sn + x1 * cs));
-  }
-  for (int t = threadIdx.x; t < M * DPH; t += blockDim.x) {
-    const int m = t / DPH;
-    const int d = t - m * DPH;
-    const int pos = a.pos_base + m;
-    const int lb = pos / bs;
-    const int slot = pos - lb * bs;
-    uint16_t* vd = rp.pool + ((size_t)(uint32_t)a.src.table[lb] * 2u * bs + bs + slot) * kvd +
-                   (size_t)kvh * DPH;
-    vd[d] = __builtin_bit_cast(uint16_t, (_Float16)rp.v_new[(size_t)m * kvd + (size_t)kvh * DPH + d]);
+                   (size_t)kvh * DPH + j;
+    uint16_t* vd = kd + (size_t)bs * kvd;
+    float sn, cs;
+    sincosf(rope_angle(rp, pos, j), &sn, &cs);
+    kd[0] = __builtin_bit_cast(uint16_t, (_Float16)(x0 * cs - x1 * sn));
+    kd[HALF] = __builtin_bit_cast(uint16_t, (_Float16)(x0 * sn + x1 * cs));
+    vd[0] = __builtin_bit_cast(uint16_t, (_Float16)v0);
+    vd[HALF] = __builtin_bit_cast(uint16_t, (_Float16)v1);
   }
   __syncthreads();
 }
@@ -766,18 +759,19 @@ __device__ __forceinline__ void masked_pv(int ts, int q, int l16, int lim, const
 }
 
 // This lane's q operand (row l%16, features 32ks + 8(l/16) + e) from its
-// raw fp32 values: rotated by RoPE when cs (the row's (cos, sin) table
-// entries, feature-pair-indexed) is given -- the partner of feature f is
-// f +- dph/2, k-step ks +- KS/2 of the same lane -- then scaled into the
-// exp2 domain and split into fp16 hi and lo parts, stored to the
-// workgroup's q operand area: hi of k-step ks at qop[ks*64 + lane], lo at
-// qop[(KS + ks)*64 + lane].  Every wave of a workgroup serves the same rows
-// and stores the same bytes, so a wave reads back what it wrote (a wave's
-// LDS operations complete in order) whatever the other waves do: no
-// barrier.
+// raw fp32 values: rotated by RoPE when rq is given -- the wave first
+// writes the (cos, sin) table of its rows' queries (one sincos per lane and
+// query for dph 128) to tab, its own LDS, free until its first tile is
+// staged; the partner of feature f is f +- dph/2, k-step ks +- KS/2 of the
+// same lane -- then scaled into the exp2 domain and split into fp16 hi and
+// lo parts, stored to the workgroup's q operand area: hi of k-step ks at
+// qop[ks*64 + lane], lo at qop[(KS + ks)*64 + lane].  Every wave of a
+// workgroup serves the same rows and stores the same bytes, so a wave reads
+// back what it wrote (a wave's LDS operations complete in order) whatever
+// the other waves do: no barrier.
 template <int DPH>
 __device__ __forceinline__ void mfma_pack_q(const float2 (&qr)[MfmaShape<DPH>::KS][4], float sc,
-                                            const float2* cs, int lane, h8_t* qop) {
+                                            const QRope* rq, int lane, char* tab, h8_t* qop) {
   const int grp = lane >> 4;
   constexpr int KS = MfmaShape<DPH>::KS;
   float x[KS][8];
@@ -788,7 +782,17 @@ __device__ __forceinline__ void mfma_pack_q(const float2 (&qr)[MfmaShape<DPH>::K
       x[ks][2 * w] = qr[ks][w].x;
       x[ks][2 * w + 1] = qr[ks][w].y;
     }
-  if (cs) {
+  if (rq) {
+    constexpr int HALF = DPH / 2;
+    float2* ct = reinterpret_cast<float2*>(tab);
+    // entry t = query (t / HALF), pair t % HALF = lane % HALF (64 is a
+    // multiple of HALF)
+    for (int t = lane; t < rq->nm * HALF; t += 64) {
+      float sn, c;
+      sincosf(((float)(rq->p0 + t / HALF) / rq->pos_div) * rq->fr, &sn, &c);
+      ct[t] = make_float2(c, sn);
+    }
+    const float2* cs = ct + rq->mi * HALF;
 #pragma unroll
     for (int ks = 0; ks < KS / 2; ks++)
 #pragma unroll
@@ -835,7 +839,7 @@ struct MfmaWave {
 template <int DPH, int CHUNK, bool FIRST>
 __device__ __forceinline__ void mfma_chunk(const TileSource& src, const MfmaWave& w, int c0,
                                            const float2 (&qr)[MfmaShape<DPH>::KS][4], float qsc,
-                                           const float2* cs, float& m_run, float& l_run,
+                                           const QRope* rq, float& m_run, float& l_run,
                                            f4_t (&o)[MfmaShape<DPH>::DB], bool balance) {
   constexpr int SL = 512 / DPH, NLD = kTile / SL;
   char* vst = w.kst + MfmaShape<DPH>::TILEB;
@@ -856,7 +860,7 @@ __device__ __forceinline__ void mfma_chunk(const TileSource& src, const MfmaWave
     if (i + 1 < CHUNK)
       stream_load<DPH>(src, w.head_base, tn * kTile, w.sl, w.lane_off, w.chunk_off, false,
                        blk[nb], slot[nb], kbuf[nb]);
-    if (FIRST && i == 0) mfma_pack_q<DPH>(qr, qsc, cs, w.lane, w.qop);
+    if (FIRST && i == 0) mfma_pack_q<DPH>(qr, qsc, rq, w.lane, w.kst, w.qop);
     if (balance) {
       if (2 * i < CHUNK) __builtin_amdgcn_s_setprio(1);
       else __builtin_amdgcn_s_setprio(0);
@@ -890,14 +894,14 @@ __device__ __forceinline__ void mfma_chunk(const TileSource& src, const MfmaWave
 
 // A wave's tiles first, first+stride, ... < te of KV head kvh on the MFMA
 // path.  lim: last visible position of this lane's row (-1: a padding
-// row); wmin: the smallest lim over the wave's real rows.  qr, qsc, cs: the
-// lane's raw q values, their scale and RoPE table (mfma_pack_q); qop: the
+// row); wmin: the smallest lim over the wave's real rows.  qr, qsc, rq: the
+// lane's raw q values, their scale and RoPE (mfma_pack_q); qop: the
 // workgroup's q operand area.  st: this wave's LDS (K tile, then V tile).
 template <int DPH, int CHUNK>
 __device__ __forceinline__ void mfma_attend(const TileSource& src, int lane, int kvh, int first,
                                             int te, int stride, int lim, int wmin,
                                             const float2 (&qr)[MfmaShape<DPH>::KS][4], float qsc,
-                                            const float2* cs, char* st, h8_t* qop, float& m_run,
+                                            const QRope* rq, char* st, h8_t* qop, float& m_run,
                                             float& l_run, f4_t (&o)[MfmaShape<DPH>::DB],
                                             bool balance) {
   constexpr int CH = DPH / 8;
@@ -918,9 +922,9 @@ __device__ __forceinline__ void mfma_attend(const TileSource& src, int lane, int
   w.wmin = wmin;
   w.kst = st;
   w.qop = qop;
-  mfma_chunk<DPH, CHUNK, true>(src, w, first, qr, qsc, cs, m_run, l_run, o, balance);
+  mfma_chunk<DPH, CHUNK, true>(src, w, first, qr, qsc, rq, m_run, l_run, o, balance);
   for (int c0 = first + CHUNK * stride; c0 < te; c0 += CHUNK * stride)
-    mfma_chunk<DPH, CHUNK, false>(src, w, c0, qr, qsc, cs, m_run, l_run, o, balance);
+    mfma_chunk<DPH, CHUNK, false>(src, w, c0, qr, qsc, rq, m_run, l_run, o, balance);
   if (balance) __builtin_amdgcn_s_setprio(0);
 }
 
@@ -988,7 +992,6 @@ template <int DPH, int RPW, int CHUNK, int WAVES, bool ROPE = false, class Lds,
 __device__ __forceinline__ void stream_item(const AttnArgs& a, int part, int kvh, int rg,
                                             Lds& lds, int nwaves = WAVES,
                                             const RopeArgs* rp = nullptr,
-                                            float2* rope_cs = nullptr,
                                             const GatherArgs* ga = nullptr) {
   static_assert(DPH == 64 || DPH == 128, "head_dim");
   static_assert(RPW == 2 || RPW == 4 || RPW == 8 || RPW == 16, "rows per group");
@@ -1006,12 +1009,11 @@ __device__ __forceinline__ void stream_item(const AttnArgs& a, int part, int kvh
   const int te = part == a.n_parts - 1 ? n_tiles : min(n_tiles, tb + a.tiles_per_part);
 
   if constexpr (ROPE) {
-    rope_table<DPH>(*rp, a.pos_base, a.R / a.G, rope_cs);
     // A partition that reads window positions first writes the window's K
     // (rotated) and V slice of this KV head itself, so no other workgroup
     // has to finish first; partitions sharing the window write the same
-    // bytes.
-    if (te * kTile > a.pos_base) rope_append_slice<DPH>(a, *rp, rope_cs, kvh);
+    // bytes.  (q rotates in mfma_pack_q, behind the first tile loads.)
+    if (te * kTile > a.pos_base) rope_append_slice<DPH>(a, *rp, kvh);
   }
   if constexpr (GATHER) {
     // (as above: a partition reading window positions writes them first)
@@ -1032,6 +1034,8 @@ __device__ __forceinline__ void stream_item(const AttnArgs& a, int part, int kvh
     else
       qrow = a.q + (size_t)m * a.nh * DPH;
     const float2* qp = reinterpret_cast<const float2*>(qrow + (size_t)h * DPH + 8 * grp);
+    QRope rq_v;
+    if constexpr (ROPE) rq_v.fr = rp->inv_freq[lane % (DPH / 2)];  // (before q: see QRope)
     float2 qr[Mh::KS][4];
 #pragma unroll
     for (int ks = 0; ks < Mh::KS; ks++)
@@ -1051,8 +1055,15 @@ __device__ __forceinline__ void stream_item(const AttnArgs& a, int part, int kvh
           }
       }
     }
-    const float2* cs = nullptr;
-    if constexpr (ROPE) cs = rope_cs + m * (DPH / 2);
+    const QRope* rq = nullptr;
+    if constexpr (ROPE) {
+      const int m0 = r0 / a.G;
+      rq_v.pos_div = rp->pos_div;
+      rq_v.p0 = a.pos_base + m0;
+      rq_v.nm = (r0 + nrows - 1) / a.G - m0 + 1;
+      rq_v.mi = real ? m - m0 : 0;
+      rq = &rq_v;
+    }
     const int lim = real ? a.pos_base + (r0 + l16) / a.G : -1;
     const int wmin = a.pos_base + r0 / a.G;  // row r0 is the group's first query
     float m_run = -INFINITY, l_run = 0.f;
@@ -1063,7 +1074,7 @@ __device__ __forceinline__ void stream_item(const AttnArgs& a, int part, int kvh
     // runs at raised wave priority, so a wave past its midpoint yields issue
     // to the other wave of its SIMD that is behind.
     mfma_attend<DPH, CHUNK>(a.src, lane, kvh, tb + wave, te, nwaves, lim, wmin, qr,
-                            real ? a.qscale : 0.f, cs, lds.staging(wave), lds.qop, m_run, l_run,
+                            real ? a.qscale : 0.f, rq, lds.staging(wave), lds.qop, m_run, l_run,
                             o, a.row_groups > 1);
     const float l_row = groups_sum(l_run);
     // The staged tiles are dead: records go over them (DS operations of a
@@ -1317,7 +1328,7 @@ __device__ __forceinline__ void grid_items(const AttnArgs& a, const GatherArgs* 
       rg = unit / a.nkv;
     }
     stream_item<DPH, RPW, CHUNK, WAVES, false, MfmaLds<DPH, MaxWaves>, GATHER>(
-        a, part, kvh, rg, lds, WAVES, nullptr, nullptr, ga);
+        a, part, kvh, rg, lds, WAVES, nullptr, ga);
     if (it + n_blocks < items) __syncthreads();  // this item's readers of lds are done
   }
 }

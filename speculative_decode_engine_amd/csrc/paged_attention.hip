@@ -53,10 +53,9 @@ __global__ __launch_bounds__(64 * kStreamWaves) void attn_mfma_kernel(AttnArgs a
 template <int DPH, int RPW, int CHUNK>
 __global__ __launch_bounds__(64 * kStreamWaves) void attn_rope_kernel(AttnArgs a, RopeArgs rp) {
   __shared__ MfmaLds<DPH, kStreamWaves> lds;
-  __shared__ float2 rope_cs[kRopeMaxQueries * (DPH / 2)];
   const int3 w = stream_coords<CHUNK>();
   stream_item<DPH, RPW, CHUNK, kStreamWaves, true, MfmaLds<DPH, kStreamWaves>, false, true>(
-      a, w.x, w.y, w.z, lds, kStreamWaves, &rp, rope_cs);
+      a, w.x, w.y, w.z, lds, kStreamWaves, &rp);
 }
 
 }  // namespace attn
