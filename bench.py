@@ -54,6 +54,7 @@ CONFIG_WORKLOAD = {"llama3_8b_4k_decode": "llama3_8b_verify",
                    "llama3_8b_4k_attn": "llama3_8b_verify",
                    "llama3_8b_verify_fused": "llama3_8b_verify",
                    "llama3_8b_4k_decode_fused": "llama3_8b_verify",
+                   "tinyllama_decode_fused": "tinyllama",
                    "qwen25_7b_selfspec_verify": "qwen25_7b_selfspec",
                    "qwen25_7b_selfspec_draft": "qwen25_7b_selfspec",
                    "qwen25_7b_selfspec_verify_fused": "qwen25_7b_selfspec"}
@@ -765,7 +766,8 @@ def main():
         modes = {"llama3_8b_verify": "verify", "llama3_8b_4k_decode": "decode",
                  "llama3_8b_4k_attn": "attn", "llama3_8b_verify_fused": "verify_fused",
                  "llama3_8b_4k_decode_fused": "decode_fused", "tiny": "decode",
-                 "tinyllama": "decode", "qwen25_7b_selfspec_verify": "verify",
+                 "tinyllama": "decode", "tinyllama_decode_fused": "decode_fused",
+                 "qwen25_7b_selfspec_verify": "verify",
                  "qwen25_7b_selfspec_draft": "decode",
                  "qwen25_7b_selfspec_verify_fused": "verify_fused", HEADLINE: "attn"}
         wl = W.CONFIGS[CONFIG_WORKLOAD.get(args.only, args.only)]
@@ -804,6 +806,8 @@ def main():
                                                   decf["us_per_layer_step"], 3)
         for name in ("tiny", "tinyllama"):
             configs[name] = bench_config(torch, W, W.CONFIGS[name], steps, warmup, "decode")
+        configs["tinyllama_decode_fused"] = bench_config(torch, W, W.CONFIGS["tinyllama"], steps,
+                                                         warmup, "decode_fused")
         w5 = W.CONFIGS["qwen25_7b_selfspec"]
         configs["qwen25_7b_selfspec_verify"] = bench_config(torch, W, w5, steps, warmup, "verify")
         configs["qwen25_7b_selfspec_draft"] = bench_config(torch, W, w5, steps, warmup, "decode")
