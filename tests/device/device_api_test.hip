@@ -197,6 +197,12 @@ __global__ void stochastic_grid_kernel(const float* tl, const float* dl, const i
   if (threadIdx.x == 0) status[blockIdx.x] = st;
 }
 
+// sde::attn::rope_sincos (the fused RoPE step's sin / cos) over n angles.
+__global__ void rope_sincos_kernel(const float* x, float* sn, float* cs, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) sde::attn::rope_sincos(x[i], sn[i], cs[i]);
+}
+
 int status_of(hipError_t e) { return e == hipSuccess ? 0 : 6; }
 
 }  // namespace
@@ -362,6 +368,12 @@ int sdet_grid_matvec(const float* x, const uint16_t* W, float* out, int d_in, in
   if (blocks < 1 || threads < 64 || threads % 64 != 0 || threads > 1024) return 1;
   grid_matvec_kernel<<<blocks, threads, 0, (hipStream_t)stream>>>(
       x, W, out, d_in, d_out, M, accumulate, ws, ws_bytes, status);
+  return status_of(hipGetLastError());
+}
+
+int sdet_rope_sincos(const float* x, float* sn, float* cs, int n, void* stream) {
+  if (n < 1) return 1;
+  rope_sincos_kernel<<<(n + 255) / 256, 256, 0, (hipStream_t)stream>>>(x, sn, cs, n);
   return status_of(hipGetLastError());
 }
 

@@ -7,13 +7,16 @@ Oracle: oracle.rope_rotate_half_f64 (rope_apply_inplace, model.cu:281-323,
 with the library's stated frequency rule) rotates q and k in float64.
   * V rows of the window: bit-exact fp16 (RNE) of v.
   * K rows: within one fp16 ulp of the float64-rotated k rounded to fp16
-    (the kernel rotates in fp32 with sincosf; the reference's fast-math
-    fp32 RoPE is not reproducible bit for bit), and at least 99 % exact.
+    (the kernel rotates in fp32 with rope_sincos -- a reduction by 2 pi,
+    then the hardware's sin / cos, pinned against float64 below; the
+    reference's fast-math fp32 RoPE is not reproducible bit for bit), and at
+    least 99 % exact.
   * Every other pool byte unchanged.
   * Output within 2e-3 abs + 1e-2 rel of fp64 attention of the rotated q
     over the context and the window rows the kernel stored.
 """
 import ctypes
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -151,3 +154,44 @@ def test_fused_argument_errors_do_no_device_work(gpu):
     torch.cuda.synchronize()
     assert torch.isnan(out).all() and torch.equal(cache.pool, before)
     cache.free()
+
+
+def test_rope_sincos_against_float64(gpu):
+    """sde::attn::rope_sincos, the fused step's sin / cos (Cody-Waite
+    reduction by 2 pi, then the hardware's sin / cos of the revolutions;
+    sincosf from 2^17 on), against float64 sin / cos of the same fp32
+    angles: every angle the step forms for positions up to 2^17 + 2^12 at
+    the benchmark models' frequencies (dph 64 and 128, theta 1e4, 5e5, 1e6),
+    random angles of either sign, points around multiples of pi/2 (where
+    the reduction's cancellation is largest) and large angles."""
+    lib = ctypes.CDLL(str(Path(__file__).resolve().parent / "device" / "libsde_device_test.so"))
+    lib.sdet_rope_sincos.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_int, ctypes.c_void_p]
+    lib.sdet_rope_sincos.restype = ctypes.c_int
+    rng = np.random.default_rng(7)
+    pos = np.arange(0, 2 ** 17 + 2 ** 12, 7, dtype=np.float32)
+    parts = []
+    for theta in (1e4, 5e5, 1e6):
+        for dph in (64, 128):
+            inv = (theta ** (-np.arange(0, dph, 2, dtype=np.float64) / dph)).astype(np.float32)
+            parts.append((pos[:, None] * inv[None, :]).ravel())
+    k = np.arange(-40000, 40000, dtype=np.float64)
+    near = (k * (np.pi / 2)).astype(np.float32)
+    parts += [rng.uniform(-2.0 ** 17, 2.0 ** 17, 1 << 20).astype(np.float32), near,
+              np.nextafter(near, np.float32(np.inf)), np.nextafter(near, np.float32(-np.inf)),
+              rng.uniform(2.0 ** 17, 1e7, 1 << 16).astype(np.float32)]
+    x = np.concatenate(parts).astype(np.float32)
+    case_banner("rope_sincos", x.size)
+    xt = torch.from_numpy(x).cuda()
+    sn = torch.empty_like(xt)
+    cs = torch.empty_like(xt)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    assert lib.sdet_rope_sincos(xt.data_ptr(), sn.data_ptr(), cs.data_ptr(), x.size, stream) == 0
+    torch.cuda.synchronize()
+    x64 = x.astype(np.float64)
+    es = np.abs(sn.cpu().numpy().astype(np.float64) - np.sin(x64))
+    ec = np.abs(cs.cpu().numpy().astype(np.float64) - np.cos(x64))
+    small = np.abs(x) < 2.0 ** 17
+    print(f"rope_sincos max abs error: below 2^17 sin {es[small].max():.3g} cos "
+          f"{ec[small].max():.3g}; above sin {es[~small].max():.3g} cos {ec[~small].max():.3g}")
+    assert es[small].max() <= 1e-6 and ec[small].max() <= 1e-6
+    assert es[~small].max() <= 2e-7 and ec[~small].max() <= 2e-7
