@@ -223,10 +223,12 @@ __device__ __forceinline__ float rope_angle(const RopeArgs& rp, int pos, int j) 
 // r = x - k (C1 + C2 + C3) with 2 pi = C1 + C2 + C3 to 2e-14 (C1 = 201/32 and
 // C2 = 507 * 2^-18 short enough that every partial difference is exact for
 // |x| < 2^17, C3 = the fp32 remainder), then r / 2 pi, within [-0.51, 0.51].
-// Before the hardware step the error is at most 4.2e-7 (checked against
-// float64 over 4.3M angles below 2^17); the reference's fast-math sinf /
-// cosf (model.cu:308-309 under --use_fast_math) reduce nothing at all.
-// Angles of 2^17 or more take sincosf.
+// Measured error at most 4.3e-7 against float64 (sincosf: ~6e-8), nearly
+// all of it the reduction's and the revolution product's rounding
+// (tests/test_gpu_fused_rope.py, test_rope_sincos_against_float64); the
+// reference's fast-math sinf / cosf (model.cu:308-309 under
+// --use_fast_math) reduce nothing at all.  Angles of 2^17 or more take
+// sincosf.
 __device__ __forceinline__ void rope_sincos(float x, float& sn, float& cs) {
   if (fabsf(x) < 131072.f) {
     constexpr float kInv2Pi = 0x1.45f306p-3f;
