@@ -244,7 +244,8 @@ __device__ __forceinline__ void rope_sincos(float x, float& sn, float& cs) {
   }
 }
 
-// Window rows the fused path supports.
+// Window rows the fused entry point takes (a speculative window is k + 1
+// rows; each wave's rotation table covers only its own group's queries).
 constexpr int kRopeMaxQueries = 32;
 
 // RoPE of a wave's q rows (mfma_pack_q): the window queries its rows
@@ -546,7 +547,7 @@ __device__ __forceinline__ int slice_arrive(uint32_t* ctr, uint32_t prev, int n_
 // The window's rows (positions pos_base .. pos_base+M-1) of KV head kvh:
 // k rotated by RoPE, k and v rounded to fp16 (RNE) into the pool
 // (kv_cache_append, kv_cache.cu:70-93), by the whole workgroup, one thread
-// per (row, rotation pair) -- its k pair, v pair and sincos, all loads
+// per (row, rotation pair) -- its k pair, v pair and rope_sincos, all loads
 // issued together; returns once the stores are visible to the workgroup's
 // loads.
 template <int DPH>
@@ -787,8 +788,8 @@ __device__ __forceinline__ void masked_pv(int ts, int q, int l16, int lim, const
 
 // This lane's q operand (row l%16, features 32ks + 8(l/16) + e) from its
 // raw fp32 values: rotated by RoPE when rq is given -- the wave first
-// writes the (cos, sin) table of its rows' queries (one sincos per lane and
-// query for dph 128) to tab, its own LDS, free until its first tile is
+// writes the (cos, sin) table of its rows' queries (one rope_sincos per lane
+// and query for dph 128) to tab, its own LDS, free until its first tile is
 // staged; the partner of feature f is f +- dph/2, k-step ks +- KS/2 of the
 // same lane -- then scaled into the exp2 domain and split into fp16 hi and
 // lo parts, stored to the workgroup's q operand area: hi of k-step ks at
