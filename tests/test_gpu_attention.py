@@ -168,6 +168,18 @@ def test_long_context_windows(gpu, oracle, nh, nkv, dph, M):
              f"long {nh}/{nkv} dph{dph} M{M}")
 
 
+@pytest.mark.parametrize("nh,nkv,dph,bs,ctx,M", [(28, 4, 128, 32, 8192, 9),
+                                                 (32, 8, 128, 16, 16384, 5)])
+def test_plans_with_extra_tiles(gpu, oracle, nh, nkv, dph, bs, ctx, M):
+    """Windows whose plan leaves one tile per wave or less past its whole
+    partitions (the Qwen2.5-7B 9-query window over 8K keys: 257 tiles on 16
+    partitions of 16; a 5-query window over 16K: 513 on 16 of 32): those
+    tiles go to the first partition, the window stays in the last."""
+    case_banner("extra tiles", nh, nkv, dph, bs, ctx, M)
+    run_case(oracle, nh, nkv, dph, bs, ctx, M, -(-(ctx + M) // bs) + 5, ctx + M,
+             f"extra tiles {nh}/{nkv} ctx{ctx} M{M}")
+
+
 @pytest.mark.parametrize("bs", [8, 16, 32, 64, 128])
 @pytest.mark.parametrize("dph", [64, 128])
 def test_block_sizes(gpu, oracle, bs, dph):

@@ -62,6 +62,7 @@ CASES = [
     (8, 8, 128, 8, 30, 4, 0, 1.0, 10000.0),        # window across a tile boundary
     (8, 2, 64, 16, 0, 32, 0, 1.0, 10000.0),        # empty context, 32-row window
     (32, 8, 128, 16, 17000, 5, 0, 1.0, 500000.0),  # window past 16K keys: 16-row groups
+    (32, 8, 128, 16, 16384, 5, 0, 1.0, 500000.0),  # 513 tiles: the extra one in partition 0
     # one q head per KV head: a 16-row group spans 16 window queries, the
     # largest per-wave (cos, sin) table (16 queries x dph/2 pairs)
     (8, 8, 128, 16, 17000, 20, 0, 1.0, 500000.0),
