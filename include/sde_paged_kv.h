@@ -309,8 +309,10 @@ typedef struct sde_rope_config {
  * the projections BEFORE RoPE (not modified).  q and k are rotated by
  * rotate-half RoPE at positions pos_base+m (rope_apply_inplace,
  * model.cu:281-323: pair (j, j+dph/2), angle = pos' * theta^(-2j/dph), the
- * frequencies computed in double precision and rounded to fp32; the
- * rotation in fp32), k and v are appended (fp16 RNE) at those positions,
+ * frequencies computed in double precision and rounded to fp32; the angle
+ * and the rotation in fp32, sin / cos within 4.3e-7 of float64 -- for head
+ * sizes 64 / 128 a 2 pi reduction and the hardware's sin / cos, sincosf
+ * otherwise), k and v are appended (fp16 RNE) at those positions,
  * and query m attends causally to [0, pos_base+m].  Same shapes, limits,
  * workspace and errors as sde_paged_attention, plus SDE_ERR_INVALID_ARGUMENT
  * for a NULL d_k / d_v / rope, an unknown scaling type, or unaligned
