@@ -1312,10 +1312,24 @@ __host__ __device__ inline int stream_rows(int R, int L_max) {
 // with two tiles per wave 15.9 us, one 8-row group with one 15.6 us).
 __host__ __device__ inline StreamPlan stream_plan8(int L_max, int nkv, int R, int blocks) {
   const int rows = stream_rows(R, L_max);
-  const StreamPlan p = stream_plan(L_max, nkv, R, blocks, 8, 4, rows);
-  if (rows >= 16 || R <= rows) return p;
-  const StreamPlan w = stream_plan(L_max, nkv, R, blocks, 8, 4, 2 * rows);
-  return w.tiles_per_part < p.tiles_per_part ? w : p;
+  StreamPlan p = stream_plan(L_max, nkv, R, blocks, 8, 4, rows);
+  if (rows < 16 && R > rows) {
+    const StreamPlan w = stream_plan(L_max, nkv, R, blocks, 8, 4, 2 * rows);
+    if (w.tiles_per_part < p.tiles_per_part) p = w;
+  }
+  // Then half-size groups (down to 2 rows) when each wave keeps its tiles
+  // and the grid still fits one workgroup per CU: more workgroups pull the
+  // same K/V (measured on MI355X: TinyLlama's 8 rows per KV head at 2K in
+  // groups of 2 instead of 4, attention 6.98 -> 6.84 us, fused step 7.36 ->
+  // 7.25; groups that would take more tiles per wave, such as the Qwen2.5-7B
+  // draft step's, measured 11.9 -> 13.8 and are not taken).
+  if (p.rpw >= 4 && R > 2) {
+    const StreamPlan h = stream_plan(L_max, nkv, R, blocks, 8, 4, p.rpw / 2);
+    if (h.tiles_per_part <= p.tiles_per_part &&
+        (int64_t)nkv * h.row_groups * h.n_parts <= blocks)
+      p = h;
+  }
+  return p;
 }
 
 // Rows per group of the 4-wave device functions: 4 (decode of up to 4 q
