@@ -529,8 +529,8 @@ def cpu_model() -> str:
 
 def cpu_step(W, w, mode, seconds, reps_min=5):
     """One layer-step of `mode` (bench_config's modes) at workload w's shape
-    on the CPU, BASELINE.md's torch-CPU restatement of the reference
-    semantics (oracle.attention_torch_cpu: block-table index_select gather,
+    on the CPU, the torch-CPU restatement of the reference semantics that
+    the baseline names (oracle.attention_torch_cpu: block-table index_select gather,
     fp32 q.K^T * dph^-1/2, causal mask, softmax, .V; the window's append as
     an fp32 -> fp16 scatter into the pool), torch on cpu_threads() threads.
     2 warm-ups, then at least reps_min repetitions and about `seconds`;
@@ -732,7 +732,8 @@ def main():
     args = parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); this build's "
-              "path is single-GPU, see DESIGN.md for how it would shard.", file=sys.stderr)
+              "path is single-GPU (the design notes describe how it would shard).",
+              file=sys.stderr)
         sys.exit(2)
     import torch
     from speculative_decode_engine_amd import _native
