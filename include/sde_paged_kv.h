@@ -240,6 +240,17 @@ int sde_paged_attention_noalloc(sde_kv_cache* cache, int layer, const float* d_q
  * parallelism changes.  Returns the previous value (the default is 16384). */
 uint32_t sde_debug_set_slice_spin(uint32_t polls);
 
+/* Test hook, no counterpart in the reference: the plan the tile path of
+ * sde_paged_attention / sde_rope_append_attention takes for total_len keys,
+ * nkv KV heads, `rows` = n_queries * (nh / nkv) rows per KV head, on a
+ * device of n_cus compute units (host arithmetic only, no device call):
+ * out[0] rows per group, out[1] row groups, out[2] tiles per wave in flight,
+ * out[3] tiles per partition, out[4] partitions, out[5] the partition count
+ * the workspace of sde_paged_attention_workspace_size(.., total_len) is
+ * sized for.  SDE_ERR_INVALID_ARGUMENT for a non-positive size or a NULL
+ * out. */
+int sde_debug_attention_plan(int total_len, int nkv, int rows, int n_cus, int32_t out[6]);
+
 /* Greedy acceptance + O(1) rewind of speculative decoding on the device,
  * with no host round trip (the reference's host loop kernels.cu:2428-2466
  * copies the tokens back and rewinds from the host; its megakernel does it

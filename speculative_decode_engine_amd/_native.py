@@ -180,6 +180,8 @@ PROTOTYPES = {
     "sde_paged_attention_noalloc": (_c_int, [_vp, _c_int, _vp, _vp, _c_int, _c_int, _c_int,
                                              _c_int, _c_int, _vp]),
     "sde_debug_set_slice_spin": (ctypes.c_uint32, [ctypes.c_uint32]),
+    "sde_debug_attention_plan": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                                ctypes.c_int, ctypes.POINTER(ctypes.c_int32)]),
     "sde_spec_accept_stochastic": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int,
                                             ctypes.c_float, ctypes.c_float, ctypes.c_uint64, _vp,
                                             _c_int, _c_int, _vp, _vp]),

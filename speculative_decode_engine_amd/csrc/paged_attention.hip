@@ -329,6 +329,18 @@ uint32_t sde_debug_set_slice_spin(uint32_t polls) {
   return g_slice_spin.exchange(polls == 0 ? 0u : polls, std::memory_order_relaxed);
 }
 
+int sde_debug_attention_plan(int total_len, int nkv, int rows, int n_cus, int32_t* out) {
+  if (total_len < 1 || nkv < 1 || rows < 1 || n_cus < 1 || !out) return SDE_ERR_INVALID_ARGUMENT;
+  const StreamPlan p = plan_for(total_len, nkv, rows, n_cus);
+  out[0] = p.rpw;
+  out[1] = p.row_groups;
+  out[2] = p.chunk;
+  out[3] = p.tiles_per_part;
+  out[4] = p.n_parts;
+  out[5] = parts_bound(total_len);
+  return SDE_OK;
+}
+
 int sde_attention_dispatch(int attn_type, sde_kv_cache* cache, int layer,
                            const float* d_q, float* d_out, int nh, int nkv,
                            int dph, int pos_base, int n_queries,
