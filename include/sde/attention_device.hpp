@@ -1112,10 +1112,17 @@ __device__ __forceinline__ void stream_item(const AttnArgs& a, int part, int kvh
     for (int db = 0; db < Mh::DB; db++) o[db] = f4_t{0.f, 0.f, 0.f, 0.f};
     // Several row groups per KV head: the first half of every chunk's tiles
     // runs at raised wave priority, so a wave past its midpoint yields issue
-    // to the other wave of its SIMD that is behind.
+    // to the other wave of its SIMD that is behind -- for chunks of up to 3
+    // tiles, and in the plain kernel for groups of fewer than 16 rows only.
+    // Measured on MI355X (two runs each, us): a 5-query window over 16K keys
+    // (16-row groups, chunks of 4) 29.0 -> 27.4 without, fused 26.7 -> 25.3;
+    // the Qwen2.5-7B window (16-row groups, chunks of 2) 19.6 -> 19.2
+    // without, but fused 17.7 with against 18.2 without; the 4K window and
+    // TinyLlama (groups of 8 and 2) slower without.
+    constexpr bool kBalanceable = CHUNK < 4 && (ROPE || RPW < 16);
     mfma_attend<DPH, CHUNK>(a.src, lane, kvh, tb + wave, te, nwaves, lim, wmin, qr,
                             real ? a.qscale : 0.f, rq, lds.staging(wave), lds.qop, m_run, l_run,
-                            o, a.row_groups > 1);
+                            o, kBalanceable && a.row_groups > 1);
     const float l_row = groups_sum(l_run);
     // The staged tiles are dead: records go over them (DS operations of a
     // wave complete in order).
