@@ -291,6 +291,15 @@ struct AttnArgs {
 constexpr int kStreamWaves = 8;      // waves per workgroup of libsde_paged's kernel
 constexpr int kStreamMaxParts = 64;  // partitions per (KV head, row group)
 constexpr int kSliceRows = 4;        // rows per slice of a split combine (stream_item)
+
+// Rows per slice for groups of RPW rows: 16-row groups in 2-row slices (8,
+// the most the arrival word's give-up bits track), the others in 4-row
+// slices (measured on MI355X, two boxes: the Qwen2.5-7B window 19.3 ->
+// 19.1-19.3 us, fused 18.0-18.5 -> 17.9, a 5-query window over 16K keys
+// 27.4-27.7 -> 27.1-27.4; 2-row slices of the decodes' 4-row groups
+// measured slower).
+template <int RPW>
+constexpr int slice_rows() { return RPW == 16 ? 2 : kSliceRows; }
 constexpr uint32_t kSliceSpinLimit = 1u << 14;  // polls of a slice's wait (~10 ms)
 
 // Device-scope (agent) relaxed atomic accesses for the partition partials.
@@ -1007,8 +1016,8 @@ __device__ __forceinline__ void gather_append_slice(const AttnArgs& a, const Gat
 // the normalised output (one partition) or publish a partial and count the
 // arrival; the last arrival combines all partitions (with WAVES waves).
 // SPLIT (libsde_paged's kernels, one item per workgroup, arrival counters
-// a line apart): a group of more than kSliceRows rows is combined in
-// slices of up to kSliceRows rows, slice s by the workgroup that arrived s
+// a line apart): a group of more than slice_rows rows is combined in
+// slices of up to slice_rows rows, slice s by the workgroup that arrived s
 // places before the last -- the last arrival takes slice 0 at once, the
 // ones before it wait (bounded) for it -- so several CUs read the partials
 // at once (one CU reads them at ~35 GB/s); see slice_arrive.
@@ -1187,7 +1196,8 @@ __device__ __forceinline__ void stream_item(const AttnArgs& a, int part, int kvh
   // Slices of a split combine (SPLIT, counters a line apart).
   int n_slices = 1;
   if constexpr (SPLIT)
-    if (a.ctr_stride > 1) n_slices = min((nrows + kSliceRows - 1) / kSliceRows, a.n_parts);
+    if (a.ctr_stride > 1)
+      n_slices = min((nrows + slice_rows<RPW>() - 1) / slice_rows<RPW>(), a.n_parts);
   if (tid == 0) {
     uint32_t* ctr = a.counters + ((size_t)kvh * a.row_groups + rg) * a.ctr_stride;
     const uint32_t prev =
