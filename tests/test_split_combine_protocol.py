@@ -87,6 +87,34 @@ def test_every_interleaving_combines_each_slice_once_and_resets(n_parts):
     assert checked > 0
 
 
+@pytest.mark.parametrize("n_parts", [8, 9, 16, 64])
+def test_sampled_interleavings_up_to_eight_slices(n_parts):
+    """16-row groups combine in up to eight 2-row slices (the give-up bits
+    track ranks 1-7): seeded random arrival orders and final operations."""
+    import random
+    rng = random.Random(n_parts)
+    checked = 0
+    for n_slices in range(5, min(n_parts, 8) + 1):
+        for _ in range(400):
+            order = list(range(n_parts))
+            rng.shuffle(order)
+            at = {wg: i for i, wg in enumerate(order)}
+            finals = {}
+            for i, wg in enumerate(order):
+                if 1 <= n_parts - 1 - i < n_slices:
+                    opts = [("give", t + 0.5) for t in range(at[wg], n_parts - 1)]
+                    opts += [(k, n_parts - 1 + d) for k in ("pass", "give") for d in (0.25, 0.75)]
+                    finals[wg] = rng.choice(opts)
+            r = run(n_parts, n_slices, order, finals)
+            if r is None:
+                continue
+            done, word, after_reset = r
+            assert done == list(range(n_slices)), (order, finals)
+            assert word == 0 and not after_reset, (order, finals)
+            checked += 1
+    assert checked > 100
+
+
 def test_a_wrong_reset_rule_is_caught():
     """The checks have teeth: with the last arrival clearing the word at
     once, a waiter polling for every arrival can only give up, and its
