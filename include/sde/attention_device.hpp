@@ -292,14 +292,15 @@ constexpr int kStreamWaves = 8;      // waves per workgroup of libsde_paged's ke
 constexpr int kStreamMaxParts = 64;  // partitions per (KV head, row group)
 constexpr int kSliceRows = 4;        // rows per slice of a split combine (stream_item)
 
-// Rows per slice for groups of RPW rows: 16-row groups in 2-row slices (8,
-// the most the arrival word's give-up bits track), the others in 4-row
-// slices (measured on MI355X, two boxes: the Qwen2.5-7B window 19.3 ->
-// 19.1-19.3 us, fused 18.0-18.5 -> 17.9, a 5-query window over 16K keys
-// 27.4-27.7 -> 27.1-27.4; 2-row slices of the decodes' 4-row groups
-// measured slower).
+// Rows per slice for groups of RPW rows: groups of 8 and 16 rows in 2-row
+// slices (at most 8, the most the arrival word's give-up bits track), the
+// decodes' 4-row groups whole (measured on MI355X, two boxes: the
+// Qwen2.5-7B window 19.3 -> 19.1-19.3 us, fused 18.0-18.5 -> 17.9, a
+// 5-query window over 16K keys 27.4-27.7 -> 27.1-27.4, the Qwen2.5-7B
+// draft step's 7-row group 14.2 -> 14.1, the 4K windows unchanged; 2-row
+// slices of the decodes' 4-row groups measured slower).
 template <int RPW>
-constexpr int slice_rows() { return RPW == 16 ? 2 : kSliceRows; }
+constexpr int slice_rows() { return RPW >= 8 ? 2 : kSliceRows; }
 constexpr uint32_t kSliceSpinLimit = 1u << 14;  // polls of a slice's wait (~10 ms)
 
 // Device-scope (agent) relaxed atomic accesses for the partition partials.
