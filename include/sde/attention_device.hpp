@@ -1335,12 +1335,20 @@ __host__ __device__ inline StreamPlan stream_plan8(int L_max, int nkv, int R, in
     const StreamPlan w = stream_plan(L_max, nkv, R, blocks, 8, 4, 2 * rows);
     if (w.tiles_per_part < p.tiles_per_part) p = w;
   }
-  // Then half-size groups (down to 2 rows) when each wave keeps its tiles
-  // and the grid still fits one workgroup per CU: more workgroups pull the
-  // same K/V (measured on MI355X: TinyLlama's 8 rows per KV head at 2K in
-  // groups of 2 instead of 4, attention 6.98 -> 6.84 us, fused step 7.36 ->
-  // 7.25; groups that would take more tiles per wave, such as the Qwen2.5-7B
-  // draft step's, measured 11.9 -> 13.8 and are not taken).
+  return p;
+}
+
+// libsde_paged's plan (host side): stream_plan8's, then half-size groups
+// (down to 2 rows) when each wave keeps its tiles and the grid still fits
+// one workgroup per CU: more workgroups pull the same K/V (measured on
+// MI355X: TinyLlama's 8 rows per KV head at 2K in groups of 2 instead of 4,
+// attention 6.98 -> 6.84 us, fused step 7.36 -> 7.25; groups that would
+// take more tiles per wave, such as the Qwen2.5-7B draft step's, measured
+// 11.9 -> 13.8 and are not taken).  The grid device function keeps
+// stream_plan8: every block computes its plan, and the third candidate's
+// registers made its largest item variant spill.
+inline StreamPlan stream_plan8_spread(int L_max, int nkv, int R, int blocks) {
+  StreamPlan p = stream_plan8(L_max, nkv, R, blocks);
   if (p.rpw >= 4 && R > 2) {
     const StreamPlan h = stream_plan(L_max, nkv, R, blocks, 8, 4, p.rpw / 2);
     if (h.tiles_per_part <= p.tiles_per_part &&

@@ -185,7 +185,7 @@ int sde_measure_attention_loads(const sde_kv_cache* cache, int layer, int nh, in
   for (int b = 0; b < nblk; b++)
     if (table[b] < 0 || table[b] >= v.pool_blocks) return SDE_ERR_CAPACITY;
   const int R = n_queries * (nh / nkv);
-  const StreamPlan p = stream_plan8(L_max, nkv, R, n_cus);
+  const StreamPlan p = stream_plan8_spread(L_max, nkv, R, n_cus);
   AttnArgs a{};
   a.src.pool = v.pool;
   a.src.table = v.block_tables + (size_t)layer * v.max_blocks_per_layer;

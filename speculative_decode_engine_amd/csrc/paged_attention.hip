@@ -77,7 +77,7 @@ int parts_bound(int max_total_len) {
 
 // The plan of a call: 8-wave workgroups, one per CU.
 StreamPlan plan_for(int L_max, int nkv, int R, int n_cus) {
-  return stream_plan8(L_max, nkv, R, n_cus);
+  return stream_plan8_spread(L_max, nkv, R, n_cus);
 }
 
 // Polls of a split combine's wait (sde_debug_set_slice_spin).
