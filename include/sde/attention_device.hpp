@@ -1424,7 +1424,8 @@ __device__ __forceinline__ void grid_dispatch4(const AttnArgs& a, int rpw,
     grid_items<DPH, 16, 2, 4, MaxWaves, GATHER>(a, ga);
 }
 
-// 8-wave blocks: the plans of libsde_paged's kernel (2-16 rows per group,
+// 8-wave blocks: stream_plan8, libsde_paged's plans without the host's
+// half-size rule (2-16 rows per group,
 // 1-4 tiles per wave in flight; a wave with one tile and a chunk of two
 // loads and multiplies a second, masked tile: measured on MI355X at the 4K
 // decode, 15.3 against 11.8 us with a chunk of one).
